@@ -1,0 +1,90 @@
+/*
+ * TEST INFRASTRUCTURE ONLY.  A CPU restatement of inference.rs's GGUF QMatMul
+ * arithmetic for Q8_0, Q4_K, Q6_K (and the Q8_K activation blocks), used as the
+ * checker for the HIP library.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  Nothing in the product links it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the inference.rs repository root).
+ */
+#ifndef QMM_ORACLE_H
+#define QMM_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* crates/inference-tensor/src/quantized/k_quants.rs:22-31 */
+#define OR_QK_K 256
+#define OR_QK8_0 32
+
+/* crates/inference-tensor/src/quantized/k_quants.rs:152-157 */
+typedef struct { uint16_t d; int8_t qs[32]; } or_block_q8_0;
+/* k_quants.rs:188-195 */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } or_block_q4k;
+/* k_quants.rs:208-215 */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } or_block_q6k;
+/* k_quants.rs:217-223 */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } or_block_q8k;
+
+/* GGUF type ids, crates/inference-tensor/src/quantized/mod.rs:582-603 */
+enum { OR_Q8_0 = 8, OR_Q4K = 12, OR_Q6K = 14, OR_Q8K = 15 };
+
+/* IEEE binary16 conversions, round to nearest even (the `half` crate 2.7.1's f16::from_f32 / to_f32) */
+uint16_t oracle_f32_to_f16(float f);
+float oracle_f16_to_f32(uint16_t h);
+
+/* bytes per block and values per block for a GGUF type id (mod.rs:669-703); 0 for an unknown id */
+size_t oracle_type_size(int type);
+size_t oracle_block_size(int type);
+
+/* quantizers (weights and activations) */
+float oracle_quantize_block32(const float *x, int8_t *qs);                  /* mod.rs:43-56 */
+void oracle_quantize_q8_0(const float *x, int64_t n, or_block_q8_0 *y);     /* k_quants.rs:923-949 */
+void oracle_quantize_q8k(const float *x, int64_t n, or_block_q8k *y);       /* k_quants.rs:2721-2760 */
+void oracle_quantize_q4k(const float *x, int64_t n, or_block_q4k *y);       /* k_quants.rs:1930-2001 */
+void oracle_quantize_q6k(const float *x, int64_t n, or_block_q6k *y);       /* k_quants.rs:2590-2646 */
+/* generic: quantize n values (multiple of the block size) of `type` into `out` */
+int oracle_quantize(int type, const float *x, int64_t n, void *out);
+
+/* dequantizers */
+void oracle_dequantize(int type, const void *blocks, int64_t n, float *y);
+
+/* vec_dot_unopt: one weight row (nblk blocks) against one activation row */
+float oracle_vec_dot_q8_0_q8_0(int64_t n, const or_block_q8_0 *x, const or_block_q8_0 *y); /* k_quants.rs:982-999 */
+float oracle_vec_dot_q4k_q8k(int64_t n, const or_block_q4k *x, const or_block_q8k *y);     /* k_quants.rs:1848-1928 */
+float oracle_vec_dot_q6k_q8k(int64_t n, const or_block_q6k *x, const or_block_q8k *y);     /* k_quants.rs:2518-2575 */
+
+/* k_quants::matmul (k_quants.rs:2776-2894): dst[m][n] = vec_dot(W row n, Q8(lhs row m)).
+ * `threads` <= 0 uses every available thread. Returns 0, or -1 on a bad type/shape. */
+int oracle_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const void *rhs, float *dst,
+                  int threads);
+
+/* The same with the activations already quantized (Q8_K rows for K-quants, Q8_0 rows for Q8_0). */
+int oracle_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const void *lhs_q, const void *rhs, float *dst,
+                       int threads);
+
+/* Expert-indexed matmul, the contract of QuantMethod::gather_forward
+ * (crates/inference-quant/src/gguf/mod.rs:573-608, cpu.rs:23-104, quantized/mod.rs:1457-1461):
+ * y[b][s][:] = W[ids[b][s]] . Q8(x[b][s % xdim1][:]),  W [E, n, k], x [batch, xdim1, k], ids [batch, topk],
+ * y [batch, topk, n].  xdim1 is 1 or topk.  Returns -1 on an out-of-range expert id. */
+int oracle_indexed_moe(int type, int64_t n_experts, int64_t n, int64_t k, const void *w, const float *x,
+                       int64_t batch, int64_t xdim1, int64_t topk, const uint32_t *ids, float *y, int threads);
+
+/* moe_dispatch (crates/inference-quant/kernels/cuda/moe_dispatch/moe_dispatch.cu:8-104): expert_bounds[E+1]
+ * exclusive prefix of route counts; sorted_token_ids[pos] = flat route, sorted_source_ids[pos] = route / topk,
+ * routes of one expert in ascending order (the stable order; the GPU may order within an expert freely). */
+int oracle_moe_dispatch(const int32_t *topk_ids, int32_t total, int32_t n_experts, int32_t topk,
+                        int32_t *expert_bounds, int32_t *sorted_token_ids, int32_t *sorted_source_ids);
+
+/* moe_weighted_reduce_flat (moe_dispatch.cu:106-154): out[t][h] = sum_s w[t][s] * in[t][s][h] */
+void oracle_moe_weighted_reduce(const float *in, const float *w, float *out, int32_t tokens, int32_t hidden,
+                                int32_t topk);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

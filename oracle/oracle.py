@@ -1,0 +1,171 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes front end of the C oracle (oracle.c).
+
+The checker for the HIP library.  Only tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` may import this module.  It restates
+inference.rs's CPU QMatMul (crates/inference-tensor/src/quantized/k_quants.rs);
+each C function cites the lines it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+# GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603)
+Q8_0, Q4K, Q6K, Q8K = 8, 12, 14, 15
+
+# block layouts (k_quants.rs:152-223), as numpy structured dtypes
+BLOCK_DTYPES = {
+    Q8_0: np.dtype([("d", "<u2"), ("qs", "i1", 32)]),
+    Q4K: np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", 12), ("qs", "u1", 128)]),
+    Q6K: np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("scales", "i1", 16), ("d", "<u2")]),
+    Q8K: np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)]),
+}
+BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+TYPE_SIZE = {t: d.itemsize for t, d in BLOCK_DTYPES.items()}
+ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "liboracle.so"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+        L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f16_to_f32.restype = ctypes.c_float
+        L.oracle_quantize_block32.argtypes = [vp, vp]
+        L.oracle_quantize_block32.restype = ctypes.c_float
+        L.oracle_quantize.argtypes = [ctypes.c_int, vp, i64, vp]
+        L.oracle_dequantize.argtypes = [ctypes.c_int, vp, i64, vp]
+        L.oracle_matmul.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, ctypes.c_int]
+        L.oracle_matmul_preq.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, ctypes.c_int]
+        L.oracle_indexed_moe.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, i64, i64, i64, vp, vp, ctypes.c_int]
+        L.oracle_moe_dispatch.argtypes = [vp, i32, i32, i32, vp, vp, vp]
+        L.oracle_moe_weighted_reduce.argtypes = [vp, vp, vp, i32, i32, i32]
+        for name in ("oracle_vec_dot_q8_0_q8_0", "oracle_vec_dot_q4k_q8k", "oracle_vec_dot_q6k_q8k"):
+            getattr(L, name).argtypes = [i64, vp, vp]
+            getattr(L, name).restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().oracle_f32_to_f16(float(x)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().oracle_f16_to_f32(int(h)))
+
+
+def quantize_block32(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.shape == (32,)
+    qs = np.zeros(32, dtype=np.int8)
+    d = lib().oracle_quantize_block32(_p(x), _p(qs))
+    return np.float32(d), qs
+
+
+def quantize(gtype: int, x: np.ndarray) -> np.ndarray:
+    """Quantize a float32 array (last dim a multiple of the block size) into a uint8 byte array of blocks."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size
+    bs = BLOCK_SIZE[gtype]
+    assert x.shape[-1] % bs == 0
+    out = np.zeros(n // bs * TYPE_SIZE[gtype], dtype=np.uint8)
+    rc = lib().oracle_quantize(gtype, _p(x), n, _p(out))
+    assert rc == 0
+    return out.reshape(x.shape[:-1] + (x.shape[-1] // bs * TYPE_SIZE[gtype],))
+
+
+def blocks(gtype: int, data: np.ndarray) -> np.ndarray:
+    """View quantized bytes as structured blocks."""
+    return np.ascontiguousarray(data).reshape(-1).view(BLOCK_DTYPES[gtype])
+
+
+def dequantize(gtype: int, data: np.ndarray, n: int) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    y = np.zeros(n, dtype=np.float32)
+    lib().oracle_dequantize(gtype, _p(data), n, _p(y))
+    return y
+
+
+def vec_dot(gtype: int, k: int, w_row: np.ndarray, a_row: np.ndarray) -> float:
+    name = {Q8_0: "oracle_vec_dot_q8_0_q8_0", Q4K: "oracle_vec_dot_q4k_q8k", Q6K: "oracle_vec_dot_q6k_q8k"}[gtype]
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    a_row = np.ascontiguousarray(a_row, dtype=np.uint8)
+    return float(getattr(lib(), name)(k, _p(w_row), _p(a_row)))
+
+
+def matmul(gtype: int, x: np.ndarray, w: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    """The reference CPU QMatMul: x [m, k] f32 against quantized weight bytes of n rows -> [m, n] f32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    assert w.size == n * k // BLOCK_SIZE[gtype] * TYPE_SIZE[gtype]
+    dst = np.zeros((m, n), dtype=np.float32)
+    rc = lib().oracle_matmul(gtype, m, k, n, _p(x), _p(w), _p(dst), threads)
+    assert rc == 0
+    return dst
+
+
+def matmul_preq(gtype: int, a_q: np.ndarray, m: int, k: int, w: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    a_q = np.ascontiguousarray(a_q, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    dst = np.zeros((m, n), dtype=np.float32)
+    rc = lib().oracle_matmul_preq(gtype, m, k, n, _p(a_q), _p(w), _p(dst), threads)
+    assert rc == 0
+    return dst
+
+
+def indexed_moe(gtype: int, w: np.ndarray, n_experts: int, n: int, k: int, x: np.ndarray, ids: np.ndarray,
+                threads: int = 0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    batch, xdim1, kk = x.shape
+    assert kk == k
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    topk = ids.shape[1]
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    y = np.zeros((batch, topk, n), dtype=np.float32)
+    rc = lib().oracle_indexed_moe(gtype, n_experts, n, k, _p(w), _p(x), batch, xdim1, topk, _p(ids), _p(y), threads)
+    assert rc == 0, "bad expert id or shape"
+    return y
+
+
+def moe_dispatch(topk_ids: np.ndarray, n_experts: int, topk: int):
+    ids = np.ascontiguousarray(topk_ids, dtype=np.int32).reshape(-1)
+    total = ids.size
+    bounds = np.zeros(n_experts + 1, dtype=np.int32)
+    tok = np.zeros(total, dtype=np.int32)
+    src = np.zeros(total, dtype=np.int32)
+    rc = lib().oracle_moe_dispatch(_p(ids), total, n_experts, topk, _p(bounds), _p(tok), _p(src))
+    assert rc == 0
+    return bounds, tok, src
+
+
+def moe_weighted_reduce(inp: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    inp = np.ascontiguousarray(inp, dtype=np.float32)
+    tokens, topk, hidden = inp.shape
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    out = np.zeros((tokens, hidden), dtype=np.float32)
+    lib().oracle_moe_weighted_reduce(_p(inp), _p(weights), _p(out), tokens, hidden, topk)
+    return out
