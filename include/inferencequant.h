@@ -1,0 +1,168 @@
+/*
+ * libinferencequant.so -- the C ABI of the MI355X (gfx950) GGUF quantized-linear kernels.
+ *
+ * Every entry point has the argument list of the inference.rs kernel-library symbol it replaces
+ * (crates/inference-quant/src/gguf/ffi.rs, bound through inference_tensor::kernel_library!,
+ * crates/inference-tensor/src/kernel_library.rs:315-393).  Pointers are device pointers unless
+ * noted; `stream` is a hipStream_t (null = the default stream).  The caller owns every buffer and
+ * no entry point allocates device memory, as in the reference.
+ *
+ * Activation blocks.  The reference quantizes activations to Q8_1 on the GPU; its CPU QMatMul -- the
+ * parity oracle -- uses Q8_K blocks for K-quant weights and Q8_0 blocks for Q8_0 weights
+ * (k_quants.rs:2824-2830).  This library quantizes exactly as that CPU path does, so the quantize
+ * launchers are named for the block they write (q8k / q8_0) and keep the Q8_1 launchers' argument
+ * lists.  `vy` / `y` buffers are produced and consumed only inside this library.
+ *
+ *   decode layout (launch_mmvq_gguf_quantize_*):   row r = blocks [r * stride_col_y, ...), each block
+ *       a qmm_block_q8k (292 B per 256 values) or qmm_block_q8_0 (34 B per 32 values) as in qmm_blocks.h.
+ *   prefill layout (launch_mmq_quantize_*):        per channel, for ne1 rows and nsb = ne0 / 256
+ *       256-value chunks: qs[nsb][ne1][256] int8, then d[nsb][ne1], then
+ *         Q8_K: d f32, bsums[nsb][ne1][16] int16         (292 B per 256 values)
+ *         Q8_0: d f16 [nsb][ne1][8] (one per 32 values)  (272 B per 256 values)
+ *       i.e. ne0 * ne1 * 292 / 256 (Q8_K) or ne0 * ne1 * 272 / 256 (Q8_0) bytes per channel.
+ *
+ * Errors.  A launcher given arguments it cannot serve launches nothing, records a message readable
+ * with qmm_last_error(), and (for the int-returning ones) returns a nonzero code.  The reference's
+ * launchers are void and unchecked (gguf/cuda.rs:187-193 checks only the reduce); its Rust callers
+ * validate shapes first, as the C++ host (inference.rs_amd/host) does here.
+ */
+#ifndef INFERENCEQUANT_H
+#define INFERENCEQUANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Build id every kernel library exports (kernel_library.rs:8, 288-297). */
+extern const char inference_kernel_build_id[];
+
+/* Last error recorded on the calling host thread, "" if none; cleared by qmm_clear_error().
+ * No counterpart in the reference, whose launchers report nothing. */
+const char *qmm_last_error(void);
+void qmm_clear_error(void);
+
+/* ------------------------------------------------------------------ decode activation quantizers
+ * Replace launch_mmvq_gguf_quantize_q8_1_{bf16,f16,f32} (gguf/ffi.rs:602-630; kernel
+ * mmvq_gguf/mmvq_quantize.cu:10-145).  x: num_rows rows of kx values (row stride kx);
+ * vy: num_rows rows of kx_padded values in blocks, zero beyond kx.  kx_padded is a multiple of 256
+ * (q8k) or 32 (q8_0) and at least kx; stride_col_y of the matvec = kx_padded / block size.
+ * Q8_K: BlockQ8K::from_float (k_quants.rs:2721-2760); Q8_0: quantize_block32 (quantized/mod.rs:41-56).
+ * Both bit-exact with the reference CPU quantizers. */
+void launch_mmvq_gguf_quantize_q8k_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream);
+void launch_mmvq_gguf_quantize_q8k_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream);
+void launch_mmvq_gguf_quantize_q8k_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream);
+void launch_mmvq_gguf_quantize_q8_0_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream);
+void launch_mmvq_gguf_quantize_q8_0_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream);
+void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows,
+                                         void *stream);
+
+/* ------------------------------------------------------------------ decode matvec
+ * launch_mmvq_gguf_<t>_{bf16,f16,f32}_plain (gguf/ffi.rs:846-876; kernel mmvq_gguf.cuh:650-759,
+ * 1762-1834).  dst[j * stride_col_dst + row] = sum_k W[row, k] * Q(y_j)[k] for j < b_size, row < nrows_x;
+ * vx = nrows_x rows of ncols_x / block values (GGUF bytes); vy = b_size activation rows from the
+ * decode quantizer above, stride_col_y blocks apart.  The dtype suffix is dst's element type.
+ * b_size 1..16 (the reference's plain launcher takes 1..8, its tensor-core one up to 16). */
+#define QMM_DECLARE_MMVQ_PLAIN(t)                                                                                 \
+  void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream);         \
+  void launch_mmvq_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream);         \
+  void launch_mmvq_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,   \
+                                         int stride_col_y, int stride_col_dst, int b_size, void *stream);
+QMM_DECLARE_MMVQ_PLAIN(q8_0)
+QMM_DECLARE_MMVQ_PLAIN(q4_k)
+QMM_DECLARE_MMVQ_PLAIN(q6_k)
+
+/* ------------------------------------------------------------------ MoE decode matvec
+ * launch_mmvq_gguf_<t>_moe (gguf/ffi.rs:877-893; kernel mmvq_gguf.cuh:961-1038, 1600-1643).
+ * For routed pair p < n_pairs: expert e = ids[p] (u32), activation row p / y_div of vy (stride_col_y
+ * blocks apart), weights vx_gate + e * expert_stride bytes.
+ *   vx_up == NULL: dst[p * nrows_x + row] = W_gate[e] . y
+ *   vx_up != NULL: dst[p * nrows_x + row] = act(W_gate[e] . y) * (W_up[e] . y), activation 0 = SiLU,
+ *                  1 = GELU (tanh form), 2 = ReLU (inference-quant/kernels/cuda/glu_activation.cuh).
+ * `grouped` only orders the grid in the reference (pairs sharing an expert run together); accepted, and
+ * the gfx950 grid always walks pairs innermost. */
+#define QMM_DECLARE_MMVQ_MOE(t)                                                                               \
+  void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, \
+                                  const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \
+                                  int y_div, int n_pairs, int activation, int grouped, void *stream);
+QMM_DECLARE_MMVQ_MOE(q8_0)
+QMM_DECLARE_MMVQ_MOE(q4_k)
+QMM_DECLARE_MMVQ_MOE(q6_k)
+
+/* ------------------------------------------------------------------ prefill activation quantizers
+ * Replace launch_mmq_quantize_q8_1_{D4,DS4,D2S6} (gguf/ffi.rs:657-700; kernel mmq_gguf/mmq_quantize.cu:
+ * 98-195, 395-415), same arguments: x of type_x (0 f32, 1 f16, 30 bf16); output row i1 < ne1 of channel
+ * (i2, i3) reads input row ids ? ids[i1] : i1 at x + i3*s03 + i2*s02 + row*s01 (element strides), ne00 valid
+ * values, zero up to ne0 (a multiple of 256).  Output: the prefill layout above. */
+void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                             void *stream);
+void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                              int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                              void *stream);
+
+/* ------------------------------------------------------------------ prefill matmul
+ * launch_mmq_gguf_<t> (gguf/ffi.rs:902-918; host fast_mmq.rs:446-524, 604-715; kernel mmq_instance.cuh:
+ * 217-256, mmq_gguf.cuh:3533-3875).  dst[col * stride_col_dst + row] for row < nrows_x (weight rows),
+ * col < ncols_y (activation rows); x = weight rows of stride_row_x blocks; y = prefill-layout activations
+ * with ne0 = ncols_x padded to 256 and ne1 = ncols_y.  type_dst 0 f32, 1 f16, 30 bf16.  tmp_fixup, cc,
+ * nsm, smpbo and warp_size are the reference's device hints: accepted, unused (tmp_fixup may be NULL). */
+#define QMM_DECLARE_MMQ(t)                                                                                     \
+  void launch_mmq_gguf_##t(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,          \
+                           int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc, \
+                           int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream);                  \
+  void launch_mmq_gguf_##t##_moe(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,        \
+                                 const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,     \
+                                 int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,               \
+                                 int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,        \
+                                 int warp_size, void *stream);
+QMM_DECLARE_MMQ(q8_0)
+QMM_DECLARE_MMQ(q4_k)
+QMM_DECLARE_MMQ(q6_k)
+/* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
+ * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
+ * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by
+ * the quantizer's ids); column c of the grouped product is written to dst[ids_dst[c] * stride_col_dst + row]
+ * (f32).  ncols_max bounds the rows of any one expert. */
+
+/* ------------------------------------------------------------------ op-level indexed MoE
+ * Replace launch_indexed_moe_forward_{q8_0,q4k,q6k}_q8_1 (gguf/ffi.rs:90-147; kernel indexed_moe.cu:
+ * 664-1000; host gguf/cuda.rs:271-498), same arguments, activations from the decode quantizer:
+ * all_outputs[(b * topk + s) * n + row] = W[indices[b * topk + s]][row] . Q(x[b * input_dim1 + (input_dim1 == 1 ?
+ * 0 : s)]) with W [E, n, k] GGUF bytes, inputs rows k_padded values apart (k_padded / block blocks). */
+void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream);
+void launch_indexed_moe_forward_q4k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream);
+void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream);
+
+/* ------------------------------------------------------------------ MoE dispatch and reduce
+ * launch_moe_dispatch (gguf/ffi.rs:227-238; moe_dispatch.cu:78-104): expert_bounds[num_experts + 1],
+ * sorted_token_ids[pos] = flat route index, sorted_source_ids[pos] = route / topk, grouped by expert.
+ * expert_counts / expert_cursors: caller-owned int32[num_experts] scratch. */
+void launch_moe_dispatch(const int32_t *topk_ids, int32_t *expert_bounds, int32_t *sorted_token_ids,
+                         int32_t *sorted_source_ids, int total_assignments, int num_experts, int topk,
+                         int32_t *expert_counts, int32_t *expert_cursors, void *stream);
+
+/* launch_moe_weighted_reduce_flat* (gguf/ffi.rs:240-276; moe_dispatch.cu:47-154):
+ * out[t][h] = sum over slots s with w[t][s] != 0 of in[t][s][h] * w[t][s].  Returns 0 or a hipError_t. */
+int launch_moe_weighted_reduce_flat(const void *inputs, const float *topk_weights, void *outputs, int num_tokens,
+                                    int hidden, int topk, void *stream);
+int launch_moe_weighted_reduce_flat_bf16(const void *inputs, const float *topk_weights, void *outputs,
+                                         int num_tokens, int hidden, int topk, void *stream);
+int launch_moe_weighted_reduce_flat_f16_input(const void *inputs, const float *topk_weights, void *outputs,
+                                              int num_tokens, int hidden, int topk, void *stream);
+int launch_moe_weighted_reduce_flat_bf16_input(const void *inputs, const float *topk_weights, void *outputs,
+                                               int num_tokens, int hidden, int topk, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

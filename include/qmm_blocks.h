@@ -1,0 +1,96 @@
+/*
+ * GGUF block layouts and type ids for the quantized-linear path (Q8_0, Q4_K, Q6_K weights;
+ * Q8_0 and Q8_K activation blocks).  Plain C so the C ABI, the C++ host and the HIP kernels
+ * share one definition.
+ *
+ * Layouts follow crates/inference-tensor/src/quantized/k_quants.rs:152-223 byte for byte, since
+ * weights arrive as GGUF bytes; type ids follow quantized/mod.rs:582-603.
+ */
+#ifndef QMM_BLOCKS_H
+#define QMM_BLOCKS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define QMM_QK_K 256
+#define QMM_QK8_0 32
+
+/* GGUF type ids (GgmlDType::to_u32, quantized/mod.rs:605-624) */
+enum qmm_ggml_type {
+  QMM_TYPE_F32 = 0,
+  QMM_TYPE_F16 = 1,
+  QMM_TYPE_Q8_0 = 8,
+  QMM_TYPE_Q4K = 12,
+  QMM_TYPE_Q6K = 14,
+  QMM_TYPE_Q8K = 15,
+  QMM_TYPE_BF16 = 30,
+};
+
+/* BlockQ8_0: f16 scale, 32 int8 values; 34 bytes (k_quants.rs:152-157) */
+typedef struct {
+  uint16_t d;
+  int8_t qs[32];
+} qmm_block_q8_0;
+
+/* BlockQ4K: f16 d, f16 dmin, 12 bytes of packed 6-bit scales/mins, 128 bytes of nibbles; 144 bytes
+ * (k_quants.rs:188-195).  qs[32c + l]: low nibble = value 64c + l, high nibble = value 64c + 32 + l. */
+typedef struct {
+  uint16_t d;
+  uint16_t dmin;
+  uint8_t scales[12];
+  uint8_t qs[128];
+} qmm_block_q4k;
+
+/* BlockQ6K: low 4 bits, high 2 bits, int8 scale per 16 values, f16 d; 210 bytes (k_quants.rs:208-215) */
+typedef struct {
+  uint8_t ql[128];
+  uint8_t qh[64];
+  int8_t scales[16];
+  uint16_t d;
+} qmm_block_q6k;
+
+/* BlockQ8K: f32 d, 256 int8 values, int16 sums of each 16; 292 bytes (k_quants.rs:217-223) */
+typedef struct {
+  float d;
+  int8_t qs[256];
+  int16_t bsums[16];
+} qmm_block_q8k;
+
+#ifdef __cplusplus
+static_assert(sizeof(qmm_block_q8_0) == 34, "BlockQ8_0 is 34 bytes");
+static_assert(sizeof(qmm_block_q4k) == 144, "BlockQ4K is 144 bytes");
+static_assert(sizeof(qmm_block_q6k) == 210, "BlockQ6K is 210 bytes");
+static_assert(sizeof(qmm_block_q8k) == 292, "BlockQ8K is 292 bytes");
+#else
+_Static_assert(sizeof(qmm_block_q8_0) == 34, "BlockQ8_0 is 34 bytes");
+_Static_assert(sizeof(qmm_block_q4k) == 144, "BlockQ4K is 144 bytes");
+_Static_assert(sizeof(qmm_block_q6k) == 210, "BlockQ6K is 210 bytes");
+_Static_assert(sizeof(qmm_block_q8k) == 292, "BlockQ8K is 292 bytes");
+#endif
+
+/* bytes per block and values per block (GgmlDType::type_size / block_size, quantized/mod.rs:669-703) */
+static inline size_t qmm_type_size(int t) {
+  switch (t) {
+    case QMM_TYPE_F32: return 4;
+    case QMM_TYPE_F16: case QMM_TYPE_BF16: return 2;
+    case QMM_TYPE_Q8_0: return 34;
+    case QMM_TYPE_Q4K: return 144;
+    case QMM_TYPE_Q6K: return 210;
+    case QMM_TYPE_Q8K: return 292;
+    default: return 0;
+  }
+}
+
+static inline size_t qmm_block_size(int t) {
+  switch (t) {
+    case QMM_TYPE_F32: case QMM_TYPE_F16: case QMM_TYPE_BF16: return 1;
+    case QMM_TYPE_Q8_0: return 32;
+    case QMM_TYPE_Q4K: case QMM_TYPE_Q6K: case QMM_TYPE_Q8K: return 256;
+    default: return 0;
+  }
+}
+
+/* the activation block type a weight type is dotted with (GgmlType::VecDotType) */
+static inline int qmm_vec_dot_type(int t) { return t == QMM_TYPE_Q8_0 ? QMM_TYPE_Q8_0 : QMM_TYPE_Q8K; }
+
+#endif

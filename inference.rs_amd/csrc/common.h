@@ -1,0 +1,89 @@
+// Shared device and host helpers for the gfx950 GGUF kernels (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmm_blocks.h"
+
+#define QMM_WAVE 64
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------------ host-side error reporting
+void qmm_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// ------------------------------------------------------------------ scalar conversions (device)
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);  // exact
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32: round to nearest even
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                             // round to nearest even
+  return (uint16_t)(u >> 16);
+}
+
+// Rust's `f32 as i8`: saturating, NaN -> 0
+__device__ __forceinline__ int32_t sat_i8(float v) {
+  if (v != v) return 0;
+  v = v < -128.0f ? -128.0f : v;
+  v = v > 127.0f ? 127.0f : v;
+  return (int32_t)v;
+}
+
+// Element loads of the three activation dtypes.
+struct in_f32 {
+  typedef float T;
+  static __device__ __forceinline__ float load(const float *p, int64_t i) { return p[i]; }
+};
+struct in_f16 {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const uint16_t *p, int64_t i) { return f16_bits_to_f32(p[i]); }
+};
+struct in_bf16 {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const uint16_t *p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+};
+
+// Output stores.
+struct out_f32 {
+  typedef float T;
+  static __device__ __forceinline__ void store(float *p, int64_t i, float v) { p[i] = v; }
+};
+struct out_f16 {
+  typedef uint16_t T;
+  static __device__ __forceinline__ void store(uint16_t *p, int64_t i, float v) { p[i] = f32_to_f16_bits(v); }
+};
+struct out_bf16 {
+  typedef uint16_t T;
+  static __device__ __forceinline__ void store(uint16_t *p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+};
+
+// ------------------------------------------------------------------ wave64 reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, QMM_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Bytes [shift, shift + 4) of the 8-byte little-endian pair (lo, hi), shift in 0..3.
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {
+  return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+static inline int64_t qmm_ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

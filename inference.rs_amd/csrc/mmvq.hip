@@ -1,0 +1,314 @@
+// Decode matvec for GGUF Q8_0 / Q4_K / Q6_K weights against Q8_0 / Q8_K activations (b = 1..16 rows),
+// plus the expert-indexed MoE matvec (optionally fused gate/up with the GLU activation).
+//
+// Replaces mmvq_gguf.cuh:650-759 (mmvq_core_impl) and its launchers (1542-1553, 1647-1702, 1762-1834),
+// mmvq_gguf.cuh:961-1038 / 1600-1643 (MoE) and indexed_moe.cu:664-1000, all in
+// crates/inference-quant/kernels/cuda/.  HBM-bound: each wave owns R consecutive weight rows; its 64 lanes
+// stride over the rows' units (units.h), issue every 16-byte weight load of the R rows before using any,
+// dot them with v_dot4 against activation units read once per column, and reduce each row with a wave
+// butterfly.  Activations are tiny and hit L2.
+#include "common.h"
+#include "inferencequant.h"
+#include "units.h"
+
+namespace {
+
+constexpr int kWaves = 4;  // waves per workgroup
+
+template <class U, class Out, int NC, int R>
+__global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ vy,
+                                              typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
+                                              int nunits, int64_t act_row_bytes, int stride_col_dst) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
+  if (row0 >= nrows) return;  // whole wave
+  float acc[R][NC];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < NC; j++) acc[r][j] = 0.0f;
+
+  for (int u = lane; u < nunits; u += QMM_WAVE) {
+    typename U::W w[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int row = min(row0 + r, nrows - 1);  // a short last group re-reads its last row; never stored
+      U::load_w(vx + (int64_t)row * row_bytes, u, w[r]);
+    }
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      typename U::A a;
+      U::load_a(vy + (int64_t)j * act_row_bytes, u, a);
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r][j] += U::dot(w[r], a, u);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      const float v = wave_sum(acc[r][j]);
+      if (lane == 0 && row0 + r < nrows) Out::store(dst, (int64_t)j * stride_col_dst + row0 + r, v);
+    }
+}
+
+// GLU activations (inference-quant/kernels/cuda/glu_activation.cuh): 0 SiLU, 1 GELU (tanh), 2 ReLU
+__device__ __forceinline__ float glu_act(int activation, float g) {
+  switch (activation) {
+    case 1: {
+      const float c = 0.7978845608028654f;  // sqrt(2 / pi)
+      return 0.5f * g * (1.0f + tanhf(c * (g + 0.044715f * g * g * g)));
+    }
+    case 2: return g > 0.0f ? g : 0.0f;
+    default: return g / (1.0f + expf(-g));
+  }
+}
+
+// MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's
+// weights through L2.  dst[p * nrows + row] = W_gate[ids[p]] . y[p / y_div]  (or act(gate) * up).
+template <class U, int R, bool GLU>
+__global__ __launch_bounds__(256) void k_mmvq_moe(const uint8_t *__restrict__ vx_gate, const uint8_t *__restrict__ vx_up,
+                                                  int64_t expert_stride, const uint8_t *__restrict__ vy,
+                                                  const uint32_t *__restrict__ ids, float *__restrict__ dst, int nrows,
+                                                  int64_t row_bytes, int nunits, int64_t act_row_bytes, int y_div,
+                                                  int activation) {
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x;
+  const int row0 = (blockIdx.y * kWaves + (threadIdx.x >> 6)) * R;
+  if (row0 >= nrows) return;
+  const int64_t e = ids[pair];
+  const uint8_t *wg = vx_gate + e * expert_stride;
+  const uint8_t *wu = GLU ? vx_up + e * expert_stride : nullptr;
+  const uint8_t *act = vy + (int64_t)(pair / y_div) * act_row_bytes;
+  float ag[R], au[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) ag[r] = au[r] = 0.0f;
+  for (int u = lane; u < nunits; u += QMM_WAVE) {
+    typename U::W w[R], w2[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int row = min(row0 + r, nrows - 1);
+      U::load_w(wg + (int64_t)row * row_bytes, u, w[r]);
+      if (GLU) U::load_w(wu + (int64_t)row * row_bytes, u, w2[r]);
+    }
+    typename U::A a;
+    U::load_a(act, u, a);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      ag[r] += U::dot(w[r], a, u);
+      if (GLU) au[r] += U::dot(w2[r], a, u);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float g = wave_sum(ag[r]);
+    float v = g;
+    if (GLU) v = glu_act(activation, g) * wave_sum(au[r]);
+    if (lane == 0 && row0 + r < nrows) dst[(int64_t)pair * nrows + row0 + r] = v;
+  }
+}
+
+template <class U, class Out, int NC>
+void launch_nc(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
+               int stride_col_dst, hipStream_t s) {
+  constexpr int R = NC <= 2 ? 4 : 2;
+  const dim3 grid((unsigned)qmm_ceil_div(nrows, kWaves * R));
+  k_mmvq<U, Out, NC, R><<<grid, 256, 0, s>>>(vx, vy, dst, nrows, U::row_bytes(k), U::units(k), act_row_bytes,
+                                             stride_col_dst);
+}
+
+template <class U, class Out>
+void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
+                 int stride_col_dst, int b, hipStream_t s) {
+  // up to 8 columns per pass; weights are re-streamed once per further pass
+  for (int j0 = 0; j0 < b; j0 += 8) {
+    const int nc = b - j0 < 8 ? b - j0 : 8;
+    const uint8_t *y = vy + (int64_t)j0 * act_row_bytes;
+    typename Out::T *d = dst + (int64_t)j0 * stride_col_dst;
+    switch (nc) {
+      case 1: launch_nc<U, Out, 1>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 2: launch_nc<U, Out, 2>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 3: launch_nc<U, Out, 3>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 4: launch_nc<U, Out, 4>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 5: launch_nc<U, Out, 5>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 6: launch_nc<U, Out, 6>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 7: launch_nc<U, Out, 7>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      default: launch_nc<U, Out, 8>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+    }
+  }
+}
+
+// Shape checks shared by the plain and MoE launchers. Returns false (and records why) when the
+// arguments cannot be served.
+bool check_mmvq(const char *who, int type, const void *vx, int ncols_x, int nrows_x, int stride_col_y, int b) {
+  const int bs = (int)qmm_block_size(type);
+  const int abs_ = type == QMM_TYPE_Q8_0 ? 32 : 256;
+  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0) {
+    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x, bs);
+    return false;
+  }
+  if ((int64_t)stride_col_y * abs_ < ncols_x) {
+    qmm_set_error("%s: stride_col_y=%d blocks holds fewer than ncols_x=%d values", who, stride_col_y, ncols_x);
+    return false;
+  }
+  if (b < 0 || b > 16) {
+    qmm_set_error("%s: b_size=%d outside 1..16", who, b);
+    return false;
+  }
+  const uintptr_t align = type == QMM_TYPE_Q4K ? 16 : (type == QMM_TYPE_Q8_0 ? 2 : 2);
+  if ((uintptr_t)vx % align != 0) {
+    qmm_set_error("%s: weight pointer not %zu-byte aligned", who, (size_t)align);
+    return false;
+  }
+  return true;
+}
+
+template <class Out>
+void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_y,
+           int stride_col_dst, int b, void *stream, const char *who) {
+  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, stride_col_y, b)) return;
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+  typename Out::T *d = (typename Out::T *)dst;
+  switch (type) {
+    case QMM_TYPE_Q4K:
+      launch_cols<unit_q4k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
+      break;
+    case QMM_TYPE_Q6K:
+      launch_cols<unit_q6k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
+      break;
+    default:  // Q8_0
+      if (ncols_x % 64 == 0 && stride_col_y % 2 == 0 && (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0)
+        launch_cols<unit_q8_0, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 34, stride_col_dst, b, s);
+      else
+        launch_cols<unit_q8_0_odd, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 34, stride_col_dst, b, s);
+      break;
+  }
+}
+
+template <class U>
+void moe_launch(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
+                float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int y_div, int n_pairs, int activation,
+                hipStream_t s) {
+  constexpr int R = 2;
+  const dim3 grid((unsigned)n_pairs, (unsigned)qmm_ceil_div(nrows_x, kWaves * R));
+  if (vx_up)
+    k_mmvq_moe<U, R, true><<<grid, 256, 0, s>>>((const uint8_t *)vx_gate, (const uint8_t *)vx_up, expert_stride,
+                                                (const uint8_t *)vy, (const uint32_t *)ids, dst, nrows_x,
+                                                U::row_bytes(ncols_x), U::units(ncols_x), act_row_bytes, y_div,
+                                                activation);
+  else
+    k_mmvq_moe<U, R, false><<<grid, 256, 0, s>>>((const uint8_t *)vx_gate, nullptr, expert_stride,
+                                                 (const uint8_t *)vy, (const uint32_t *)ids, dst, nrows_x,
+                                                 U::row_bytes(ncols_x), U::units(ncols_x), act_row_bytes, y_div,
+                                                 activation);
+}
+
+void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
+         float *dst, int ncols_x, int nrows_x, int stride_col_y, int y_div, int n_pairs, int activation,
+         void *stream, const char *who) {
+  if (!check_mmvq(who, type, vx_gate, ncols_x, nrows_x, stride_col_y, 1)) return;
+  if (n_pairs < 0 || y_div <= 0 || activation < 0 || activation > 2 || expert_stride < 0) {
+    qmm_set_error("%s: n_pairs=%d y_div=%d activation=%d expert_stride=%lld", who, n_pairs, y_div, activation,
+                  (long long)expert_stride);
+    return;
+  }
+  if (n_pairs == 0) return;
+  if (n_pairs > 65535 * 1024) {
+    qmm_set_error("%s: n_pairs=%d too large", who, n_pairs);
+    return;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (type) {
+    case QMM_TYPE_Q4K:
+      if (expert_stride % 16 != 0 || (vx_up && (uintptr_t)vx_up % 16 != 0)) {
+        qmm_set_error("%s: Q4_K expert_stride / vx_up not 16-byte aligned", who);
+        return;
+      }
+      moe_launch<unit_q4k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
+      break;
+    case QMM_TYPE_Q6K:
+      moe_launch<unit_q6k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
+      break;
+    default: {
+      const bool fast = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
+                        (uintptr_t)vx_gate % 4 == 0 && (!vx_up || (uintptr_t)vx_up % 4 == 0) && (uintptr_t)vy % 4 == 0;
+      if (fast)
+        moe_launch<unit_q8_0>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                              (int64_t)stride_col_y * 34, y_div, n_pairs, activation, s);
+      else
+        moe_launch<unit_q8_0_odd>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                                  (int64_t)stride_col_y * 34, y_div, n_pairs, activation, s);
+    }
+  }
+}
+
+void indexed(int type, const void *w, const void *x, const uint32_t *ids, float *out, int n, int k, int batch,
+             int topk, int k_padded, int input_dim1, void *stream, const char *who) {
+  if (batch < 0 || topk <= 0 || (input_dim1 != 1 && input_dim1 != topk) || k_padded < k) {
+    qmm_set_error("%s: batch=%d topk=%d input_dim1=%d k=%d k_padded=%d", who, batch, topk, input_dim1, k, k_padded);
+    return;
+  }
+  const int abs_ = type == QMM_TYPE_Q8_0 ? 32 : 256;
+  if (k_padded % abs_ != 0) {
+    qmm_set_error("%s: k_padded=%d not a multiple of %d", who, k_padded, abs_);
+    return;
+  }
+  const int64_t expert_stride = (int64_t)n * (k / (int)qmm_block_size(type)) * (int64_t)qmm_type_size(type);
+  moe(type, w, nullptr, expert_stride, x, ids, out, k, n, k_padded / abs_, input_dim1 == 1 ? topk : 1, batch * topk,
+      0, stream, who);
+}
+
+}  // namespace
+
+#define QMM_DEFINE_PLAIN(t, TYPE)                                                                                 \
+  void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
+    plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
+                   "mmvq_" #t "_f32");                                                                            \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
+    plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
+                   "mmvq_" #t "_f16");                                                                            \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,   \
+                                         int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
+    plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
+                    "mmvq_" #t "_bf16");                                                                          \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy,  \
+                                  const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \
+                                  int y_div, int n_pairs, int activation, int grouped, void *stream) {            \
+    (void)grouped;                                                                                                \
+    moe(TYPE, vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, stride_col_y, y_div, n_pairs,        \
+        activation, stream, "mmvq_" #t "_moe");                                                                   \
+  }
+
+extern "C" {
+QMM_DEFINE_PLAIN(q8_0, QMM_TYPE_Q8_0)
+QMM_DEFINE_PLAIN(q4_k, QMM_TYPE_Q4K)
+QMM_DEFINE_PLAIN(q6_k, QMM_TYPE_Q6K)
+
+void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q8_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q8_0");
+}
+void launch_indexed_moe_forward_q4k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q4K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q4k");
+}
+void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q6K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q6k");
+}
+}

@@ -1,0 +1,287 @@
+// Activation quantizers for the decode and prefill paths, bit-exact with the reference CPU quantizers:
+//   Q8_K  BlockQ8K::from_float        crates/inference-tensor/src/quantized/k_quants.rs:2721-2760
+//   Q8_0  quantize_block32 + f16 d    crates/inference-tensor/src/quantized/mod.rs:41-56, k_quants.rs:923-949
+// Built with -ffp-contract=off; division and roundf are IEEE (no fast-math), so every step rounds as the
+// CPU's does.  Q8_K: one wave per 256-value block, 4 values per lane; the signed value of largest magnitude
+// is found with a (|x|, first index) wave reduction so ties resolve to the first occurrence as in the
+// reference's sequential scan.
+#include "common.h"
+#include "inferencequant.h"
+
+namespace {
+
+// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k) or the prefill
+// tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16]).
+struct q8k_dst {
+  uint8_t *qs;
+  float *d;
+  int16_t *bsums;
+};
+
+__device__ __forceinline__ q8k_dst q8k_decode_dst(uint8_t *vy, int64_t block) {
+  uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8k);
+  return {b + 4, (float *)b, (int16_t *)(b + 260)};
+}
+
+__device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
+  const int64_t i = sb * rows + r;
+  uint8_t *qs = chan + i * 256;
+  float *d = (float *)(chan + nsb * rows * 256) + i;
+  int16_t *bs = (int16_t *)(chan + nsb * rows * 260) + i * 16;
+  return {qs, d, bs};
+}
+
+// One wave quantizes v[0..3] of lanes 0..63 (values 4*lane .. 4*lane+3 of the block) and writes it.
+__device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst) {
+  float best = 0.0f;
+  int bidx = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float a = fabsf(v[i]);
+    if (a > best) {  // strictly greater: the first of equal magnitudes stays
+      best = a;
+      bidx = lane * 4 + i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off, QMM_WAVE);
+    const int oi = __shfl_xor(bidx, off, QMM_WAVE);
+    if (ob > best || (ob == best && oi < bidx)) {
+      best = ob;
+      bidx = oi;
+    }
+  }
+  if (best == 0.0f) {  // amax == 0: an all-zero block (k_quants.rs:2740-2743)
+    *(uint32_t *)(dst.qs + 4 * lane) = 0u;
+    if (lane == 0) *dst.d = 0.0f;
+    if ((lane & 3) == 0) dst.bsums[lane >> 2] = 0;
+    return;
+  }
+  const float mine = v[bidx & 3];
+  const float mx = __shfl(mine, bidx >> 2, QMM_WAVE);
+  const float iscale = -127.0f / mx;
+  int q[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(iscale * v[i]));
+  int s = q[0] + q[1] + q[2] + q[3];
+  s += __shfl_xor(s, 1, QMM_WAVE);
+  s += __shfl_xor(s, 2, QMM_WAVE);
+  const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+                          ((uint32_t)(q[3] & 0xff) << 24);
+  *(uint32_t *)(dst.qs + 4 * lane) = packed;
+  if ((lane & 3) == 0) dst.bsums[lane >> 2] = (int16_t)s;
+  if (lane == 0) *dst.d = 1.0f / iscale;
+}
+
+// Eight lanes quantize one 32-value Q8_0 block (4 values each); writes qs (4 bytes/lane) and the f16 scale.
+__device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs, uint16_t *d_out) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, QMM_WAVE));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, QMM_WAVE));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, QMM_WAVE));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  int q[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(v[i] * id));
+  // qs may be only 2-byte aligned (34-byte blocks): two 16-bit stores
+  uint16_t *q16 = (uint16_t *)(qs + 4 * sub);
+  q16[0] = (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));
+  q16[1] = (uint16_t)((q[2] & 0xff) | ((q[3] & 0xff) << 8));
+  if (sub == 0) *d_out = f32_to_f16_bits(d);
+}
+
+template <class In>
+__device__ __forceinline__ void load4(const typename In::T *row, int64_t k0, int64_t kx, float v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) v[i] = (k0 + i < kx) ? In::load(row, k0 + i) : 0.0f;
+}
+
+// ------------------------------------------------------------------ decode layout kernels
+
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_q8k_rows(const typename In::T *__restrict__ x, uint8_t *__restrict__ vy,
+                                                           int kx, int kx_padded, int num_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nsb = kx_padded / 256;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nsb * num_rows) return;  // whole wave
+  const int64_t row = blk / nsb, sb = blk % nsb;
+  float v[4];
+  load4<In>(x + row * (int64_t)kx, sb * 256 + lane * 4, kx, v);
+  q8k_wave(v, lane, q8k_decode_dst(vy, blk));
+}
+
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_q8_0_rows(const typename In::T *__restrict__ x,
+                                                            uint8_t *__restrict__ vy, int kx, int kx_padded,
+                                                            int num_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = kx_padded / 32;
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+  const bool valid = blk < nb * num_rows;
+  const int64_t b = valid ? blk : 0;
+  const int64_t row = b / nb, ib = b % nb;
+  float v[4];
+  load4<In>(x + row * (int64_t)kx, ib * 32 + (lane & 7) * 4, valid ? kx : 0, v);
+  uint8_t *blkp = vy + b * 34;
+  if (valid) q8_0_group(v, lane & 7, (int8_t *)(blkp + 2), (uint16_t *)blkp);
+}
+
+// ------------------------------------------------------------------ prefill (tile) layout kernels
+
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_q8k_tiles(const typename In::T *__restrict__ x,
+                                                            const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
+                                                            int64_t ne00, int64_t s01, int64_t s02, int64_t s03,
+                                                            int64_t ne0, int64_t ne1, int64_t ne2, int64_t nblk) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nblk) return;
+  const int64_t nsb = ne0 / 256;
+  const int64_t per_chan = nsb * ne1;
+  const int64_t ch = blk / per_chan, rem = blk % per_chan;
+  const int64_t sb = rem / ne1, r = rem % ne1;
+  const int64_t i2 = ch % ne2, i3 = ch / ne2;
+  const int64_t src_row = ids ? ids[r] : r;
+  float v[4];
+  load4<In>(x + i3 * s03 + i2 * s02 + src_row * s01, sb * 256 + lane * 4, ne00, v);
+  q8k_wave(v, lane, q8k_tile_dst(vy + ch * per_chan * 292, ne1, nsb, sb, r));
+}
+
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_q8_0_tiles(const typename In::T *__restrict__ x,
+                                                             const int32_t *__restrict__ ids,
+                                                             uint8_t *__restrict__ vy, int64_t ne00, int64_t s01,
+                                                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1,
+                                                             int64_t ne2, int64_t nblk32) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+  const bool valid = blk < nblk32;
+  const int64_t b = valid ? blk : 0;
+  const int64_t nsb = ne0 / 256;
+  const int64_t per_chan = nsb * ne1 * 8;  // 32-value blocks per channel
+  const int64_t ch = b / per_chan, rem = b % per_chan;
+  const int64_t sb = rem / (ne1 * 8), r = (rem / 8) % ne1, j = rem % 8;
+  const int64_t i2 = ch % ne2, i3 = ch / ne2;
+  const int64_t src_row = valid ? (ids ? ids[r] : r) : 0;
+  float v[4];
+  load4<In>(x + i3 * s03 + i2 * s02 + src_row * s01, sb * 256 + j * 32 + (lane & 7) * 4, valid ? ne00 : 0, v);
+  uint8_t *chan = vy + ch * nsb * ne1 * 272;
+  int8_t *qs = (int8_t *)(chan + (sb * ne1 + r) * 256 + j * 32);
+  uint16_t *d = (uint16_t *)(chan + nsb * ne1 * 256) + (sb * ne1 + r) * 8 + j;
+  if (valid) q8_0_group(v, lane & 7, qs, d);
+}
+
+template <class In>
+void decode_q8k(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  if (kx < 0 || num_rows < 0 || kx_padded % 256 != 0 || kx_padded < kx) {
+    qmm_set_error("quantize_q8k: kx=%d kx_padded=%d num_rows=%d (kx_padded must be a multiple of 256, >= kx)", kx,
+                  kx_padded, num_rows);
+    return;
+  }
+  const int64_t blocks = (int64_t)kx_padded / 256 * num_rows;
+  if (blocks == 0) return;
+  k_quantize_q8k_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
+      (const typename In::T *)x, (uint8_t *)vy, kx, kx_padded, num_rows);
+}
+
+template <class In>
+void decode_q8_0(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  if (kx < 0 || num_rows < 0 || kx_padded % 32 != 0 || kx_padded < kx) {
+    qmm_set_error("quantize_q8_0: kx=%d kx_padded=%d num_rows=%d (kx_padded must be a multiple of 32, >= kx)", kx,
+                  kx_padded, num_rows);
+    return;
+  }
+  const int64_t blocks = (int64_t)kx_padded / 32 * num_rows;
+  if (blocks == 0) return;
+  k_quantize_q8_0_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 32)), 256, 0, (hipStream_t)stream>>>(
+      (const typename In::T *)x, (uint8_t *)vy, kx, kx_padded, num_rows);
+}
+
+bool tile_args_ok(const char *who, int64_t ne00, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3) {
+  if (ne00 < 0 || ne0 % 256 != 0 || ne0 < ne00 || ne1 < 0 || ne2 < 1 || ne3 < 1) {
+    qmm_set_error("%s: ne00=%lld ne0=%lld ne1=%lld ne2=%lld ne3=%lld (ne0 must be a multiple of 256, >= ne00)", who,
+                  (long long)ne00, (long long)ne0, (long long)ne1, (long long)ne2, (long long)ne3);
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+void launch_mmvq_gguf_quantize_q8k_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8k<in_f32>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_gguf_quantize_q8k_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8k<in_f16>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_gguf_quantize_q8k_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8k<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_gguf_quantize_q8_0_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8_0<in_f32>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_gguf_quantize_q8_0_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8_0<in_f16>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows,
+                                         void *stream) {
+  decode_q8_0<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
+}
+
+void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                             void *stream) {
+  if (!tile_args_ok("mmq_quantize_q8k", ne00, ne0, ne1, ne2, ne3)) return;
+  const int64_t nblk = ne0 / 256 * ne1 * ne2 * ne3;
+  if (nblk == 0) return;
+  const dim3 grid((unsigned)qmm_ceil_div(nblk, 4));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t *y = (uint8_t *)vy;
+  switch (type_x) {
+    case QMM_TYPE_F32:
+      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2, nblk);
+      break;
+    case QMM_TYPE_F16:
+      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2,
+                                                        nblk);
+      break;
+    case QMM_TYPE_BF16:
+      k_quantize_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+                                                         ne2, nblk);
+      break;
+    default: qmm_set_error("mmq_quantize_q8k: unsupported input type %d", type_x);
+  }
+}
+
+void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                              int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                              void *stream) {
+  if (!tile_args_ok("mmq_quantize_q8_0", ne00, ne0, ne1, ne2, ne3)) return;
+  const int64_t nblk = ne0 / 32 * ne1 * ne2 * ne3;
+  if (nblk == 0) return;
+  const dim3 grid((unsigned)qmm_ceil_div(nblk, 32));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t *y = (uint8_t *)vy;
+  switch (type_x) {
+    case QMM_TYPE_F32:
+      k_quantize_q8_0_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2,
+                                                         nblk);
+      break;
+    case QMM_TYPE_F16:
+      k_quantize_q8_0_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+                                                         ne2, nblk);
+      break;
+    case QMM_TYPE_BF16:
+      k_quantize_q8_0_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+                                                          ne2, nblk);
+      break;
+    default: qmm_set_error("mmq_quantize_q8_0: unsupported input type %d", type_x);
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,297 @@
+"""Python front end of libinferencequant.so (the C ABI in include/inferencequant.h).
+
+Device buffers and streams come from PyTorch (ROCm build): tensors' data pointers and
+``torch.cuda.current_stream().cuda_stream`` are handed to the C ABI through ctypes.  Every launcher
+is asynchronous on that stream.  There is no fallback: if the library is missing this module raises.
+
+The helpers below mirror how inference.rs's Rust host drives the same symbols
+(crates/inference-quant/src/gguf/fast_mmvq.rs:477-665 for decode, fast_mmq.rs:604-715 for prefill,
+gguf/cuda.rs:259-625 for the MoE paths).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "lib", "libinferencequant.so")
+HOST_LIB_PATH = os.path.join(HERE, "lib", "libinferencequant_host.so")
+HEADERS = [os.path.join(REPO, "include", "inferencequant.h"), os.path.join(REPO, "include", "qmm_host.h")]
+
+# GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603) and block geometry
+F32, F16, Q8_0, Q4K, Q6K, Q8K, BF16 = 0, 1, 8, 12, 14, 15, 30
+BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+TYPE_SIZE = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
+ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+TYPE_NAME = {Q8_0: "q8_0", Q4K: "q4_k", Q6K: "q6_k"}
+MOE_NAME = {Q8_0: "q8_0_q8_0", Q4K: "q4k_q8k", Q6K: "q6k_q8k"}
+
+_lib = None
+
+
+class QmmError(RuntimeError):
+    pass
+
+
+def build(force: bool = True) -> None:
+    """Compile the kernel and host libraries in-tree (hipcc --offload-arch=gfx950)."""
+    cmd = ["make", "-s", "-C", HERE, "-j8"]
+    if force:
+        cmd.insert(1, "-B")
+    subprocess.run(cmd, check=True)
+
+
+def declared_symbols(header: str | None = None) -> list[str]:
+    """Every function and object the C headers declare, after macro expansion (gcc -E)."""
+    names: list[str] = []
+    for h in ([header] if header else HEADERS):
+        if not os.path.exists(h):
+            continue
+        out = subprocess.run(["gcc", "-E", "-P", "-x", "c", "-I", os.path.join(REPO, "include"), h],
+                             check=True, capture_output=True, text=True).stdout
+        own = out[out.find("extern") if "extern" in out else 0:]
+        for m in re.finditer(r"\b((?:launch|qmm|inference)_\w+)\s*(?:\(|\[)", own):
+            if m.group(1) not in names:
+                names.append(m.group(1))
+    return names
+
+
+def lib() -> ctypes.CDLL:
+    """Load libinferencequant.so (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QmmError(f"{LIB_PATH} is missing: run `make -C {HERE}` (or __graft_entry__.build())")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    L.qmm_last_error.restype = ctypes.c_char_p
+    L.qmm_last_error.argtypes = []
+    L.qmm_clear_error.argtypes = []
+    for src in ("f32", "f16", "bf16"):
+        for blk in ("q8k", "q8_0"):
+            getattr(L, f"launch_mmvq_gguf_quantize_{blk}_{src}").argtypes = [vp, vp, i32, i32, i32, vp]
+    for t in TYPE_NAME.values():
+        for o in ("f32", "f16", "bf16"):
+            getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+        getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                                            i32, vp]
+    for name in MOE_NAME.values():
+        getattr(L, f"launch_indexed_moe_forward_{name}").argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
+    L.launch_moe_dispatch.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]
+    for suffix in ("", "_bf16", "_f16_input", "_bf16_input"):
+        f = getattr(L, f"launch_moe_weighted_reduce_flat{suffix}")
+        f.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+        f.restype = ctypes.c_int
+    for blk in ("q8k", "q8_0"):
+        f = getattr(L, f"launch_mmq_quantize_{blk}", None)
+        if f is not None:
+            f.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
+    for t in TYPE_NAME.values():
+        f = getattr(L, f"launch_mmq_gguf_{t}", None)
+        if f is not None:
+            f.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i64, i32, i32, vp]
+        f = getattr(L, f"launch_mmq_gguf_{t}_moe", None)
+        if f is not None:
+            f.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i32, i32, i64, i32, vp]
+
+
+def last_error() -> str:
+    return lib().qmm_last_error().decode()
+
+
+def check() -> None:
+    """Raise if the last launcher on this thread recorded an error (then clear it)."""
+    msg = last_error()
+    if msg:
+        lib().qmm_clear_error()
+        raise QmmError(msg)
+
+
+def build_id() -> str:
+    arr = ctypes.c_char.in_dll(lib(), "inference_kernel_build_id")
+    return ctypes.cast(ctypes.addressof(arr), ctypes.c_char_p).value.decode()
+
+
+# ------------------------------------------------------------------------------------------------ torch helpers
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream():
+    return ctypes.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def pad_to(k: int, m: int) -> int:
+    return (k + m - 1) // m * m
+
+
+def act_bytes(wtype: int, rows: int, kp: int) -> int:
+    at = ACT_TYPE[wtype]
+    return rows * kp // BLOCK_SIZE[at] * TYPE_SIZE[at]
+
+
+_DT = {}
+
+
+def _src_name(x) -> str:
+    torch = _torch()
+    return {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[x.dtype]
+
+
+def quantize_decode(wtype: int, x, kp: int | None = None, out=None):
+    """Quantize activation rows x [rows, k] (f32/f16/bf16, on the GPU) to the decode layout of wtype's
+    activation blocks.  Returns (uint8 tensor, k_padded)."""
+    torch = _torch()
+    rows, k = x.shape
+    at = ACT_TYPE[wtype]
+    kp = kp or pad_to(k, BLOCK_SIZE[at])
+    if out is None:
+        out = torch.empty(act_bytes(wtype, rows, kp), dtype=torch.uint8, device=x.device)
+    blk = "q8k" if at == Q8K else "q8_0"
+    getattr(lib(), f"launch_mmvq_gguf_quantize_{blk}_{_src_name(x)}")(_ptr(x), _ptr(out), k, kp, rows, _stream())
+    check()
+    return out, kp
+
+
+def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out=None, stride_col_dst=None):
+    """Decode matvec: dst [b, n] = Q(y) . W^T through launch_mmvq_gguf_<t>_<dtype>_plain."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.float32
+    if out is None:
+        out = torch.empty((b, stride_col_dst or n), dtype=out_dtype, device=w.device)
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_plain")(
+        _ptr(w), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], stride_col_dst or n, b, _stream())
+    check()
+    return out
+
+
+def qmatmul_decode(wtype: int, w, x, n: int, out_dtype=None):
+    """x [b, k] -> [b, n]: quantize then matvec (the two launches fast_mmvq::plain makes)."""
+    vy, kp = quantize_decode(wtype, x)
+    return mmvq(wtype, w, vy, x.shape[1], n, x.shape[0], kp, out_dtype=out_dtype)
+
+
+def mmvq_moe(wtype: int, w_gate, w_up, expert_stride: int, vy, ids, k: int, n: int, kp: int, y_div: int,
+             n_pairs: int, activation: int = 0, out=None):
+    torch = _torch()
+    if out is None:
+        out = torch.empty((n_pairs, n), dtype=torch.float32, device=w_gate.device)
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_moe")(
+        _ptr(w_gate), _ptr(w_up), expert_stride, _ptr(vy), _ptr(ids), _ptr(out), k, n,
+        kp // BLOCK_SIZE[ACT_TYPE[wtype]], y_div, n_pairs, activation, 1, _stream())
+    check()
+    return out
+
+
+def indexed_moe(wtype: int, w, x, ids, n: int, out=None):
+    """The op-level gather_forward: x [batch, xdim1, k] f32, ids [batch, topk] u32 -> [batch, topk, n]."""
+    torch = _torch()
+    batch, xdim1, k = x.shape
+    topk = ids.shape[1]
+    vy, kp = quantize_decode(wtype, x.reshape(batch * xdim1, k))
+    if out is None:
+        out = torch.zeros((batch, topk, n), dtype=torch.float32, device=x.device)
+    getattr(lib(), f"launch_indexed_moe_forward_{MOE_NAME[wtype]}")(
+        _ptr(w), _ptr(vy), _ptr(ids), _ptr(out), n, k, batch, topk, kp, xdim1, _stream())
+    check()
+    return out
+
+
+def moe_dispatch(topk_ids, n_experts: int, topk: int):
+    torch = _torch()
+    total = topk_ids.numel()
+    dev = topk_ids.device
+    bounds = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    tok = torch.empty(max(total, 1), dtype=torch.int32, device=dev)
+    src = torch.empty(max(total, 1), dtype=torch.int32, device=dev)
+    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    cursors = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    lib().launch_moe_dispatch(_ptr(topk_ids), _ptr(bounds), _ptr(tok), _ptr(src), total, n_experts, topk,
+                              _ptr(counts), _ptr(cursors), _stream())
+    check()
+    return bounds, tok[:total], src[:total], counts, cursors
+
+
+def moe_weighted_reduce(inp, weights, out_dtype=None):
+    torch = _torch()
+    tokens, topk, hidden = inp.shape
+    if inp.dtype == torch.float32:
+        suffix = "_bf16" if out_dtype == torch.bfloat16 else ""
+        odt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
+    elif inp.dtype == torch.float16:
+        suffix, odt = "_f16_input", torch.float16
+    else:
+        suffix, odt = "_bf16_input", torch.bfloat16
+    out = torch.empty((tokens, hidden), dtype=odt, device=inp.device)
+    rc = getattr(lib(), f"launch_moe_weighted_reduce_flat{suffix}")(_ptr(inp), _ptr(weights), _ptr(out), tokens,
+                                                                    hidden, topk, _stream())
+    check()
+    if rc != 0:
+        raise QmmError(f"moe_weighted_reduce returned {rc}")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ prefill
+
+def mmq_act_bytes(wtype: int, rows: int, kp: int) -> int:
+    return rows * kp // 256 * (292 if ACT_TYPE[wtype] == Q8K else 272)
+
+
+def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None):
+    """Quantize x [rows, k] (or the rows ids selects) into the prefill tile layout.  Returns (uint8 tensor, kp)."""
+    torch = _torch()
+    k = x.shape[-1]
+    kp = pad_to(k, 256)
+    ne1 = rows if rows is not None else (ids.numel() if ids is not None else x.shape[0])
+    if out is None:
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp), 1), dtype=torch.uint8, device=x.device)
+    type_x = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[x.dtype]
+    blk = "q8k" if ACT_TYPE[wtype] == Q8K else "q8_0"
+    getattr(lib(), f"launch_mmq_quantize_{blk}")(_ptr(x), _ptr(ids), _ptr(out), type_x, k, x.stride(0),
+                                                 x.stride(0) * x.shape[0], x.stride(0) * x.shape[0], kp, ne1, 1, 1,
+                                                 _stream())
+    check()
+    return out, kp
+
+
+def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None):
+    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t>."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.float32
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=w.device)
+    type_dst = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[out.dtype]
+    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME[wtype]}")(
+        None, _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, 256, 160 * 1024, 64, type_dst,
+        _stream())
+    check()
+    return out
+
+
+def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None):
+    y, _ = quantize_prefill(wtype, x)
+    return mmq(wtype, w, y, x.shape[1], n, x.shape[0], out_dtype=out_dtype)
+
+
+def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
+            ncols_max: int, out):
+    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME[wtype]}_moe")(
+        None, _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
+        k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, 256, 160 * 1024, 64, _stream())
+    check()
+    return out

@@ -152,9 +152,8 @@ void oracle_quantize_q8k(const float *x, int64_t n, or_block_q8k *y) {
         }
         float iscale = -127.0f / max;
         for (int j = 0; j < 256; j++) {
-            float v = roundf(iscale * xs[j]);
-            v = v < -128.0f ? -128.0f : (v > 127.0f ? 127.0f : v);
-            y[b].qs[j] = (int8_t)v;
+            /* clamp(-128, 127) then `as i8`: saturating, a NaN (clamp keeps it) becomes 0 */
+            y[b].qs[j] = sat_i8(roundf(iscale * xs[j]));
         }
         for (int j = 0; j < 16; j++) {
             int32_t s = 0;
