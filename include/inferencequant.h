@@ -80,8 +80,10 @@ QMM_DECLARE_MMVQ_PLAIN(q6_k)
  * For routed pair p < n_pairs: expert e = ids[p] (u32), activation row p / y_div of vy (stride_col_y
  * blocks apart), weights vx_gate + e * expert_stride bytes.
  *   vx_up == NULL: dst[p * nrows_x + row] = W_gate[e] . y
- *   vx_up != NULL: dst[p * nrows_x + row] = act(W_gate[e] . y) * (W_up[e] . y), activation 0 = SiLU,
- *                  1 = GELU (tanh form), 2 = ReLU (inference-quant/kernels/cuda/glu_activation.cuh).
+ *   vx_up != NULL: dst[p * nrows_x + row] = act(W_gate[e] . y) * (W_up[e] . y), activation 0 SiLU,
+ *                  1 GELU (tanh form), 2 ReLU, 3 GELU (erf form), 4 sigmoid (glu_activation.cuh).
+ * Expert ids must be valid (< the number of experts behind vx_gate); they are not checked on the device, as in
+ * the reference.
  * `grouped` only orders the grid in the reference (pairs sharing an expert run together); accepted, and
  * the gfx950 grid always walks pairs innermost. */
 #define QMM_DECLARE_MMVQ_MOE(t)                                                                               \
@@ -103,6 +105,15 @@ void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int ty
 void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
                               int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
                               void *stream);
+
+/* Replace launch_mmq_quantize_glu_q8_1_{D4,DS4}_f32 (gguf/ffi.rs:700-724; mmq_quantize.cu:238-330): output row
+ * i1 < ne1 = act(gate[r]) * up[r] for r = ids ? ids[i1] : i1 (row stride s01, ne00 valid values, zero up to ne0),
+ * quantized into the prefill layout.  activation: 0 SiLU, 1 GELU (tanh), 2 ReLU, 3 GELU (erf), 4 sigmoid
+ * (glu_activation.cuh). */
+void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                     int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream);
+void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                      int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream);
 
 /* ------------------------------------------------------------------ prefill matmul
  * launch_mmq_gguf_<t> (gguf/ffi.rs:902-918; host fast_mmq.rs:446-524, 604-715; kernel mmq_instance.cuh:

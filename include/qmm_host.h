@@ -1,0 +1,55 @@
+/*
+ * libinferencequant_host.so -- C entry points of the C++ host layer (inference.rs_amd/host/qtensor.h), the
+ * QTensor / QMatMul / MoE-experts operator API of inference.rs restated over the kernel ABI
+ * (include/inferencequant.h).  Handles are opaque; every function returns 0 on success or -1 with a message
+ * in qmm_host_last_error().  Device pointers are HIP device memory; `stream` is a hipStream_t.
+ */
+#ifndef QMM_HOST_H
+#define QMM_HOST_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qmm_qtensor qmm_qtensor;
+typedef struct qmm_moe qmm_moe;
+
+const char *qmm_host_last_error(void);
+
+/* CPU block quantizers / dequantizer of QTensor::quantize and ::dequantize (quantized/mod.rs:391-479):
+ * n values (a multiple of the block size) of GGUF type `dtype` (8 Q8_0, 12 Q4_K, 14 Q6_K, 15 Q8_K). */
+int qmm_quantize_cpu(uint32_t dtype, const float *x, int64_t n, void *out);
+int qmm_dequantize_cpu(uint32_t dtype, const void *blocks, int64_t n, float *y);
+
+/* QTensor::new(QStorage::from_data(bytes, device, dtype), dims) for dims [rows, cols] or [experts, rows, cols];
+ * device_ordinal < 0 keeps the tensor on the CPU.  QTensor::quantize_onto quantizes f32 values first. */
+int qmm_qtensor_from_data(uint32_t dtype, const void *bytes, int64_t len, int64_t experts, int64_t rows, int64_t cols,
+                          int device_ordinal, qmm_qtensor **out);
+int qmm_qtensor_quantize(uint32_t dtype, const float *values, int64_t experts, int64_t rows, int64_t cols,
+                         int device_ordinal, qmm_qtensor **out);
+void qmm_qtensor_free(qmm_qtensor *t);
+const void *qmm_qtensor_device_ptr(const qmm_qtensor *t);
+int64_t qmm_qtensor_storage_bytes(const qmm_qtensor *t);
+
+/* QMatMul::forward: ys[rows, N] = xs[rows, K] . W^T; in_dtype 0 f32, 1 f16, 30 bf16 (xs and ys share it).
+ * Decode matvec for rows <= 16, prefill matmul above (gguf/mod.rs:434-452). */
+int qmm_qmatmul_forward(const qmm_qtensor *w, const void *xs, uint32_t in_dtype, int64_t rows, void *ys, void *stream);
+/* QuantMethod::gather_forward: W [E, N, K]; xs [batch, xdim1, K] f32; ids [batch, topk] u32 -> ys [batch, topk, N]. */
+int qmm_qmatmul_gather_forward(const qmm_qtensor *w, const float *xs, int64_t batch, int64_t xdim1,
+                               const uint32_t *ids, int64_t topk, float *ys, void *stream);
+
+/* MoE experts block: gate/up [E, inter, hidden], down [E, hidden, inter]; activation 0 SiLU, 1 GELU, 2 ReLU, 3 GELU (erf), 4 sigmoid.
+ * forward: out[t] = sum_s w[t,s] * down_e(act(gate_e(x_t)) * up_e(x_t)), e = ids[t,s]; f32 / int32 device
+ * pointers.  force_grouped = 1 takes the grouped prefill path at any token count. */
+int qmm_moe_new(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, int activation,
+                qmm_moe **out);
+void qmm_moe_free(qmm_moe *m);
+int qmm_moe_forward(const qmm_moe *m, const float *xs, int64_t tokens, const int32_t *ids, const float *weights,
+                    int64_t topk, float *out, void *stream, int force_grouped);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -86,4 +86,17 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
   return __builtin_amdgcn_alignbyte(hi, lo, shift);
 }
 
+// GLU activations, numbered as the reference's GluActivation (inference-quant/kernels/cuda/glu_activation.cuh):
+// 0 SiLU, 1 GELU (tanh form), 2 ReLU, 3 GELU (erf form), 4 sigmoid
+__device__ __forceinline__ float glu_act(int activation, float x) {
+  switch (activation) {
+    case 1: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * (x * x * x))));
+    case 2: return fmaxf(x, 0.0f);
+    case 3: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    case 4: return 1.0f / (1.0f + expf(-x));
+    default: return x / (1.0f + expf(-x));
+  }
+}
+constexpr int kGluActivations = 5;
+
 static inline int64_t qmm_ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -52,18 +52,6 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, co
     }
 }
 
-// GLU activations (inference-quant/kernels/cuda/glu_activation.cuh): 0 SiLU, 1 GELU (tanh), 2 ReLU
-__device__ __forceinline__ float glu_act(int activation, float g) {
-  switch (activation) {
-    case 1: {
-      const float c = 0.7978845608028654f;  // sqrt(2 / pi)
-      return 0.5f * g * (1.0f + tanhf(c * (g + 0.044715f * g * g * g)));
-    }
-    case 2: return g > 0.0f ? g : 0.0f;
-    default: return g / (1.0f + expf(-g));
-  }
-}
-
 // MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's
 // weights through L2.  dst[p * nrows + row] = W_gate[ids[p]] . y[p / y_div]  (or act(gate) * up).
 template <class U, int R, bool GLU>
@@ -209,7 +197,7 @@ void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride
          float *dst, int ncols_x, int nrows_x, int stride_col_y, int y_div, int n_pairs, int activation,
          void *stream, const char *who) {
   if (!check_mmvq(who, type, vx_gate, ncols_x, nrows_x, stride_col_y, 1)) return;
-  if (n_pairs < 0 || y_div <= 0 || activation < 0 || activation > 2 || expert_stride < 0) {
+  if (n_pairs < 0 || y_div <= 0 || activation < 0 || activation >= kGluActivations || expert_stride < 0) {
     qmm_set_error("%s: n_pairs=%d y_div=%d activation=%d expert_stride=%lld", who, n_pairs, y_div, activation,
                   (long long)expert_stride);
     return;

@@ -174,6 +174,51 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_tiles(const typename In::
   if (valid) q8_0_group(v, lane & 7, qs, d);
 }
 
+// act(gate) * up of row ids[r] (or r), quantized into the prefill tile layout: the fused GLU requantization
+// between the gate/up and down matmuls (mmq_gguf/mmq_quantize.cu:238-330).
+__global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const float *__restrict__ gate, const float *__restrict__ up,
+                                                                const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
+                                                                int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1,
+                                                                int activation, int64_t nblk) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nblk) return;
+  const int64_t nsb = ne0 / 256;
+  const int64_t sb = blk / ne1, r = blk % ne1;
+  const int64_t src = (ids ? ids[r] : r) * s01;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int64_t k = sb * 256 + lane * 4 + i;
+    v[i] = k < ne00 ? glu_act(activation, gate[src + k]) * up[src + k] : 0.0f;
+  }
+  q8k_wave(v, lane, q8k_tile_dst(vy, ne1, nsb, sb, r));
+}
+
+__global__ __launch_bounds__(256) void k_quantize_glu_q8_0_tiles(const float *__restrict__ gate,
+                                                                 const float *__restrict__ up,
+                                                                 const int32_t *__restrict__ ids,
+                                                                 uint8_t *__restrict__ vy, int64_t ne00, int64_t s01,
+                                                                 int64_t ne0, int64_t ne1, int activation,
+                                                                 int64_t nblk32) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+  const bool valid = blk < nblk32;
+  const int64_t b = valid ? blk : 0;
+  const int64_t nsb = ne0 / 256;
+  const int64_t sb = b / (ne1 * 8), r = (b / 8) % ne1, j = b % 8;
+  const int64_t src = valid ? (ids ? ids[r] : r) * s01 : 0;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int64_t k = sb * 256 + j * 32 + (lane & 7) * 4 + i;
+    v[i] = (valid && k < ne00) ? glu_act(activation, gate[src + k]) * up[src + k] : 0.0f;
+  }
+  int8_t *qs = (int8_t *)(vy + (sb * ne1 + r) * 256 + j * 32);
+  uint16_t *d = (uint16_t *)(vy + nsb * ne1 * 256) + (sb * ne1 + r) * 8 + j;
+  if (valid) q8_0_group(v, lane & 7, qs, d);
+}
+
 template <class In>
 void decode_q8k(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
   if (kx < 0 || num_rows < 0 || kx_padded % 256 != 0 || kx_padded < kx) {
@@ -282,6 +327,32 @@ void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int t
       break;
     default: qmm_set_error("mmq_quantize_q8_0: unsupported input type %d", type_x);
   }
+}
+
+void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                     int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
+  if (!tile_args_ok("mmq_quantize_glu_q8k", ne00, ne0, ne1, 1, 1)) return;
+  if (activation < 0 || activation >= kGluActivations) {
+    qmm_set_error("mmq_quantize_glu_q8k: activation %d", activation);
+    return;
+  }
+  const int64_t nblk = ne0 / 256 * ne1;
+  if (nblk == 0) return;
+  k_quantize_glu_q8k_tiles<<<dim3((unsigned)qmm_ceil_div(nblk, 4)), 256, 0, (hipStream_t)stream>>>(
+      gate, up, ids, (uint8_t *)vy, ne00, s01, ne0, ne1, activation, nblk);
+}
+
+void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                      int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
+  if (!tile_args_ok("mmq_quantize_glu_q8_0", ne00, ne0, ne1, 1, 1)) return;
+  if (activation < 0 || activation >= kGluActivations) {
+    qmm_set_error("mmq_quantize_glu_q8_0: activation %d", activation);
+    return;
+  }
+  const int64_t nblk = ne0 / 32 * ne1;
+  if (nblk == 0) return;
+  k_quantize_glu_q8_0_tiles<<<dim3((unsigned)qmm_ceil_div(nblk, 32)), 256, 0, (hipStream_t)stream>>>(
+      gate, up, ids, (uint8_t *)vy, ne00, s01, ne0, ne1, activation, nblk);
 }
 
 }  // extern "C"

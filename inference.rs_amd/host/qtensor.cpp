@@ -1,0 +1,412 @@
+// QTensor / QMatMul / MoeExperts over the kernel C ABI.  Route choices follow
+// crates/inference-quant/src/gguf/mod.rs:434-452 (decode vs prefill) and
+// crates/inference-nn/src/moe/experts/backends.rs:1442-1454 (indexed decode vs grouped prefill); scratch for
+// quantized activations is a per-(thread, device) growing workspace as in gguf/thread_workspace.rs.
+#include "qtensor.h"
+
+#include <cstring>
+#include <map>
+#include <string>
+
+#include "inferencequant.h"
+
+namespace inference_rs_amd {
+namespace {
+
+void hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void abi_check(const char *what) {
+  const char *msg = qmm_last_error();
+  if (msg && msg[0]) {
+    std::string m = std::string(what) + ": " + msg;
+    qmm_clear_error();
+    throw Error(m);
+  }
+}
+
+int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Per-(thread, device) scratch: grows, never shrinks.  Growing waits for the stream, since earlier launches
+// may still read the old buffer.
+class Workspace {
+ public:
+  void *get(int ordinal, size_t bytes, hipStream_t stream) {
+    Slot &s = slots_[ordinal];
+    if (!s.buf || s.buf->size() < bytes) {
+      if (s.buf) hip_check(hipStreamSynchronize(stream), "workspace: hipStreamSynchronize");
+      s.buf.reset();
+      s.buf = std::make_unique<DeviceBuffer>(ordinal, bytes + bytes / 4 + 4096);
+    }
+    return s.buf->ptr();
+  }
+
+ private:
+  struct Slot {
+    std::unique_ptr<DeviceBuffer> buf;
+  };
+  std::map<int, Slot> slots_;
+};
+
+Workspace &workspace() {
+  thread_local Workspace ws;
+  return ws;
+}
+
+// Carves consecutive 256-byte aligned slices out of one workspace allocation.
+struct Carver {
+  size_t total = 0;
+  size_t add(size_t bytes) {
+    const size_t off = total;
+    total += (bytes + 255) / 256 * 256;
+    return off;
+  }
+};
+
+typedef void (*quant_fn)(const void *, void *, int, int, int, void *);
+typedef void (*mmvq_fn)(const void *, const void *, void *, int, int, int, int, int, void *);
+typedef void (*mmq_fn)(void *, const void *, const void *, void *, int64_t, int64_t, int64_t, int64_t, int64_t, int,
+                       int, int64_t, int, int, void *);
+typedef void (*mmq_moe_fn)(void *, const void *, const void *, const int32_t *, const int32_t *, void *, int64_t,
+                           int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int64_t, int, void *);
+typedef void (*mmvq_moe_fn)(const void *, const void *, int64_t, const void *, const void *, float *, int, int, int,
+                            int, int, int, int, void *);
+typedef void (*indexed_fn)(const void *, const void *, const uint32_t *, float *, int, int, int, int, int, int,
+                           void *);
+
+quant_fn decode_quantizer(GgmlDType w, GgmlDType in) {
+  const bool k = w != GgmlDType::Q8_0;
+  switch (in) {
+    case GgmlDType::F32: return k ? launch_mmvq_gguf_quantize_q8k_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
+    case GgmlDType::F16: return k ? launch_mmvq_gguf_quantize_q8k_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
+    case GgmlDType::BF16: return k ? launch_mmvq_gguf_quantize_q8k_bf16 : launch_mmvq_gguf_quantize_q8_0_bf16;
+    default: throw Error("QMatMul: activations must be F32, F16 or BF16");
+  }
+}
+
+mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
+#define QMM_PICK(t)                                                              \
+  switch (out) {                                                                 \
+    case GgmlDType::F32: return launch_mmvq_gguf_##t##_f32_plain;                \
+    case GgmlDType::F16: return launch_mmvq_gguf_##t##_f16_plain;                \
+    case GgmlDType::BF16: return launch_mmvq_gguf_##t##_bf16_plain;              \
+    default: throw Error("QMatMul: output must be F32, F16 or BF16");            \
+  }
+  switch (w) {
+    case GgmlDType::Q8_0: QMM_PICK(q8_0)
+    case GgmlDType::Q4K: QMM_PICK(q4_k)
+    case GgmlDType::Q6K: QMM_PICK(q6_k)
+    default: throw Error("QMatMul: unsupported weight type");
+  }
+#undef QMM_PICK
+}
+
+mmq_fn prefill_matmul(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0;
+    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k;
+    case GgmlDType::Q6K: return launch_mmq_gguf_q6_k;
+    default: throw Error("QMatMul: unsupported weight type");
+  }
+}
+
+mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_moe;
+    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe;
+    case GgmlDType::Q6K: return launch_mmq_gguf_q6_k_moe;
+    default: throw Error("MoE: unsupported weight type");
+  }
+}
+
+mmvq_moe_fn decode_matvec_moe(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe;
+    case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_moe;
+    case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_moe;
+    default: throw Error("MoE: unsupported weight type");
+  }
+}
+
+indexed_fn indexed_moe(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_indexed_moe_forward_q8_0_q8_0;
+    case GgmlDType::Q4K: return launch_indexed_moe_forward_q4k_q8k;
+    case GgmlDType::Q6K: return launch_indexed_moe_forward_q6k_q8k;
+    default: throw Error("gather_forward: unsupported weight type");
+  }
+}
+
+// activation block geometry of a weight type (GgmlType::VecDotType)
+int64_t act_block(GgmlDType w) { return w == GgmlDType::Q8_0 ? 32 : 256; }
+int64_t act_block_bytes(GgmlDType w) { return w == GgmlDType::Q8_0 ? 34 : 292; }
+int64_t tile_bytes_per_256(GgmlDType w) { return w == GgmlDType::Q8_0 ? 272 : 292; }
+
+void check_weight(const QTensor &w, const char *who) {
+  if (!w.device().is_hip()) throw Error(std::string(who) + ": the weight is not on a HIP device");
+  const GgmlDType t = w.dtype();
+  if (t != GgmlDType::Q8_0 && t != GgmlDType::Q4K && t != GgmlDType::Q6K)
+    throw Error(std::string(who) + ": weight type " + dtype_name(t) + " has no kernels here");
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------ dtypes
+
+GgmlDType dtype_from_u32(uint32_t u) {
+  switch (u) {
+    case 0: return GgmlDType::F32;
+    case 1: return GgmlDType::F16;
+    case 8: return GgmlDType::Q8_0;
+    case 12: return GgmlDType::Q4K;
+    case 14: return GgmlDType::Q6K;
+    case 15: return GgmlDType::Q8K;
+    case 30: return GgmlDType::BF16;
+    default: throw Error("unknown dtype for tensor " + std::to_string(u));
+  }
+}
+
+size_t type_size(GgmlDType t) { return qmm_type_size((int)t); }
+size_t block_size(GgmlDType t) { return qmm_block_size((int)t); }
+
+const char *dtype_name(GgmlDType t) {
+  switch (t) {
+    case GgmlDType::F32: return "F32";
+    case GgmlDType::F16: return "F16";
+    case GgmlDType::Q8_0: return "Q8_0";
+    case GgmlDType::Q4K: return "Q4K";
+    case GgmlDType::Q6K: return "Q6K";
+    case GgmlDType::Q8K: return "Q8K";
+    case GgmlDType::BF16: return "BF16";
+  }
+  return "?";
+}
+
+// ------------------------------------------------------------------------------------------------ storage
+
+DeviceBuffer::DeviceBuffer(int ordinal, size_t bytes) : size_(bytes), ordinal_(ordinal) {
+  hip_check(hipSetDevice(ordinal), "hipSetDevice");
+  hip_check(hipMalloc(&ptr_, bytes ? bytes : 1), "hipMalloc");
+}
+
+DeviceBuffer::~DeviceBuffer() {
+  if (ptr_) (void)hipFree(ptr_);
+}
+
+int64_t QTensor::elem_count() const {
+  int64_t n = 1;
+  for (int64_t d : dims_) n *= d;
+  return n;
+}
+
+std::shared_ptr<QTensor> QTensor::from_data(const void *bytes, size_t len, const std::vector<int64_t> &dims,
+                                            GgmlDType dtype, Device device) {
+  if (dims.size() < 2 || dims.size() > 3) throw Error("QTensor: dims must be [rows, cols] or [experts, rows, cols]");
+  const size_t bs = block_size(dtype);
+  if (bs == 0 || dtype == GgmlDType::F32 || dtype == GgmlDType::F16 || dtype == GgmlDType::BF16)
+    throw Error(std::string("QTensor: ") + dtype_name(dtype) + " is not a block type");
+  for (int64_t d : dims)
+    if (d <= 0) throw Error("QTensor: empty dimension");
+  if (dims.back() % (int64_t)bs != 0)
+    throw Error("QTensor: the last dimension " + std::to_string(dims.back()) + " is not a multiple of " +
+                std::to_string(bs));
+  std::shared_ptr<QTensor> t(new QTensor(dtype, dims, device));
+  const size_t need = t->storage_size_in_bytes();
+  if (len != need) throw Error("QTensor: " + std::to_string(len) + " bytes for a tensor of " + std::to_string(need));
+  if (device.is_cpu()) {
+    t->host_.assign((const uint8_t *)bytes, (const uint8_t *)bytes + len);
+  } else {
+    // MATRIX_ROW_PADDING (quantized/cuda.rs:25): 512 values of zero blocks past the end
+    const size_t pad = 512 / bs * type_size(dtype);
+    t->dev_ = std::make_unique<DeviceBuffer>(device.ordinal, len + pad);
+    hip_check(hipMemcpy(t->dev_->ptr(), bytes, len, hipMemcpyHostToDevice), "QTensor upload");
+    hip_check(hipMemset((uint8_t *)t->dev_->ptr() + len, 0, pad), "QTensor padding");
+  }
+  return t;
+}
+
+std::shared_ptr<QTensor> QTensor::quantize(const float *src, const std::vector<int64_t> &dims, GgmlDType dtype,
+                                           Device device) {
+  int64_t n = 1;
+  for (int64_t d : dims) n *= d;
+  const size_t bs = block_size(dtype);
+  if (bs == 0 || dims.empty() || dims.back() % (int64_t)bs != 0)
+    throw Error("QTensor::quantize: the last dimension is not a multiple of the block size");
+  std::vector<uint8_t> bytes((size_t)(n / (int64_t)bs) * type_size(dtype));
+  if (!cpu::quantize(dtype, src, n, bytes.data()))
+    throw Error(std::string("QTensor::quantize: no quantizer for ") + dtype_name(dtype));
+  return from_data(bytes.data(), bytes.size(), dims, dtype, device);
+}
+
+std::vector<uint8_t> QTensor::data() const {
+  if (device_.is_cpu()) return host_;
+  std::vector<uint8_t> out(storage_size_in_bytes());
+  hip_check(hipMemcpy(out.data(), dev_->ptr(), out.size(), hipMemcpyDeviceToHost), "QTensor download");
+  return out;
+}
+
+std::vector<float> QTensor::dequantize() const {
+  const std::vector<uint8_t> bytes = data();
+  std::vector<float> out((size_t)elem_count());
+  if (!cpu::dequantize(dtype_, bytes.data(), elem_count(), out.data()))
+    throw Error(std::string("QTensor::dequantize: no dequantizer for ") + dtype_name(dtype_));
+  return out;
+}
+
+const void *QTensor::device_ptr() const {
+  if (!dev_) throw Error("QTensor: not on a HIP device");
+  return dev_->ptr();
+}
+
+// ------------------------------------------------------------------------------------------------ QMatMul
+
+QMatMul::QMatMul(std::shared_ptr<QTensor> w) : w_(std::move(w)) {
+  if (!w_) throw Error("QMatMul: null weight");
+}
+
+bool QMatMul::prefers_mmvq(GgmlDType, int64_t rows) { return rows <= kMaxDecodeRows; }
+
+void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys, hipStream_t stream) const {
+  const QTensor &w = *w_;
+  check_weight(w, "QMatMul::forward");
+  if (w.shape().size() != 2) throw Error("QMatMul::forward: the weight must be 2-D");
+  if (in_dtype != GgmlDType::F32 && in_dtype != GgmlDType::F16 && in_dtype != GgmlDType::BF16)
+    throw Error("QMatMul::forward: activations must be F32, F16 or BF16");
+  if (rows < 0) throw Error("QMatMul::forward: negative row count");
+  if (rows == 0) return;
+  const int64_t k = w.cols(), n = w.rows();
+  const GgmlDType t = w.dtype();
+  hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
+  if (prefers_mmvq(t, rows)) {
+    const int64_t kp = pad_to(k, act_block(t));
+    void *vy = workspace().get(w.device().ordinal, (size_t)(rows * (kp / act_block(t)) * act_block_bytes(t)), stream);
+    decode_quantizer(t, in_dtype)(xs, vy, (int)k, (int)kp, (int)rows, stream);
+    abi_check("QMatMul::forward (quantize)");
+    decode_matvec(t, in_dtype)(w.device_ptr(), vy, ys, (int)k, (int)n, (int)(kp / act_block(t)), (int)n, (int)rows,
+                               stream);
+    abi_check("QMatMul::forward (matvec)");
+  } else {
+    const int64_t kp = pad_to(k, 256);
+    void *y = workspace().get(w.device().ordinal, (size_t)(rows * kp / 256 * tile_bytes_per_256(t)), stream);
+    (t == GgmlDType::Q8_0 ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
+        xs, nullptr, y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
+    abi_check("QMatMul::forward (quantize)");
+    prefill_matmul(t)(nullptr, w.device_ptr(), y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, 256, 160 * 1024,
+                      64, (int)in_dtype, stream);
+    abi_check("QMatMul::forward (matmul)");
+  }
+}
+
+void QMatMul::gather_forward(const float *xs, int64_t batch, int64_t xdim1, const uint32_t *ids, int64_t topk,
+                             float *ys, hipStream_t stream) const {
+  const QTensor &w = *w_;
+  check_weight(w, "QMatMul::gather_forward");
+  if (w.shape().size() != 3) throw Error("gather_forward: the weight must be [experts, rows, cols]");
+  if (xdim1 != 1 && xdim1 != topk) throw Error("gather_forward: x's second dim must be 1 or topk");
+  if (batch <= 0 || topk <= 0) return;
+  const int64_t k = w.cols(), n = w.rows();
+  const GgmlDType t = w.dtype();
+  const int64_t kp = pad_to(k, act_block(t));
+  hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
+  void *vy = workspace().get(w.device().ordinal, (size_t)(batch * xdim1 * (kp / act_block(t)) * act_block_bytes(t)),
+                             stream);
+  decode_quantizer(t, GgmlDType::F32)(xs, vy, (int)k, (int)kp, (int)(batch * xdim1), stream);
+  abi_check("gather_forward (quantize)");
+  indexed_moe(t)(w.device_ptr(), vy, ids, ys, (int)n, (int)k, (int)batch, (int)topk, (int)kp, (int)xdim1, stream);
+  abi_check("gather_forward (matvec)");
+}
+
+// ------------------------------------------------------------------------------------------------ MoE experts
+
+MoeExperts::MoeExperts(std::shared_ptr<QTensor> gate, std::shared_ptr<QTensor> up, std::shared_ptr<QTensor> down,
+                       int activation)
+    : gate_(std::move(gate)), up_(std::move(up)), down_(std::move(down)), activation_(activation) {
+  if (!gate_ || !up_ || !down_) throw Error("MoeExperts: null weight");
+  for (const QTensor *t : {gate_.get(), up_.get(), down_.get()}) {
+    check_weight(*t, "MoeExperts");
+    if (t->shape().size() != 3) throw Error("MoeExperts: weights must be [experts, rows, cols]");
+  }
+  if (gate_->shape() != up_->shape() || gate_->dtype() != up_->dtype())
+    throw Error("MoeExperts: gate and up must match");
+  if (down_->experts() != gate_->experts() || down_->cols() != gate_->rows() || down_->rows() != gate_->cols())
+    throw Error("MoeExperts: down must be [experts, hidden, intermediate]");
+  if (activation < 0 || activation > 4) throw Error("MoeExperts: activation must be 0..4 (SiLU, GELU, ReLU, GELU-erf, sigmoid)");
+}
+
+void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, const float *weights, int64_t topk,
+                         float *out, hipStream_t stream, bool force_grouped) const {
+  if (tokens <= 0) return;
+  if (topk <= 0) throw Error("MoeExperts::forward: topk must be positive");
+  const int64_t E = gate_->experts(), hidden = gate_->cols(), inter = gate_->rows();
+  const int64_t pairs = tokens * topk;
+  const int ordinal = gate_->device().ordinal;
+  hip_check(hipSetDevice(ordinal), "hipSetDevice");
+  const GgmlDType tg = gate_->dtype(), td = down_->dtype();
+  const bool grouped = force_grouped || tokens > kIndexedMaxTokens;
+  if (!grouped) {
+    // decode: fused gate/up matvec per routed pair, then down, then the weighted sum over slots
+    const int64_t kp1 = pad_to(hidden, act_block(tg)), kp2 = pad_to(inter, act_block(td));
+    Carver c;
+    const size_t o_x = c.add((size_t)(tokens * (kp1 / act_block(tg)) * act_block_bytes(tg)));
+    const size_t o_mid = c.add((size_t)(pairs * inter * 4));
+    const size_t o_midq = c.add((size_t)(pairs * (kp2 / act_block(td)) * act_block_bytes(td)));
+    const size_t o_y = c.add((size_t)(pairs * hidden * 4));
+    uint8_t *ws = (uint8_t *)workspace().get(ordinal, c.total, stream);
+    decode_quantizer(tg, GgmlDType::F32)(xs, ws + o_x, (int)hidden, (int)kp1, (int)tokens, stream);
+    abi_check("MoE decode (quantize x)");
+    decode_matvec_moe(tg)(gate_->device_ptr(), up_->device_ptr(), (int64_t)(inter * gate_->row_bytes()), ws + o_x,
+                          ids, (float *)(ws + o_mid), (int)hidden, (int)inter, (int)(kp1 / act_block(tg)), (int)topk,
+                          (int)pairs, activation_, 1, stream);
+    abi_check("MoE decode (gate/up)");
+    decode_quantizer(td, GgmlDType::F32)(ws + o_mid, ws + o_midq, (int)inter, (int)kp2, (int)pairs, stream);
+    abi_check("MoE decode (quantize mid)");
+    decode_matvec_moe(td)(down_->device_ptr(), nullptr, (int64_t)(hidden * down_->row_bytes()), ws + o_midq, ids,
+                          (float *)(ws + o_y), (int)inter, (int)hidden, (int)(kp2 / act_block(td)), 1, (int)pairs, 0,
+                          1, stream);
+    abi_check("MoE decode (down)");
+    launch_moe_weighted_reduce_flat(ws + o_y, weights, out, (int)tokens, (int)hidden, (int)topk, stream);
+    abi_check("MoE decode (reduce)");
+    return;
+  }
+  // grouped prefill: dispatch tables, gate and up as expert-grouped matmuls over the gathered rows, the GLU
+  // fused into the requantization of the intermediate, down, then the weighted sum over slots
+  const int64_t kp1 = pad_to(hidden, 256), kp2 = pad_to(inter, 256);
+  Carver c;
+  const size_t o_bounds = c.add((size_t)(E + 1) * 4);
+  const size_t o_tok = c.add((size_t)pairs * 4);
+  const size_t o_src = c.add((size_t)pairs * 4);
+  const size_t o_cnt = c.add((size_t)E * 4);
+  const size_t o_cur = c.add((size_t)E * 4);
+  const size_t o_x = c.add((size_t)(pairs * kp1 / 256 * tile_bytes_per_256(tg)));
+  const size_t o_g = c.add((size_t)(pairs * inter * 4));
+  const size_t o_u = c.add((size_t)(pairs * inter * 4));
+  const size_t o_mq = c.add((size_t)(pairs * kp2 / 256 * tile_bytes_per_256(td)));
+  const size_t o_y = c.add((size_t)(pairs * hidden * 4));
+  uint8_t *ws = (uint8_t *)workspace().get(ordinal, c.total, stream);
+  int32_t *bounds = (int32_t *)(ws + o_bounds), *tok = (int32_t *)(ws + o_tok), *src = (int32_t *)(ws + o_src);
+  launch_moe_dispatch(ids, bounds, tok, src, (int)pairs, (int)E, (int)topk, (int32_t *)(ws + o_cnt),
+                      (int32_t *)(ws + o_cur), stream);
+  abi_check("MoE grouped (dispatch)");
+  (tg == GgmlDType::Q8_0 ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
+      xs, src, ws + o_x, 0, hidden, hidden, hidden * tokens, hidden * tokens, kp1, pairs, 1, 1, stream);
+  abi_check("MoE grouped (quantize x)");
+  for (int which = 0; which < 2; which++) {
+    const QTensor &w = which == 0 ? *gate_ : *up_;
+    prefill_matmul_moe(tg)(nullptr, w.device_ptr(), ws + o_x, tok, bounds, ws + (which == 0 ? o_g : o_u), hidden,
+                           inter, pairs, hidden / (int64_t)block_size(tg), inter, E, pairs, 0, 256, 160 * 1024, 64,
+                           stream);
+    abi_check("MoE grouped (gate/up)");
+  }
+  (td == GgmlDType::Q8_0 ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8k_f32)(
+      (const float *)(ws + o_g), (const float *)(ws + o_u), tok, ws + o_mq, inter, inter, kp2, pairs, activation_,
+      stream);
+  abi_check("MoE grouped (GLU + quantize)");
+  prefill_matmul_moe(td)(nullptr, down_->device_ptr(), ws + o_mq, tok, bounds, ws + o_y, inter, hidden, pairs,
+                         inter / (int64_t)block_size(td), hidden, E, pairs, 0, 256, 160 * 1024, 64, stream);
+  abi_check("MoE grouped (down)");
+  launch_moe_weighted_reduce_flat(ws + o_y, weights, out, (int)tokens, (int)hidden, (int)topk, stream);
+  abi_check("MoE grouped (reduce)");
+}
+
+}  // namespace inference_rs_amd

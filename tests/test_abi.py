@@ -59,3 +59,12 @@ def test_bad_arguments_are_rejected_before_any_launch():
     rc = L.launch_moe_weighted_reduce_flat(None, None, None, 1, 1, 0, None)
     assert rc != 0 and "topk" in qmm.last_error()
     L.qmm_clear_error()
+
+
+def test_host_library_exports_its_header():
+    import ctypes as C
+    L = C.CDLL(qmm.HOST_LIB_PATH)
+    names = qmm.declared_symbols(qmm.HEADERS[1])
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing

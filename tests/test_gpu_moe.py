@@ -1,0 +1,128 @@
+"""GPU parity of the MoE paths through the C ABI: the expert-indexed matvec (op-level gather_forward and the
+fused gate/up decode form), the dispatch tables, the expert-grouped prefill matmul and the weighted reduce."""
+import numpy as np
+import pytest
+
+import oracle as O
+import qmm
+from helpers import acts, assert_parity, weights
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def experts(rng, gtype, E, n, k):
+    w = weights(rng, E * n, k)
+    return O.quantize(gtype, w).reshape(E, -1)
+
+
+def routing(rng, tokens, E, topk):
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk]
+    w = np.take_along_axis(p, ids, 1)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    return ids.astype(np.int32), w
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("xdim1", [1, 2])
+def test_indexed_moe_matches_the_oracle(gtype, xdim1):
+    rng = np.random.default_rng(gtype + xdim1)
+    E, n, k, batch, topk = 4, 96, 512, 5, 2
+    wq = experts(rng, gtype, E, n, k)
+    ids = rng.integers(0, E, (batch, topk)).astype(np.uint32)
+    x = acts(rng, batch * xdim1, k).reshape(batch, xdim1, k)
+    want = O.indexed_moe(gtype, wq, E, n, k, x, ids)
+    got = qmm.indexed_moe(gtype, to_dev(wq), to_dev(x), to_dev(ids), n).cpu().numpy()
+    assert_parity(got, want)
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K])
+def test_moe_decode_fused_glu(gtype):
+    rng = np.random.default_rng(5)
+    E, inter, hidden, tokens, topk = 4, 128, 512, 3, 2
+    gate = experts(rng, gtype, E, inter, hidden)
+    up = experts(rng, gtype, E, inter, hidden)
+    ids = rng.integers(0, E, (tokens, topk)).astype(np.uint32)
+    x = acts(rng, tokens, hidden)
+    g = O.indexed_moe(gtype, gate, E, inter, hidden, x[:, None], ids).reshape(-1, inter)
+    u = O.indexed_moe(gtype, up, E, inter, hidden, x[:, None], ids).reshape(-1, inter)
+    vy, kp = qmm.quantize_decode(gtype, to_dev(x))
+    stride = gate.shape[1]
+    for act, f in ((0, lambda v: v / (1 + np.exp(-v))), (2, lambda v: np.maximum(v, 0))):
+        got = qmm.mmvq_moe(gtype, to_dev(gate), to_dev(up), stride, vy, to_dev(ids.reshape(-1)), hidden, inter, kp,
+                           topk, tokens * topk, activation=act).cpu().numpy()
+        assert_parity(got, f(g.astype(np.float64)) * u, rel=2e-3)
+    got = qmm.mmvq_moe(gtype, to_dev(gate), None, stride, vy, to_dev(ids.reshape(-1)), hidden, inter, kp, topk,
+                       tokens * topk).cpu().numpy()
+    assert_parity(got, g)
+
+
+def test_moe_dispatch_groups_routes_by_expert():
+    rng = np.random.default_rng(6)
+    E, tokens, topk = 8, 64, 2
+    ids, _ = routing(rng, tokens, E, topk)
+    bounds, tok, src, counts, cursors = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
+    wb, _, _ = O.moe_dispatch(ids, E, topk)
+    b, t, s = bounds.cpu().numpy(), tok.cpu().numpy(), src.cpu().numpy()
+    assert np.array_equal(b, wb)
+    assert np.array_equal(counts.cpu().numpy(), np.diff(wb))
+    assert np.array_equal(cursors.cpu().numpy(), wb[1:])
+    flat = ids.reshape(-1)
+    for e in range(E):
+        seg = t[b[e]:b[e + 1]]
+        assert np.all(flat[seg] == e)
+        assert np.array_equal(s[b[e]:b[e + 1]], seg // topk)
+    assert np.array_equal(np.sort(t), np.arange(tokens * topk))
+
+
+def test_moe_dispatch_many_experts_and_empty():
+    rng = np.random.default_rng(7)
+    E, tokens, topk = 1500, 700, 3
+    ids = np.stack([rng.choice(E, topk, replace=False) for _ in range(tokens)]).astype(np.int32)
+    bounds, tok, src, _, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
+    assert np.array_equal(bounds.cpu().numpy(), O.moe_dispatch(ids, E, topk)[0])
+    b0, _, _, c0, _ = qmm.moe_dispatch(torch.zeros(0, dtype=torch.int32, device=DEV), 4, 2)
+    assert np.all(b0.cpu().numpy() == 0) and np.all(c0.cpu().numpy() == 0)
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+def test_grouped_prefill_matches_the_oracle(gtype):
+    rng = np.random.default_rng(8 + gtype)
+    E, n, k, tokens, topk = 8, 160, 1024, 64, 2
+    wq = experts(rng, gtype, E, n, k)
+    ids, _ = routing(rng, tokens, E, topk)
+    x = acts(rng, tokens, k)
+    want = O.indexed_moe(gtype, wq, E, n, k, x[:, None], ids.astype(np.uint32)).reshape(tokens * topk, n)
+    bounds, tok, src, counts, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
+    y, kp = qmm.quantize_prefill(gtype, to_dev(x), ids=src)
+    out = torch.full((tokens * topk, n), float("nan"), device=DEV)
+    ncols_max = int(counts.max().item())
+    qmm.mmq_moe(gtype, to_dev(wq), y, tok, bounds, E, k, n, tokens * topk, ncols_max, out)
+    assert_parity(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16_out", "f16_in", "bf16_in"])
+def test_weighted_reduce(kind):
+    rng = np.random.default_rng(9)
+    tokens, topk, hidden = 37, 3, 300
+    inp = rng.standard_normal((tokens, topk, hidden)).astype(np.float32)
+    w = rng.random((tokens, topk)).astype(np.float32)
+    w[4, 2] = 0.0
+    inp[4, 2] = np.nan  # never read
+    want = O.moe_weighted_reduce(inp, w)
+    t = to_dev(inp)
+    if kind == "f16_in":
+        t = t.half()
+    elif kind == "bf16_in":
+        t = t.bfloat16()
+    got = qmm.moe_weighted_reduce(t, to_dev(w), out_dtype=torch.bfloat16 if kind == "bf16_out" else None)
+    tol = 1e-6 if kind == "f32" else 2e-2
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, rtol=tol, atol=tol)
