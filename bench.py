@@ -1,0 +1,380 @@
+#!/usr/bin/env python3
+"""Benchmark of the GGUF quantized-linear hot path on one MI355X ("Q4_K bs=1 matvec GB/s (% of
+HBM peak); prefill int8 TOPS at M=512").
+
+One step = one pass of the hot path over one batch of synthetic input, with every input resident in HBM:
+  headline: activation f32 [1, 4096] -> Q8_K -> Q4_K 14336x4096 matvec -> f32 [1, 14336],
+  i.e. launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, the two launches of the
+  reference's fast_mmvq::plain.  Weights rotate over 16 copies (528 MB > the 256 MB Infinity Cache), so every
+  step streams its weight from HBM.  K steps are captured in one HIP graph and replayed once between a
+  synchronize on both sides; `value` = algorithmic bytes per step / time per step.
+Extra lines in "extra": Q4_K decode at b = 4 and 16, Q8_0 4096^2 decode, the M = 512 prefill (Q4_K and Q6_K,
+int8 TOPS), the Llama-3-8B linear stack (tokens/s) and the 8-expert MoE (64 tokens, top-2).
+`roofline` is the matvec kernel alone (its own graph of K launches), `cpu_baseline` the oracle's CPU QMatMul
+(oracle/, a C restatement of the reference's) on the box's host cores over a bounded sample.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "inference.rs_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published (POP/s)
+SEED = 20261201
+
+Q8_0, Q4K, Q6K = 8, 12, 14
+BS = {Q8_0: 32, Q4K: 256, Q6K: 256}
+TS = {Q8_0: 34, Q4K: 144, Q6K: 210}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ data
+
+_host = None
+
+
+def host_lib():
+    global _host
+    if _host is None:
+        import qmm
+        _host = ctypes.CDLL(qmm.HOST_LIB_PATH)
+        _host.qmm_quantize_cpu.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        _host.qmm_host_last_error.restype = ctypes.c_char_p
+        for n in ("qmm_qtensor_from_data",):
+            getattr(_host, n).argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+        _host.qmm_moe_new.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+        _host.qmm_moe_forward.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_int]
+        _host.qmm_qtensor_device_ptr.argtypes = [ctypes.c_void_p]
+        _host.qmm_qtensor_device_ptr.restype = ctypes.c_void_p
+    return _host
+
+
+def quantized_weight(gtype, n, k, seed):
+    """N(0, 0.02) f32 weights quantized on the host by the library's QTensor quantizer."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    out = np.empty(n * k // BS[gtype] * TS[gtype], dtype=np.uint8)
+    rc = host_lib().qmm_quantize_cpu(gtype, w.ctypes.data, w.size, out.ctypes.data)
+    if rc != 0:
+        raise RuntimeError(host_lib().qmm_host_last_error().decode())
+    return out
+
+
+def device_copies(torch, data, copies):
+    t = torch.from_numpy(data).cuda()
+    return [t] + [t.clone() for _ in range(copies - 1)]
+
+
+# ------------------------------------------------------------------------------------------------ timing
+
+def graph_time(torch, fn, steps, warmup):
+    """Capture `steps` calls of fn(i) in one HIP graph and replay it once between synchronizes; the same for
+    `warmup` calls first (untimed).  Returns seconds for the timed replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(3):
+            fn(i)  # eager: sizes workspaces, loads code objects
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    if warmup > 0:
+        gw = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gw):
+            for i in range(warmup):
+                fn(i)
+        gw.replay()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+# ------------------------------------------------------------------------------------------------ workloads
+
+def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
+    wq = quantized_weight(gtype, n, k, seed)
+    ws = device_copies(torch, wq, copies)
+    rng = np.random.default_rng(seed + 1)
+    x = torch.from_numpy(rng.standard_normal((b, k), dtype=np.float32)).cuda()
+    vy, kp = qmm.quantize_decode(gtype, x)
+    out = torch.empty((b, n), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        qmm.quantize_decode(gtype, x, kp=kp, out=vy)
+        qmm.mmvq(gtype, ws[i % copies], vy, k, n, b, kp, out=out)
+
+    def matvec_only(i):
+        qmm.mmvq(gtype, ws[i % copies], vy, k, n, b, kp, out=out)
+
+    t = graph_time(torch, step, steps, warmup)
+    t_kernel = graph_time(torch, matvec_only, steps, warmup)
+    w_bytes = wq.size
+    act_q_bytes = qmm.act_bytes(gtype, b, kp)
+    step_bytes = w_bytes + b * k * 4 + b * n * 4            # f32 activation in, f32 out
+    kernel_bytes = w_bytes + act_q_bytes + b * n * 4        # what the matvec itself must move
+    return {
+        "seconds": t, "ms_per_step": t / steps * 1e3, "gb_s": step_bytes / (t / steps) / 1e9,
+        "step_bytes": step_bytes, "kernel_us": t_kernel / steps * 1e6,
+        "kernel_gb_s": kernel_bytes / (t_kernel / steps) / 1e9, "kernel_bytes": kernel_bytes,
+        "weights": wq, "x": x.cpu().numpy(), "y": out.cpu().numpy(),
+    }
+
+
+def prefill_workload(torch, qmm, gtype, n, k, m, copies, steps, warmup, seed):
+    wq = quantized_weight(gtype, n, k, seed)
+    ws = device_copies(torch, wq, copies)
+    rng = np.random.default_rng(seed + 1)
+    x = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).cuda()
+    y, kp = qmm.quantize_prefill(gtype, x)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        qmm.quantize_prefill(gtype, x, out=y)
+        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out)
+
+    def mmq_only(i):
+        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out)
+
+    t = graph_time(torch, step, steps, warmup)
+    tk = graph_time(torch, mmq_only, steps, warmup)
+    ops = 2.0 * m * n * k
+    return {"ms_per_step": t / steps * 1e3, "tops": ops / (t / steps) / 1e12, "kernel_us": tk / steps * 1e6,
+            "kernel_tops": ops / (tk / steps) / 1e12, "ops": ops,
+            "frac_int8_peak": ops / (tk / steps) / 1e12 / INT8_PEAK_TOPS}
+
+
+def stack_workload(torch, qmm, batches, steps, warmup, seed):
+    """Llama-3-8B linears, Q4_K for q/k/o/gate/up and Q6_K for v/down, 32 layers; one weight per shape is
+    quantized and its bytes copied to every layer (distinct HBM copies, so every step streams 4.44 GB)."""
+    shapes = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
+              ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
+    layers = 32
+    base = {name: quantized_weight(t, n, k, seed + i) for i, (name, t, n, k) in enumerate(shapes)}
+    dev = {name: [torch.from_numpy(base[name]).cuda() for _ in range(layers)] for name, _, _, _ in shapes}
+    total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
+    res = {"weight_bytes_per_step": total_bytes}
+    import qmm as Q
+    for b in batches:
+        rng = np.random.default_rng(seed + 100 + b)
+        xs = {4096: torch.from_numpy(rng.standard_normal((b, 4096), dtype=np.float32)).cuda(),
+              14336: torch.from_numpy(rng.standard_normal((b, 14336), dtype=np.float32)).cuda()}
+        outs = {name: torch.empty((b, n), dtype=torch.float32, device="cuda") for name, _, n, _ in shapes}
+        decode = b <= 16
+        bufs = {}
+        for name, t, n, k in shapes:
+            if decode:
+                bufs[name] = Q.quantize_decode(t, xs[k])
+            else:
+                bufs[name] = Q.quantize_prefill(t, xs[k])
+
+        def step(i):
+            for layer in range(layers):
+                for name, t, n, k in shapes:
+                    vy, kp = bufs[name]
+                    if decode:
+                        Q.quantize_decode(t, xs[k], kp=kp, out=vy)
+                        Q.mmvq(t, dev[name][layer], vy, k, n, b, kp, out=outs[name])
+                    else:
+                        Q.quantize_prefill(t, xs[k], out=vy)
+                        Q.mmq(t, dev[name][layer], vy, k, n, b, out=outs[name])
+
+        st = max(2, steps // 50)
+        t = graph_time(torch, step, st, 1)
+        per = t / st
+        res[f"b{b}"] = {"ms_per_step": per * 1e3, "tokens_per_s": b / per,
+                        "gb_s": total_bytes / per / 1e9, "frac_hbm_peak": total_bytes / per / 1e9 / HBM_PEAK_GBS}
+    return res
+
+
+def moe_workload(torch, qmm, steps, warmup, seed):
+    """8 experts, gate/up Q4_K 14336x4096 and down Q4_K 4096x14336; 64 tokens, top-2 from softmax(N(0,1) logits)
+    (Mixtral renormalisation); the grouped prefill path of the MoE experts block."""
+    E, hidden, inter, tokens, topk = 8, 4096, 14336, 64, 2
+    H = host_lib()
+    gate = quantized_weight(Q4K, inter, hidden, seed)
+    up = quantized_weight(Q4K, inter, hidden, seed + 1)
+    down = quantized_weight(Q4K, hidden, inter, seed + 2)
+    handles = []
+    for data, rows, cols in ((gate, inter, hidden), (up, inter, hidden), (down, hidden, inter)):
+        stack = np.concatenate([data] * E)
+        h = ctypes.c_void_p()
+        if H.qmm_qtensor_from_data(Q4K, stack.ctypes.data, stack.size, E, rows, cols, 0, ctypes.byref(h)) != 0:
+            raise RuntimeError(H.qmm_host_last_error().decode())
+        handles.append(h)
+    moe = ctypes.c_void_p()
+    if H.qmm_moe_new(handles[0], handles[1], handles[2], 0, ctypes.byref(moe)) != 0:
+        raise RuntimeError(H.qmm_host_last_error().decode())
+    rng = np.random.default_rng(seed + 3)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :topk].astype(np.int32)
+    w = np.take_along_axis(p, ids, 1)
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((tokens, hidden), dtype=np.float32)).cuda()
+    ids_d, w_d = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    out = torch.empty((tokens, hidden), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        rc = H.qmm_moe_forward(moe, x.data_ptr(), tokens, ids_d.data_ptr(), w_d.data_ptr(), topk, out.data_ptr(),
+                               torch.cuda.current_stream().cuda_stream, 1)
+        if rc != 0:
+            raise RuntimeError(H.qmm_host_last_error().decode())
+
+    st = max(4, steps // 10)
+    t = graph_time(torch, step, st, 2)
+    per = t / st
+    wbytes = 3 * E * gate.size
+    ops = 2.0 * tokens * topk * 3 * inter * hidden
+    return {"ms_per_step": per * 1e3, "weight_bytes": wbytes, "gb_s": wbytes / per / 1e9,
+            "frac_hbm_peak": wbytes / per / 1e9 / HBM_PEAK_GBS, "tops": ops / per / 1e12}
+
+
+# ------------------------------------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(wq, n, k, seconds=10.0):
+    """The oracle's CPU QMatMul (a C restatement of the reference's, oracle/) on the headline workload: Q4_K
+    14336x4096 at b = 1, rotating 8 weight copies (264 MB, beyond any host L3) for about `seconds`."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    rng = np.random.default_rng(SEED + 7)
+    x = rng.standard_normal((1, k), dtype=np.float32)
+    copies = [wq] + [wq.copy() for _ in range(7)]
+    O.matmul(O.Q4K, x, copies[0], n, threads)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.matmul(O.Q4K, x, copies[reps % 8], n, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= 8:
+            break
+    per = el / reps
+    step_bytes = wq.size + k * 4 + n * 4
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} Q4_K 14336x4096 b=1 matvecs (8 rotating weight copies) in {el:.1f} s; "
+                      f"oracle/oracle.c vec_dot_unopt + matmul, OpenMP over output rows; host CPU: {cpu}",
+            "ms_per_step": per * 1e3}
+
+
+# ------------------------------------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--quick", action="store_true", help="headline only: no extra workloads, no CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Decode and prefill shard by output rows with no exchange; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import qmm
+    qmm.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(1)
+    log(f"device: {torch.cuda.get_device_name(0)}; library {qmm.build_id()}")
+
+    n, k = 14336, 4096
+    log("headline: Q4_K 14336x4096 decode b=1")
+    head = decode_workload(torch, qmm, Q4K, n, k, 1, 16, args.steps, args.warmup, SEED)
+    log(f"  {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_s']:.0f} GB/s; kernel {head['kernel_us']:.2f} us")
+
+    extra = {}
+    if not args.quick:
+        for b in (4, 16):
+            log(f"Q4_K decode b={b}")
+            r = decode_workload(torch, qmm, Q4K, n, k, b, 16, args.steps // 2, args.warmup // 2, SEED)
+            extra[f"q4_k_decode_b{b}"] = {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
+        log("Q8_0 4096x4096 decode b=1")
+        r = decode_workload(torch, qmm, Q8_0, 4096, 4096, 1, 32, args.steps, args.warmup, SEED + 5)
+        extra["q8_0_decode_4096"] = {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
+        log("prefill Q4_K [512,4096]x[14336,4096]")
+        extra["q4_k_prefill_m512"] = prefill_workload(torch, qmm, Q4K, 14336, 4096, 512, 4, max(20, args.steps // 20),
+                                                      5, SEED + 9)
+        log("prefill Q6_K [512,14336]x[4096,14336]")
+        extra["q6_k_prefill_m512"] = prefill_workload(torch, qmm, Q6K, 4096, 14336, 512, 4, max(20, args.steps // 20),
+                                                      5, SEED + 11)
+        log("Llama-3-8B linear stack")
+        extra["llama3_8b_linear_stack"] = stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20)
+        log("MoE 8 experts, 64 tokens top-2")
+        extra["moe_8x_q4_k_64tok_top2"] = moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30)
+
+    base = None
+    if not args.quick:
+        log("CPU baseline (oracle)")
+        base = cpu_baseline(head["weights"], n, k, args.cpu_seconds)
+
+    kb = head["kernel_bytes"]
+    achieved = head["kernel_gb_s"]
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "traffic_q4_k_decode_14336x4096_b1.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    line = {
+        "metric": "Q4_K bs=1 matvec GB/s (% of HBM peak); prefill int8 TOPS at M=512",
+        "value": round(head["gb_s"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: weights N(0,0.02) quantized by the library's QTensor quantizer, activations N(0,1), "
+                f"seed {SEED}; 16 weight copies rotated (528 MB)",
+        "config": {"workload": "q4_k_decode_14336x4096_b1", "weight": "Q4_K 14336x4096", "batch": 1,
+                   "activation": "f32 [1,4096] -> Q8_K", "frac_hbm_peak": round(head["gb_s"] / HBM_PEAK_GBS, 4),
+                   "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, HIP graph of K steps"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_mmvq<unit_q4k, out_f32, 1, 4>", "kernel_us": round(head["kernel_us"], 3),
+                     "algorithmic_bytes": kb},
+        "cpu_baseline": base,
+        "extra": extra,
+    }
+    if "q4_k_prefill_m512" in extra:
+        line["prefill_int8_tops_m512"] = round(extra["q4_k_prefill_m512"]["kernel_tops"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
