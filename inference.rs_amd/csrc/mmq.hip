@@ -28,6 +28,11 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef short s2 __attribute__((ext_vector_type(2)));
 
+// waves per SIMD the K-quant prefill kernels are register-limited to
+#ifndef QMM_MMQ_WAVES
+#define QMM_MMQ_WAVES 2
+#endif
+
 constexpr int BM = 128;
 constexpr int BN = 128;
 constexpr int TM = BM / 32;
@@ -171,48 +176,79 @@ struct wq6k {
 
 // ------------------------------------------------------------------------------------------ K-quant kernel
 
-// Loads the activation tile of superblock sb (rows [m0, m0 + BM) of `a`) into LDS; rows past `mrows` are 0.
-__device__ __forceinline__ void stage_q8k(const ActTile &a, int64_t sb, int64_t m0, int64_t mrows,
-                                          const int32_t *__restrict__ row_map, uint8_t *s_qs, float *s_dy,
-                                          _Float16 *s_bs) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int it = 0; it < BM * 16 / 256; it++) {
-    const int i = it * 256 + tid;
-    const int row = i >> 4, c = i & 15;
-    const int64_t m = m0 + row;
-    u32x4 v = {0, 0, 0, 0};
-    if (m < mrows) {
-      const int64_t src = row_map ? row_map[m] : m;
-      v = ld_a16(a.qs + (sb * a.rows + src) * 256 + 16 * c);
-    }
-    *(u32x4 *)(s_qs + row * QS_STRIDE + 16 * c) = v;
-  }
-  if (tid < BM) {
-    const int64_t m = m0 + tid;
-    float dv = 0.0f;
-    if (m < mrows) {
-      const int64_t src = row_map ? row_map[m] : m;
-      dv = a.d[sb * a.rows + src];
-      const int16_t *bs = a.bsums + (sb * a.rows + src) * 16;
-#pragma unroll
-      for (int i = 0; i < 16; i++) s_bs[tid * 16 + i] = (_Float16)(float)bs[i];  // |bsum16| <= 2032: exact
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; i++) s_bs[tid * 16 + i] = (_Float16)0.0f;
-    }
-    s_dy[tid] = dv;
-  }
-}
+// One superblock of the activation tile (BMt rows x 256 values: int8 qs, f32 d, bsums as f16) moves
+// global -> registers -> LDS; the caller double-buffers the LDS copy so the next superblock's loads are in
+// flight during this one's MFMAs.  Rows past `mrows` stage as zeros.
+template <int BMt>
+struct StageQ8K {
+  static constexpr int QCH = BMt * 16 / 256;  // 16-byte qs chunks per thread
+  u32x4 qs[QCH];
+  u32x4 bs;  // threads < 2 BMt: 8 bsums (half a row)
+  float dy;  // threads < BMt
 
-template <class WT, class Out>
+  __device__ __forceinline__ void load(const ActTile &a, int64_t sb, int64_t m0, int64_t mrows,
+                                       const int32_t *__restrict__ row_map) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < QCH; it++) {
+      const int i = it * 256 + tid;
+      const int64_t m = m0 + (i >> 4);
+      qs[it] = (u32x4){0, 0, 0, 0};
+      if (m < mrows) {
+        const int64_t src = row_map ? row_map[m] : m;
+        qs[it] = ld_a16(a.qs + (sb * a.rows + src) * 256 + 16 * (i & 15));
+      }
+    }
+    bs = (u32x4){0, 0, 0, 0};
+    dy = 0.0f;
+    if (tid < 2 * BMt) {
+      const int64_t m = m0 + (tid >> 1);
+      if (m < mrows) {
+        const int64_t src = row_map ? row_map[m] : m;
+        bs = ld_a16((const uint8_t *)(a.bsums + (sb * a.rows + src) * 16) + 16 * (tid & 1));
+      }
+    }
+    if (tid < BMt) {
+      const int64_t m = m0 + tid;
+      dy = 0.0f;
+      if (m < mrows) dy = a.d[sb * a.rows + (row_map ? row_map[m] : m)];
+    }
+  }
+
+  __device__ __forceinline__ void store(uint8_t *s_qs, float *s_dy, _Float16 *s_bs) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < QCH; it++) {
+      const int i = it * 256 + tid;
+      *(u32x4 *)(s_qs + (i >> 4) * QS_STRIDE + 16 * (i & 15)) = qs[it];
+    }
+    if (tid < 2 * BMt) {
+      // |bsum16| <= 16 * 127 = 2032: exact in f16
+      const uint32_t w[4] = {bs.x, bs.y, bs.z, bs.w};
+      v8h h;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        h[2 * i] = (_Float16)(float)(int16_t)(w[i] & 0xffff);
+        h[2 * i + 1] = (_Float16)(float)(int16_t)(w[i] >> 16);
+      }
+      *(v8h *)(s_bs + (tid >> 1) * 16 + 8 * (tid & 1)) = h;
+    }
+    if (tid < BMt) s_dy[tid] = dy;
+  }
+};
+
+// One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows; wave w's lanes hold
+// weight row n0 + 32w + (lane % 32) as the MFMA B column and TM 32x32 output tiles.
+template <class WT, class Out, int TM>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, const int32_t *__restrict__ row_map, int64_t m0,
-                                            int64_t mrows, int64_t n0, int64_t nsb, typename Out::T *__restrict__ dst,
-                                            int64_t ldd, const int32_t *__restrict__ dst_rows) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_qs[BM * QS_STRIDE];
-  __shared__ float s_dy[BM];
-  __shared__ __attribute__((aligned(16))) _Float16 s_bs[BM * 16];
+                                            int64_t mrows, int64_t n0, int64_t sb0, int64_t sb1,
+                                            typename Out::T *__restrict__ dst, int64_t ldd,
+                                            const int32_t *__restrict__ dst_rows, bool accumulate) {
+  constexpr int BMt = 32 * TM;
+  __shared__ __attribute__((aligned(16))) uint8_t s_qs[2][BMt * QS_STRIDE];
+  __shared__ __attribute__((aligned(16))) float s_dy[2][BMt];
+  __shared__ __attribute__((aligned(16))) _Float16 s_bs[2][BMt * 16];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
@@ -223,13 +259,20 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
   for (int t = 0; t < TM; t++) fa[t] = (v16f){};
 
-  for (int64_t sb = 0; sb < nsb; sb++) {
-    typename WT::Raw raw;
-    WT::load(wrow + sb * WT::kBytes, g, raw);  // in flight while the tile is staged
-    __syncthreads();
-    stage_q8k(a, sb, m0, mrows, row_map, s_qs, s_dy, s_bs);
-    __syncthreads();
+  StageQ8K<BMt> st;
+  typename WT::Raw raw, raw_next;
+  WT::load(wrow + sb0 * WT::kBytes, g, raw);
+  st.load(a, sb0, m0, mrows, row_map);
+  st.store(s_qs[0], s_dy[0], s_bs[0]);
+  __syncthreads();
 
+  for (int64_t sb = sb0; sb < sb1; sb++) {
+    const int buf = (int)((sb - sb0) & 1);
+    const bool more = sb + 1 < sb1;
+    if (more) {  // next superblock's weights and activations, in flight during this one's MFMAs
+      WT::load(wrow + (sb + 1) * WT::kBytes, g, raw_next);
+      st.load(a, sb + 1, m0, mrows, row_map);
+    }
     typename WT::Prep p;
     WT::prepare(raw, g, p);
     v16i acc1[TM], acc2[TM];
@@ -241,7 +284,7 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
       WT::planes(raw, p, j, b1, b2);
 #pragma unroll
       for (int t = 0; t < TM; t++) {
-        const v4i av = *(const v4i *)(s_qs + (32 * t + li) * QS_STRIDE + 32 * j + 16 * g);
+        const v4i av = *(const v4i *)(s_qs[buf] + (32 * t + li) * QS_STRIDE + 32 * j + 16 * g);
         acc1[t] = mfma_i8(av, b1, acc1[t]);
         acc2[t] = mfma_i8(av, b2, acc2[t]);
       }
@@ -250,18 +293,27 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     for (int t = 0; t < TM; t++) {
       v16f fmin = (v16f){};
       if (WT::kMin) {
-        const v8h abs_ = *(const v8h *)(s_bs + (32 * t + li) * 16 + 8 * g);
+        const v8h abs_ = *(const v8h *)(s_bs[buf] + (32 * t + li) * 16 + 8 * g);
         fmin = mfma_f16(abs_, p.bmin, fmin);
       }
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float dy = s_dy[32 * t + out_row(r, g)];
-        const int iv = (acc1[t][r] << WT::kShift) + acc2[t][r];
-        float v = p.d * (float)iv;
-        if (WT::kMin) v -= p.dmin * fmin[r];
-        fa[t][r] += dy * v;
+      for (int q = 0; q < 4; q++) {
+        const v4f dy4 = *(const v4f *)(s_dy[buf] + 32 * t + 8 * q + 4 * g);  // rows 8q + 4g + 0..3
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int r = 4 * q + i;
+          const int iv = (acc1[t][r] << WT::kShift) + acc2[t][r];
+          float v = p.d * (float)iv;
+          if (WT::kMin) v -= p.dmin * fmin[r];
+          fa[t][r] += dy4[i] * v;
+        }
       }
     }
+    if (more) {
+      st.store(s_qs[buf ^ 1], s_dy[buf ^ 1], s_bs[buf ^ 1]);
+      raw = raw_next;
+    }
+    __syncthreads();
   }
   if (n >= nrows_w) return;
 #pragma unroll
@@ -271,11 +323,24 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
       const int64_t m = m0 + 32 * t + out_row(r, g);
       if (m < mrows) {
         const int64_t drow = dst_rows ? dst_rows[m] : m;
-        Out::store(dst, drow * ldd + n, fa[t][r]);
+        if (accumulate)  // split K: f32 partial sums meet in dst (zeroed first)
+          __hip_atomic_fetch_add((float *)dst + drow * ldd + n, fa[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          Out::store(dst, drow * ldd + n, fa[t][r]);
       }
     }
 }
 
+// Zero rows of an f32 matrix before split-K partial sums land in it (a kernel, not a memset node, so the
+// launch sequence can sit in a HIP graph).  rows_map != nullptr: zero rows rows_map[0..rows).
+__global__ __launch_bounds__(256) void k_zero_rows(float *__restrict__ dst, int64_t rows, int64_t cols, int64_t ldd,
+                                                   const int32_t *__restrict__ rows_map) {
+  const int64_t r = blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows || c >= cols) return;
+  const int64_t dr = rows_map ? rows_map[r] : r;
+  dst[dr * ldd + c] = 0.0f;
+}
 
 // ------------------------------------------------------------------------------------------ Q8_0 kernel
 
@@ -362,13 +427,16 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
 
 // Workgroups are numbered so that the BM-row tiles sharing one weight tile are consecutive, then spread over
 // the 8 XCDs (dispatch assigns workgroup i to XCD i % 8): each XCD's L2 sees whole weight tiles.
-__device__ __forceinline__ void tile_of(int64_t mtiles, int64_t ntiles, int64_t &mt, int64_t &nt) {
-  const int64_t total = mtiles * ntiles;
+__device__ __forceinline__ void tile_of(int64_t mtiles, int64_t ntiles, int64_t splits, int64_t &mt, int64_t &nt,
+                                        int64_t &split) {
+  const int64_t total = mtiles * ntiles * splits;
   const int64_t b = blockIdx.x;
   int64_t id = b;
   if (total % 8 == 0) id = (b % 8) * (total / 8) + b / 8;
-  mt = id % mtiles;
-  nt = id / mtiles;
+  split = id % splits;
+  const int64_t tile = id / splits;
+  mt = tile % mtiles;
+  nt = tile / mtiles;
 }
 
 ActTile act_tile(int wtype, const void *y, int64_t rows, int64_t nsb) {
@@ -383,37 +451,46 @@ ActTile act_tile(int wtype, const void *y, int64_t rows, int64_t nsb) {
   return a;
 }
 
-template <class WT, class Out>
-__global__ __launch_bounds__(256) void k_mmq_kq(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
-                                                ActTile a, int64_t mrows, int64_t nsb, typename Out::T *__restrict__ dst,
-                                                int64_t ldd) {
-  int64_t mt, nt;
-  tile_of((mrows + BM - 1) / BM, (nrows_w + BN - 1) / BN, mt, nt);
-  mmq_kq_tile<WT, Out>(W, nrows_w, w_row_bytes, a, nullptr, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
+// grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst
+template <class WT, class Out, int TMv>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAVES))) void k_mmq_kq(
+    const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
+    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
+  constexpr int BMt = 32 * TMv;
+  int64_t mt, nt, split;
+  tile_of((mrows + BMt - 1) / BMt, (nrows_w + BN - 1) / BN, splits, mt, nt, split);
+  const int64_t per = (nsb + splits - 1) / splits;
+  const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
+  if (sb0 >= sb1) return;
+  mmq_kq_tile<WT, Out, TMv>(W, nrows_w, w_row_bytes, a, nullptr, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd,
+                            nullptr, splits > 1);
 }
 
 template <class Out>
 __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                                   int64_t nblk_w, ActTile a, int64_t mrows, int64_t nsb,
                                                   typename Out::T *__restrict__ dst, int64_t ldd) {
-  int64_t mt, nt;
-  tile_of((mrows + BM - 1) / BM, (nrows_w + BN - 1) / BN, mt, nt);
+  int64_t mt, nt, split;
+  tile_of((mrows + BM - 1) / BM, (nrows_w + BN - 1) / BN, 1, mt, nt, split);
   mmq_q8_0_tile<Out>(W, nrows_w, w_row_bytes, nblk_w, a, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
 }
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
-template <class WT>
-__global__ __launch_bounds__(256) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
+template <class WT, int TMv>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAVES))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
-                                                    const int32_t *__restrict__ ids_dst, int64_t nsb,
+                                                    const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
                                                     float *__restrict__ dst, int64_t ldd) {
   const int64_t e = blockIdx.z;
-  const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * BM, m1 = bounds[e + 1];
+  const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
   if (m0 >= m1) return;  // uniform over the workgroup
-  mmq_kq_tile<WT, out_f32>(W + e * expert_bytes, nrows_w, w_row_bytes, a, nullptr, m0, m1, (int64_t)blockIdx.x * BN,
-                           nsb, dst, ldd, ids_dst);
+  const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
+  const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
+  if (sb0 >= sb1) return;
+  mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, nullptr, m0, m1,
+                                (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
 }
 
 __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
@@ -446,20 +523,59 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
   return true;
 }
 
+// Compute units of the current device (cached per device id).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// K splits so that tiles x splits fills every CU twice over, each split keeping at least 4 superblocks;
+// only for f32 outputs (the partial sums meet through f32 atomics).
+int64_t k_splits(int64_t tiles, int64_t nsb, bool f32_out) {
+  if (!f32_out) return 1;
+  const int64_t want = 2 * device_cus();
+  int64_t s = 1;
+  while (tiles * s < want && nsb / (s * 2) >= 4) s *= 2;
+  return s;
+}
+
+template <class WT, class Out>
+void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y, int64_t nsb,
+               typename Out::T *d, int64_t ldd, hipStream_t s) {
+  const int64_t ntiles = (nrows_x + BN - 1) / BN;
+  const int tm = ncols_y <= 32 ? 1 : 2;  // 32 activation rows per wave when that covers the batch, else 64
+  const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
+  const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
+  if (splits > 1)
+    k_zero_rows<<<dim3((unsigned)((nrows_x + 255) / 256), (unsigned)ncols_y), 256, 0, s>>>((float *)d, ncols_y, nrows_x,
+                                                                                          ldd, nullptr);
+  const dim3 grid((unsigned)(tiles * splits));
+  if (tm == 1) k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  else k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+}
+
 template <class Out>
 void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_y,
                int64_t stride_row_x, int64_t ldd, hipStream_t s) {
   const int64_t nsb = (ncols_x + 255) / 256;
   const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
   const ActTile a = act_tile(type, y, ncols_y, nsb);
-  const int64_t tiles = ((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN);
-  const dim3 grid((unsigned)tiles);
   typename Out::T *d = (typename Out::T *)dst;
   const uint8_t *w = (const uint8_t *)x;
   switch (type) {
-    case QMM_TYPE_Q4K: k_mmq_kq<wq4k, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd); break;
-    case QMM_TYPE_Q6K: k_mmq_kq<wq6k, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd); break;
-    default: k_mmq_q8_0<Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+    case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
+    case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
+    default: {
+      const dim3 grid((unsigned)(((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN)));
+      k_mmq_q8_0<Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+    }
   }
 }
 
@@ -499,14 +615,32 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   hipStream_t s = (hipStream_t)stream;
   const uint8_t *w = (const uint8_t *)x;
   float *d = (float *)dst;
+  const bool small = ncols_max <= 32;
+  const int64_t ntiles = (nrows_x + BN - 1) / BN;
+  const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
+  // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
+  const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
+  const int64_t splits = type == QMM_TYPE_Q8_0 ? 1 : k_splits(busy, nsb, true);
+  if (splits > 1)
+    k_zero_rows<<<dim3((unsigned)((nrows_x + 255) / 256), (unsigned)ncols_dst), 256, 0, s>>>(d, ncols_dst, nrows_x,
+                                                                                            stride_col_dst, ids_dst);
+  const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
   switch (type) {
     case QMM_TYPE_Q4K:
-      k_mmq_kq_moe<wq4k><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d,
-                                              stride_col_dst);
+      if (small)
+        k_mmq_kq_moe<wq4k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
+      else
+        k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
       break;
     case QMM_TYPE_Q6K:
-      k_mmq_kq_moe<wq6k><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d,
-                                              stride_col_dst);
+      if (small)
+        k_mmq_kq_moe<wq6k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
+      else
+        k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
       break;
     default:
       k_mmq_q8_0_moe<<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds, ids_dst, nsb,
