@@ -81,9 +81,23 @@ def device_copies(torch, data, copies):
 
 # ------------------------------------------------------------------------------------------------ timing
 
+EAGER = False  # --eager: launch every step directly (for counter collection, which wants plain dispatches)
+
+
 def graph_time(torch, fn, steps, warmup):
     """Capture `steps` calls of fn(i) in one HIP graph and replay it once between synchronizes; the same for
     `warmup` calls first (untimed).  Returns seconds for the timed replay."""
+    if EAGER:
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(i)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 1e3
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -113,6 +127,8 @@ def graph_time(torch, fn, steps, warmup):
 # ------------------------------------------------------------------------------------------------ workloads
 
 def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
+    """One step = the reference's two launches: launch_mmvq_gguf_quantize_* (f32 activation -> Q8 blocks) and
+    launch_mmvq_gguf_<t>_f32_plain (the matvec).  The matvec alone is timed in a second graph."""
     wq = quantized_weight(gtype, n, k, seed)
     ws = device_copies(torch, wq, copies)
     rng = np.random.default_rng(seed + 1)
@@ -132,7 +148,8 @@ def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
     w_bytes = wq.size
     act_q_bytes = qmm.act_bytes(gtype, b, kp)
     step_bytes = w_bytes + b * k * 4 + b * n * 4            # f32 activation in, f32 out
-    kernel_bytes = w_bytes + act_q_bytes + b * n * 4        # what the matvec itself must move
+    # what the matvec itself must move: weights, the Q8 activation blocks, the f32 outputs
+    kernel_bytes = w_bytes + act_q_bytes + b * n * 4
     return {
         "seconds": t, "ms_per_step": t / steps * 1e3, "gb_s": step_bytes / (t / steps) / 1e9,
         "step_bytes": step_bytes, "kernel_us": t_kernel / steps * 1e6,
@@ -296,7 +313,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline only: no extra workloads, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="no HIP graphs: one dispatch per launch (for rocprofv3 --pmc)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="only copy MB megabytes device-to-device 20 times (the known-size kernel that scales HBM "
+                         "counters), then exit")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Decode and prefill shard by output rows with no exchange; see DESIGN.md.", file=sys.stderr)
@@ -308,6 +331,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy:
+        nbytes = args.calibrate_copy * 1000 * 1000
+        a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 20}))
+        return
     log(f"device: {torch.cuda.get_device_name(0)}; library {qmm.build_id()}")
 
     n, k = 14336, 4096
@@ -363,10 +396,11 @@ def main():
                 f"seed {SEED}; 16 weight copies rotated (528 MB)",
         "config": {"workload": "q4_k_decode_14336x4096_b1", "weight": "Q4_K 14336x4096", "batch": 1,
                    "activation": "f32 [1,4096] -> Q8_K", "frac_hbm_peak": round(head["gb_s"] / HBM_PEAK_GBS, 4),
-                   "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, HIP graph of K steps"},
+                   "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, "
+                           "HIP graph of K steps"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_mmvq<unit_q4k, out_f32, 1, 4>", "kernel_us": round(head["kernel_us"], 3),
+                     "kernel": "k_mmvq_p<unit_q4k, 1, 1, true>", "kernel_us": round(head["kernel_us"], 3),
                      "algorithmic_bytes": kb},
         "cpu_baseline": base,
         "extra": extra,

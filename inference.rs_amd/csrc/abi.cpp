@@ -1,4 +1,5 @@
 // Library identity and the per-thread error slot of the C ABI.
+#include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -24,6 +25,18 @@ void qmm_set_error(const char *fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_error, sizeof g_error, fmt, ap);
   va_end(ap);
+}
+
+int qmm_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
 }
 
 extern "C" const char *qmm_last_error(void) { return g_error; }

@@ -15,6 +15,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ host-side error reporting
 void qmm_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+// compute units of the current device (queried once per device)
+int qmm_device_cus();
 
 // ------------------------------------------------------------------ scalar conversions (device)
 

@@ -523,24 +523,11 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
   return true;
 }
 
-// Compute units of the current device (cached per device id).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 // K splits so that tiles x splits fills every CU twice over, each split keeping at least 4 superblocks;
 // only for f32 outputs (the partial sums meet through f32 atomics).
 int64_t k_splits(int64_t tiles, int64_t nsb, bool f32_out) {
   if (!f32_out) return 1;
-  const int64_t want = 2 * device_cus();
+  const int64_t want = 2 * qmm_device_cus();
   int64_t s = 1;
   while (tiles * s < want && nsb / (s * 2) >= 4) s *= 2;
   return s;

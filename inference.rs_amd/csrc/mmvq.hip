@@ -15,6 +15,7 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
 
+
 template <class U, class Out, int NC, int R>
 __global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ vy,
                                               typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
@@ -50,6 +51,77 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, co
       const float v = wave_sum(acc[r][j]);
       if (lane == 0 && row0 + r < nrows) Out::store(dst, (int64_t)j * stride_col_dst + row0 + r, v);
     }
+}
+
+// ------------------------------------------------------------------------------------------------ persistent form
+
+__device__ __forceinline__ void store_any(void *dst, int type, int64_t i, float v) {
+  switch (type) {
+    case QMM_TYPE_F16: ((uint16_t *)dst)[i] = f32_to_f16_bits(v); break;
+    case QMM_TYPE_BF16: ((uint16_t *)dst)[i] = f32_to_bf16_bits(v); break;
+    default: ((float *)dst)[i] = v;
+  }
+}
+
+// Persistent decode matvec: wave w of the grid takes rows w, w + T, w + 2T, ... (T waves in the grid), so a few
+// thousand resident waves keep the HBM queues full, and each wave requests its next row's weights before it
+// does the current row's math.  Lane l owns units l + 64 s (s < S) of every row, so with NC * S <= 2 its
+// activation units stay in registers for the whole launch.  FULL: every lane has all S units (no guards).
+template <class U, int NC, int S, bool FULL>
+__global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
+                                                void *__restrict__ dst, int out_type, int nrows, int64_t row_bytes,
+                                                int nunits, int64_t act_row_bytes, int stride_col_dst) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tw = gridDim.x * kWaves;
+  int row = blockIdx.x * kWaves + wave;
+  if (row >= nrows) return;  // whole wave
+  auto has = [&](int s) { return FULL || lane + 64 * s < nunits; };
+  constexpr bool kRegs = NC * S <= 2;
+  typename U::A areg[kRegs ? NC * S : 1];
+  if (kRegs) {
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+      for (int j = 0; j < NC; j++)
+        if (has(s)) U::load_a(act + j * act_row_bytes, lane + 64 * s, areg[kRegs ? s * NC + j : 0]);
+  }
+  typename U::W w[S];
+#pragma unroll
+  for (int s = 0; s < S; s++)
+    if (has(s)) U::load_w(vx + (int64_t)row * row_bytes, lane + 64 * s, w[s]);
+  for (; row < nrows; row += tw) {
+    typename U::W wn[S];  // the next row's weights, in flight during this row's math
+    if (row + tw < nrows) {
+#pragma unroll
+      for (int s = 0; s < S; s++)
+        if (has(s)) U::load_w(vx + (int64_t)(row + tw) * row_bytes, lane + 64 * s, wn[s]);
+    }
+    float acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) acc[j] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      if (!has(s)) continue;
+      const int u = lane + 64 * s;
+#pragma unroll
+      for (int j = 0; j < NC; j++) {
+        if (kRegs) {
+          acc[j] += U::dot(w[s], areg[s * NC + j], u);
+        } else {
+          typename U::A a;
+          U::load_a(act + j * act_row_bytes, u, a);
+          acc[j] += U::dot(w[s], a, u);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      const float v = wave_sum(acc[j]);
+      if (lane == 0) store_any(dst, out_type, (int64_t)j * stride_col_dst + row, v);
+    }
+#pragma unroll
+    for (int s = 0; s < S; s++) w[s] = wn[s];
+  }
 }
 
 // MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's
@@ -105,9 +177,60 @@ void launch_nc(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k
                                              stride_col_dst);
 }
 
+// Persistent launch of NC columns with S units per lane: grid capped at 8 workgroups per CU.
+template <class U>
+void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, void *dst, int out_type, int k, int nrows,
+              int64_t act_row_bytes, int stride_col_dst, hipStream_t s) {
+  const int64_t wgs = qmm_ceil_div(nrows, kWaves);
+  const dim3 grid((unsigned)(wgs < 8 * qmm_device_cus() ? wgs : 8 * qmm_device_cus()));
+  const int64_t rb = U::row_bytes(k);
+  const int nu = U::units(k);
+  const bool full = nu % 64 == 0;
+#define QMM_P(NC, SS)                                                                                             \
+  do {                                                                                                            \
+    if (full)                                                                                                     \
+      k_mmvq_p<U, NC, SS, true><<<grid, 256, 0, s>>>(vx, act, dst, out_type, nrows, rb, nu, act_row_bytes,        \
+                                                     stride_col_dst);                                             \
+    else                                                                                                          \
+      k_mmvq_p<U, NC, SS, false><<<grid, 256, 0, s>>>(vx, act, dst, out_type, nrows, rb, nu, act_row_bytes,       \
+                                                      stride_col_dst);                                            \
+  } while (0)
+#define QMM_P_S(NC)                \
+  switch (S) {                     \
+    case 1: QMM_P(NC, 1); break;   \
+    case 2: QMM_P(NC, 2); break;   \
+    default: QMM_P(NC, 4); break;  \
+  }
+  switch (nc) {
+    case 1: QMM_P_S(1) break;
+    case 2: QMM_P_S(2) break;
+    case 3: QMM_P_S(3) break;
+    case 4: QMM_P_S(4) break;
+    case 5: QMM_P_S(5) break;
+    case 6: QMM_P_S(6) break;
+    case 7: QMM_P_S(7) break;
+    default: QMM_P_S(8) break;
+  }
+#undef QMM_P_S
+#undef QMM_P
+}
+
+int out_type_of(const out_f32 *) { return QMM_TYPE_F32; }
+int out_type_of(const out_f16 *) { return QMM_TYPE_F16; }
+int out_type_of(const out_bf16 *) { return QMM_TYPE_BF16; }
+
 template <class U, class Out>
 void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
                  int stride_col_dst, int b, hipStream_t s) {
+  const int S = (int)qmm_ceil_div(U::units(k), 64);
+  if (S <= 4) {
+    for (int j0 = 0; j0 < b; j0 += 8) {
+      const int nc = b - j0 < 8 ? b - j0 : 8;
+      launch_p<U>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst,
+                  out_type_of((const Out *)nullptr), k, nrows, act_row_bytes, stride_col_dst, s);
+    }
+    return;
+  }
   // up to 8 columns per pass; weights are re-streamed once per further pass
   for (int j0 = 0; j0 < b; j0 += 8) {
     const int nc = b - j0 < 8 ? b - j0 : 8;
@@ -300,3 +423,4 @@ void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all
           stream, "indexed_moe_q6k");
 }
 }
+

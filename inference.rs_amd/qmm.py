@@ -295,3 +295,4 @@ def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n:
         k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, 256, 160 * 1024, 64, _stream())
     check()
     return out
+

@@ -143,3 +143,4 @@ def test_row_stride_and_dst_stride():
     got = out.cpu().numpy()
     assert_parity(got[:, :n], O.matmul(O.Q6K, x, wq, n))
     assert np.all(got[:, n:] == 123.0)  # nothing written past nrows
+
