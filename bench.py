@@ -306,6 +306,14 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 
 # ------------------------------------------------------------------------------------------------ main
 
+EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
+               "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2"}
+
+
+def decode_summary(r):
+    return {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,6 +322,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no extra workloads, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs: one dispatch per launch (for rocprofv3 --pmc)")
+    ap.add_argument("--only", choices=sorted(EXTRA_NAMES), default=None,
+                    help="run only this extra workload (no headline, no CPU baseline) and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only copy MB megabytes device-to-device 20 times (the known-size kernel that scales HBM "
                          "counters), then exit")
@@ -322,7 +332,7 @@ def main():
     EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
-              "Decode and prefill shard by output rows with no exchange; see DESIGN.md.", file=sys.stderr)
+              "Decode and prefill would shard by output rows with no exchange.", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -344,29 +354,35 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}; library {qmm.build_id()}")
 
     n, k = 14336, 4096
+    extra_runs = {
+        "q4_k_decode_b4": lambda: decode_summary(decode_workload(torch, qmm, Q4K, n, k, 4, 16, args.steps // 2,
+                                                                 args.warmup // 2, SEED)),
+        "q4_k_decode_b16": lambda: decode_summary(decode_workload(torch, qmm, Q4K, n, k, 16, 16, args.steps // 2,
+                                                                  args.warmup // 2, SEED)),
+        "q8_0_decode_4096": lambda: decode_summary(decode_workload(torch, qmm, Q8_0, 4096, 4096, 1, 32, args.steps,
+                                                                   args.warmup, SEED + 5)),
+        "q4_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q4K, 14336, 4096, 512, 4,
+                                                      max(20, args.steps // 20), 5, SEED + 9),
+        "q6_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q6K, 4096, 14336, 512, 4,
+                                                      max(20, args.steps // 20), 5, SEED + 11),
+        "llama3_8b_linear_stack": lambda: stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20),
+        "moe_8x_q4_k_64tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30),
+    }
+    assert set(extra_runs) == EXTRA_NAMES
+    if args.only:
+        log(f"only: {args.only}")
+        print(json.dumps({args.only: extra_runs[args.only]()}), flush=True)
+        return
+
     log("headline: Q4_K 14336x4096 decode b=1")
     head = decode_workload(torch, qmm, Q4K, n, k, 1, 16, args.steps, args.warmup, SEED)
     log(f"  {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_s']:.0f} GB/s; kernel {head['kernel_us']:.2f} us")
 
     extra = {}
     if not args.quick:
-        for b in (4, 16):
-            log(f"Q4_K decode b={b}")
-            r = decode_workload(torch, qmm, Q4K, n, k, b, 16, args.steps // 2, args.warmup // 2, SEED)
-            extra[f"q4_k_decode_b{b}"] = {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
-        log("Q8_0 4096x4096 decode b=1")
-        r = decode_workload(torch, qmm, Q8_0, 4096, 4096, 1, 32, args.steps, args.warmup, SEED + 5)
-        extra["q8_0_decode_4096"] = {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
-        log("prefill Q4_K [512,4096]x[14336,4096]")
-        extra["q4_k_prefill_m512"] = prefill_workload(torch, qmm, Q4K, 14336, 4096, 512, 4, max(20, args.steps // 20),
-                                                      5, SEED + 9)
-        log("prefill Q6_K [512,14336]x[4096,14336]")
-        extra["q6_k_prefill_m512"] = prefill_workload(torch, qmm, Q6K, 4096, 14336, 512, 4, max(20, args.steps // 20),
-                                                      5, SEED + 11)
-        log("Llama-3-8B linear stack")
-        extra["llama3_8b_linear_stack"] = stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20)
-        log("MoE 8 experts, 64 tokens top-2")
-        extra["moe_8x_q4_k_64tok_top2"] = moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30)
+        for name, run in extra_runs.items():
+            log(name)
+            extra[name] = run()
 
     base = None
     if not args.quick:

@@ -17,7 +17,7 @@
  *       a qmm_block_q8k (292 B per 256 values) or qmm_block_q8_0 (34 B per 32 values) as in qmm_blocks.h.
  *   prefill layout (launch_mmq_quantize_*):        per channel, for ne1 rows and nsb = ne0 / 256
  *       256-value chunks: qs[nsb][ne1][256] int8, then d[nsb][ne1], then
- *         Q8_K: d f32, bsums[nsb][ne1][16] int16         (292 B per 256 values)
+ *         Q8_K: d f32, bsums[nsb][ne1][16] as f16 (exact)  (292 B per 256 values)
  *         Q8_0: d f16 [nsb][ne1][8] (one per 32 values)  (272 B per 256 values)
  *       i.e. ne0 * ne1 * 292 / 256 (Q8_K) or ne0 * ne1 * 272 / 256 (Q8_0) bytes per channel.
  *

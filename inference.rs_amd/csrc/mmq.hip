@@ -20,18 +20,11 @@
 // lane/byte -> k assignment, so the hardware's k order inside an MFMA does not matter.
 #include "common.h"
 #include "inferencequant.h"
+#include "planes.h"
 #include "units.h"
 
 namespace {
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-typedef short s2 __attribute__((ext_vector_type(2)));
-
-// waves per SIMD the K-quant prefill kernels are register-limited to
-#ifndef QMM_MMQ_WAVES
-#define QMM_MMQ_WAVES 2
-#endif
 
 constexpr int BM = 128;
 constexpr int BN = 128;
@@ -41,250 +34,113 @@ constexpr int QS_STRIDE = 272;  // LDS row stride of the activation tile: 256 + 
 struct ActTile {
   // global views of one channel of the prefill activation layout (include/inferencequant.h)
   const uint8_t *qs;     // [nsb][rows][256]
-  const float *d;        // [nsb][rows]             (Q8_K)
-  const int16_t *bsums;  // [nsb][rows][16]         (Q8_K)
-  const uint16_t *d8;    // [nsb][rows][8] f16      (Q8_0)
-  int64_t rows;
+  const uint16_t *d8;    // [nsb][rows][8] f16      (Q8_0; Q8_K's d f32 [nsb][rows] and bsums f16 [nsb][rows][16]
+                         //                          follow qs and are addressed from qs)
+  int64_t rows, nsb;
 };
 
-__device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
-__device__ __forceinline__ v16f mfma_f16(v8h a, v8h b, v16f c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t v, uint32_t s) {
-  // four byte lanes times a small factor; every product < 256 so no lane carries into the next
-  const us2 r = __builtin_bit_cast(us2, v) * (us2){(unsigned short)s, (unsigned short)s};
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-// Row of 32x32 output register r of lane group g (v_mfma 32x32 D layout): 8 (r / 4) + 4 g + r % 4
-__device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
-
-// ------------------------------------------------------------------------------------------ weight policies
-
-// Q4_K: per lane (weight row n, lane group g), per superblock: 16 B header + 4 x 16 B of nibbles
-// (qs[32c + 16g .. +16], c = 0..3) -> sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles).
-struct wq4k {
-  static constexpr int kBytes = 144;
-  static constexpr int kShift = 3;  // I1 = 8 * plane1 + plane2
-  static constexpr bool kMin = true;
-  struct Raw {
-    u32x4 hdr, q[4];
-  };
-  static __device__ __forceinline__ void load(const uint8_t *blk, int g, Raw &r) {
-    r.hdr = ld_a16(blk);
-#pragma unroll
-    for (int c = 0; c < 4; c++) r.q[c] = ld_a16(blk + 16 + 32 * c + 16 * g);
-  }
-  struct Prep {
-    uint32_t sh[8], sl[8];
-    float d, dmin;
-    v8h bmin;
-  };
-  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
-    const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
-    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-    uint32_t m[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {  // get_scale_min_k4 (quantized/utils.rs:119-129)
-      uint32_t sc;
-      if (j < 4) {
-        sc = byte(j) & 63;
-        m[j] = byte(j + 4) & 63;
-      } else {
-        sc = (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
-        m[j] = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
-      }
-      p.sh[j] = sc >> 3;
-      p.sl[j] = sc & 7;
-    }
-    p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
-    p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
-    // B operand of the min-term MFMA: k = 8g + b <-> bsum16 index 8g + b <-> sub-block (8g + b) / 2
-#pragma unroll
-    for (int b = 0; b < 8; b++) p.bmin[b] = (_Float16)(float)m[4 * g + (b >> 1)];
-  }
-  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
-    const u32x4 q = r.q[j >> 1];
-    const uint32_t sh = p.sh[j], sl = p.sl[j];
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t nib = (j & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
-      b1[i] = (int)mul_bytes(nib, sh);
-      b2[i] = (int)mul_bytes(nib, sl);
-    }
-  }
-};
-
-// Q6_K: per lane, per superblock: ql[64h + 32p + 16g ..+16], qh[32h + 16g ..+16] (h, p in {0,1}), the 8 scales
-// sc[2j + g] and d.  Chunk j (32 values 32j..32j+31) covers h = j / 4, q = j % 4, l = 16g + (0..15).
-struct wq6k {
-  static constexpr int kBytes = 210;
-  static constexpr int kShift = 6;  // I = 64 * wh + wl
-  static constexpr bool kMin = false;
-  struct Raw {
-    uint32_t ql[2][2][4], qh[2][4];
-    uint32_t sc[4];
-    uint32_t d;
-  };
-  static __device__ __forceinline__ void load(const uint8_t *blk, int g, Raw &r) {
-    const uint32_t off = (uint32_t)((uintptr_t)blk & 3);
-    const uint8_t *a4 = blk - off;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-#pragma unroll
-      for (int p = 0; p < 2; p++) unit_q6k::ld16_off(a4 + 64 * h + 32 * p + 16 * g, off, r.ql[h][p]);
-      unit_q6k::ld16_off(a4 + 128 + 32 * h + 16 * g, off, r.qh[h]);
-    }
-    unit_q6k::ld16_off(a4 + 192, off, r.sc);
-    r.d = ld16(blk + 208);
-  }
-  struct Prep {
-    int sc[8];
-    float d;
-    float dmin;  // unused: Q6_K has no min term
-    v8h bmin;
-  };
-  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int idx = 2 * j + g;  // scale of values 16 (2j + g) .. +16
-      p.sc[j] = (int)(int8_t)((r.sc[idx >> 2] >> (8 * (idx & 3))) & 0xff);
-    }
-    p.d = f16_bits_to_f32(r.d);
-    p.dmin = 0.0f;
-    p.bmin = (v8h){};
-  }
-  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
-    const int h = j >> 2, q = j & 3;
-    const uint32_t *ql = r.ql[h][q & 1];
-    const int nsh = (q >> 1) * 4;
-    const s2 sc2 = {(short)p.sc[j], (short)p.sc[j]};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((r.qh[h][i] >> (2 * q)) & 0x03030303u) << 4);
-      // bytes 0,2 and 1,3 in 16-bit lanes, minus 32, times the scale: w in [-4096, 4064]
-      const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
-      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
-      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
-      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
-    }
-  }
-};
 
 // ------------------------------------------------------------------------------------------ K-quant kernel
 
-// One superblock of the activation tile (BMt rows x 256 values: int8 qs, f32 d, bsums as f16) moves
-// global -> registers -> LDS; the caller double-buffers the LDS copy so the next superblock's loads are in
-// flight during this one's MFMAs.  Rows past `mrows` stage as zeros.
-template <int BMt>
-struct StageQ8K {
-  static constexpr int QCH = BMt * 16 / 256;  // 16-byte qs chunks per thread
-  u32x4 qs[QCH];
-  u32x4 bs;  // threads < 2 BMt: 8 bsums (half a row)
-  float dy;  // threads < BMt
 
-  __device__ __forceinline__ void load(const ActTile &a, int64_t sb, int64_t m0, int64_t mrows,
-                                       const int32_t *__restrict__ row_map) {
+// One superblock of the activation tile (BMt rows x 256 values: int8 qs, f16 bsums, f32 d) in registers on its
+// way from global memory to an LDS slot.  The prefill layout keeps a superblock's rows contiguous, so thread t
+// moves 16-byte chunks t, t + 256, ... of each section; every address is a per-thread constant plus a scalar.
+template <int BMt, bool MIN>
+struct ActStage {
+  static constexpr int NQ = BMt * 16 / 256;  // qs chunks per thread
+  static constexpr int QS = BMt * 256;       // LDS bytes: qs, row r's chunk c at chunk slot c ^ (r % 16)
+  static constexpr int BSB = MIN ? BMt * 32 : 0;
+  static constexpr int STAGE = QS + BSB + BMt * 4;
+  u32x4 q[NQ];
+  u32x4 bs;  // MIN, threads < 2 BMt: 8 bsums
+  u32x4 d;   // threads < BMt / 4: 4 scales
+
+  // voff: per-thread byte offsets (qs, bsums, d) of row m0; s_*: offsets of superblock sb.  The whole offset
+  // goes in the vector operand, where the buffer range check applies: rows past the channel read as zero.
+  __device__ __forceinline__ void load(rsrc_t r, const uint32_t voff[3], uint32_t s_qs, uint32_t s_bs,
+                                       uint32_t s_d) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < QCH; it++) {
-      const int i = it * 256 + tid;
-      const int64_t m = m0 + (i >> 4);
-      qs[it] = (u32x4){0, 0, 0, 0};
-      if (m < mrows) {
-        const int64_t src = row_map ? row_map[m] : m;
-        qs[it] = ld_a16(a.qs + (sb * a.rows + src) * 256 + 16 * (i & 15));
-      }
-    }
-    bs = (u32x4){0, 0, 0, 0};
-    dy = 0.0f;
-    if (tid < 2 * BMt) {
-      const int64_t m = m0 + (tid >> 1);
-      if (m < mrows) {
-        const int64_t src = row_map ? row_map[m] : m;
-        bs = ld_a16((const uint8_t *)(a.bsums + (sb * a.rows + src) * 16) + 16 * (tid & 1));
-      }
-    }
-    if (tid < BMt) {
-      const int64_t m = m0 + tid;
-      dy = 0.0f;
-      if (m < mrows) dy = a.d[sb * a.rows + (row_map ? row_map[m] : m)];
-    }
+    for (int i = 0; i < NQ; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[0] + s_qs + 4096 * i, 0, 0);
+    if (MIN && tid < 2 * BMt) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
+    if (tid < BMt / 4) d = __builtin_amdgcn_raw_buffer_load_b128(r, voff[2] + s_d, 0, 0);
   }
-
-  __device__ __forceinline__ void store(uint8_t *s_qs, float *s_dy, _Float16 *s_bs) const {
+  __device__ __forceinline__ void store(uint8_t *slot) const {
     const int tid = threadIdx.x;
+    const int swz = (tid & 15) ^ ((tid >> 4) & 15);
 #pragma unroll
-    for (int it = 0; it < QCH; it++) {
-      const int i = it * 256 + tid;
-      *(u32x4 *)(s_qs + (i >> 4) * QS_STRIDE + 16 * (i & 15)) = qs[it];
-    }
-    if (tid < 2 * BMt) {
-      // |bsum16| <= 16 * 127 = 2032: exact in f16
-      const uint32_t w[4] = {bs.x, bs.y, bs.z, bs.w};
-      v8h h;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        h[2 * i] = (_Float16)(float)(int16_t)(w[i] & 0xffff);
-        h[2 * i + 1] = (_Float16)(float)(int16_t)(w[i] >> 16);
-      }
-      *(v8h *)(s_bs + (tid >> 1) * 16 + 8 * (tid & 1)) = h;
-    }
-    if (tid < BMt) s_dy[tid] = dy;
+    for (int i = 0; i < NQ; i++) *(u32x4 *)(slot + 4096 * i + 256 * (tid >> 4) + 16 * swz) = q[i];
+    if (MIN && tid < 2 * BMt) *(u32x4 *)(slot + QS + 16 * tid) = bs;
+    if (tid < BMt / 4) *(u32x4 *)(slot + QS + BSB + 16 * tid) = d;
   }
 };
 
+// LDS-only workgroup barrier: orders LDS accesses (lgkmcnt) but leaves global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows; wave w's lanes hold
-// weight row n0 + 32w + (lane % 32) as the MFMA B column and TM 32x32 output tiles.
+// weight row n0 + 32w + (lane % 32) as the MFMA B column and TM 32x32 output tiles.  Three LDS slots and three
+// register sets rotate: during superblock s the workgroup computes from slot s, writes the activations of s + 1
+// (loaded one step earlier) into slot s + 1, and has the activations and weights of s + 2 in flight, so global
+// latency is covered by two steps of MFMA work.  One LDS barrier per superblock.
 template <class WT, class Out, int TM>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
-                                            const ActTile &a, const int32_t *__restrict__ row_map, int64_t m0,
-                                            int64_t mrows, int64_t n0, int64_t sb0, int64_t sb1,
-                                            typename Out::T *__restrict__ dst, int64_t ldd,
+                                            const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
+                                            int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
                                             const int32_t *__restrict__ dst_rows, bool accumulate) {
   constexpr int BMt = 32 * TM;
-  __shared__ __attribute__((aligned(16))) uint8_t s_qs[2][BMt * QS_STRIDE];
-  __shared__ __attribute__((aligned(16))) float s_dy[2][BMt];
-  __shared__ __attribute__((aligned(16))) _Float16 s_bs[2][BMt * 16];
+  typedef ActStage<BMt, WT::kMin> AS;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AS::STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
-  const int64_t n_ld = n < nrows_w ? n : nrows_w - 1;
-  const uint8_t *wrow = W + n_ld * w_row_bytes;
+  const int64_t nlast = (nrows_w - n0 < BN ? nrows_w - n0 : BN) - 1;
+  const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;  // row within the tile, clamped
+
+  // activations: one resource over the channel; the scalar part of each address moves with the superblock
+  const int64_t rows = a.rows, nsb = a.nsb;
+  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 292);
+  const uint32_t voff[3] = {(uint32_t)(m0 * 256 + 16 * tid),
+                            (uint32_t)(nsb * rows * 260 + m0 * 32 + 16 * tid),
+                            (uint32_t)(nsb * rows * 256 + m0 * 4 + 16 * tid)};
+  // weights: one resource over the tile's rows
+  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, (nlast + 1) * w_row_bytes);
+  const uint32_t wrow = (uint32_t)(nl * w_row_bytes);
+
+  // LDS read offsets of this lane's A fragments: row 32t + li, chunk 2j + g, swizzled
+  uint32_t qoff[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) qoff[j] = 256 * li + 16 * ((2 * j + g) ^ (li & 15));
 
   v16f fa[TM];
 #pragma unroll
   for (int t = 0; t < TM; t++) fa[t] = (v16f){};
 
-  StageQ8K<BMt> st;
-  typename WT::Raw raw, raw_next;
-  WT::load(wrow + sb0 * WT::kBytes, g, raw);
-  st.load(a, sb0, m0, mrows, row_map);
-  st.store(s_qs[0], s_dy[0], s_bs[0]);
-  __syncthreads();
+  AS st[3];
+  typename WT::Raw raw[3];
+  auto issue = [&](int64_t sb, AS &as, typename WT::Raw &rr) {
+    as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 32), (uint32_t)(sb * rows * 4));
+    WT::load(rw, wrow, (uint32_t)sb, g, rr);
+  };
 
-  for (int64_t sb = sb0; sb < sb1; sb++) {
-    const int buf = (int)((sb - sb0) & 1);
-    const bool more = sb + 1 < sb1;
-    if (more) {  // next superblock's weights and activations, in flight during this one's MFMAs
-      WT::load(wrow + (sb + 1) * WT::kBytes, g, raw_next);
-      st.load(a, sb + 1, m0, mrows, row_map);
-    }
+  auto compute = [&](const uint8_t *slot, const typename WT::Raw &rr) {
     typename WT::Prep p;
-    WT::prepare(raw, g, p);
+    WT::prepare(rr, g, p);
     v16i acc1[TM], acc2[TM];
 #pragma unroll
     for (int t = 0; t < TM; t++) acc1[t] = acc2[t] = (v16i){};
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       v4i b1, b2;
-      WT::planes(raw, p, j, b1, b2);
+      WT::planes(rr, p, j, b1, b2);
 #pragma unroll
       for (int t = 0; t < TM; t++) {
-        const v4i av = *(const v4i *)(s_qs[buf] + (32 * t + li) * QS_STRIDE + 32 * j + 16 * g);
+        const v4i av = *(const v4i *)(slot + 8192 * t + qoff[j]);
         acc1[t] = mfma_i8(av, b1, acc1[t]);
         acc2[t] = mfma_i8(av, b2, acc2[t]);
       }
@@ -293,12 +149,12 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     for (int t = 0; t < TM; t++) {
       v16f fmin = (v16f){};
       if (WT::kMin) {
-        const v8h abs_ = *(const v8h *)(s_bs[buf] + (32 * t + li) * 16 + 8 * g);
+        const v8h abs_ = *(const v8h *)(slot + AS::QS + (32 * t + li) * 32 + 16 * g);
         fmin = mfma_f16(abs_, p.bmin, fmin);
       }
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const v4f dy4 = *(const v4f *)(s_dy[buf] + 32 * t + 8 * q + 4 * g);  // rows 8q + 4g + 0..3
+        const v4f dy4 = *(const v4f *)(slot + AS::QS + AS::BSB + 4 * (32 * t + 8 * q + 4 * g));  // rows 8q + 4g + i
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int r = 4 * q + i;
@@ -309,12 +165,25 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
         }
       }
     }
-    if (more) {
-      st.store(s_qs[buf ^ 1], s_dy[buf ^ 1], s_bs[buf ^ 1]);
-      raw = raw_next;
-    }
-    __syncthreads();
+  };
+
+  auto step = [&](int64_t s, int u) {
+    // u = (s - sb0) % 3 is a constant after unrolling: slot u, register sets u, u + 1, u + 2
+    lds_barrier();
+    if (s + 2 < sb1) issue(s + 2, st[(u + 2) % 3], raw[(u + 2) % 3]);
+    compute(lds + u * AS::STAGE, raw[u]);
+    if (s + 1 < sb1) st[(u + 1) % 3].store(lds + ((u + 1) % 3) * AS::STAGE);
+  };
+
+  issue(sb0, st[0], raw[0]);
+  if (sb0 + 1 < sb1) issue(sb0 + 1, st[1], raw[1]);
+  st[0].store(lds);
+  for (int64_t sb = sb0; sb < sb1; sb += 3) {
+    step(sb, 0);
+    if (sb + 1 < sb1) step(sb + 1, 1);
+    if (sb + 2 < sb1) step(sb + 2, 2);
   }
+
   if (n >= nrows_w) return;
 #pragma unroll
   for (int t = 0; t < TM; t++)
@@ -439,21 +308,18 @@ __device__ __forceinline__ void tile_of(int64_t mtiles, int64_t ntiles, int64_t 
   nt = tile / mtiles;
 }
 
-ActTile act_tile(int wtype, const void *y, int64_t rows, int64_t nsb) {
+ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
   ActTile a;
   a.qs = (const uint8_t *)y;
   a.rows = rows;
-  const uint8_t *tail = (const uint8_t *)y + nsb * rows * 256;
-  a.d = (const float *)tail;
-  a.bsums = (const int16_t *)(tail + nsb * rows * 4);
-  a.d8 = (const uint16_t *)tail;
-  (void)wtype;
+  a.nsb = nsb;
+  a.d8 = (const uint16_t *)((const uint8_t *)y + nsb * rows * 256);
   return a;
 }
 
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst
 template <class WT, class Out, int TMv>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAVES))) void k_mmq_kq(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void k_mmq_kq(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
     int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
   constexpr int BMt = 32 * TMv;
@@ -462,8 +328,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAV
   const int64_t per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, Out, TMv>(W, nrows_w, w_row_bytes, a, nullptr, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd,
-                            nullptr, splits > 1);
+  mmq_kq_tile<WT, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
+                            splits > 1);
 }
 
 template <class Out>
@@ -478,7 +344,7 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W,
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
 template <class WT, int TMv>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAVES))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
                                                     const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
@@ -489,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QMM_MMQ_WAV
   const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, nullptr, m0, m1,
+  mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
 }
 
@@ -523,11 +389,11 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
   return true;
 }
 
-// K splits so that tiles x splits fills every CU twice over, each split keeping at least 4 superblocks;
+// K splits so that tiles x splits fills every CU once over, each split keeping at least 4 superblocks;
 // only for f32 outputs (the partial sums meet through f32 atomics).
 int64_t k_splits(int64_t tiles, int64_t nsb, bool f32_out) {
   if (!f32_out) return 1;
-  const int64_t want = 2 * qmm_device_cus();
+  const int64_t want = qmm_device_cus();
   int64_t s = 1;
   while (tiles * s < want && nsb / (s * 2) >= 4) s *= 2;
   return s;
@@ -537,7 +403,8 @@ template <class WT, class Out>
 void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y, int64_t nsb,
                typename Out::T *d, int64_t ldd, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
-  const int tm = ncols_y <= 32 ? 1 : 2;  // 32 activation rows per wave when that covers the batch, else 64
+  // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
+  const int tm = ncols_y <= 32 ? 1 : ncols_y <= 64 ? 2 : 4;
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
   const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
   if (splits > 1)
@@ -545,7 +412,8 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
                                                                                           ldd, nullptr);
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1) k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
-  else k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  else if (tm == 2) k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  else k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
 }
 
 template <class Out>
@@ -553,7 +421,7 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
                int64_t stride_row_x, int64_t ldd, hipStream_t s) {
   const int64_t nsb = (ncols_x + 255) / 256;
   const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
-  const ActTile a = act_tile(type, y, ncols_y, nsb);
+  const ActTile a = act_tile(y, ncols_y, nsb);
   typename Out::T *d = (typename Out::T *)dst;
   const uint8_t *w = (const uint8_t *)x;
   switch (type) {
@@ -566,10 +434,20 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
   }
 }
 
+// The kernels address one activation channel with 32-bit offsets.
+bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows) {
+  if ((ncols_x + 255) / 256 * rows * 292 > 0x7ffffff0) {
+    qmm_set_error("%s: activation channel of %lld x %lld values exceeds 2 GiB", who, (long long)rows,
+                  (long long)ncols_x);
+    return false;
+  }
+  return true;
+}
+
 void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x,
          int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int type_dst, void *stream, const char *who) {
   (void)tmp_fixup;
-  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x)) return;
+  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_y)) return;
   if (ncols_y < 0 || stride_col_dst < nrows_x) {
     qmm_set_error("%s: ncols_y=%lld stride_col_dst=%lld", who, (long long)ncols_y, (long long)stride_col_dst);
     return;
@@ -587,7 +465,7 @@ void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int
 void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, void *dst,
              int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,
              int64_t num_experts, int64_t ncols_max, void *stream, const char *who) {
-  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x)) return;
+  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst)) return;
   if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
     qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
                   (long long)num_experts, (long long)ncols_max, (long long)ncols_dst, (long long)stride_col_dst);
@@ -597,7 +475,7 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   const int64_t nsb = (ncols_x + 255) / 256;
   const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
   const int64_t expert_bytes = nrows_x * w_row_bytes;
-  const ActTile a = act_tile(type, y, ncols_dst, nsb);
+  const ActTile a = act_tile(y, ncols_dst, nsb);
   const dim3 grid((unsigned)((nrows_x + BN - 1) / BN), (unsigned)((ncols_max + BM - 1) / BM), (unsigned)num_experts);
   hipStream_t s = (hipStream_t)stream;
   const uint8_t *w = (const uint8_t *)x;

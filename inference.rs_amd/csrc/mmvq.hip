@@ -9,11 +9,18 @@
 // butterfly.  Activations are tiny and hit L2.
 #include "common.h"
 #include "inferencequant.h"
+#include "skinny.h"
 #include "units.h"
 
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
+// from this many activation rows on, K-quant weights go through the MFMA few-row kernel (skinny.hip), which
+// decodes each weight block once for all rows
+#ifndef QMM_SKINNY_MIN_ROWS
+#define QMM_SKINNY_MIN_ROWS 3
+#endif
+constexpr int kSkinnyMinRows = QMM_SKINNY_MIN_ROWS;
 
 
 template <class U, class Out, int NC, int R>
@@ -282,6 +289,10 @@ void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int
   hipStream_t s = (hipStream_t)stream;
   const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
   typename Out::T *d = (typename Out::T *)dst;
+  if (b >= kSkinnyMinRows &&
+      qmm_skinny_decode(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_y,
+                        stride_col_dst, b, s))
+    return;
   switch (type) {
     case QMM_TYPE_Q4K:
       launch_cols<unit_q4k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);

@@ -1,0 +1,156 @@
+// Int8 MFMA operand builders shared by the prefill matmul and the skinny (few-row) matmul: the two int8 weight
+// planes that fold the K-quant sub-block scales into the MFMA operand, the MFMA wrappers and the 32x32 output
+// layout.  Exactness: Q4_K sc (6 bit) = 8 sh + sl, so sc * q4 = 8 (sh * q4) + (sl * q4) with both planes <= 105;
+// Q6_K sc * (q6 - 32) in [-4096, 4064] = 64 wh + wl.  Each superblock's integer dot is exact in int32.
+#pragma once
+
+#include "common.h"
+#include "units.h"
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef short s2 __attribute__((ext_vector_type(2)));
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Buffer resource over [base, base + bytes) (gfx9 raw buffer, dword format): loads past the end return zero.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int n = bytes > 0x7ffffff0 ? 0x7ffffff0 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+__device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ v16f mfma_f16(v8h a, v8h b, v16f c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t v, uint32_t s) {
+  // four byte lanes times a small factor; every product < 256 so no lane carries into the next
+  const us2 r = __builtin_bit_cast(us2, v) * (us2){(unsigned short)s, (unsigned short)s};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Row of 32x32 output register r of lane group g (v_mfma 32x32 D layout): 8 (r / 4) + 4 g + r % 4
+__device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// ------------------------------------------------------------------------------------------ weight policies
+
+// Q4_K: per lane (weight row n, lane group g), per superblock: 16 B header + 4 x 16 B of nibbles
+// (qs[32c + 16g .. +16], c = 0..3) -> sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles).
+struct wq4k {
+  static constexpr int kBytes = 144;
+  static constexpr int kShift = 3;  // I1 = 8 * plane1 + plane2
+  static constexpr bool kMin = true;
+  struct Raw {
+    u32x4 hdr, q[4];
+  };
+  // superblock sb of the row at byte offset `row` of the resource
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
+    const uint32_t o = row + sb * kBytes;
+    r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * c + 16 * g, 0, 0);
+  }
+  struct Prep {
+    uint32_t sh[8], sl[8];
+    float d, dmin;
+    v8h bmin;
+  };
+  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
+    const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
+    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+#pragma unroll
+    for (int j = 0; j < 8; j++) {  // 6-bit scales, get_scale_min_k4 (quantized/utils.rs:119-129)
+      const uint32_t sc = j < 4 ? byte(j) & 63 : (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
+      p.sh[j] = sc >> 3;
+      p.sl[j] = sc & 7;
+    }
+    p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
+    p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
+    // B operand of the min-term MFMA: k = 8g + b <-> bsum16 index 8g + b <-> sub-block 4g + b / 2, whose 6-bit
+    // min is byte(4 + i) & 63 (g = 0) or (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4) (g = 1), i = b / 2
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = byte(4 + i) & 63, hi = (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4);
+      const _Float16 m = (_Float16)(float)(g ? hi : lo);
+      p.bmin[2 * i] = m;
+      p.bmin[2 * i + 1] = m;
+    }
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
+    const u32x4 q = r.q[j >> 1];
+    const uint32_t sh = p.sh[j], sl = p.sl[j];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t nib = (j & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
+      b1[i] = (int)mul_bytes(nib, sh);
+      b2[i] = (int)mul_bytes(nib, sl);
+    }
+  }
+};
+
+// Q6_K: per lane, per superblock: ql[64h + 32p + 16g ..+16], qh[32h + 16g ..+16] (h, p in {0,1}), the 8 scales
+// sc[2j + g] and d.  Chunk j (32 values 32j..32j+31) covers h = j / 4, q = j % 4, l = 16g + (0..15).
+struct wq6k {
+  static constexpr int kBytes = 210;
+  static constexpr int kShift = 6;  // I = 64 * wh + wl
+  static constexpr bool kMin = false;
+  struct Raw {
+    uint32_t ql[2][2][4], qh[2][4];
+    uint32_t sc[4];
+    uint32_t d;
+  };
+  // 16 bytes at a4 + x + off (a4 dword aligned, off 0 or 2) from five dwords
+  static __device__ __forceinline__ void ld16(rsrc_t rs, uint32_t a4, uint32_t x, uint32_t off, uint32_t out[4]) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, a4 + x, 0, 0);
+    const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(rs, a4 + x + 16, 0, 0);
+    out[0] = align_bytes(v.y, v.x, off);
+    out[1] = align_bytes(v.z, v.y, off);
+    out[2] = align_bytes(v.w, v.z, off);
+    out[3] = align_bytes(e, v.w, off);
+  }
+  // superblock sb of the row at byte offset `row` of the resource (210-byte blocks are 2-byte aligned)
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
+    const uint32_t o = row + sb * kBytes, off = o & 3, a4 = o - off;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+      for (int p = 0; p < 2; p++) ld16(rs, a4, 64 * h + 32 * p + 16 * g, off, r.ql[h][p]);
+      ld16(rs, a4, 128 + 32 * h + 16 * g, off, r.qh[h]);
+    }
+    ld16(rs, a4, 192, off, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
+  }
+  struct Prep {
+    int sc[8];
+    float d;
+    float dmin;  // unused: Q6_K has no min term
+    v8h bmin;
+  };
+  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int idx = 2 * j + g;  // scale of values 16 (2j + g) .. +16
+      p.sc[j] = (int)(int8_t)((r.sc[idx >> 2] >> (8 * (idx & 3))) & 0xff);
+    }
+    p.d = f16_bits_to_f32(r.d);
+    p.dmin = 0.0f;
+    p.bmin = (v8h){};
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
+    const int h = j >> 2, q = j & 3;
+    const uint32_t *ql = r.ql[h][q & 1];
+    const int nsh = (q >> 1) * 4;
+    const s2 sc2 = {(short)p.sc[j], (short)p.sc[j]};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((r.qh[h][i] >> (2 * q)) & 0x03030303u) << 4);
+      // bytes 0,2 and 1,3 in 16-bit lanes, minus 32, times the scale: w in [-4096, 4064]
+      const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
+      const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
+      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
+      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
+      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
+      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+    }
+  }
+};

@@ -10,25 +10,31 @@
 
 namespace qmm_q8 {
 
-// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k) or the prefill
-// tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16]).
+// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k, bsums int16) or the
+// prefill tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16] as f16, which holds every
+// bsum exactly: |bsum| <= 16 * 128 = 2048).
 struct q8k_dst {
   uint8_t *qs;
   float *d;
-  int16_t *bsums;
+  uint16_t *bsums;
+  bool bsums_f16;
 };
 
 __device__ __forceinline__ q8k_dst q8k_decode_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8k);
-  return {b + 4, (float *)b, (int16_t *)(b + 260)};
+  return {b + 4, (float *)b, (uint16_t *)(b + 260), false};
 }
 
 __device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
   const int64_t i = sb * rows + r;
   uint8_t *qs = chan + i * 256;
   float *d = (float *)(chan + nsb * rows * 256) + i;
-  int16_t *bs = (int16_t *)(chan + nsb * rows * 260) + i * 16;
-  return {qs, d, bs};
+  uint16_t *bs = (uint16_t *)(chan + nsb * rows * 260) + i * 16;
+  return {qs, d, bs, true};
+}
+
+__device__ __forceinline__ uint16_t bsum_bits(int s, bool f16) {
+  return f16 ? f32_to_f16_bits((float)s) : (uint16_t)(int16_t)s;
 }
 
 // One wave quantizes v[0..3] of lanes 0..63 (values 4*lane .. 4*lane+3 of the block) and writes it.
@@ -56,7 +62,7 @@ __device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst
   if (best == 0.0f) {  // amax == 0: an all-zero block (k_quants.rs:2740-2743)
     *(uint32_t *)(dst.qs + 4 * lane) = 0u;
     if (lane == 0) *dst.d = 0.0f;
-    if ((lane & 3) == 0) dst.bsums[lane >> 2] = 0;
+    if ((lane & 3) == 0) dst.bsums[lane >> 2] = 0;  // +0 in both encodings
     return;
   }
   const float mine = v[bidx & 3];
@@ -71,7 +77,7 @@ __device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst
   const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
                           ((uint32_t)(q[3] & 0xff) << 24);
   *(uint32_t *)(dst.qs + 4 * lane) = packed;
-  if ((lane & 3) == 0) dst.bsums[lane >> 2] = (int16_t)s;
+  if ((lane & 3) == 0) dst.bsums[lane >> 2] = bsum_bits(s, dst.bsums_f16);
   if (lane == 0) *dst.d = 1.0f / iscale;
 }
 

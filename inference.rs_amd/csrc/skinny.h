@@ -1,0 +1,10 @@
+// Internal entry of the few-row MFMA matmul (skinny.hip), used by the decode launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+// Decode-layout activations (b rows of Q8_K blocks, stride_col_y blocks apart) against Q4_K / Q6_K weights;
+// dst[j * stride_col_dst + row] of element type out_type (QMM_TYPE_F32 / F16 / BF16).  Returns false, launching
+// nothing, for a case it does not serve (other weight types, b outside 1..32, K not a multiple of 256).
+bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                       int stride_col_y, int stride_col_dst, int b, hipStream_t s);

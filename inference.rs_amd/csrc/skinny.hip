@@ -1,0 +1,187 @@
+// Few-row matmul for Q4_K / Q6_K weights on int8 MFMA: up to 32 activation rows against a weight matrix
+// streamed once from HBM.  Serves the decode matvec at b >= 2 (the reference's tensor-core matvec,
+// mmvq_tc_k.cuh, fast_mmvq.rs:1897-2126, and its plain launcher at b <= 8) and any matmul whose activation side
+// is at most 32 rows (the expert-grouped prefill at a handful of tokens per expert).
+//
+// A workgroup owns 32 (or, for short weights, 16) weight rows and all activation rows; its 4 waves split the
+// superblocks of K, so every weight byte is loaded by exactly one wave, straight into registers, two superblocks
+// ahead.
+// Each wave's lane (g, li) builds the two int8 weight planes of row n0 + li (planes.h) as the MFMA B column and
+// loads activation row li's int8 values as the A row; one 32x32x32 MFMA per plane per 32 values, the Q4_K min
+// term through one f16 MFMA per superblock, and the per-superblock f32 scaling of the reference
+// (k_quants.rs:1848-1928, 2518-2575).  The four waves' partial tiles are summed through LDS at the end.
+#include "common.h"
+#include "inferencequant.h"
+#include "planes.h"
+#include "skinny.h"
+#include "units.h"
+
+namespace {
+
+// weights with fewer 32-row tiles than this go in 16-row tiles (twice the workgroups)
+#ifndef QMM_SKINNY_WIDE_TILES
+#define QMM_SKINNY_WIDE_TILES 384
+#endif
+
+// A-side fragments of one superblock for activation row li: 8 x 16 int8 (k = 32j + 16g + 0..15), the 8 bsums of
+// 16 values 8g .. 8g + 7 as f16, and the row's scale d.
+struct ActFrag {
+  v4i q[8];
+  v8h bs;
+  float d;
+};
+
+// Decode layout: row m = blocks [m * stride, ...) of 292-byte qmm_block_q8k (f32 d, int8 qs[256], int16 bsums[16]).
+struct act_decode {
+  const uint8_t *base;
+  int64_t bytes;
+  uint32_t row_bytes;
+  __device__ __forceinline__ rsrc_t rsrc() const { return make_rsrc(base, bytes); }
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t row_off, int64_t sb, int g, bool min, ActFrag &f) const {
+    const uint32_t o = row_off + (uint32_t)sb * 292;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, o + 4 + 32 * j + 16 * g, 0, 0));
+    if (min) {
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, o + 260 + 16 * g, 0, 0);
+      const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {  // int16 -> f16, exact (|bsum| <= 2048)
+        f.bs[2 * i] = (_Float16)(float)(int16_t)(w[i] & 0xffff);
+        f.bs[2 * i + 1] = (_Float16)(float)(int16_t)(w[i] >> 16);
+      }
+    }
+    f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
+  }
+};
+
+// The NW waves' partial 32x32 tiles, summed through LDS; lane (g, li) of wave w then stores output registers
+// (16 / NW) w ... (16 / NW) (w + 1) - 1.
+template <class Out, int NW>
+__device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane, int g, int li, int64_t n0,
+                                             int64_t n1, int64_t mrows, typename Out::T *__restrict__ dst,
+                                             int64_t ldd) {
+  __shared__ float red[NW][16][64];
+#pragma unroll
+  for (int r = 0; r < 16; r++) red[wave][r][lane] = fa[r];
+  __syncthreads();
+  const int64_t n = n0 + li;
+  constexpr int RPW = 16 / NW;
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const int r = RPW * wave + i;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) v += red[w][r][lane];
+    const int64_t m = out_row(r, g);
+    if (m < mrows && n < n1) Out::store(dst, m * ldd + n, v);
+  }
+}
+
+// TR: weight rows per workgroup, 32 (every MFMA column used) or 16 (twice the workgroups for short weights; lanes
+// 16..31 load nothing and their columns come out zero)
+template <class WT, class AP, class Out, int NW, int TR>
+__global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, int64_t nrows_w,
+                                                    int64_t w_row_bytes, AP ap, int mrows, int64_t nsb,
+                                                    typename Out::T *__restrict__ dst, int64_t ldd) {
+  __shared__ float dys[NW][32];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int64_t n0 = (int64_t)blockIdx.x * TR;
+  const int64_t rows_here = nrows_w - n0 < TR ? nrows_w - n0 : TR;
+  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, rows_here * w_row_bytes);
+  const uint32_t wrow = li < rows_here ? (uint32_t)(li * w_row_bytes) : 0x80000000u;
+  // rows past the batch read as zero: their offset lies beyond every buffer's end
+  const uint32_t arow = li < mrows ? (uint32_t)li * ap.row_bytes : 0x80000000u;
+  const rsrc_t ra = ap.rsrc();
+
+  const int64_t per = (nsb + NW - 1) / NW;
+  const int64_t s0 = wave * per, s1 = s0 + per < nsb ? s0 + per : nsb;
+
+  v16f fa = (v16f){};
+  typename WT::Raw raw[2];
+  ActFrag af[2];
+  auto issue = [&](int64_t sb, int u) {
+    WT::load(rw, wrow, (uint32_t)sb, g, raw[u]);
+    ap.load(ra, arow, sb, g, WT::kMin, af[u]);
+  };
+  auto compute = [&](int u) {
+    typename WT::Prep p;
+    WT::prepare(raw[u], g, p);
+    v16i acc1 = (v16i){}, acc2 = (v16i){};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      v4i b1, b2;
+      WT::planes(raw[u], p, j, b1, b2);
+      acc1 = mfma_i8(af[u].q[j], b1, acc1);
+      acc2 = mfma_i8(af[u].q[j], b2, acc2);
+    }
+    v16f fmin = (v16f){};
+    if (WT::kMin) fmin = mfma_f16(af[u].bs, p.bmin, fmin);
+    // the scales of output rows 8q + 4g + i, from the lanes that loaded them
+    if (g == 0) dys[wave][li] = af[u].d;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const v4f dy4 = *(const v4f *)&dys[wave][8 * q + 4 * g];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = 4 * q + i;
+        const int iv = (acc1[r] << WT::kShift) + acc2[r];
+        float v = p.d * (float)iv;
+        if (WT::kMin) v -= p.dmin * fmin[r];
+        fa[r] += dy4[i] * v;
+      }
+    }
+  };
+
+  if (s0 < s1) issue(s0, 0);
+  if (s0 + 1 < s1) issue(s0 + 1, 1);
+  for (int64_t sb = s0; sb < s1; sb += 2) {
+    compute(0);
+    if (sb + 2 < s1) issue(sb + 2, 0);
+    if (sb + 1 < s1) {
+      compute(1);
+      if (sb + 3 < s1) issue(sb + 3, 1);
+    }
+  }
+  reduce_store<Out, NW>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd);
+}
+
+template <class WT, class Out>
+void launch_decode(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_y,
+                   int stride_col_dst, int b, hipStream_t s) {
+  const int64_t nsb = ncols_x / 256;
+  act_decode ap;
+  ap.row_bytes = (uint32_t)stride_col_y * 292;
+  ap.base = (const uint8_t *)vy;
+  ap.bytes = (int64_t)b * ap.row_bytes;
+  const uint8_t *w = (const uint8_t *)vx;
+  typename Out::T *d = (typename Out::T *)dst;
+  const int64_t wrb = nsb * WT::kBytes;
+  if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
+    k_skinny<WT, act_decode, Out, 4, 32><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
+        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+  else
+    k_skinny<WT, act_decode, Out, 4, 16><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
+        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+}
+
+}  // namespace
+
+bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                       int stride_col_y, int stride_col_dst, int b, hipStream_t s) {
+  if (b < 1 || b > 32 || ncols_x % 256 != 0 || (int64_t)b * stride_col_y * 292 > 0x7ffffff0) return false;
+  if (type != QMM_TYPE_Q4K && type != QMM_TYPE_Q6K) return false;
+#define QMM_SK(WT)                                                                                              \
+  switch (out_type) {                                                                                           \
+    case QMM_TYPE_F16: launch_decode<WT, out_f16>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s); break; \
+    case QMM_TYPE_BF16: launch_decode<WT, out_bf16>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s); break; \
+    default: launch_decode<WT, out_f32>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s);     \
+  }
+  if (type == QMM_TYPE_Q4K) {
+    QMM_SK(wq4k)
+  } else {
+    QMM_SK(wq6k)
+  }
+#undef QMM_SK
+  return true;
+}

@@ -23,7 +23,8 @@ def tiles_to_blocks(buf, rows, kp, at):
     qs = b[: nsb * rows * 256].reshape(nsb, rows, 256)
     if at == O.Q8K:
         d = b[nsb * rows * 256: nsb * rows * 260].view(np.float32).reshape(nsb, rows)
-        bs = b[nsb * rows * 260:].view(np.int16).reshape(nsb, rows, 16)
+        # bsums are stored as f16 (exact for |bsum| <= 2048)
+        bs = b[nsb * rows * 260:].view(np.float16).reshape(nsb, rows, 16).astype(np.int16)
         out = np.zeros((rows, nsb), dtype=O.BLOCK_DTYPES[O.Q8K])
         out["d"] = d.T
         out["qs"] = qs.transpose(1, 0, 2)
