@@ -317,9 +317,16 @@ ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
   return a;
 }
 
+// Q4_K (measured on MI355X): 64 activation rows per wave at 2 waves per SIMD beats 128 rows at 1 wave; Q6_K, whose
+// plane building needs more registers, runs 1 wave per SIMD and takes 128 rows.
+template <class WT>
+constexpr int kq_tm_max() { return WT::kMin ? 2 : 4; }
+template <class WT, int TMv>
+constexpr int kq_waves() { return WT::kMin && TMv <= 2 ? 2 : 1; }
+
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst
 template <class WT, class Out, int TMv>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void k_mmq_kq(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
     int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
   constexpr int BMt = 32 * TMv;
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W,
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
 template <class WT, int TMv>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
                                                     const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
@@ -404,7 +411,7 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
                typename Out::T *d, int64_t ldd, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
-  const int tm = ncols_y <= 32 ? 1 : ncols_y <= 64 ? 2 : 4;
+  const int tm = ncols_y <= 32 ? 1 : ncols_y <= 64 || kq_tm_max<WT>() < 4 ? 2 : 4;
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
   const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
   if (splits > 1)
