@@ -13,18 +13,18 @@
 // Each superblock's integer result is exact in int32; the f32 epilogue per superblock mirrors the
 // reference's d * dy * integer (k_quants.rs:1848-1928, 2518-2575).
 //
-// Tiling: a 256-thread workgroup owns BM = 128 activation rows x BN = 128 weight rows; wave w takes weight
-// rows [32w, 32w+32) against all 128 activation rows (4 MFMA tiles of 32x32).  Per 256-value K step the
-// workgroup stages the activation tile (int8 qs, f32 d, f16 bsums) in LDS; each wave streams its weight
-// rows straight from HBM into registers and builds the B operands there.  A and B fragments use the same
-// lane/byte -> k assignment, so the hardware's k order inside an MFMA does not matter.
+// Tiling: a 256-thread workgroup owns BN = 128 weight rows x 32 TM activation rows (TM = 1, 2 or 4); wave w takes
+// weight rows [32w, 32w+32) against all of them (TM MFMA tiles of 32x32).  Per 256-value K step the workgroup
+// moves the activation superblock (int8 qs, f32 d, f16 bsums) global -> registers -> one of three LDS slots, and
+// each wave loads its weight rows straight from HBM into registers two superblocks ahead and builds the B
+// operands there.  A and B fragments use the same lane/byte -> k assignment, so the hardware's k order inside an
+// MFMA does not matter.  The Q8_0 kernel keeps a simpler single-buffered loop.
 #include "common.h"
 #include "inferencequant.h"
 #include "planes.h"
 #include "units.h"
 
 namespace {
-
 
 constexpr int BM = 128;
 constexpr int BN = 128;
@@ -39,9 +39,7 @@ struct ActTile {
   int64_t rows, nsb;
 };
 
-
 // ------------------------------------------------------------------------------------------ K-quant kernel
-
 
 // One superblock of the activation tile (BMt rows x 256 values: int8 qs, f16 bsums, f32 d) in registers on its
 // way from global memory to an LDS slot.  The prefill layout keeps a superblock's rows contiguous, so thread t
@@ -204,11 +202,22 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 // launch sequence can sit in a HIP graph).  rows_map != nullptr: zero rows rows_map[0..rows).
 __global__ __launch_bounds__(256) void k_zero_rows(float *__restrict__ dst, int64_t rows, int64_t cols, int64_t ldd,
                                                    const int32_t *__restrict__ rows_map) {
-  const int64_t r = blockIdx.y;
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows || c >= cols) return;
-  const int64_t dr = rows_map ? rows_map[r] : r;
-  dst[dr * ldd + c] = 0.0f;
+  // workgroup (x, y) clears 1024 columns of rows y, y + gridDim.y, ...; 4 columns per thread
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= cols) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    float *p = dst + (rows_map ? rows_map[r] : r) * ldd + c;
+    if (c + 4 <= cols && ((uintptr_t)p & 15) == 0) {
+      *(v4f *)p = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    } else {
+      for (int64_t i = 0; i < 4 && c + i < cols; i++) p[i] = 0.0f;
+    }
+  }
+}
+
+void zero_rows(float *dst, int64_t rows, int64_t cols, int64_t ldd, const int32_t *rows_map, hipStream_t s) {
+  const dim3 grid((unsigned)qmm_ceil_div(cols, 1024), (unsigned)(rows < 64 ? rows : 64));
+  k_zero_rows<<<grid, 256, 0, s>>>(dst, rows, cols, ldd, rows_map);
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 kernel
@@ -415,8 +424,7 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
   const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
   if (splits > 1)
-    k_zero_rows<<<dim3((unsigned)((nrows_x + 255) / 256), (unsigned)ncols_y), 256, 0, s>>>((float *)d, ncols_y, nrows_x,
-                                                                                          ldd, nullptr);
+    zero_rows((float *)d, ncols_y, nrows_x, ldd, nullptr, s);
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1) k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
   else if (tm == 2) k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
@@ -494,8 +502,7 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
   const int64_t splits = type == QMM_TYPE_Q8_0 ? 1 : k_splits(busy, nsb, true);
   if (splits > 1)
-    k_zero_rows<<<dim3((unsigned)((nrows_x + 255) / 256), (unsigned)ncols_dst), 256, 0, s>>>(d, ncols_dst, nrows_x,
-                                                                                            stride_col_dst, ids_dst);
+    zero_rows(d, ncols_dst, nrows_x, stride_col_dst, ids_dst, s);
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
   switch (type) {
     case QMM_TYPE_Q4K:
