@@ -75,9 +75,22 @@ struct out_bf16 {
 
 // ------------------------------------------------------------------ wave64 reductions
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, QMM_WAVE);
+
+// Sum over the wave through DPP (no LDS round trips); the total lands in lane 63 (other lanes hold partial sums).
+//   quad_perm [1,0,3,2], [2,3,0,1]: quad sums; row_half_mirror, row_mirror: 16-lane row sums;
+//   row_bcast15 into rows 1, 3 and row_bcast31 into rows 2, 3: row 3 ends with the total.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf,
+                                                                   false));
+}
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast15
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast31
   return v;
 }
 

@@ -16,11 +16,12 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
 // from this many activation rows on, K-quant weights go through the MFMA few-row kernel (skinny.hip), which
-// decodes each weight block once for all rows
-#ifndef QMM_SKINNY_MIN_ROWS
-#define QMM_SKINNY_MIN_ROWS 3
+// decodes each weight block once for all rows (measured crossover on MI355X: Q4_K 4 rows, Q6_K 3)
+constexpr int skinny_min_rows(int type) { return type == QMM_TYPE_Q6K ? 3 : 4; }
+// rows of up to this many 64-value units per lane go through the persistent kernel, longer ones through k_mmvq
+#ifndef QMM_PERSISTENT_MAX_S
+#define QMM_PERSISTENT_MAX_S 4
 #endif
-constexpr int kSkinnyMinRows = QMM_SKINNY_MIN_ROWS;
 
 
 template <class U, class Out, int NC, int R>
@@ -55,28 +56,20 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, co
   for (int r = 0; r < R; r++)
 #pragma unroll
     for (int j = 0; j < NC; j++) {
-      const float v = wave_sum(acc[r][j]);
-      if (lane == 0 && row0 + r < nrows) Out::store(dst, (int64_t)j * stride_col_dst + row0 + r, v);
+      const float v = wave_sum_to_lane63(acc[r][j]);
+      if (lane == 63 && row0 + r < nrows) Out::store(dst, (int64_t)j * stride_col_dst + row0 + r, v);
     }
 }
 
 // ------------------------------------------------------------------------------------------------ persistent form
 
-__device__ __forceinline__ void store_any(void *dst, int type, int64_t i, float v) {
-  switch (type) {
-    case QMM_TYPE_F16: ((uint16_t *)dst)[i] = f32_to_f16_bits(v); break;
-    case QMM_TYPE_BF16: ((uint16_t *)dst)[i] = f32_to_bf16_bits(v); break;
-    default: ((float *)dst)[i] = v;
-  }
-}
-
 // Persistent decode matvec: wave w of the grid takes rows w, w + T, w + 2T, ... (T waves in the grid), so a few
 // thousand resident waves keep the HBM queues full, and each wave requests its next row's weights before it
 // does the current row's math.  Lane l owns units l + 64 s (s < S) of every row, so with NC * S <= 2 its
 // activation units stay in registers for the whole launch.  FULL: every lane has all S units (no guards).
-template <class U, int NC, int S, bool FULL>
+template <class U, class Out, int NC, int S, bool FULL>
 __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
-                                                void *__restrict__ dst, int out_type, int nrows, int64_t row_bytes,
+                                                typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
                                                 int nunits, int64_t act_row_bytes, int stride_col_dst) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tw = gridDim.x * kWaves;
@@ -123,8 +116,8 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
     }
 #pragma unroll
     for (int j = 0; j < NC; j++) {
-      const float v = wave_sum(acc[j]);
-      if (lane == 0) store_any(dst, out_type, (int64_t)j * stride_col_dst + row, v);
+      const float v = wave_sum_to_lane63(acc[j]);
+      if (lane == 63) Out::store(dst, (int64_t)j * stride_col_dst + row, v);
     }
 #pragma unroll
     for (int s = 0; s < S; s++) w[s] = wn[s];
@@ -168,10 +161,10 @@ __global__ __launch_bounds__(256) void k_mmvq_moe(const uint8_t *__restrict__ vx
   }
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const float g = wave_sum(ag[r]);
+    const float g = wave_sum_to_lane63(ag[r]);
     float v = g;
-    if (GLU) v = glu_act(activation, g) * wave_sum(au[r]);
-    if (lane == 0 && row0 + r < nrows) dst[(int64_t)pair * nrows + row0 + r] = v;
+    if (GLU) v = glu_act(activation, g) * wave_sum_to_lane63(au[r]);
+    if (lane == 63 && row0 + r < nrows) dst[(int64_t)pair * nrows + row0 + r] = v;
   }
 }
 
@@ -185,8 +178,8 @@ void launch_nc(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k
 }
 
 // Persistent launch of NC columns with S units per lane: grid capped at 8 workgroups per CU.
-template <class U>
-void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, void *dst, int out_type, int k, int nrows,
+template <class U, class Out>
+void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows,
               int64_t act_row_bytes, int stride_col_dst, hipStream_t s) {
   const int64_t wgs = qmm_ceil_div(nrows, kWaves);
   const dim3 grid((unsigned)(wgs < 8 * qmm_device_cus() ? wgs : 8 * qmm_device_cus()));
@@ -196,11 +189,11 @@ void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, void *dst, i
 #define QMM_P(NC, SS)                                                                                             \
   do {                                                                                                            \
     if (full)                                                                                                     \
-      k_mmvq_p<U, NC, SS, true><<<grid, 256, 0, s>>>(vx, act, dst, out_type, nrows, rb, nu, act_row_bytes,        \
-                                                     stride_col_dst);                                             \
+      k_mmvq_p<U, Out, NC, SS, true><<<grid, 256, 0, s>>>(vx, act, dst, nrows, rb, nu, act_row_bytes,             \
+                                                          stride_col_dst);                                        \
     else                                                                                                          \
-      k_mmvq_p<U, NC, SS, false><<<grid, 256, 0, s>>>(vx, act, dst, out_type, nrows, rb, nu, act_row_bytes,       \
-                                                      stride_col_dst);                                            \
+      k_mmvq_p<U, Out, NC, SS, false><<<grid, 256, 0, s>>>(vx, act, dst, nrows, rb, nu, act_row_bytes,            \
+                                                           stride_col_dst);                                       \
   } while (0)
 #define QMM_P_S(NC)                \
   switch (S) {                     \
@@ -230,11 +223,11 @@ template <class U, class Out>
 void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
                  int stride_col_dst, int b, hipStream_t s) {
   const int S = (int)qmm_ceil_div(U::units(k), 64);
-  if (S <= 4) {
+  if (S <= QMM_PERSISTENT_MAX_S) {
     for (int j0 = 0; j0 < b; j0 += 8) {
       const int nc = b - j0 < 8 ? b - j0 : 8;
-      launch_p<U>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst,
-                  out_type_of((const Out *)nullptr), k, nrows, act_row_bytes, stride_col_dst, s);
+      launch_p<U, Out>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
+                       act_row_bytes, stride_col_dst, s);
     }
     return;
   }
@@ -289,7 +282,7 @@ void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int
   hipStream_t s = (hipStream_t)stream;
   const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
   typename Out::T *d = (typename Out::T *)dst;
-  if (b >= kSkinnyMinRows &&
+  if (b >= skinny_min_rows(type) &&
       qmm_skinny_decode(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_y,
                         stride_col_dst, b, s))
     return;

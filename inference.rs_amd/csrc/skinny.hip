@@ -160,6 +160,9 @@ void launch_decode(const void *vx, const void *vy, void *dst, int ncols_x, int n
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
     k_skinny<WT, act_decode, Out, 4, 32><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
         w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+  else if (nsb >= 32)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
+    k_skinny<WT, act_decode, Out, 8, 16><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
   else
     k_skinny<WT, act_decode, Out, 4, 16><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
         w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
