@@ -183,38 +183,54 @@ def prefill_workload(torch, qmm, gtype, n, k, m, copies, steps, warmup, seed):
 
 def stack_workload(torch, qmm, batches, steps, warmup, seed):
     """Llama-3-8B linears, Q4_K for q/k/o/gate/up and Q6_K for v/down, 32 layers; one weight per shape is
-    quantized and its bytes copied to every layer (distinct HBM copies, so every step streams 4.44 GB)."""
+    quantized and its bytes copied to every layer (distinct HBM copies, so every step streams 4.44 GB).
+    Per layer, as the reference's decode path runs them: the attention input is quantized once and q, k, v read
+    that one activation; o and down quantize their own inputs; gate and up are one fused-GLU launch
+    (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  Rows > 16 take the prefill matmul, one quantized
+    activation per distinct input.  The inputs are synthetic, one per projection group."""
     shapes = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
               ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
     layers = 32
     base = {name: quantized_weight(t, n, k, seed + i) for i, (name, t, n, k) in enumerate(shapes)}
     dev = {name: [torch.from_numpy(base[name]).cuda() for _ in range(layers)] for name, _, _, _ in shapes}
     total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
-    res = {"weight_bytes_per_step": total_bytes}
+    res = {"weight_bytes_per_step": total_bytes,
+           "launches_per_layer": "decode: 4 quantize + q, k, v, o, gate/up (fused GLU), down = 10; "
+                                 "prefill: 4 quantize + 7 matmuls"}
     import qmm as Q
     for b in batches:
         rng = np.random.default_rng(seed + 100 + b)
-        xs = {4096: torch.from_numpy(rng.standard_normal((b, 4096), dtype=np.float32)).cuda(),
-              14336: torch.from_numpy(rng.standard_normal((b, 14336), dtype=np.float32)).cuda()}
+        xs = {g: torch.from_numpy(rng.standard_normal((b, kk), dtype=np.float32)).cuda()
+              for g, kk in (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
         outs = {name: torch.empty((b, n), dtype=torch.float32, device="cuda") for name, _, n, _ in shapes}
         decode = b <= 16
-        bufs = {}
-        for name, t, n, k in shapes:
-            if decode:
-                bufs[name] = Q.quantize_decode(t, xs[k])
-            else:
-                bufs[name] = Q.quantize_prefill(t, xs[k])
+        # all seven types here quantize activations to Q8_K, so one buffer per input serves every projection on it
+        bufs = {g: (Q.quantize_decode(Q4K, x) if decode else Q.quantize_prefill(Q4K, x)) for g, x in xs.items()}
+        group = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "ffn", "up": "ffn", "down": "down"}
+        kdim = {name: k for name, _, _, k in shapes}
+        tdim = {name: t for name, t, _, _ in shapes}
+        ndim = {name: n for name, _, n, _ in shapes}
 
         def step(i):
             for layer in range(layers):
-                for name, t, n, k in shapes:
-                    vy, kp = bufs[name]
+                for g, x in xs.items():
+                    vy, kp = bufs[g]
                     if decode:
-                        Q.quantize_decode(t, xs[k], kp=kp, out=vy)
+                        Q.quantize_decode(Q4K, x, kp=kp, out=vy)
+                    else:
+                        Q.quantize_prefill(Q4K, x, out=vy)
+                for name in ("q", "k", "v", "o", "gate", "down"):
+                    vy, kp = bufs[group[name]]
+                    t, n, k = tdim[name], ndim[name], kdim[name]
+                    if decode and name == "gate":
+                        Q.mmvq_fused_glu(Q4K, dev["gate"][layer], dev["up"][layer], vy, k, n, b, kp,
+                                         out=outs["gate"])
+                    elif decode:
                         Q.mmvq(t, dev[name][layer], vy, k, n, b, kp, out=outs[name])
                     else:
-                        Q.quantize_prefill(t, xs[k], out=vy)
                         Q.mmq(t, dev[name][layer], vy, k, n, b, out=outs[name])
+                        if name == "gate":
+                            Q.mmq(Q4K, dev["up"][layer], vy, k, n, b, out=outs["up"])
 
         st = max(2, steps // 50)
         t = graph_time(torch, step, st, 1)

@@ -75,6 +75,28 @@ QMM_DECLARE_MMVQ_PLAIN(q8_0)
 QMM_DECLARE_MMVQ_PLAIN(q4_k)
 QMM_DECLARE_MMVQ_PLAIN(q6_k)
 
+/* ------------------------------------------------------------------ fused decode forms
+ * launch_mmvq_gguf_<t>_{bf16,f16,f32}_fused_glu (gguf/ffi.rs:1032-1069; kernel mmvq_gguf.cuh:761-842):
+ * dst[j * stride_col_dst + row] = act(W_gate[row] . Q(y_j)) * (W_up[row] . Q(y_j)) for j < b_size (1..16),
+ * activation 0 SiLU, 1 GELU (tanh form), 2 ReLU, 3 GELU (erf form), 4 sigmoid; vy from the decode quantizer.
+ * launch_mmvq_gguf_<t>_{bf16,f16,f32}_fused_qkv (gguf/ffi.rs:1071-1118; kernel mmvq_gguf.cuh:844-959):
+ * q_dst[j * nrows_q + row] = W_q[row] . Q(y_j), likewise k and v, one launch over one activation. */
+#define QMM_DECLARE_MMVQ_FUSED_DT(t, dt)                                                                       \
+  void launch_mmvq_gguf_##t##_##dt##_fused_glu(const void *vx_gate, const void *vx_up, const void *vy, void *dst, \
+                                               int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst,   \
+                                               int b_size, int activation, void *stream);                       \
+  void launch_mmvq_gguf_##t##_##dt##_fused_qkv(const void *vx_q, const void *vx_k, const void *vx_v,             \
+                                               const void *vy, void *q_dst, void *k_dst, void *v_dst,            \
+                                               int ncols_x, int nrows_q, int nrows_k, int nrows_v,               \
+                                               int stride_col_y, int b_size, void *stream);
+#define QMM_DECLARE_MMVQ_FUSED(t)      \
+  QMM_DECLARE_MMVQ_FUSED_DT(t, bf16)   \
+  QMM_DECLARE_MMVQ_FUSED_DT(t, f16)    \
+  QMM_DECLARE_MMVQ_FUSED_DT(t, f32)
+QMM_DECLARE_MMVQ_FUSED(q8_0)
+QMM_DECLARE_MMVQ_FUSED(q4_k)
+QMM_DECLARE_MMVQ_FUSED(q6_k)
+
 /* ------------------------------------------------------------------ MoE decode matvec
  * launch_mmvq_gguf_<t>_moe (gguf/ffi.rs:877-893; kernel mmvq_gguf.cuh:961-1038, 1600-1643).
  * For routed pair p < n_pairs: expert e = ids[p] (u32), activation row p / y_div of vy (stride_col_y

@@ -15,9 +15,6 @@
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
-// from this many activation rows on, K-quant weights go through the MFMA few-row kernel (skinny.hip), which
-// decodes each weight block once for all rows (measured crossover on MI355X: Q4_K 4 rows, Q6_K 3)
-constexpr int skinny_min_rows(int type) { return type == QMM_TYPE_Q6K ? 3 : 4; }
 // rows of up to this many 64-value units per lane go through the persistent kernel, longer ones through k_mmvq
 #ifndef QMM_PERSISTENT_MAX_S
 #define QMM_PERSISTENT_MAX_S 4
@@ -282,7 +279,7 @@ void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int
   hipStream_t s = (hipStream_t)stream;
   const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
   typename Out::T *d = (typename Out::T *)dst;
-  if (b >= skinny_min_rows(type) &&
+  if (b >= qmm_skinny_min_rows(type) &&
       qmm_skinny_decode(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_y,
                         stride_col_dst, b, s))
     return;

@@ -3,8 +3,19 @@
 
 #include <hip/hip_runtime.h>
 
+#include "qmm_blocks.h"
+
+// From this many activation rows on, K-quant weights go through the MFMA few-row kernel, which decodes each weight
+// block once for all rows (measured crossover on MI355X: Q4_K 4 rows, Q6_K 3).
+inline int qmm_skinny_min_rows(int type) { return type == QMM_TYPE_Q6K ? 3 : 4; }
+
 // Decode-layout activations (b rows of Q8_K blocks, stride_col_y blocks apart) against Q4_K / Q6_K weights;
 // dst[j * stride_col_dst + row] of element type out_type (QMM_TYPE_F32 / F16 / BF16).  Returns false, launching
 // nothing, for a case it does not serve (other weight types, b outside 1..32, K not a multiple of 256).
 bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
                        int stride_col_y, int stride_col_dst, int b, hipStream_t s);
+
+// The same for the fused GLU form: dst[j * stride_col_dst + row] = act(W_gate . y_j) * (W_up . y_j).
+bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_up, const void *vy, void *dst,
+                    int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation,
+                    hipStream_t s);

@@ -55,24 +55,33 @@ struct act_decode {
   }
 };
 
-// The NW waves' partial 32x32 tiles, summed through LDS; lane (g, li) of wave w then stores output registers
-// (16 / NW) w ... (16 / NW) (w + 1) - 1.
-template <class Out, int NW>
+// The NW waves' partial 32x32 tiles, summed through LDS.  Plain: lane (g, li) of wave w stores output registers
+// (16 / NW) w ...; GLU (waves [0, NW/2) hold gate partials, [NW/2, NW) up partials): the first NW/2 waves store
+// act(gate) * up.
+template <class Out, int NW, bool GLU>
 __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane, int g, int li, int64_t n0,
                                              int64_t n1, int64_t mrows, typename Out::T *__restrict__ dst,
-                                             int64_t ldd) {
+                                             int64_t ldd, int activation) {
   __shared__ float red[NW][16][64];
 #pragma unroll
   for (int r = 0; r < 16; r++) red[wave][r][lane] = fa[r];
   __syncthreads();
   const int64_t n = n0 + li;
-  constexpr int RPW = 16 / NW;
+  constexpr int KW = GLU ? NW / 2 : NW;  // waves per K split
+  constexpr int RPW = 16 / KW;
+  if (GLU && wave >= KW) return;
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
     const int r = RPW * wave + i;
     float v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; w++) v += red[w][r][lane];
+    for (int w = 0; w < KW; w++) v += red[w][r][lane];
+    if (GLU) {
+      float u = 0.0f;
+#pragma unroll
+      for (int w = KW; w < NW; w++) u += red[w][r][lane];
+      v = glu_act(activation, v) * u;
+    }
     const int64_t m = out_row(r, g);
     if (m < mrows && n < n1) Out::store(dst, m * ldd + n, v);
   }
@@ -80,22 +89,26 @@ __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane,
 
 // TR: weight rows per workgroup, 32 (every MFMA column used) or 16 (twice the workgroups for short weights; lanes
 // 16..31 load nothing and their columns come out zero)
-template <class WT, class AP, class Out, int NW, int TR>
-__global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, int64_t nrows_w,
-                                                    int64_t w_row_bytes, AP ap, int mrows, int64_t nsb,
-                                                    typename Out::T *__restrict__ dst, int64_t ldd) {
+// GLU: W2 holds the up weights; waves [0, NW/2) take the gate rows and [NW/2, NW) the up rows.
+template <class WT, class AP, class Out, int NW, int TR, bool GLU>
+__global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
+                                                    int64_t nrows_w, int64_t w_row_bytes, AP ap, int mrows,
+                                                    int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
+                                                    int activation) {
   __shared__ float dys[NW][32];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  constexpr int KW = GLU ? NW / 2 : NW;  // waves splitting K
+  const int kw = wave % KW;
   const int64_t n0 = (int64_t)blockIdx.x * TR;
   const int64_t rows_here = nrows_w - n0 < TR ? nrows_w - n0 : TR;
-  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, rows_here * w_row_bytes);
+  const rsrc_t rw = make_rsrc((GLU && wave >= KW ? W2 : W) + n0 * w_row_bytes, rows_here * w_row_bytes);
   const uint32_t wrow = li < rows_here ? (uint32_t)(li * w_row_bytes) : 0x80000000u;
   // rows past the batch read as zero: their offset lies beyond every buffer's end
   const uint32_t arow = li < mrows ? (uint32_t)li * ap.row_bytes : 0x80000000u;
   const rsrc_t ra = ap.rsrc();
 
-  const int64_t per = (nsb + NW - 1) / NW;
-  const int64_t s0 = wave * per, s1 = s0 + per < nsb ? s0 + per : nsb;
+  const int64_t per = (nsb + KW - 1) / KW;
+  const int64_t s0 = kw * per, s1 = s0 + per < nsb ? s0 + per : nsb;
 
   v16f fa = (v16f){};
   typename WT::Raw raw[2];
@@ -143,42 +156,54 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
       if (sb + 3 < s1) issue(sb + 3, 1);
     }
   }
-  reduce_store<Out, NW>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd);
+  reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd, activation);
 }
 
 template <class WT, class Out>
-void launch_decode(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_y,
-                   int stride_col_dst, int b, hipStream_t s) {
+void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, int ncols_x, int nrows_x,
+                   int stride_col_y, int stride_col_dst, int b, int activation, hipStream_t s) {
   const int64_t nsb = ncols_x / 256;
   act_decode ap;
   ap.row_bytes = (uint32_t)stride_col_y * 292;
   ap.base = (const uint8_t *)vy;
   ap.bytes = (int64_t)b * ap.row_bytes;
-  const uint8_t *w = (const uint8_t *)vx;
+  const uint8_t *w = (const uint8_t *)vx, *w2 = (const uint8_t *)vx2;
   typename Out::T *d = (typename Out::T *)dst;
   const int64_t wrb = nsb * WT::kBytes;
+  if (w2) {  // gate and up in one workgroup: 4 waves each
+    if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
+      k_skinny<WT, act_decode, Out, 8, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 512, 0, s>>>(
+          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation);
+    else
+      k_skinny<WT, act_decode, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation);
+    return;
+  }
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
-    k_skinny<WT, act_decode, Out, 4, 32><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
-        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+    k_skinny<WT, act_decode, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
   else if (nsb >= 32)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
-    k_skinny<WT, act_decode, Out, 8, 16><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
-        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+    k_skinny<WT, act_decode, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
   else
-    k_skinny<WT, act_decode, Out, 4, 16><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
-        w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+    k_skinny<WT, act_decode, Out, 4, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
 }
 
-}  // namespace
-
-bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
-                       int stride_col_y, int stride_col_dst, int b, hipStream_t s) {
+bool dispatch(int type, int out_type, const void *vx, const void *vx2, const void *vy, void *dst, int ncols_x,
+              int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation, hipStream_t s) {
   if (b < 1 || b > 32 || ncols_x % 256 != 0 || (int64_t)b * stride_col_y * 292 > 0x7ffffff0) return false;
   if (type != QMM_TYPE_Q4K && type != QMM_TYPE_Q6K) return false;
 #define QMM_SK(WT)                                                                                              \
   switch (out_type) {                                                                                           \
-    case QMM_TYPE_F16: launch_decode<WT, out_f16>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s); break; \
-    case QMM_TYPE_BF16: launch_decode<WT, out_bf16>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s); break; \
-    default: launch_decode<WT, out_f32>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, s);     \
+    case QMM_TYPE_F16:                                                                                          \
+      launch_decode<WT, out_f16>(vx, vx2, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, activation, s); \
+      break;                                                                                                    \
+    case QMM_TYPE_BF16:                                                                                         \
+      launch_decode<WT, out_bf16>(vx, vx2, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, activation, s); \
+      break;                                                                                                    \
+    default:                                                                                                    \
+      launch_decode<WT, out_f32>(vx, vx2, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, activation, s); \
   }
   if (type == QMM_TYPE_Q4K) {
     QMM_SK(wq4k)
@@ -187,4 +212,18 @@ bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, v
   }
 #undef QMM_SK
   return true;
+}
+
+}  // namespace
+
+bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                       int stride_col_y, int stride_col_dst, int b, hipStream_t s) {
+  return dispatch(type, out_type, vx, nullptr, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b, 0, s);
+}
+
+bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_up, const void *vy, void *dst,
+                    int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation,
+                    hipStream_t s) {
+  return dispatch(type, out_type, vx_gate, vx_up, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b,
+                  activation, s);
 }

@@ -81,6 +81,8 @@ def _declare(L: ctypes.CDLL) -> None:
     for t in TYPE_NAME.values():
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+            getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_glu").argtypes = [vp, vp, vp, vp] + [i32] * 6 + [vp]
+            getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
         getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
                                                             i32, vp]
     for name in MOE_NAME.values():
@@ -178,6 +180,35 @@ def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out
         _ptr(w), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], stride_col_dst or n, b, _stream())
     check()
     return out
+
+
+def mmvq_fused_glu(wtype: int, w_gate, w_up, vy, k: int, n: int, b: int, kp: int, activation: int = 0,
+                   out_dtype=None, out=None):
+    """dst [b, n] = act(Q(y) . W_gate^T) * (Q(y) . W_up^T) through launch_mmvq_gguf_<t>_<dtype>_fused_glu."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((b, n), dtype=out_dtype or torch.float32, device=w_gate.device)
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_fused_glu")(
+        _ptr(w_gate), _ptr(w_up), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], out.shape[1], b,
+        activation, _stream())
+    check()
+    return out
+
+
+def mmvq_fused_qkv(wtype: int, wq, wk, wv, vy, k: int, nq: int, nk: int, nv: int, b: int, kp: int, out_dtype=None,
+                   outs=None):
+    """(q [b, nq], k [b, nk], v [b, nv]) through one launch_mmvq_gguf_<t>_<dtype>_fused_qkv."""
+    torch = _torch()
+    if outs is None:
+        dt = out_dtype or torch.float32
+        outs = tuple(torch.empty((b, n), dtype=dt, device=wq.device) for n in (nq, nk, nv))
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[outs[0].dtype]
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_fused_qkv")(
+        _ptr(wq), _ptr(wk), _ptr(wv), _ptr(vy), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), k, nq, nk, nv,
+        kp // BLOCK_SIZE[ACT_TYPE[wtype]], b, _stream())
+    check()
+    return outs
 
 
 def qmatmul_decode(wtype: int, w, x, n: int, out_dtype=None):
