@@ -154,3 +154,143 @@ struct wq6k {
     }
   }
 };
+
+// ------------------------------------------------------------------------------------------ 16x16x64 policies
+
+// Operands of v_mfma_i32_16x16x64_i8 for 16 weight rows x 16 activation rows.  Lane l = 16 kg + r holds weight row
+// r (B column) and activation row r (A row); per 256-value superblock four MFMA steps t = 0..3 of 64 values, where
+// lane group kg supplies 16 values.  The value order is chosen per weight type so that every 16-byte load a lane
+// makes is used whole and every lane's 16 values share one sub-block scale; the activation side takes the same
+// values, 16 contiguous bytes at act_offset(t, kg) of the activation superblock.
+__device__ __forceinline__ v4i mfma16_i8(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4f mfma16_f16(v4h a, v4h b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Q4_K: step t = 2p + h takes nibble h of bytes qs[64p + 16kg .. +16], i.e. values 128p + 64(kg/2) + 32h +
+// 16(kg%2) + (0..15) of sub-block 4p + 2(kg/2) + h.  Per lane per superblock: the 16-byte header and two 16-byte
+// chunks of nibbles.
+struct wq4k16 {
+  static constexpr int kBytes = 144;
+  static constexpr int kShift = 3;
+  static constexpr bool kMin = true;
+  struct Raw {
+    u32x4 hdr, q[2];
+  };
+  static __device__ __forceinline__ uint32_t act_offset(int t, int kg) {
+    return 128 * (t >> 1) + 64 * (kg >> 1) + 32 * (t & 1) + 16 * (kg & 1);
+  }
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int kg, Raw &r) {
+    const uint32_t o = row + sb * kBytes;
+    r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+#pragma unroll
+    for (int p = 0; p < 2; p++) r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 64 * p + 16 * kg, 0, 0);
+  }
+  struct Prep {
+    uint32_t sh[4], sl[4];
+    float d, dmin;
+    v4h bmin;
+  };
+  static __device__ __forceinline__ void prepare(const Raw &r, int kg, Prep &p) {
+    const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
+    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+    uint32_t sc[8], m[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {  // get_scale_min_k4 (quantized/utils.rs:119-129)
+      sc[j] = j < 4 ? byte(j) & 63 : (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
+      m[j] = j < 4 ? byte(j + 4) & 63 : (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+    const bool hi = kg >= 2;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int j = 4 * (t >> 1) + (t & 1);  // sub-block for kg < 2; kg >= 2 adds 2
+      const uint32_t v = hi ? sc[j + 2] : sc[j];
+      p.sh[t] = v >> 3;
+      p.sl[t] = v & 7;
+    }
+    p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
+    p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
+    // min-term B: bsum16 index 4kg + i <-> sub-block 2kg + i / 2
+    uint32_t m0 = m[0], m1 = m[1];
+#pragma unroll
+    for (int q = 1; q < 4; q++)
+      if (kg == q) {
+        m0 = m[2 * q];
+        m1 = m[2 * q + 1];
+      }
+    const _Float16 h0 = (_Float16)(float)m0, h1 = (_Float16)(float)m1;
+    p.bmin = (v4h){h0, h0, h1, h1};
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int t, v4i &b1, v4i &b2, int) {
+    const u32x4 q = r.q[t >> 1];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t nib = (t & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
+      b1[i] = (int)mul_bytes(nib, p.sh[t]);
+      b2[i] = (int)mul_bytes(nib, p.sl[t]);
+    }
+  }
+};
+
+// Q6_K: step t takes values 64t + 16kg + (0..15): low (t even) or high (t odd) nibbles of ql[64(t/2) + 16kg ..],
+// the 2-bit fields 2q, q = 2(t%2) + kg/2, of qh[32(t/2) + 16(kg%2) ..], scale sc[4t + kg].
+struct wq6k16 {
+  static constexpr int kBytes = 210;
+  static constexpr int kShift = 6;
+  static constexpr bool kMin = false;
+  struct Raw {
+    uint32_t ql[2][4], qh[2][4], sc[4];
+    uint32_t d;
+  };
+  static __device__ __forceinline__ uint32_t act_offset(int t, int kg) { return 64 * t + 16 * kg; }
+  static __device__ __forceinline__ void ld16(rsrc_t rs, uint32_t a4, uint32_t x, uint32_t off, uint32_t out[4]) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, a4 + x, 0, 0);
+    const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(rs, a4 + x + 16, 0, 0);
+    out[0] = align_bytes(v.y, v.x, off);
+    out[1] = align_bytes(v.z, v.y, off);
+    out[2] = align_bytes(v.w, v.z, off);
+    out[3] = align_bytes(e, v.w, off);
+  }
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int kg, Raw &r) {
+    const uint32_t o = row + sb * kBytes, off = o & 3, a4 = o - off;
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+      ld16(rs, a4, 64 * x + 16 * kg, off, r.ql[x]);
+      ld16(rs, a4, 128 + 32 * x + 16 * (kg & 1), off, r.qh[x]);
+    }
+    ld16(rs, a4, 192, off, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
+  }
+  struct Prep {
+    int sc[4];
+    float d, dmin;
+    v4h bmin;
+  };
+  static __device__ __forceinline__ void prepare(const Raw &r, int kg, Prep &p) {
+#pragma unroll
+    for (int t = 0; t < 4; t++)  // byte 4t + kg of the 16 scales = byte kg of dword t
+      p.sc[t] = (int)(int8_t)((r.sc[t] >> (8 * kg)) & 0xff);
+    p.d = f16_bits_to_f32(r.d);
+    p.dmin = 0.0f;
+    p.bmin = (v4h){};
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int t, v4i &b1, v4i &b2, int kg) {
+    const uint32_t *ql = r.ql[t >> 1], *qh = r.qh[t >> 1];
+    const int nsh = 4 * (t & 1), hsh = 4 * (t & 1) + 2 * (kg >> 1);
+    const s2 sc2 = {(short)p.sc[t], (short)p.sc[t]};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
+      const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
+      const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
+      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
+      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
+      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
+      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+    }
+  }
+};

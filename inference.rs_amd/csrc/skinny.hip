@@ -3,9 +3,10 @@
 // mmvq_tc_k.cuh, fast_mmvq.rs:1897-2126, and its plain launcher at b <= 8) and any matmul whose activation side
 // is at most 32 rows (the expert-grouped prefill at a handful of tokens per expert).
 //
-// A workgroup owns 32 (or, for short weights, 16) weight rows and all activation rows; its 4 waves split the
-// superblocks of K, so every weight byte is loaded by exactly one wave, straight into registers, two superblocks
-// ahead.
+// Two forms.  32x32x32: a workgroup owns 32 (or 16) weight rows and all activation rows; its 4 or 8 waves split
+// the superblocks of K, so every weight byte is loaded by exactly one wave, straight into registers, two
+// superblocks ahead.  16x16x64 (narrower weights, at most 16 activation rows): 16 weight rows per workgroup and a
+// quarter of the registers, so 4 waves fit per SIMD and K is split up to 16 ways.
 // Each wave's lane (g, li) builds the two int8 weight planes of row n0 + li (planes.h) as the MFMA B column and
 // loads activation row li's int8 values as the A row; one 32x32x32 MFMA per plane per 32 values, the Q4_K min
 // term through one f16 MFMA per superblock, and the per-superblock f32 scaling of the reference
@@ -18,6 +19,15 @@
 
 namespace {
 
+// Q4_K weight superblocks in flight per wave (a register ring; a multiple of 2)
+#ifndef QMM_SKINNY_WDEPTH
+#define QMM_SKINNY_WDEPTH 2
+#endif
+// 1: the 16x16x64 form serves every weight at b <= 16; 0 (measured faster on MI355X): only weights with fewer
+// 32-row tiles than QMM_SKINNY_WIDE_TILES, wide weights keep the 32x32x32 form
+#ifndef QMM_SKINNY16_WIDE
+#define QMM_SKINNY16_WIDE 0
+#endif
 // weights with fewer 32-row tiles than this go in 16-row tiles (twice the workgroups)
 #ifndef QMM_SKINNY_WIDE_TILES
 #define QMM_SKINNY_WIDE_TILES 384
@@ -111,27 +121,26 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
   const int64_t s0 = kw * per, s1 = s0 + per < nsb ? s0 + per : nsb;
 
   v16f fa = (v16f){};
-  typename WT::Raw raw[2];
+  // weights WD superblocks ahead (a register ring), activations two ahead.  Q4_K: 4 (fits 256 VGPRs); Q6_K's
+  // larger raw blocks: 2
+  constexpr int WD = WT::kMin ? QMM_SKINNY_WDEPTH : 2;
+  typename WT::Raw raw[WD];
   ActFrag af[2];
-  auto issue = [&](int64_t sb, int u) {
-    WT::load(rw, wrow, (uint32_t)sb, g, raw[u]);
-    ap.load(ra, arow, sb, g, WT::kMin, af[u]);
-  };
-  auto compute = [&](int u) {
+  auto compute = [&](const typename WT::Raw &rr, const ActFrag &a) {
     typename WT::Prep p;
-    WT::prepare(raw[u], g, p);
+    WT::prepare(rr, g, p);
     v16i acc1 = (v16i){}, acc2 = (v16i){};
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       v4i b1, b2;
-      WT::planes(raw[u], p, j, b1, b2);
-      acc1 = mfma_i8(af[u].q[j], b1, acc1);
-      acc2 = mfma_i8(af[u].q[j], b2, acc2);
+      WT::planes(rr, p, j, b1, b2);
+      acc1 = mfma_i8(a.q[j], b1, acc1);
+      acc2 = mfma_i8(a.q[j], b2, acc2);
     }
     v16f fmin = (v16f){};
-    if (WT::kMin) fmin = mfma_f16(af[u].bs, p.bmin, fmin);
+    if (WT::kMin) fmin = mfma_f16(a.bs, p.bmin, fmin);
     // the scales of output rows 8q + 4g + i, from the lanes that loaded them
-    if (g == 0) dys[wave][li] = af[u].d;
+    if (g == 0) dys[wave][li] = a.d;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const v4f dy4 = *(const v4f *)&dys[wave][8 * q + 4 * g];
@@ -146,6 +155,111 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
     }
   };
 
+#pragma unroll
+  for (int u = 0; u < WD; u++)
+    if (s0 + u < s1) WT::load(rw, wrow, (uint32_t)(s0 + u), g, raw[u]);
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+    if (s0 + u < s1) ap.load(ra, arow, s0 + u, g, WT::kMin, af[u]);
+  for (int64_t sb = s0; sb < s1; sb += WD) {
+#pragma unroll
+    for (int u = 0; u < WD; u++) {
+      const int64_t s = sb + u;
+      if (s < s1) {
+        compute(raw[u], af[u & 1]);
+        if (s + 2 < s1) ap.load(ra, arow, s + 2, g, WT::kMin, af[u & 1]);
+        if (s + WD < s1) WT::load(rw, wrow, (uint32_t)(s + WD), g, raw[u]);
+      }
+    }
+  }
+  reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd, activation);
+}
+
+// ------------------------------------------------------------------------------------------ 16-row form
+
+template <class WT>
+struct Wt16;
+template <>
+struct Wt16<wq4k> {
+  typedef wq4k16 T;
+};
+template <>
+struct Wt16<wq6k> {
+  typedef wq6k16 T;
+};
+
+// A-side fragments of one superblock for the 16x16x64 form: lane (kg, r) holds activation row r's values
+// act_offset(t, kg) .. +16 for the four steps, the bsums 4kg .. 4kg + 3 of row r as f16, and the scales of output
+// rows 4kg + i.
+struct ActFrag16 {
+  v4i q[4];
+  v4h bs;
+  v4f dy;
+};
+
+// Up to 16 activation rows: NW waves split K, 16 weight rows per workgroup; output register i of lane (kg, r) is
+// D[activation row 4kg + i][weight row r] (v_mfma 16x16 D layout).
+template <class WT, class Out, int NW>
+__global__ __launch_bounds__(64 * NW) void k_skinny16(const uint8_t *__restrict__ W, int64_t nrows_w,
+                                                      int64_t w_row_bytes, act_decode ap, int mrows, int64_t nsb,
+                                                      typename Out::T *__restrict__ dst, int64_t ldd) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kg = lane >> 4, r = lane & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t rows_here = nrows_w - n0 < 16 ? nrows_w - n0 : 16;
+  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, rows_here * w_row_bytes);
+  const uint32_t wrow = r < rows_here ? (uint32_t)(r * w_row_bytes) : 0x80000000u;
+  const rsrc_t ra = ap.rsrc();
+  // rows past the batch read as zero: their offset lies beyond every buffer's end
+  const uint32_t arow = r < mrows ? (uint32_t)r * ap.row_bytes : 0x80000000u;
+  uint32_t dyrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) dyrow[i] = 4 * kg + i < mrows ? (uint32_t)(4 * kg + i) * ap.row_bytes : 0x80000000u;
+
+  const int64_t per = (nsb + NW - 1) / NW;
+  const int64_t s0 = wave * per, s1 = s0 + per < nsb ? s0 + per : nsb;
+
+  v4f fa = (v4f){};
+  typename WT::Raw raw[2];
+  ActFrag16 af[2];
+  auto issue = [&](int64_t sb, int u) {
+    WT::load(rw, wrow, (uint32_t)sb, kg, raw[u]);
+    const uint32_t o = arow + (uint32_t)sb * 292;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      af[u].q[t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, o + 4 + WT::act_offset(t, kg), 0, 0));
+    if (WT::kMin) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(ra, o + 260 + 8 * kg, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++)  // int16 -> f16, exact
+        af[u].bs[i] = (_Float16)(float)(int16_t)(((i < 2 ? b.x : b.y) >> (16 * (i & 1))) & 0xffff);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      af[u].dy[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, dyrow[i] + (uint32_t)sb * 292, 0, 0));
+  };
+  auto compute = [&](int u) {
+    typename WT::Prep p;
+    WT::prepare(raw[u], kg, p);
+    v4i acc1 = (v4i){}, acc2 = (v4i){};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      v4i b1, b2;
+      WT::planes(raw[u], p, t, b1, b2, kg);
+      acc1 = mfma16_i8(af[u].q[t], b1, acc1);
+      acc2 = mfma16_i8(af[u].q[t], b2, acc2);
+    }
+    v4f fmin = (v4f){};
+    if (WT::kMin) fmin = mfma16_f16(af[u].bs, p.bmin, fmin);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int iv = (acc1[i] << WT::kShift) + acc2[i];
+      float v = p.d * (float)iv;
+      if (WT::kMin) v -= p.dmin * fmin[i];
+      fa[i] += af[u].dy[i] * v;
+    }
+  };
+
   if (s0 < s1) issue(s0, 0);
   if (s0 + 1 < s1) issue(s0 + 1, 1);
   for (int64_t sb = s0; sb < s1; sb += 2) {
@@ -156,7 +270,17 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
       if (sb + 3 < s1) issue(sb + 3, 1);
     }
   }
-  reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd, activation);
+
+  __shared__ float red[NW][4][64];
+#pragma unroll
+  for (int i = 0; i < 4; i++) red[wave][i][lane] = fa[i];
+  __syncthreads();
+  if (wave >= 4) return;
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; w++) v += red[w][wave][lane];
+  const int m = 4 * kg + wave;
+  if (m < mrows && r < rows_here) Out::store(dst, (int64_t)m * ldd + n0 + r, v);
 }
 
 template <class WT, class Out>
@@ -177,6 +301,19 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
     else
       k_skinny<WT, act_decode, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
           w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation);
+    return;
+  }
+  const unsigned g16 = (unsigned)qmm_ceil_div(nrows_x, 16);
+  if (b <= 16 && (QMM_SKINNY16_WIDE || qmm_ceil_div(nrows_x, 32) < QMM_SKINNY_WIDE_TILES)) {
+    // 16x16x64 form: a quarter of the registers, 4 waves per SIMD; the widest K split whose waves are all resident
+    // at once (16 x CUs of them)
+    const int64_t slots = 16 * (int64_t)qmm_device_cus();
+    if (WT::kMin && nsb >= 16 && (int64_t)g16 * 16 <= slots)  // Q4_K fits 128 VGPRs at 16 waves; Q6_K does not
+      k_skinny16<typename Wt16<WT>::T, Out, 16><<<g16, 1024, 0, s>>>(w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+    else if (nsb >= 8 && (int64_t)g16 * 8 <= slots)
+      k_skinny16<typename Wt16<WT>::T, Out, 8><<<g16, 512, 0, s>>>(w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
+    else
+      k_skinny16<typename Wt16<WT>::T, Out, 4><<<g16, 256, 0, s>>>(w, nrows_x, wrb, ap, b, nsb, d, stride_col_dst);
     return;
   }
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
