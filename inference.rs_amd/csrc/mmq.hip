@@ -126,21 +126,32 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     WT::load(rw, wrow, (uint32_t)sb, g, rr);
   };
 
+  // The A-fragment LDS reads run one sub-block ahead of the MFMAs that consume them, so LDS latency overlaps
+  // matrix work.
   auto compute = [&](const uint8_t *slot, const typename WT::Raw &rr) {
     typename WT::Prep p;
     WT::prepare(rr, g, p);
     v16i acc1[TM], acc2[TM];
 #pragma unroll
     for (int t = 0; t < TM; t++) acc1[t] = acc2[t] = (v16i){};
+    // (Q4_K at TM = 2 runs at 2 waves per SIMD, where the extra registers would spill: it reads just in time)
+    constexpr bool kAhead = !(WT::kMin && TM == 2);
+    v4i av[2][TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) av[0][t] = *(const v4i *)(slot + 8192 * t + qoff[0]);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
+      if (kAhead && j < 7) {
+#pragma unroll
+        for (int t = 0; t < TM; t++) av[(j + 1) & 1][t] = *(const v4i *)(slot + 8192 * t + qoff[j + 1]);
+      }
       v4i b1, b2;
       WT::planes(rr, p, j, b1, b2);
 #pragma unroll
       for (int t = 0; t < TM; t++) {
-        const v4i av = *(const v4i *)(slot + 8192 * t + qoff[j]);
-        acc1[t] = mfma_i8(av, b1, acc1[t]);
-        acc2[t] = mfma_i8(av, b2, acc2[t]);
+        const v4i a = kAhead ? av[j & 1][t] : *(const v4i *)(slot + 8192 * t + qoff[j]);
+        acc1[t] = mfma_i8(a, b1, acc1[t]);
+        acc2[t] = mfma_i8(a, b2, acc2[t]);
       }
     }
 #pragma unroll
