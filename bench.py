@@ -432,7 +432,7 @@ def main():
                            "HIP graph of K steps"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_mmvq_p<unit_q4k, 1, 1, true>", "kernel_us": round(head["kernel_us"], 3),
+                     "kernel": "k_mmvq_p<unit_q4k, out_f32, 1, 1, true>", "kernel_us": round(head["kernel_us"], 3),
                      "algorithmic_bytes": kb},
         "cpu_baseline": base,
         "extra": extra,
