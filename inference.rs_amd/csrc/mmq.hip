@@ -22,6 +22,7 @@
 #include "common.h"
 #include "inferencequant.h"
 #include "planes.h"
+#include "skinny.h"
 #include "units.h"
 
 namespace {
@@ -504,6 +505,10 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   const ActTile a = act_tile(y, ncols_dst, nsb);
   const dim3 grid((unsigned)((nrows_x + BN - 1) / BN), (unsigned)((ncols_max + BM - 1) / BM), (unsigned)num_experts);
   hipStream_t s = (hipStream_t)stream;
+  // a few rows per expert: the few-row kernel streams each expert's weights once, without 64-row tiles of padding
+  if (type != QMM_TYPE_Q8_0 && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
+                                              ncols_dst, stride_col_dst, num_experts, s))
+    return;
   const uint8_t *w = (const uint8_t *)x;
   float *d = (float *)dst;
   const bool small = ncols_max <= 32;

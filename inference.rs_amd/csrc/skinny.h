@@ -19,3 +19,13 @@ bool qmm_skinny_decode(int type, int out_type, const void *vx, const void *vy, v
 bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_up, const void *vy, void *dst,
                     int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation,
                     hipStream_t s);
+
+// Expert-grouped matmul (launch_mmq_gguf_<t>_moe) over prefill-layout activations when the experts receive few
+// rows each: at most QMM_SKINNY_MOE_ROWS on average.  dst[ids_dst[m] * ldd + n], f32.  Returns false, launching
+// nothing, for a case it does not serve.
+#ifndef QMM_SKINNY_MOE_ROWS
+#define QMM_SKINNY_MOE_ROWS 32
+#endif
+bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
+                    int64_t ncols_x, int64_t nrows_x, int64_t w_row_bytes, int64_t ncols_dst, int64_t ldd,
+                    int64_t num_experts, hipStream_t s);

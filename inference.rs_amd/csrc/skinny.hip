@@ -47,6 +47,10 @@ struct act_decode {
   int64_t bytes;
   uint32_t row_bytes;
   __device__ __forceinline__ rsrc_t rsrc() const { return make_rsrc(base, bytes); }
+  // per-lane handle of row m; a row that is not valid reads as zero (its offset lies beyond every buffer's end)
+  __device__ __forceinline__ uint32_t handle(int64_t m, bool valid) const {
+    return valid ? (uint32_t)m * row_bytes : 0x80000000u;
+  }
   __device__ __forceinline__ void load(rsrc_t r, uint32_t row_off, int64_t sb, int g, bool min, ActFrag &f) const {
     const uint32_t o = row_off + (uint32_t)sb * 292;
 #pragma unroll
@@ -65,13 +69,48 @@ struct act_decode {
   }
 };
 
+// Prefill layout of one channel (include/inferencequant.h): qs[nsb][rows][256] int8, then d[nsb][rows] f32, then
+// bsums[nsb][rows][16] f16.  The handle is the lane's offset 256 m of row m inside one superblock's qs slab, with
+// bit 31 set for a row that reads as zero; the superblock's part of every offset is uniform and goes in the
+// scalar offset, outside the range check, which the vector part alone fails for such a row.
+struct act_tiles {
+  const uint8_t *base;
+  int64_t bytes;
+  uint32_t rows, nsb;
+  __device__ __forceinline__ rsrc_t rsrc() const { return make_rsrc(base, bytes); }
+  __device__ __forceinline__ uint32_t handle(int64_t m, bool valid) const {
+    return valid ? 256 * (uint32_t)m : 0x80000000u;
+  }
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t h, int64_t sb, int g, bool min, ActFrag &f) const {
+    const uint32_t srow = (uint32_t)sb * rows, zero = h & 0x80000000u;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, h + 32 * j + 16 * g, 256 * srow, 0));
+    if (min)
+      f.bs = __builtin_bit_cast(v8h, __builtin_amdgcn_raw_buffer_load_b128(r, ((h >> 3) + 16 * g) | zero,
+                                                                           nsb * rows * 260 + 32 * srow, 0));
+    f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (h >> 6) | zero,
+                                                                          nsb * rows * 256 + 4 * srow, 0));
+  }
+};
+
+// Expert-grouped row space: expert e = blockIdx.z owns activation rows [bounds[e], bounds[e + 1]) and weights
+// W + e * expert_bytes; row m is stored to destination row ids_dst[m].  Workgroup (x, y) takes the 32-row chunks
+// y, y + gridDim.y, ... of its expert, so every row is covered whatever the grid's height.
+struct moe_route {
+  const int32_t *bounds;
+  const int32_t *ids_dst;
+  int64_t expert_bytes;
+};
+
 // The NW waves' partial 32x32 tiles, summed through LDS.  Plain: lane (g, li) of wave w stores output registers
 // (16 / NW) w ...; GLU (waves [0, NW/2) hold gate partials, [NW/2, NW) up partials): the first NW/2 waves store
 // act(gate) * up.
+// Activation rows m0 + 0..31 below m1 are stored, to destination row ids[m] when ids is given, else m.
 template <class Out, int NW, bool GLU>
 __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane, int g, int li, int64_t n0,
-                                             int64_t n1, int64_t mrows, typename Out::T *__restrict__ dst,
-                                             int64_t ldd, int activation) {
+                                             int64_t n1, int64_t m0, int64_t m1, const int32_t *__restrict__ ids,
+                                             typename Out::T *__restrict__ dst, int64_t ldd, int activation) {
   __shared__ float red[NW][16][64];
 #pragma unroll
   for (int r = 0; r < 16; r++) red[wave][r][lane] = fa[r];
@@ -92,87 +131,103 @@ __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane,
       for (int w = KW; w < NW; w++) u += red[w][r][lane];
       v = glu_act(activation, v) * u;
     }
-    const int64_t m = out_row(r, g);
-    if (m < mrows && n < n1) Out::store(dst, m * ldd + n, v);
+    const int64_t m = m0 + out_row(r, g);
+    if (m < m1 && n < n1) Out::store(dst, (ids ? (int64_t)ids[m] : m) * ldd + n, v);
   }
 }
 
 // TR: weight rows per workgroup, 32 (every MFMA column used) or 16 (twice the workgroups for short weights; lanes
 // 16..31 load nothing and their columns come out zero)
 // GLU: W2 holds the up weights; waves [0, NW/2) take the gate rows and [NW/2, NW) the up rows.
-template <class WT, class AP, class Out, int NW, int TR, bool GLU>
+// MOE: the activation rows and weights of expert blockIdx.z (moe_route); otherwise rows [0, mrows).
+template <class WT, class AP, class Out, int NW, int TR, bool GLU, bool MOE = false>
 __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                                     int64_t nrows_w, int64_t w_row_bytes, AP ap, int mrows,
                                                     int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
-                                                    int activation) {
+                                                    int activation, moe_route route) {
   __shared__ float dys[NW][32];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   constexpr int KW = GLU ? NW / 2 : NW;  // waves splitting K
   const int kw = wave % KW;
+  int64_t m_first = 0, m_end = mrows, m_step = 32;
+  const int32_t *ids = nullptr;
+  if (MOE) {
+    const int64_t e = blockIdx.z;
+    m_first = route.bounds[e] + 32 * (int64_t)blockIdx.y;
+    m_end = route.bounds[e + 1];
+    if (m_first >= m_end) return;  // uniform over the workgroup
+    m_step = 32 * (int64_t)gridDim.y;
+    ids = route.ids_dst;
+    W += e * route.expert_bytes;
+    if (GLU) W2 += e * route.expert_bytes;
+  }
   const int64_t n0 = (int64_t)blockIdx.x * TR;
   const int64_t rows_here = nrows_w - n0 < TR ? nrows_w - n0 : TR;
   const rsrc_t rw = make_rsrc((GLU && wave >= KW ? W2 : W) + n0 * w_row_bytes, rows_here * w_row_bytes);
   const uint32_t wrow = li < rows_here ? (uint32_t)(li * w_row_bytes) : 0x80000000u;
-  // rows past the batch read as zero: their offset lies beyond every buffer's end
-  const uint32_t arow = li < mrows ? (uint32_t)li * ap.row_bytes : 0x80000000u;
   const rsrc_t ra = ap.rsrc();
 
   const int64_t per = (nsb + KW - 1) / KW;
   const int64_t s0 = kw * per, s1 = s0 + per < nsb ? s0 + per : nsb;
 
-  v16f fa = (v16f){};
-  // weights WD superblocks ahead (a register ring), activations two ahead.  Q4_K: 4 (fits 256 VGPRs); Q6_K's
-  // larger raw blocks: 2
+  // weights WD superblocks ahead (a register ring), activations two ahead
   constexpr int WD = WT::kMin ? QMM_SKINNY_WDEPTH : 2;
-  typename WT::Raw raw[WD];
-  ActFrag af[2];
-  auto compute = [&](const typename WT::Raw &rr, const ActFrag &a) {
-    typename WT::Prep p;
-    WT::prepare(rr, g, p);
-    v16i acc1 = (v16i){}, acc2 = (v16i){};
+  for (int64_t m0 = m_first; m0 < m_end; m0 += m_step) {
+    // rows past the batch (or the expert) read as zero
+    const uint32_t arow = ap.handle(m0 + li, m0 + li < m_end);
+    v16f fa = (v16f){};
+    typename WT::Raw raw[WD];
+    ActFrag af[2];
+    auto compute = [&](const typename WT::Raw &rr, const ActFrag &a) {
+      typename WT::Prep p;
+      WT::prepare(rr, g, p);
+      v16i acc1 = (v16i){}, acc2 = (v16i){};
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      v4i b1, b2;
-      WT::planes(rr, p, j, b1, b2);
-      acc1 = mfma_i8(a.q[j], b1, acc1);
-      acc2 = mfma_i8(a.q[j], b2, acc2);
-    }
-    v16f fmin = (v16f){};
-    if (WT::kMin) fmin = mfma_f16(a.bs, p.bmin, fmin);
-    // the scales of output rows 8q + 4g + i, from the lanes that loaded them
-    if (g == 0) dys[wave][li] = a.d;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const v4f dy4 = *(const v4f *)&dys[wave][8 * q + 4 * g];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = 4 * q + i;
-        const int iv = (acc1[r] << WT::kShift) + acc2[r];
-        float v = p.d * (float)iv;
-        if (WT::kMin) v -= p.dmin * fmin[r];
-        fa[r] += dy4[i] * v;
+      for (int j = 0; j < 8; j++) {
+        v4i b1, b2;
+        WT::planes(rr, p, j, b1, b2);
+        acc1 = mfma_i8(a.q[j], b1, acc1);
+        acc2 = mfma_i8(a.q[j], b2, acc2);
       }
-    }
-  };
+      v16f fmin = (v16f){};
+      if (WT::kMin) fmin = mfma_f16(a.bs, p.bmin, fmin);
+      // the scales of output rows 8q + 4g + i, from the lanes that loaded them
+      if (g == 0) dys[wave][li] = a.d;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const v4f dy4 = *(const v4f *)&dys[wave][8 * q + 4 * g];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int r = 4 * q + i;
+          const int iv = (acc1[r] << WT::kShift) + acc2[r];
+          float v = p.d * (float)iv;
+          if (WT::kMin) v -= p.dmin * fmin[r];
+          fa[r] += dy4[i] * v;
+        }
+      }
+    };
 
 #pragma unroll
-  for (int u = 0; u < WD; u++)
-    if (s0 + u < s1) WT::load(rw, wrow, (uint32_t)(s0 + u), g, raw[u]);
+    for (int u = 0; u < WD; u++)
+      if (s0 + u < s1) WT::load(rw, wrow, (uint32_t)(s0 + u), g, raw[u]);
 #pragma unroll
-  for (int u = 0; u < 2; u++)
-    if (s0 + u < s1) ap.load(ra, arow, s0 + u, g, WT::kMin, af[u]);
-  for (int64_t sb = s0; sb < s1; sb += WD) {
+    for (int u = 0; u < 2; u++)
+      if (s0 + u < s1) ap.load(ra, arow, s0 + u, g, WT::kMin, af[u]);
+    for (int64_t sb = s0; sb < s1; sb += WD) {
 #pragma unroll
-    for (int u = 0; u < WD; u++) {
-      const int64_t s = sb + u;
-      if (s < s1) {
-        compute(raw[u], af[u & 1]);
-        if (s + 2 < s1) ap.load(ra, arow, s + 2, g, WT::kMin, af[u & 1]);
-        if (s + WD < s1) WT::load(rw, wrow, (uint32_t)(s + WD), g, raw[u]);
+      for (int u = 0; u < WD; u++) {
+        const int64_t s = sb + u;
+        if (s < s1) {
+          compute(raw[u], af[u & 1]);
+          if (s + 2 < s1) ap.load(ra, arow, s + 2, g, WT::kMin, af[u & 1]);
+          if (s + WD < s1) WT::load(rw, wrow, (uint32_t)(s + WD), g, raw[u]);
+        }
       }
     }
+    reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, m0, m_end, ids, dst, ldd, activation);
+    if (!MOE) break;
+    __syncthreads();  // the next chunk rewrites the reduction buffer
   }
-  reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, mrows, dst, ldd, activation);
 }
 
 // ------------------------------------------------------------------------------------------ 16-row form
@@ -297,10 +352,10 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
   if (w2) {  // gate and up in one workgroup: 4 waves each
     if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
       k_skinny<WT, act_decode, Out, 8, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 512, 0, s>>>(
-          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation);
+          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation, moe_route{});
     else
       k_skinny<WT, act_decode, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
-          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation);
+          w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation, moe_route{});
     return;
   }
   const unsigned g16 = (unsigned)qmm_ceil_div(nrows_x, 16);
@@ -318,13 +373,33 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
   }
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
     k_skinny<WT, act_decode, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
-        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
   else if (nsb >= 32)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
     k_skinny<WT, act_decode, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
-        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
   else
     k_skinny<WT, act_decode, Out, 4, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
-        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0);
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
+}
+
+template <class WT>
+void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
+                int64_t nrows_x, int64_t w_row_bytes, int64_t nsb, int64_t ncols_dst, int64_t ldd, int64_t num_experts,
+                int64_t chunks, hipStream_t s) {
+  act_tiles ap;
+  ap.base = (const uint8_t *)y;
+  ap.rows = (uint32_t)ncols_dst;
+  ap.nsb = (uint32_t)nsb;
+  ap.bytes = nsb * ncols_dst * 292;
+  const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes};
+  const dim3 grid((unsigned)qmm_ceil_div(nrows_x, 32), (unsigned)chunks, (unsigned)num_experts);
+  const uint8_t *w = (const uint8_t *)x;
+  if (nsb >= 32)  // long rows: 8 waves split K
+    k_skinny<WT, act_tiles, out_f32, 8, 32, false, true><<<grid, 512, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
+                                                                              nsb, dst, ldd, 0, rt);
+  else
+    k_skinny<WT, act_tiles, out_f32, 4, 32, false, true><<<grid, 256, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
+                                                                              nsb, dst, ldd, 0, rt);
 }
 
 bool dispatch(int type, int out_type, const void *vx, const void *vx2, const void *vy, void *dst, int ncols_x,
@@ -363,4 +438,22 @@ bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_
                     hipStream_t s) {
   return dispatch(type, out_type, vx_gate, vx_up, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b,
                   activation, s);
+}
+
+bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
+                    int64_t ncols_x, int64_t nrows_x, int64_t w_row_bytes, int64_t ncols_dst, int64_t ldd,
+                    int64_t num_experts, hipStream_t s) {
+  if (ncols_x % 256 != 0 || ncols_dst <= 0 || num_experts <= 0 || num_experts > 65535) return false;
+  if (ncols_dst > QMM_SKINNY_MOE_ROWS * num_experts) return false;
+  const int64_t nsb = ncols_x / 256;
+  if (nsb * ncols_dst * 292 > 0x7ffffff0 || 32 * w_row_bytes > 0x7ffffff0) return false;
+  // enough 32-row chunks for an expert of average size; larger experts loop over theirs
+  const int64_t chunks = qmm_ceil_div(qmm_ceil_div(ncols_dst, num_experts), 32);
+  if (type == QMM_TYPE_Q4K)
+    launch_moe<wq4k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
+  else if (type == QMM_TYPE_Q6K)
+    launch_moe<wq6k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
+  else
+    return false;
+  return true;
 }

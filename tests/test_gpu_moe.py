@@ -93,12 +93,26 @@ def test_moe_dispatch_many_experts_and_empty():
     assert np.all(b0.cpu().numpy() == 0) and np.all(c0.cpu().numpy() == 0)
 
 
+def skewed_routing(rng, tokens, E, topk):
+    """Expert 0 on every token (more than 32 rows), experts 0..E/2 only: the rest receive none."""
+    ids = np.zeros((tokens, topk), dtype=np.int32)
+    for t in range(tokens):
+        ids[t, 1:] = rng.choice(np.arange(1, E // 2 + 1), topk - 1, replace=False)
+    return ids
+
+
+# 64 tokens x top-2 over 8 experts (16 rows each on average) and the skewed case take the few-row route of the
+# K-quant grouped matmul; 400 tokens (100 rows per expert) take the 128-row tile route.
+@pytest.mark.parametrize("case", ["uniform64", "skewed64", "uniform400"])
 @pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
-def test_grouped_prefill_matches_the_oracle(gtype):
+def test_grouped_prefill_matches_the_oracle(gtype, case):
     rng = np.random.default_rng(8 + gtype)
-    E, n, k, tokens, topk = 8, 160, 1024, 64, 2
+    E, n, k, topk = 8, 160, 1024, 2
+    tokens = 400 if case == "uniform400" else 64
+    if case == "uniform400":
+        k = 512
     wq = experts(rng, gtype, E, n, k)
-    ids, _ = routing(rng, tokens, E, topk)
+    ids = skewed_routing(rng, tokens, E, topk) if case == "skewed64" else routing(rng, tokens, E, topk)[0]
     x = acts(rng, tokens, k)
     want = O.indexed_moe(gtype, wq, E, n, k, x[:, None], ids.astype(np.uint32)).reshape(tokens * topk, n)
     bounds, tok, src, counts, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
