@@ -3,15 +3,16 @@
 HBM peak); prefill int8 TOPS at M=512").
 
 One step = one pass of the hot path over one batch of synthetic input, with every input resident in HBM:
-  headline: activation f32 [1, 4096] -> Q8_K -> Q4_K 14336x4096 matvec -> f32 [1, 14336],
-  i.e. launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, the two launches of the
-  reference's fast_mmvq::plain.  Weights rotate over 16 copies (528 MB > the 256 MB Infinity Cache), so every
-  step streams its weight from HBM.  K steps are captured in one HIP graph and replayed once between a
-  synchronize on both sides; `value` = algorithmic bytes per step / time per step.
+  headline: activation f32 [1, 4096] -> Q8_K -> Q4_K 14336x4096 matvec -> f32 [1, 14336]
+  in one launch, launch_mmvq_gguf_q4_k_f32_quantize_plain, whose output is bit-identical to the reference's two
+  launches (launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, fast_mmvq::plain); the two-launch
+  step and its matvec alone are reported in "extra".  Weights rotate over 16 copies (528 MB > the 256 MB
+  Infinity Cache), so every step streams its weight from HBM.  K steps are captured in one HIP graph and
+  replayed once between a synchronize on both sides; `value` = algorithmic bytes per step / time per step.
 Extra lines in "extra": Q4_K decode at b = 4 and 16, Q8_0 4096^2 decode, the M = 512 prefill (Q4_K and Q6_K,
 int8 TOPS), the Llama-3-8B linear stack (tokens/s) and the 8-expert MoE (64 tokens, top-2).
-`roofline` is the matvec kernel alone (its own graph of K launches), `cpu_baseline` the oracle's CPU QMatMul
-(oracle/, a C restatement of the reference's) on the box's host cores over a bounded sample.
+`roofline` is the step's one kernel, `cpu_baseline` the oracle's CPU QMatMul (oracle/, a C restatement of the
+reference's) on the box's host cores over a bounded sample.
 """
 import argparse
 import ctypes
@@ -127,8 +128,9 @@ def graph_time(torch, fn, steps, warmup):
 # ------------------------------------------------------------------------------------------------ workloads
 
 def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
-    """One step = the reference's two launches: launch_mmvq_gguf_quantize_* (f32 activation -> Q8 blocks) and
-    launch_mmvq_gguf_<t>_f32_plain (the matvec).  The matvec alone is timed in a second graph."""
+    """The reference's decode step as two launches: launch_mmvq_gguf_quantize_* (f32 activation -> Q8 blocks) and
+    launch_mmvq_gguf_<t>_f32_plain (the matvec), with the matvec alone timed in a second graph; for b <= 2 and
+    k <= 4096 also the same step as one launch, launch_mmvq_gguf_<t>_f32_quantize_plain (bit-identical output)."""
     wq = quantized_weight(gtype, n, k, seed)
     ws = device_copies(torch, wq, copies)
     rng = np.random.default_rng(seed + 1)
@@ -143,19 +145,30 @@ def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
     def matvec_only(i):
         qmm.mmvq(gtype, ws[i % copies], vy, k, n, b, kp, out=out)
 
+    def one_launch(i):
+        qmm.mmvq_quantize(gtype, ws[i % copies], x, n, out=out)
+
     t = graph_time(torch, step, steps, warmup)
+    y = out.cpu().numpy()
     t_kernel = graph_time(torch, matvec_only, steps, warmup)
     w_bytes = wq.size
     act_q_bytes = qmm.act_bytes(gtype, b, kp)
     step_bytes = w_bytes + b * k * 4 + b * n * 4            # f32 activation in, f32 out
     # what the matvec itself must move: weights, the Q8 activation blocks, the f32 outputs
     kernel_bytes = w_bytes + act_q_bytes + b * n * 4
-    return {
+    r = {
         "seconds": t, "ms_per_step": t / steps * 1e3, "gb_s": step_bytes / (t / steps) / 1e9,
         "step_bytes": step_bytes, "kernel_us": t_kernel / steps * 1e6,
         "kernel_gb_s": kernel_bytes / (t_kernel / steps) / 1e9, "kernel_bytes": kernel_bytes,
-        "weights": wq, "x": x.cpu().numpy(), "y": out.cpu().numpy(),
+        "weights": wq, "x": x.cpu().numpy(), "y": y,
     }
+    if b <= 2 and k <= 4096:
+        t1 = graph_time(torch, one_launch, steps, warmup)
+        if not np.array_equal(out.cpu().numpy().view(np.uint32), y.view(np.uint32)):
+            raise RuntimeError("one-launch decode differs from the two-launch result")
+        r["one_launch"] = {"ms_per_step": t1 / steps * 1e3, "gb_s": step_bytes / (t1 / steps) / 1e9,
+                           "kernel_us": t1 / steps * 1e6}
+    return r
 
 
 def prefill_workload(torch, qmm, gtype, n, k, m, copies, steps, warmup, seed):
@@ -185,7 +198,8 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     """Llama-3-8B linears, Q4_K for q/k/o/gate/up and Q6_K for v/down, 32 layers; one weight per shape is
     quantized and its bytes copied to every layer (distinct HBM copies, so every step streams 4.44 GB).
     Per layer, as the reference's decode path runs them: the attention input is quantized once and q, k, v read
-    that one activation; o and down quantize their own inputs; gate and up are one fused-GLU launch
+    that one activation; o and down quantize their own inputs (at b <= 2, o in one launch with its quantization,
+    launch_mmvq_gguf_q4_k_f32_quantize_plain); gate and up are one fused-GLU launch
     (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  Rows > 16 take the prefill matmul, one quantized
     activation per distinct input.  The inputs are synthetic, one per projection group."""
     shapes = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
@@ -195,8 +209,8 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     dev = {name: [torch.from_numpy(base[name]).cuda() for _ in range(layers)] for name, _, _, _ in shapes}
     total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
     res = {"weight_bytes_per_step": total_bytes,
-           "launches_per_layer": "decode: 4 quantize + q, k, v, o, gate/up (fused GLU), down = 10; "
-                                 "prefill: 4 quantize + 7 matmuls"}
+           "launches_per_layer": "decode b <= 2: 3 quantize + q, k, v, o (quantizing its input), gate/up (fused GLU), "
+                                 "down = 9; b 3..16: 4 quantize + 6 = 10; prefill: 4 quantize + 7 matmuls"}
     import qmm as Q
     for b in batches:
         rng = np.random.default_rng(seed + 100 + b)
@@ -211,10 +225,14 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
         tdim = {name: t for name, t, _, _ in shapes}
         ndim = {name: n for name, _, n, _ in shapes}
 
+        one_launch_o = b <= 2
+
         def step(i):
             for layer in range(layers):
                 for g, x in xs.items():
                     vy, kp = bufs[g]
+                    if decode and g == "o" and one_launch_o:
+                        continue
                     if decode:
                         Q.quantize_decode(Q4K, x, kp=kp, out=vy)
                     else:
@@ -222,7 +240,9 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
                 for name in ("q", "k", "v", "o", "gate", "down"):
                     vy, kp = bufs[group[name]]
                     t, n, k = tdim[name], ndim[name], kdim[name]
-                    if decode and name == "gate":
+                    if decode and name == "o" and one_launch_o:
+                        Q.mmvq_quantize(t, dev["o"][layer], xs["o"], n, out=outs["o"])
+                    elif decode and name == "gate":
                         Q.mmvq_fused_glu(Q4K, dev["gate"][layer], dev["up"][layer], vy, k, n, b, kp,
                                          out=outs["gate"])
                     elif decode:
@@ -327,7 +347,10 @@ EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_pr
 
 
 def decode_summary(r):
-    return {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
+    d = {key: r[key] for key in ("ms_per_step", "gb_s", "kernel_us", "kernel_gb_s")}
+    if "one_launch" in r:
+        d["one_launch"] = r["one_launch"]
+    return d
 
 
 def main():
@@ -392,9 +415,16 @@ def main():
 
     log("headline: Q4_K 14336x4096 decode b=1")
     head = decode_workload(torch, qmm, Q4K, n, k, 1, 16, args.steps, args.warmup, SEED)
-    log(f"  {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_s']:.0f} GB/s; kernel {head['kernel_us']:.2f} us")
+    one = head["one_launch"]
+    log(f"  one launch {one['ms_per_step'] * 1e3:.2f} us/step, {one['gb_s']:.0f} GB/s; two launches "
+        f"{head['ms_per_step'] * 1e3:.2f} us/step; plain matvec {head['kernel_us']:.2f} us")
 
-    extra = {}
+    extra = {"q4_k_decode_b1_two_launch": {
+        "ms_per_step": head["ms_per_step"], "gb_s": head["gb_s"],
+        "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain",
+        "matvec": {"kernel": "k_mmvq_p<unit_q4k, out_f32, 1, 1, true>", "kernel_us": head["kernel_us"],
+                   "gb_s": head["kernel_gb_s"], "algorithmic_bytes": head["kernel_bytes"],
+                   "frac_hbm_peak": head["kernel_gb_s"] / HBM_PEAK_GBS}}}
     if not args.quick:
         for name, run in extra_runs.items():
             log(name)
@@ -405,8 +435,9 @@ def main():
         log("CPU baseline (oracle)")
         base = cpu_baseline(head["weights"], n, k, args.cpu_seconds)
 
-    kb = head["kernel_bytes"]
-    achieved = head["kernel_gb_s"]
+    # the step is one launch: its kernel moves the step's bytes (weights, f32 activation, f32 output)
+    kb = head["step_bytes"]
+    achieved = one["gb_s"]
     traffic = None
     tpath = os.path.join(REPO, "profiles", "traffic_q4_k_decode_14336x4096_b1.json")
     if os.path.exists(tpath):
@@ -414,12 +445,12 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     line = {
         "metric": "Q4_K bs=1 matvec GB/s (% of HBM peak); prefill int8 TOPS at M=512",
-        "value": round(head["gb_s"], 1),
+        "value": round(one["gb_s"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["ms_per_step"], 6),
+        "ms_per_step": round(one["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -427,12 +458,12 @@ def main():
         "data": "synthetic: weights N(0,0.02) quantized by the library's QTensor quantizer, activations N(0,1), "
                 f"seed {SEED}; 16 weight copies rotated (528 MB)",
         "config": {"workload": "q4_k_decode_14336x4096_b1", "weight": "Q4_K 14336x4096", "batch": 1,
-                   "activation": "f32 [1,4096] -> Q8_K", "frac_hbm_peak": round(head["gb_s"] / HBM_PEAK_GBS, 4),
-                   "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, "
-                           "HIP graph of K steps"},
+                   "activation": "f32 [1,4096] -> Q8_K", "frac_hbm_peak": round(one["gb_s"] / HBM_PEAK_GBS, 4),
+                   "step": "launch_mmvq_gguf_q4_k_f32_quantize_plain (quantize + matvec in one launch, the same "
+                           "bits as the reference's two launches), HIP graph of K steps"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_mmvq_p<unit_q4k, out_f32, 1, 1, true>", "kernel_us": round(head["kernel_us"], 3),
+                     "kernel": "k_mmvq_pq<unit_q4k, out_f32, 1, 1, true, 8, 2>", "kernel_us": round(one["kernel_us"], 3),
                      "algorithmic_bytes": kb},
         "cpu_baseline": base,
         "extra": extra,

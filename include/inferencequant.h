@@ -75,6 +75,27 @@ QMM_DECLARE_MMVQ_PLAIN(q8_0)
 QMM_DECLARE_MMVQ_PLAIN(q4_k)
 QMM_DECLARE_MMVQ_PLAIN(q6_k)
 
+/* ------------------------------------------------------------------ decode matvec with its own quantization
+ * launch_mmvq_gguf_<t>_{bf16,f16,f32}_quantize_plain: no counterpart in the reference, whose decode makes two
+ * launches, launch_mmvq_gguf_quantize_q8_1_<dt> then launch_mmvq_gguf_<t>_<dt>_plain (fast_mmvq.rs:534-565,
+ * gguf/ffi.rs:602-640, 846-876).  This one takes the f32 activation rows x[j * stride_col_x + k] (j < b_size,
+ * k < ncols_x) and gives the same dst, bit for bit, as launch_mmvq_gguf_quantize_{q8k,q8_0}_f32 followed by
+ * launch_mmvq_gguf_<t>_<dt>_plain, in one launch and without the activation scratch buffer.  b_size 1 or 2;
+ * ncols_x at most 4096 (a multiple of 64 for Q8_0). */
+#define QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(t)                                                                        \
+  void launch_mmvq_gguf_##t##_f32_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
+                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
+                                                 void *stream);                                                  \
+  void launch_mmvq_gguf_##t##_f16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
+                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
+                                                 void *stream);                                                  \
+  void launch_mmvq_gguf_##t##_bf16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,         \
+                                                  int nrows_x, int stride_col_x, int stride_col_dst, int b_size, \
+                                                  void *stream);
+QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q8_0)
+QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q4_k)
+QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q6_k)
+
 /* ------------------------------------------------------------------ fused decode forms
  * launch_mmvq_gguf_<t>_{bf16,f16,f32}_fused_glu (gguf/ffi.rs:1032-1069; kernel mmvq_gguf.cuh:761-842):
  * dst[j * stride_col_dst + row] = act(W_gate[row] . Q(y_j)) * (W_up[row] . Q(y_j)) for j < b_size (1..16),

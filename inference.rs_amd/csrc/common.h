@@ -18,6 +18,18 @@ void qmm_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 // compute units of the current device (queried once per device)
 int qmm_device_cus();
 
+// Workgroups of kernel K with `threads` threads and `lds` bytes of dynamic LDS that one CU holds at once, queried
+// once per kernel (every device of the process is taken to be alike); at least 1.
+template <auto K>
+int qmm_resident_per_cu(int threads, size_t lds) {
+  static const int n = [&] {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, threads, lds) != hipSuccess || v < 1) v = 1;
+    return v;
+  }();
+  return n;
+}
+
 // ------------------------------------------------------------------ scalar conversions (device)
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -92,6 +104,29 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   v = dpp_add<0x142, 0xa>(v);  // row_bcast15
   v = dpp_add<0x143, 0xc>(v);  // row_bcast31
   return v;
+}
+
+// Maximum of non-negative values over the wave with the same DPP pattern (0, what a lane outside a row_bcast
+// mask reads, is the identity); every lane gets the result through lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                        0xf, false)));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  v = dpp_max<0xb1, 0xf>(v);
+  v = dpp_max<0x4e, 0xf>(v);
+  v = dpp_max<0x141, 0xf>(v);
+  v = dpp_max<0x140, 0xf>(v);
+  v = dpp_max<0x142, 0xa>(v);
+  v = dpp_max<0x143, 0xc>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over each quad of lanes (xor 1, xor 2 through quad_perm); every lane of the quad gets it.
+__device__ __forceinline__ int quad_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);
+  return v + __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -9,6 +9,7 @@
 // butterfly.  Activations are tiny and hit L2.
 #include "common.h"
 #include "inferencequant.h"
+#include "q8.h"
 #include "skinny.h"
 #include "units.h"
 
@@ -118,6 +119,120 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
     }
 #pragma unroll
     for (int s = 0; s < S; s++) w[s] = wn[s];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ fused quantization
+
+// The persistent matvec against NC f32 activation rows that it quantizes itself.  Every workgroup quantizes the rows
+// into LDS, in the decode activation layout, with the standalone quantizers' device code (q8.h), so the blocks are
+// bit-identical to launch_mmvq_gguf_quantize_{q8k,q8_0}_f32's.  The f32 loads go out first and the first two rows'
+// weights right after them, so the quantization runs while the weights are in flight.  A wave step quantizes one
+// Q8_K block (4 values per lane) or eight Q8_0 blocks (8 lanes each); wave w takes steps w, w + NW, ... (at most
+// G of them).
+template <class U, class Out, int NC, int S, bool FULL, int NW, int G>
+__global__ __launch_bounds__(64 * NW) void k_mmvq_pq(const uint8_t *__restrict__ vx, const float *__restrict__ x,
+                                                     int64_t stride_x, typename Out::T *__restrict__ dst, int nrows,
+                                                     int64_t row_bytes, int nunits, int stride_col_dst) {
+  extern __shared__ __align__(16) uint8_t s_act[];
+  constexpr bool kQ8K = U::kActBlockValues == 256;
+  constexpr int kBlocksPerStep = kQ8K ? 1 : 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nblk = nunits * U::kValuesPerUnit / U::kActBlockValues;  // activation blocks per row
+  const int total = NC * nblk;
+  const int64_t act_row_bytes = (int64_t)nblk * U::kActBlockBytes;
+
+  // 1. this wave's f32 values: rows hold whole blocks, so every load is in range (a lane past the last block
+  // reloads block 0 and stores nothing)
+  float v[G][4];
+  int blk[G];
+#pragma unroll
+  for (int t = 0; t < G; t++) {
+    blk[t] = (wave + NW * t) * kBlocksPerStep + (kQ8K ? 0 : lane >> 3);
+    const int b = blk[t] < total ? blk[t] : 0;
+    const int j = NC > 1 && b >= nblk ? 1 : 0;
+    const int k0 = (b - j * nblk) * U::kActBlockValues + 4 * (kQ8K ? lane : lane & 7);
+    // (a float vector: this compiler's __builtin_bit_cast of a u32 vector element reads element 0)
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 f;
+    __builtin_memcpy(&f, __builtin_assume_aligned(x + j * stride_x + k0, 4), 16);
+    v[t][0] = f.x, v[t][1] = f.y, v[t][2] = f.z, v[t][3] = f.w;
+  }
+  // 2. the first two rows' weights, without branches (a row or unit past the end is clamped to the last one and
+  // never used), so the quantization below waits for the f32 loads only
+  auto has = [&](int s) { return FULL || lane + 64 * s < nunits; };
+  const int tw = gridDim.x * NW;
+  int row = blockIdx.x * NW + wave;
+  typename U::W w[S], wn[S];
+  {
+    const int64_t r0 = row < nrows ? row : nrows - 1, r1 = row + tw < nrows ? row + tw : nrows - 1;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      const int u = has(s) ? lane + 64 * s : nunits - 1;
+      U::load_w(vx + r0 * row_bytes, u, w[s]);
+      U::load_w(vx + r1 * row_bytes, u, wn[s]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. quantize into LDS
+  if constexpr (kQ8K) {
+    qmm_q8::q8k_dst d[G];
+    bool st[G];
+#pragma unroll
+    for (int t = 0; t < G; t++) {
+      st[t] = blk[t] < total;
+      d[t] = qmm_q8::q8k_decode_dst(s_act, st[t] ? blk[t] : 0);
+    }
+    qmm_q8::q8k_waves<G>(v, lane, d, st);
+  }
+#pragma unroll
+  for (int t = 0; t < G; t++) {
+    if constexpr (!kQ8K) {
+      uint8_t *b = s_act + (int64_t)(blk[t] < total ? blk[t] : 0) * 34;
+      qmm_q8::q8_0_group(v[t], lane & 7, (int8_t *)(b + 2), (uint16_t *)b, blk[t] < total);
+    }
+  }
+  __syncthreads();
+  if (row >= nrows) return;  // whole wave
+  constexpr bool kRegs = NC * S <= 2;
+  typename U::A areg[kRegs ? NC * S : 1];
+  if (kRegs) {
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+      for (int j = 0; j < NC; j++)
+        if (has(s)) U::load_a(s_act + j * act_row_bytes, lane + 64 * s, areg[kRegs ? s * NC + j : 0]);
+  }
+  // 4. rows row, row + tw, ...; the row after next is requested before each row's math
+  for (; row < nrows; row += tw) {
+    float acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) acc[j] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      if (!has(s)) continue;
+      const int u = lane + 64 * s;
+#pragma unroll
+      for (int j = 0; j < NC; j++) {
+        if (kRegs) {
+          acc[j] += U::dot(w[s], areg[s * NC + j], u);
+        } else {
+          typename U::A a;
+          U::load_a(s_act + j * act_row_bytes, u, a);
+          acc[j] += U::dot(w[s], a, u);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      const float r = wave_sum_to_lane63(acc[j]);
+      if (lane == 63) Out::store(dst, (int64_t)j * stride_col_dst + row, r);
+    }
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      w[s] = wn[s];
+      if (row + 2 * tw < nrows && has(s)) U::load_w(vx + (int64_t)(row + 2 * tw) * row_bytes, lane + 64 * s, wn[s]);
+    }
   }
 }
 
@@ -299,6 +414,93 @@ void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int
   }
 }
 
+// Fused quantization: two workgroups per CU, of 8 waves for tall weights (at least 8192 rows: more rows per wave)
+// and of 16 below (each activation row quantized by half as many workgroups), as measured fastest on MI355X;
+// one unit per lane (rows of at most 4096 values, which keeps the kernel within 64 VGPRs).
+template <class U, class Out, int NC, int NW>
+void launch_pq_nw(const uint8_t *vx, const float *x, int64_t stride_x, typename Out::T *dst, int k, int nrows,
+                  int stride_col_dst, hipStream_t s) {
+  const int nu = U::units(k);
+  const bool full = nu % 64 == 0;
+  const int nblk = nu * U::kValuesPerUnit / U::kActBlockValues;
+  const int steps = (int)qmm_ceil_div((int64_t)NC * nblk, U::kActBlockValues == 256 ? 1 : 8);  // <= 32
+  const int64_t wgs = qmm_ceil_div(nrows, NW);
+  const size_t lds = (size_t)NC * nblk * U::kActBlockBytes;
+  const int64_t rb = U::row_bytes(k);
+  // at most two resident workgroups per CU (fewer when the kernel's registers allow only one)
+  auto grid = [&](int per_cu) {
+    const int64_t cap = (int64_t)(per_cu < 2 ? per_cu : 2) * qmm_device_cus();
+    return dim3((unsigned)(wgs < cap ? wgs : cap));
+  };
+#define QMM_PQ_F(FF, GG)                                                                                            \
+  k_mmvq_pq<U, Out, NC, 1, FF, NW, GG><<<grid(qmm_resident_per_cu<k_mmvq_pq<U, Out, NC, 1, FF, NW, GG>>(64 * NW, lds)), \
+                                         64 * NW, lds, s>>>(vx, x, stride_x, dst, nrows, rb, nu, stride_col_dst)
+#define QMM_PQ(GG)          \
+  do {                      \
+    if (full)               \
+      QMM_PQ_F(true, GG);   \
+    else                    \
+      QMM_PQ_F(false, GG);  \
+  } while (0)
+  if (steps <= NW)
+    QMM_PQ(1);
+  else if (steps <= 2 * NW)
+    QMM_PQ(2);
+  else
+    QMM_PQ(4);
+#undef QMM_PQ
+#undef QMM_PQ_F
+}
+
+template <class U, class Out, int NC>
+void launch_pq(const uint8_t *vx, const float *x, int64_t stride_x, typename Out::T *dst, int k, int nrows,
+               int stride_col_dst, hipStream_t s) {
+  if (nrows >= 8192)
+    launch_pq_nw<U, Out, NC, 8>(vx, x, stride_x, dst, k, nrows, stride_col_dst, s);
+  else
+    launch_pq_nw<U, Out, NC, 16>(vx, x, stride_x, dst, k, nrows, stride_col_dst, s);
+}
+
+template <class Out>
+void quantize_plain(int type, const void *vx, const float *x, void *dst, int ncols_x, int nrows_x, int stride_col_x,
+                    int stride_col_dst, int b, void *stream, const char *who) {
+  const int bs = (int)qmm_block_size(type);
+  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0 || (type == QMM_TYPE_Q8_0 && ncols_x % 64 != 0)) {
+    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x,
+                  type == QMM_TYPE_Q8_0 ? 64 : bs);
+    return;
+  }
+  if (b < 0 || b > 2 || (b > 1 && stride_col_x < ncols_x)) {
+    qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
+    return;
+  }
+  // one unit per lane; every activation block of the b rows within kPqSteps wave steps of one workgroup
+  if (ncols_x > 64 * 64) {
+    qmm_set_error("%s: ncols_x=%d (at most 4096)", who, ncols_x);
+    return;
+  }
+  const uintptr_t align = type == QMM_TYPE_Q6K ? 2 : (type == QMM_TYPE_Q8_0 ? 4 : 16);
+  if ((uintptr_t)vx % align != 0 || (uintptr_t)x % 4 != 0) {
+    qmm_set_error("%s: weights must be %zu-byte and x 4-byte aligned", who, (size_t)align);
+    return;
+  }
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *w = (const uint8_t *)vx;
+  typename Out::T *d = (typename Out::T *)dst;
+#define QMM_PQ_T(U)                                                                                      \
+  if (b == 1)                                                                                            \
+    launch_pq<U, Out, 1>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);                    \
+  else                                                                                                   \
+    launch_pq<U, Out, 2>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);
+  switch (type) {
+    case QMM_TYPE_Q4K: QMM_PQ_T(unit_q4k) break;
+    case QMM_TYPE_Q6K: QMM_PQ_T(unit_q6k) break;
+    default: QMM_PQ_T(unit_q8_0) break;
+  }
+#undef QMM_PQ_T
+}
+
 template <class U>
 void moe_launch(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
                 float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int y_div, int n_pairs, int activation,
@@ -391,6 +593,24 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
                                          int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
     plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
                     "mmvq_" #t "_bf16");                                                                          \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_f32_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
+                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
+                                                 void *stream) {                                                 \
+    quantize_plain<out_f32>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,     \
+                            "mmvq_" #t "_f32_quantize");                                                          \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_f16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
+                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
+                                                 void *stream) {                                                 \
+    quantize_plain<out_f16>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,     \
+                            "mmvq_" #t "_f16_quantize");                                                          \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_bf16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,         \
+                                                  int nrows_x, int stride_col_x, int stride_col_dst, int b_size, \
+                                                  void *stream) {                                                \
+    quantize_plain<out_bf16>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,    \
+                             "mmvq_" #t "_bf16_quantize");                                                        \
   }                                                                                                               \
   void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy,  \
                                   const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \

@@ -37,62 +37,76 @@ __device__ __forceinline__ uint16_t bsum_bits(int s, bool f16) {
   return f16 ? f32_to_f16_bits((float)s) : (uint16_t)(int16_t)s;
 }
 
-// One wave quantizes v[0..3] of lanes 0..63 (values 4*lane .. 4*lane+3 of the block) and writes it.
-__device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst) {
+// One wave quantizes G blocks: v[t][0..3] of lanes 0..63 are values 4*lane .. 4*lane+3 of block t, written to
+// dst[t] when store[t] (uniform over the wave).  The value of largest magnitude is the first one in index order,
+// as the reference's sequential scan with a strict '>' finds it: the wave maximum of |x| (DPP), then the first
+// lane holding it (ballot), then that lane's first such value.  NaNs are never the maximum (fmaxf drops them, as
+// the scan's comparison does).  A block whose maximum is 0 (or that holds no number) is written as zeros
+// (k_quants.rs:2740-2743), through selects rather than a branch, and each step runs for all G blocks before the
+// next, so their DPP chains interleave.
+template <int G>
+__device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, const q8k_dst (&dst)[G],
+                                          const bool (&store)[G]) {
 #pragma clang fp contract(off)
-  float best = 0.0f;
-  int bidx = 0x7fffffff;
+  float am[G], mx[G];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float a = fabsf(v[i]);
-    if (a > best) {  // strictly greater: the first of equal magnitudes stays
-      best = a;
-      bidx = lane * 4 + i;
-    }
-  }
+  for (int t = 0; t < G; t++)
+    am[t] = fmaxf(fmaxf(fabsf(v[t][0]), fabsf(v[t][1])), fmaxf(fabsf(v[t][2]), fabsf(v[t][3])));
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ob = __shfl_xor(best, off, QMM_WAVE);
-    const int oi = __shfl_xor(bidx, off, QMM_WAVE);
-    if (ob > best || (ob == best && oi < bidx)) {
-      best = ob;
-      bidx = oi;
-    }
-  }
-  if (best == 0.0f) {  // amax == 0: an all-zero block (k_quants.rs:2740-2743)
-    *(uint32_t *)(dst.qs + 4 * lane) = 0u;
-    if (lane == 0) *dst.d = 0.0f;
-    if ((lane & 3) == 0) dst.bsums[lane >> 2] = 0;  // +0 in both encodings
-    return;
-  }
-  const float mine = v[bidx & 3];
-  const float mx = __shfl(mine, bidx >> 2, QMM_WAVE);
-  const float iscale = -127.0f / mx;
-  int q[4];
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0xb1, 0xf>(am[t]);
 #pragma unroll
-  for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(iscale * v[i]));
-  int s = q[0] + q[1] + q[2] + q[3];
-  s += __shfl_xor(s, 1, QMM_WAVE);
-  s += __shfl_xor(s, 2, QMM_WAVE);
-  const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
-                          ((uint32_t)(q[3] & 0xff) << 24);
-  *(uint32_t *)(dst.qs + 4 * lane) = packed;
-  if ((lane & 3) == 0) dst.bsums[lane >> 2] = bsum_bits(s, dst.bsums_f16);
-  if (lane == 0) *dst.d = 1.0f / iscale;
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x4e, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x141, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x140, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x142, 0xa>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x143, 0xc>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) {
+    const float amax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[t]), 63));
+    const bool nz = amax > 0.0f;
+    const float *x = v[t];
+    const float first = fabsf(x[0]) == amax ? x[0] : fabsf(x[1]) == amax ? x[1] : fabsf(x[2]) == amax ? x[2] : x[3];
+    const int holder = __builtin_ctzll(__ballot(am[t] == amax)) & 63;
+    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), holder));
+    const float iscale = nz ? -127.0f / m : 0.0f;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = nz ? sat_i8(roundf(iscale * x[i])) : 0;
+    const int s = quad_sum(q[0] + q[1] + q[2] + q[3]);
+    if (!store[t]) continue;
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *(uint32_t *)(dst[t].qs + 4 * lane) = packed;
+    if ((lane & 3) == 0) dst[t].bsums[lane >> 2] = bsum_bits(s, dst[t].bsums_f16);  // +0 for a zero block
+    if (lane == 0) *dst[t].d = nz ? 1.0f / iscale : 0.0f;
+  }
 }
 
-// Eight lanes quantize one 32-value Q8_0 block (4 values each); writes qs (4 bytes/lane) and the f16 scale.
-__device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs, uint16_t *d_out) {
+__device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst) {
+  const float (&vv)[1][4] = *reinterpret_cast<const float(*)[1][4]>(v);
+  const q8k_dst d[1] = {dst};
+  const bool st[1] = {true};
+  q8k_waves<1>(vv, lane, d, st);
+}
+
+// Eight lanes quantize one 32-value Q8_0 block (4 values each); writes qs (4 bytes/lane) and the f16 scale when
+// `store`.  Every lane of the wave takes part (the 8-lane maximum goes through DPP within each group of 8).
+__device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs, uint16_t *d_out, bool store) {
 #pragma clang fp contract(off)
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, QMM_WAVE));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, QMM_WAVE));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, QMM_WAVE));
+  amax = dpp_max<0xb1, 0xf>(amax);
+  amax = dpp_max<0x4e, 0xf>(amax);
+  amax = dpp_max<0x141, 0xf>(amax);  // row_half_mirror: the other quad of the group of 8
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   int q[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(v[i] * id));
+  if (!store) return;
   // qs may be only 2-byte aligned (34-byte blocks): two 16-bit stores
   uint16_t *q16 = (uint16_t *)(qs + 4 * sub);
   q16[0] = (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));

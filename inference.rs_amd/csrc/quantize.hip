@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_rows(const typename In::T
   float v[4];
   load4<In>(x + row * (int64_t)kx, ib * 32 + (lane & 7) * 4, valid ? kx : 0, v);
   uint8_t *blkp = vy + b * 34;
-  if (valid) q8_0_group(v, lane & 7, (int8_t *)(blkp + 2), (uint16_t *)blkp);
+  q8_0_group(v, lane & 7, (int8_t *)(blkp + 2), (uint16_t *)blkp, valid);
 }
 
 // ------------------------------------------------------------------ prefill (tile) layout kernels
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_tiles(const typename In::
   uint8_t *chan = vy + ch * nsb * ne1 * 272;
   int8_t *qs = (int8_t *)(chan + (sb * ne1 + r) * 256 + j * 32);
   uint16_t *d = (uint16_t *)(chan + nsb * ne1 * 256) + (sb * ne1 + r) * 8 + j;
-  if (valid) q8_0_group(v, lane & 7, qs, d);
+  q8_0_group(v, lane & 7, qs, d, valid);
 }
 
 // act(gate) * up of row ids[r] (or r), quantized into the prefill tile layout: the fused GLU requantization
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8_0_tiles(const float *__
   }
   int8_t *qs = (int8_t *)(vy + (sb * ne1 + r) * 256 + j * 32);
   uint16_t *d = (uint16_t *)(vy + nsb * ne1 * 256) + (sb * ne1 + r) * 8 + j;
-  if (valid) q8_0_group(v, lane & 7, qs, d);
+  q8_0_group(v, lane & 7, qs, d, valid);
 }
 
 template <class In>

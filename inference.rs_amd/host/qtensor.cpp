@@ -85,6 +85,17 @@ quant_fn decode_quantizer(GgmlDType w, GgmlDType in) {
   }
 }
 
+// The decode matvec that quantizes its own f32 activations (one launch; output f32).
+using mmvq_q_fn = void (*)(const void *, const float *, void *, int, int, int, int, int, void *);
+mmvq_q_fn decode_matvec_quantize(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_f32_quantize_plain;
+    case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_f32_quantize_plain;
+    case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_f32_quantize_plain;
+    default: throw Error("QMatMul: unsupported weight type");
+  }
+}
+
 mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
 #define QMM_PICK(t)                                                              \
   switch (out) {                                                                 \
@@ -278,7 +289,12 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
   const int64_t k = w.cols(), n = w.rows();
   const GgmlDType t = w.dtype();
   hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
-  if (prefers_mmvq(t, rows)) {
+  if (prefers_mmvq(t, rows) && in_dtype == GgmlDType::F32 && rows <= 2 && k <= 4096 &&
+      (t != GgmlDType::Q8_0 || k % 64 == 0) && (uintptr_t)xs % 4 == 0) {
+    // one launch: the matvec quantizes its activations itself (the same bits as the two launches below)
+    decode_matvec_quantize(t)(w.device_ptr(), (const float *)xs, ys, (int)k, (int)n, (int)k, (int)n, (int)rows, stream);
+    abi_check("QMatMul::forward (matvec)");
+  } else if (prefers_mmvq(t, rows)) {
     const int64_t kp = pad_to(k, act_block(t));
     void *vy = workspace().get(w.device().ordinal, (size_t)(rows * (kp / act_block(t)) * act_block_bytes(t)), stream);
     decode_quantizer(t, in_dtype)(xs, vy, (int)k, (int)kp, (int)rows, stream);

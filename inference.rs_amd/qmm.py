@@ -81,6 +81,7 @@ def _declare(L: ctypes.CDLL) -> None:
     for t in TYPE_NAME.values():
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+            getattr(L, f"launch_mmvq_gguf_{t}_{o}_quantize_plain").argtypes = [vp, vp, vp] + [i32] * 5 + [vp]
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_glu").argtypes = [vp, vp, vp, vp] + [i32] * 6 + [vp]
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
         getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
@@ -178,6 +179,20 @@ def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out
     oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
     getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_plain")(
         _ptr(w), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], stride_col_dst or n, b, _stream())
+    check()
+    return out
+
+
+def mmvq_quantize(wtype: int, w, x, n: int, out_dtype=None, out=None):
+    """Decode matvec from f32 activations x [b, k] (b <= 2, k <= 4096), quantized inside the launch:
+    launch_mmvq_gguf_<t>_<dtype>_quantize_plain."""
+    torch = _torch()
+    b, k = x.shape
+    if out is None:
+        out = torch.empty((b, n), dtype=out_dtype or torch.float32, device=w.device)
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_quantize_plain")(
+        _ptr(w), _ptr(x), _ptr(out), k, n, x.stride(0), out.stride(0), b, _stream())
     check()
     return out
 
