@@ -75,6 +75,66 @@ struct ActStage {
   }
 };
 
+// The same superblock loaded by DMA straight into an LDS slot (buffer loads with the LDS flag): no registers hold
+// it on the way, so the ring can be deep without spilling.  Wave w's lane l writes LDS byte 16 l (4 l for the
+// 4-byte sections) of each 1 KB (256 B) piece it loads; it fetches the global bytes that belong at that place of
+// the swizzled layout.  Every wave issues kLoads loads per superblock.  The compiler does not order LDS reads
+// after these writes: the tile loop waits for them with an explicit vmcnt before its barrier.
+template <int BMt, bool MIN>
+struct ActDma {
+  static constexpr int QS = BMt * 256;
+  static constexpr int BSB = MIN ? BMt * 32 : 0;
+  static constexpr int STAGE = QS + BSB + BMt * 4;
+  static constexpr int NQ = BMt / 16;            // 1 KB qs pieces per wave
+  static constexpr int NB = MIN ? BMt / 32 : 0;  // 256 B bsum pieces per wave
+  static constexpr int ND = BMt / 4;             // lanes of each wave that load one f32 scale
+  static constexpr int kLoads = NQ + NB + 1;
+  uint32_t oq[NQ], ob[NB > 0 ? NB : 1], od;
+
+  // per-lane byte offsets of row block m0 in superblock 0 (the superblock's part is added at issue, in the
+  // vector operand too, so the buffer range check covers the whole offset)
+  __device__ __forceinline__ void init(int wave, int lane, int64_t m0, int64_t rows, int64_t nsb) {
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+      const int L = 64 * (4 * i + wave) + lane, r = L >> 4, c = (L & 15) ^ (r & 15);
+      oq[i] = (uint32_t)((m0 + r) * 256 + 16 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      const int D = 64 * (4 * i + wave) + lane, r = D >> 3, k = D & 7;
+      ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * 32 + 4 * k);
+    }
+    od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 4);
+  }
+  __device__ __forceinline__ void issue(rsrc_t r, uint8_t *slot, int wave, int lane, uint32_t sb_rows) const {
+#pragma unroll
+    for (int i = 0; i < NQ; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (4 * i + wave)),
+                                               16, oq[i] + 256 * sb_rows, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (4 * i + wave)), 4, ob[i] + 32 * sb_rows, 0,
+          0, 0);
+    if (lane < ND)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void *)(slot + QS + BSB + 4 * ND * wave), 4, od + 4 * sb_rows, 0, 0,
+          0);
+  }
+};
+
+// Workgroup barrier for the DMA ring: first this wave's loads but the newest N have landed (they complete in
+// order) and its LDS reads have returned, then s_barrier.  No fence: the LDS is written only by DMA, which the
+// compiler does not track (its own fence would wait for every DMA in flight); the asm's memory clobber keeps
+// LDS reads from moving across.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
 // LDS-only workgroup barrier: orders LDS accesses (lgkmcnt) but leaves global loads in flight.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -93,7 +153,12 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
                                             const int32_t *__restrict__ dst_rows, bool accumulate) {
   constexpr int BMt = 32 * TM;
+  // Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a register
+  // ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
+  constexpr bool kDma = WT::kDma;
   typedef ActStage<BMt, WT::kMin> AS;
+  typedef ActDma<BMt, WT::kMin> AD;
+  static_assert(AS::STAGE == AD::STAGE, "one LDS layout");
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AS::STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
@@ -120,11 +185,22 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
   for (int t = 0; t < TM; t++) fa[t] = (v16f){};
 
-  AS st[3];
+  AS st[kDma ? 1 : 3];
+  AD dma;
+  if (kDma) dma.init(wave, lane, m0, rows, nsb);
   typename WT::Raw raw[3];
-  auto issue = [&](int64_t sb, AS &as, typename WT::Raw &rr) {
-    as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 32), (uint32_t)(sb * rows * 4));
-    WT::load(rw, wrow, (uint32_t)sb, g, rr);
+  // DMA first, then the weights (WT::kLoads 16-byte loads, which cannot merge): the explicit wait in step()
+  // counts on that order
+  auto issue = [&](int64_t sb, int u, AS &as, typename WT::Raw &rr) {
+    if constexpr (kDma) {
+      __builtin_amdgcn_sched_barrier(0);
+      dma.issue(ra, lds + u * AS::STAGE, wave, lane, (uint32_t)(sb * rows));
+      WT::load(rw, wrow, (uint32_t)sb, g, rr);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 32), (uint32_t)(sb * rows * 4));
+      WT::load(rw, wrow, (uint32_t)sb, g, rr);
+    }
   };
 
   // The A-fragment LDS reads run one sub-block ahead of the MFMAs that consume them, so LDS latency overlaps
@@ -177,21 +253,40 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     }
   };
 
+  // Every step issues the loads of s + 2 (past the end: the last superblock again, into a slot and registers
+  // that are never read), so each step starts with the same loads outstanding and the wait counts stay exact.
   auto step = [&](int64_t s, int u) {
     // u = (s - sb0) % 3 is a constant after unrolling: slot u, register sets u, u + 1, u + 2
-    lds_barrier();
-    if (s + 2 < sb1) issue(s + 2, st[(u + 2) % 3], raw[(u + 2) % 3]);
-    compute(lds + u * AS::STAGE, raw[u]);
-    if (s + 1 < sb1) st[(u + 1) % 3].store(lds + ((u + 1) % 3) * AS::STAGE);
+    if constexpr (kDma) {
+      // this wave's DMA into slot u (issued two steps ago) has landed once at most the loads issued after it are
+      // outstanding: the weights of s, then the DMA and weights of s + 1 (counted as if the weights came
+      // first, which can only wait longer)
+      __builtin_amdgcn_sched_barrier(0);
+      dma_barrier<AD::kLoads + WT::kLoads>();
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      lds_barrier();
+    }
+    const int64_t sn = s + 2 < sb1 ? s + 2 : sb1 - 1;
+    if constexpr (kDma) {
+      issue(sn, (u + 2) % 3, st[0], raw[(u + 2) % 3]);
+      if (s < sb1) compute(lds + u * AS::STAGE, raw[u]);  // (no memory loads inside: the load pattern is uniform)
+    } else {
+      issue(sn, (u + 2) % 3, st[(u + 2) % 3], raw[(u + 2) % 3]);
+      if (s < sb1) compute(lds + u * AS::STAGE, raw[u]);
+      st[(u + 1) % 3].store(lds + ((u + 1) % 3) * AS::STAGE);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // steps do not interleave: each one's registers die at its end
   };
 
-  issue(sb0, st[0], raw[0]);
-  if (sb0 + 1 < sb1) issue(sb0 + 1, st[1], raw[1]);
-  st[0].store(lds);
+  issue(sb0, 0, st[0], raw[0]);
+  issue(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1, st[kDma ? 0 : 1], raw[1]);
+  if constexpr (!kDma) st[0].store(lds);
+  // every step runs its barrier and loads; steps past sb1 (at most two) skip only the math
   for (int64_t sb = sb0; sb < sb1; sb += 3) {
     step(sb, 0);
-    if (sb + 1 < sb1) step(sb + 1, 1);
-    if (sb + 2 < sb1) step(sb + 2, 2);
+    step(sb + 1, 1);
+    step(sb + 2, 2);
   }
 
   if (n >= nrows_w) return;
@@ -264,7 +359,7 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
         dw[j] = f16_bits_to_f32(ld16(p));
         const uint8_t *q = p + 2 + 16 * g;
         const uint32_t off = (uint32_t)((uintptr_t)q & 3);
-        unit_q6k::ld16_off(q - off, off, wq[j]);
+        unit_q6k::realign(ld_a4(q - off), ld32(q - off + 16), off, wq[j]);
       } else {
         dw[j] = 0.0f;
         wq[j][0] = wq[j][1] = wq[j][2] = wq[j][3] = 0;
@@ -438,9 +533,13 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
   if (splits > 1)
     zero_rows((float *)d, ncols_y, nrows_x, ldd, nullptr, s);
   const dim3 grid((unsigned)(tiles * splits));
-  if (tm == 1) k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
-  else if (tm == 2) k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
-  else k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  if (tm == 1) {
+    k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  } else if (tm == 2) {
+    k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  } else if constexpr (kq_tm_max<WT>() >= 4) {  // (not instantiated where it cannot be chosen)
+    k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  }
 }
 
 template <class Out>

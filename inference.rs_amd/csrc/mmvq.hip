@@ -87,12 +87,15 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
 #pragma unroll
   for (int s = 0; s < S; s++)
     if (has(s)) U::load_w(vx + (int64_t)row * row_bytes, lane + 64 * s, w[s]);
+  // the next row's weights are requested before this row's math when they fit in 64 more registers; longer rows
+  // keep enough bytes in flight within one row
+  constexpr bool kNext = S * sizeof(typename U::W) <= 64 * 4;
   for (; row < nrows; row += tw) {
-    typename U::W wn[S];  // the next row's weights, in flight during this row's math
-    if (row + tw < nrows) {
+    typename U::W wn[kNext ? S : 1];
+    if (kNext && row + tw < nrows) {
 #pragma unroll
       for (int s = 0; s < S; s++)
-        if (has(s)) U::load_w(vx + (int64_t)(row + tw) * row_bytes, lane + 64 * s, wn[s]);
+        if (has(s)) U::load_w(vx + (int64_t)(row + tw) * row_bytes, lane + 64 * s, wn[kNext ? s : 0]);
     }
     float acc[NC];
 #pragma unroll
@@ -117,8 +120,14 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
       const float v = wave_sum_to_lane63(acc[j]);
       if (lane == 63) Out::store(dst, (int64_t)j * stride_col_dst + row, v);
     }
+    if (kNext) {
 #pragma unroll
-    for (int s = 0; s < S; s++) w[s] = wn[s];
+      for (int s = 0; s < S; s++) w[s] = wn[kNext ? s : 0];
+    } else if (row + tw < nrows) {
+#pragma unroll
+      for (int s = 0; s < S; s++)
+        if (has(s)) U::load_w(vx + (int64_t)(row + tw) * row_bytes, lane + 64 * s, w[s]);
+    }
   }
 }
 

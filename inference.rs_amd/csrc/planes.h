@@ -39,6 +39,8 @@ struct wq4k {
   static constexpr int kBytes = 144;
   static constexpr int kShift = 3;  // I1 = 8 * plane1 + plane2
   static constexpr bool kMin = true;
+  static constexpr bool kDma = true;  // prefill stages activations by DMA (see mmq.hip)
+  static constexpr int kLoads = 5;    // load() issues five 16-byte loads
   struct Raw {
     u32x4 hdr, q[4];
   };
@@ -50,19 +52,19 @@ struct wq4k {
     for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * c + 16 * g, 0, 0);
   }
   struct Prep {
-    uint32_t sh[8], sl[8];
     float d, dmin;
     v8h bmin;
   };
+  // 6-bit scale of sub-block j, get_scale_min_k4 (quantized/utils.rs:119-129); unpacked where it is used, so
+  // the eight scales are not all live at once
+  static __device__ __forceinline__ uint32_t scale(const Raw &r, int j) {
+    const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
+    auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+    return j < 4 ? byte(j) & 63 : (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
+  }
   static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
     const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
     auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-#pragma unroll
-    for (int j = 0; j < 8; j++) {  // 6-bit scales, get_scale_min_k4 (quantized/utils.rs:119-129)
-      const uint32_t sc = j < 4 ? byte(j) & 63 : (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
-      p.sh[j] = sc >> 3;
-      p.sl[j] = sc & 7;
-    }
     p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
     p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
     // B operand of the min-term MFMA: k = 8g + b <-> bsum16 index 8g + b <-> sub-block 4g + b / 2, whose 6-bit
@@ -76,8 +78,9 @@ struct wq4k {
     }
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
+    (void)p;
     const u32x4 q = r.q[j >> 1];
-    const uint32_t sh = p.sh[j], sl = p.sl[j];
+    const uint32_t sc = scale(r, j), sh = sc >> 3, sl = sc & 7;
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -94,19 +97,28 @@ struct wq6k {
   static constexpr int kBytes = 210;
   static constexpr int kShift = 6;  // I = 64 * wh + wl
   static constexpr bool kMin = false;
+  static constexpr bool kDma = false;
+  static constexpr int kLoads = 6;  // at least six loads (16-byte ones; the 4-byte ones may merge)
+  // 16 bytes at a 2-byte aligned offset, kept as the five dwords that cover them: realigned only when used, so a
+  // prefetch does not wait for its data at issue time
+  struct Chunk {
+    u32x4 v;
+    uint32_t e;
+  };
   struct Raw {
-    uint32_t ql[2][2][4], qh[2][4];
-    uint32_t sc[4];
+    Chunk ql[2][2], qh[2], sc;
+    uint32_t off;  // the block's byte offset within its first dword: 0 or 2
     uint32_t d;
   };
-  // 16 bytes at a4 + x + off (a4 dword aligned, off 0 or 2) from five dwords
-  static __device__ __forceinline__ void ld16(rsrc_t rs, uint32_t a4, uint32_t x, uint32_t off, uint32_t out[4]) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, a4 + x, 0, 0);
-    const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(rs, a4 + x + 16, 0, 0);
-    out[0] = align_bytes(v.y, v.x, off);
-    out[1] = align_bytes(v.z, v.y, off);
-    out[2] = align_bytes(v.w, v.z, off);
-    out[3] = align_bytes(e, v.w, off);
+  static __device__ __forceinline__ void ld16(rsrc_t rs, uint32_t a4, uint32_t x, Chunk &c) {
+    c.v = __builtin_amdgcn_raw_buffer_load_b128(rs, a4 + x, 0, 0);
+    c.e = __builtin_amdgcn_raw_buffer_load_b32(rs, a4 + x + 16, 0, 0);
+  }
+  static __device__ __forceinline__ void words(const Chunk &c, uint32_t off, uint32_t out[4]) {
+    out[0] = align_bytes(c.v.y, c.v.x, off);
+    out[1] = align_bytes(c.v.z, c.v.y, off);
+    out[2] = align_bytes(c.v.w, c.v.z, off);
+    out[3] = align_bytes(c.e, c.v.w, off);
   }
   // superblock sb of the row at byte offset `row` of the resource (210-byte blocks are 2-byte aligned)
   static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
@@ -114,10 +126,11 @@ struct wq6k {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
 #pragma unroll
-      for (int p = 0; p < 2; p++) ld16(rs, a4, 64 * h + 32 * p + 16 * g, off, r.ql[h][p]);
-      ld16(rs, a4, 128 + 32 * h + 16 * g, off, r.qh[h]);
+      for (int p = 0; p < 2; p++) ld16(rs, a4, 64 * h + 32 * p + 16 * g, r.ql[h][p]);
+      ld16(rs, a4, 128 + 32 * h + 16 * g, r.qh[h]);
     }
-    ld16(rs, a4, 192, off, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    ld16(rs, a4, 192, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    r.off = off;
     r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
   }
   struct Prep {
@@ -125,25 +138,35 @@ struct wq6k {
     float d;
     float dmin;  // unused: Q6_K has no min term
     v8h bmin;
+    uint32_t ql[2][2][4], qh[2][4];  // realigned
   };
   static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
+    uint32_t sc[4];
+    words(r.sc, r.off, sc);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       const int idx = 2 * j + g;  // scale of values 16 (2j + g) .. +16
-      p.sc[j] = (int)(int8_t)((r.sc[idx >> 2] >> (8 * (idx & 3))) & 0xff);
+      p.sc[j] = (int)(int8_t)((sc[idx >> 2] >> (8 * (idx & 3))) & 0xff);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+      for (int q = 0; q < 2; q++) words(r.ql[h][q], r.off, p.ql[h][q]);
+      words(r.qh[h], r.off, p.qh[h]);
     }
     p.d = f16_bits_to_f32(r.d);
     p.dmin = 0.0f;
     p.bmin = (v8h){};
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
+    (void)r;
     const int h = j >> 2, q = j & 3;
-    const uint32_t *ql = r.ql[h][q & 1];
+    const uint32_t *ql = p.ql[h][q & 1];
     const int nsh = (q >> 1) * 4;
     const s2 sc2 = {(short)p.sc[j], (short)p.sc[j]};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((r.qh[h][i] >> (2 * q)) & 0x03030303u) << 4);
+      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((p.qh[h][i] >> (2 * q)) & 0x03030303u) << 4);
       // bytes 0,2 and 1,3 in 16-bit lanes, minus 32, times the scale: w in [-4096, 4064]
       const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
       const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
@@ -242,44 +265,49 @@ struct wq6k16 {
   static constexpr int kBytes = 210;
   static constexpr int kShift = 6;
   static constexpr bool kMin = false;
+  // chunks kept unaligned until prepare(), as in wq6k
+  typedef wq6k::Chunk Chunk;
   struct Raw {
-    uint32_t ql[2][4], qh[2][4], sc[4];
+    Chunk ql[2], qh[2], sc;
+    uint32_t off;
     uint32_t d;
   };
   static __device__ __forceinline__ uint32_t act_offset(int t, int kg) { return 64 * t + 16 * kg; }
-  static __device__ __forceinline__ void ld16(rsrc_t rs, uint32_t a4, uint32_t x, uint32_t off, uint32_t out[4]) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, a4 + x, 0, 0);
-    const uint32_t e = __builtin_amdgcn_raw_buffer_load_b32(rs, a4 + x + 16, 0, 0);
-    out[0] = align_bytes(v.y, v.x, off);
-    out[1] = align_bytes(v.z, v.y, off);
-    out[2] = align_bytes(v.w, v.z, off);
-    out[3] = align_bytes(e, v.w, off);
-  }
   static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int kg, Raw &r) {
     const uint32_t o = row + sb * kBytes, off = o & 3, a4 = o - off;
 #pragma unroll
     for (int x = 0; x < 2; x++) {
-      ld16(rs, a4, 64 * x + 16 * kg, off, r.ql[x]);
-      ld16(rs, a4, 128 + 32 * x + 16 * (kg & 1), off, r.qh[x]);
+      wq6k::ld16(rs, a4, 64 * x + 16 * kg, r.ql[x]);
+      wq6k::ld16(rs, a4, 128 + 32 * x + 16 * (kg & 1), r.qh[x]);
     }
-    ld16(rs, a4, 192, off, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    wq6k::ld16(rs, a4, 192, r.sc);  // the fifth dword may end past the last row: it then reads as 0, unused
+    r.off = off;
     r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
   }
   struct Prep {
     int sc[4];
     float d, dmin;
     v4h bmin;
+    uint32_t ql[2][4], qh[2][4];  // realigned
   };
   static __device__ __forceinline__ void prepare(const Raw &r, int kg, Prep &p) {
+    uint32_t sc[4];
+    wq6k::words(r.sc, r.off, sc);
 #pragma unroll
     for (int t = 0; t < 4; t++)  // byte 4t + kg of the 16 scales = byte kg of dword t
-      p.sc[t] = (int)(int8_t)((r.sc[t] >> (8 * kg)) & 0xff);
+      p.sc[t] = (int)(int8_t)((sc[t] >> (8 * kg)) & 0xff);
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+      wq6k::words(r.ql[x], r.off, p.ql[x]);
+      wq6k::words(r.qh[x], r.off, p.qh[x]);
+    }
     p.d = f16_bits_to_f32(r.d);
     p.dmin = 0.0f;
     p.bmin = (v4h){};
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int t, v4i &b1, v4i &b2, int kg) {
-    const uint32_t *ql = r.ql[t >> 1], *qh = r.qh[t >> 1];
+    (void)r;
+    const uint32_t *ql = p.ql[t >> 1], *qh = p.qh[t >> 1];
     const int nsh = 4 * (t & 1), hsh = 4 * (t & 1) + 2 * (kg >> 1);
     const s2 sc2 = {(short)p.sc[t], (short)p.sc[t]};
 #pragma unroll

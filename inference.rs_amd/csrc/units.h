@@ -114,10 +114,14 @@ struct unit_q6k {
   static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 256 * 210; }
   static __host__ __device__ int units(int64_t k) { return (int)(k / 64); }
 
+  // Weight loads only fill registers; realignment and decoding happen in dot(), so a prefetched row does not
+  // wait for its data when it is requested.
   struct W {
-    uint32_t qa[4], qb[4], qh[4];
-    int sc[4];
-    float d;
+    u32x4 qa, qb, qh;      // the dwords covering 16 bytes at a 2-byte aligned address each
+    uint32_t ea, eb, eh;   // and the dword after each
+    uint32_t off;          // the unit's byte offset within those dwords: 0 or 2
+    uint32_t sc[4];        // 16-bit loads holding the four int8 scales
+    uint32_t d;            // f16 bits
   };
   struct A {
     uint32_t q[16];
@@ -125,10 +129,7 @@ struct unit_q6k {
     float d;
   };
 
-  // 16 bytes at p = a4 + off (a4 dword aligned, off 0 or 2): five dwords from a4, realigned
-  static __device__ __forceinline__ void ld16_off(const uint8_t *a4, uint32_t off, uint32_t out[4]) {
-    const u32x4 v = ld_a4(a4);
-    const uint32_t e = ld32(a4 + 16);
+  static __device__ __forceinline__ void realign(const u32x4 &v, uint32_t e, uint32_t off, uint32_t out[4]) {
     out[0] = align_bytes(v.y, v.x, off);
     out[1] = align_bytes(v.z, v.y, off);
     out[2] = align_bytes(v.w, v.z, off);
@@ -138,14 +139,17 @@ struct unit_q6k {
   static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
     const uint8_t *sb = row + (int64_t)(u >> 2) * 210;
     const int h = (u >> 1) & 1, p = u & 1;
-    const uint32_t off = (uint32_t)((uintptr_t)sb & 3);
-    const uint8_t *a4 = sb - off;
-    ld16_off(a4 + 64 * h + 16 * p, off, w.qa);
-    ld16_off(a4 + 64 * h + 32 + 16 * p, off, w.qb);
-    ld16_off(a4 + 128 + 32 * h + 16 * p, off, w.qh);
+    w.off = (uint32_t)((uintptr_t)sb & 3);
+    const uint8_t *a4 = sb - w.off;
+    w.qa = ld_a4(a4 + 64 * h + 16 * p);
+    w.ea = ld32(a4 + 64 * h + 16 * p + 16);
+    w.qb = ld_a4(a4 + 64 * h + 32 + 16 * p);
+    w.eb = ld32(a4 + 64 * h + 32 + 16 * p + 16);
+    w.qh = ld_a4(a4 + 128 + 32 * h + 16 * p);
+    w.eh = ld32(a4 + 128 + 32 * h + 16 * p + 16);
 #pragma unroll
-    for (int q = 0; q < 4; q++) w.sc[q] = (int)(int8_t)(ld16(sb + 192 + 8 * h + 2 * q) >> (8 * p));
-    w.d = f16_bits_to_f32(ld16(sb + 208));
+    for (int q = 0; q < 4; q++) w.sc[q] = ld16(sb + 192 + 8 * h + 2 * q);
+    w.d = ld16(sb + 208);
   }
 
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
@@ -166,21 +170,27 @@ struct unit_q6k {
     a.d = __builtin_bit_cast(float, ld32(p0));
   }
 
-  static __device__ __forceinline__ float dot(const W &w, const A &a, int) {
+  static __device__ __forceinline__ float dot(const W &w, const A &a, int u) {
+    uint32_t qa[4], qb[4], qh[4];
+    realign(w.qa, w.ea, w.off, qa);
+    realign(w.qb, w.eb, w.off, qb);
+    realign(w.qh, w.eh, w.off, qh);
+    const int p = u & 1;
     int isum = 0;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const uint32_t *src = (q & 1) ? w.qb : w.qa;
+      const uint32_t *src = (q & 1) ? qb : qa;
       const int nsh = (q >> 1) * 4;
       int s = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const uint32_t v = ((src[k] >> nsh) & 0x0f0f0f0fu) | (((w.qh[k] >> (2 * q)) & 0x03030303u) << 4);
+        const uint32_t v = ((src[k] >> nsh) & 0x0f0f0f0fu) | (((qh[k] >> (2 * q)) & 0x03030303u) << 4);
         s = sdot4((int)v, (int)a.q[4 * q + k], s);
       }
-      isum += w.sc[q] * (s - 32 * a.bs[q]);  // (q6 - 32) . q8 = q6 . q8 - 32 * bsum
+      const int sc = (int)(int8_t)(w.sc[q] >> (8 * p));
+      isum += sc * (s - 32 * a.bs[q]);  // (q6 - 32) . q8 = q6 . q8 - 32 * bsum
     }
-    return a.d * w.d * (float)isum;
+    return a.d * f16_bits_to_f32(w.d) * (float)isum;
   }
 };
 
@@ -194,14 +204,16 @@ struct unit_q8_0 {
   static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 32 * 34; }
   static __host__ __device__ int units(int64_t k) { return (int)(k / 64); }
 
-  struct W {
+  // activations: decoded at load (once per launch); weights: the 17 dwords of a block pair, decoded in dot()
+  struct A {
     uint32_t qa[8], qb[8];
     float da, db;
   };
-  typedef W A;
-
-  static __device__ __forceinline__ void load_pair(const uint8_t *p, W &w) {
+  struct W {
     uint32_t dw[17];
+  };
+
+  static __device__ __forceinline__ void load_raw(const uint8_t *p, uint32_t dw[17]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const u32x4 v = ld_a4(p + 16 * i);
@@ -211,18 +223,26 @@ struct unit_q8_0 {
       dw[4 * i + 3] = v.w;
     }
     dw[16] = ld32(p + 64);
-    w.da = f16_bits_to_f32(dw[0] & 0xffff);
+  }
+  static __device__ __forceinline__ void decode(const uint32_t dw[17], A &a) {
+    a.da = f16_bits_to_f32(dw[0] & 0xffff);
 #pragma unroll
-    for (int i = 0; i < 8; i++) w.qa[i] = align_bytes(dw[i + 1], dw[i], 2);
-    w.db = f16_bits_to_f32(dw[8] >> 16);
+    for (int i = 0; i < 8; i++) a.qa[i] = align_bytes(dw[i + 1], dw[i], 2);
+    a.db = f16_bits_to_f32(dw[8] >> 16);
 #pragma unroll
-    for (int i = 0; i < 8; i++) w.qb[i] = dw[9 + i];
+    for (int i = 0; i < 8; i++) a.qb[i] = dw[9 + i];
   }
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_pair(row + (int64_t)u * 68, w); }
-  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { load_pair(row + (int64_t)u * 68, a); }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_raw(row + (int64_t)u * 68, w.dw); }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    uint32_t dw[17];
+    load_raw(row + (int64_t)u * 68, dw);
+    decode(dw, a);
+  }
 
-  static __device__ __forceinline__ float dot(const W &w, const A &a, int) {
+  static __device__ __forceinline__ float dot(const W &wr, const A &a, int) {
+    A w;
+    decode(wr.dw, w);
     int sa = 0, sb = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -243,20 +263,32 @@ struct unit_q8_0_odd {
   static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 32 * 34; }
   static __host__ __device__ int units(int64_t k) { return (int)(k / 32); }
 
-  struct W {
+  struct A {
     uint32_t q[8];
     float d;
   };
-  typedef W A;
+  struct W {
+    uint32_t h[17];  // the block's 17 16-bit words (weights: decoded in dot())
+  };
 
-  static __device__ __forceinline__ void load_blk(const uint8_t *p, W &w) {
-    w.d = f16_bits_to_f32(ld16(p));
+  static __device__ __forceinline__ void load_raw(const uint8_t *p, uint32_t h[17]) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) w.q[i] = ld16(p + 2 + 4 * i) | (ld16(p + 4 + 4 * i) << 16);
+    for (int i = 0; i < 17; i++) h[i] = ld16(p + 2 * i);
   }
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_blk(row + (int64_t)u * 34, w); }
-  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { load_blk(row + (int64_t)u * 34, a); }
-  static __device__ __forceinline__ float dot(const W &w, const A &a, int) {
+  static __device__ __forceinline__ void decode(const uint32_t h[17], A &a) {
+    a.d = f16_bits_to_f32(h[0]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) a.q[i] = h[1 + 2 * i] | (h[2 + 2 * i] << 16);
+  }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_raw(row + (int64_t)u * 34, w.h); }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    uint32_t h[17];
+    load_raw(row + (int64_t)u * 34, h);
+    decode(h, a);
+  }
+  static __device__ __forceinline__ float dot(const W &wr, const A &a, int) {
+    A w;
+    decode(wr.h, w);
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) s = sdot4((int)w.q[i], (int)a.q[i], s);
