@@ -216,6 +216,33 @@ int launch_moe_weighted_reduce_flat_f16_input(const void *inputs, const float *t
 int launch_moe_weighted_reduce_flat_bf16_input(const void *inputs, const float *topk_weights, void *outputs,
                                                int num_tokens, int hidden, int topk, void *stream);
 
+/* ------------------------------------------------------------------ dequantization and the exact Q8_0 matvec
+ * launch_dequantize_<t>_{f32,f16,bf16}: y[0..n) = the values of n / block_size consecutive blocks at x, as f32 or
+ * rounded (nearest even) to f16 / bf16.  Replaces QCudaStorage::dequantize / dequantize_f16
+ * (quantized/cuda.rs:31-135, 283-334) and its kernels dequantize_block_<t>_{f32,f16}
+ * (inference-tensor-kernels/src/quantized.cu:440-608, 647-660), which the reference loads by name rather than
+ * through a C launcher; the f32 values are bit-identical to the CPU to_float (k_quants.rs:905-921, 2096-2123,
+ * 2649-2680).  n a multiple of the block size, y 16-byte aligned. */
+#define QMM_DECLARE_DEQUANTIZE(t)                                                                                \
+  void launch_dequantize_##t##_f32(const void *x, void *y, int64_t n, void *stream);                            \
+  void launch_dequantize_##t##_f16(const void *x, void *y, int64_t n, void *stream);                            \
+  void launch_dequantize_##t##_bf16(const void *x, void *y, int64_t n, void *stream);                           \
+  /* get_rows_<t> (quantized.cu:900-975; host quantized/cuda.rs:150-240): dst row r (ne00 f32 values) = row    \
+   * ids[r] of src0, whose rows are nb01 bytes apart; n_ids <= 65535 rows (the reference's grid.x) */           \
+  void launch_get_rows_##t(const void *src0, const uint32_t *ids, float *dst, int64_t ne00, int64_t nb01,       \
+                           int64_t n_ids, void *stream);
+QMM_DECLARE_DEQUANTIZE(q8_0)
+QMM_DECLARE_DEQUANTIZE(q4_k)
+QMM_DECLARE_DEQUANTIZE(q6_k)
+
+/* launch_mmvq_gguf_q8_0_{bf16,f32}_exact (gguf/ffi.rs:1001-1022; host fast_mmvq.rs:415-472; kernel
+ * mmvq_instance_q8_0.cu:15-146): dst[b][row] = sum_k d q_k x[b][k] with the activations x [b_size, ncols_x] left
+ * unquantized (bf16 or f32), f32 sums, output in the input's dtype; b_size 1..8. */
+void launch_mmvq_gguf_q8_0_f32_exact(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                                     int b_size, void *stream);
+void launch_mmvq_gguf_q8_0_bf16_exact(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                                      int b_size, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

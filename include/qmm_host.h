@@ -32,6 +32,9 @@ int qmm_qtensor_quantize(uint32_t dtype, const float *values, int64_t experts, i
 void qmm_qtensor_free(qmm_qtensor *t);
 const void *qmm_qtensor_device_ptr(const qmm_qtensor *t);
 int64_t qmm_qtensor_storage_bytes(const qmm_qtensor *t);
+/* QTensor::dequantize on the tensor's HIP device (quantized/cuda.rs:283-334): all its values into the device
+ * buffer `out` as out_dtype 0 f32, 1 f16 or 30 bf16, asynchronously on `stream`. */
+int qmm_qtensor_dequantize_device(const qmm_qtensor *t, void *out, uint32_t out_dtype, void *stream);
 
 /* QMatMul::forward: ys[rows, N] = xs[rows, K] . W^T; in_dtype 0 f32, 1 f16, 30 bf16 (xs and ys share it).
  * Decode matvec for rows <= 16, prefill matmul above (gguf/mod.rs:434-452). */

@@ -81,6 +81,10 @@ const void *qmm_qtensor_device_ptr(const qmm_qtensor *t) {
 
 int64_t qmm_qtensor_storage_bytes(const qmm_qtensor *t) { return (int64_t)t->t->storage_size_in_bytes(); }
 
+int qmm_qtensor_dequantize_device(const qmm_qtensor *t, void *out, uint32_t out_dtype, void *stream) {
+  return guarded([&] { t->t->dequantize_on_device(out, dtype_from_u32(out_dtype), (hipStream_t)stream); });
+}
+
 int qmm_qmatmul_forward(const qmm_qtensor *w, const void *xs, uint32_t in_dtype, int64_t rows, void *ys, void *stream) {
   return guarded([&] { QMatMul(w->t).forward(xs, dtype_from_u32(in_dtype), rows, ys, (hipStream_t)stream); });
 }

@@ -265,6 +265,21 @@ std::vector<float> QTensor::dequantize() const {
   return out;
 }
 
+void QTensor::dequantize_on_device(void *out, GgmlDType out_dtype, hipStream_t stream) const {
+  typedef void (*fn)(const void *, void *, int64_t, void *);
+  static const fn table[3][3] = {
+      {launch_dequantize_q8_0_f32, launch_dequantize_q8_0_f16, launch_dequantize_q8_0_bf16},
+      {launch_dequantize_q4_k_f32, launch_dequantize_q4_k_f16, launch_dequantize_q4_k_bf16},
+      {launch_dequantize_q6_k_f32, launch_dequantize_q6_k_f16, launch_dequantize_q6_k_bf16}};
+  const int ti = dtype_ == GgmlDType::Q8_0 ? 0 : dtype_ == GgmlDType::Q4K ? 1 : dtype_ == GgmlDType::Q6K ? 2 : -1;
+  const int oi = out_dtype == GgmlDType::F32 ? 0 : out_dtype == GgmlDType::F16 ? 1 : out_dtype == GgmlDType::BF16 ? 2 : -1;
+  if (ti < 0 || oi < 0)
+    throw Error(std::string("QTensor::dequantize_on_device: ") + dtype_name(dtype_) + " -> " + dtype_name(out_dtype));
+  hip_check(hipSetDevice(device().ordinal), "hipSetDevice");
+  table[ti][oi](device_ptr(), out, elem_count(), stream);
+  abi_check("QTensor::dequantize_on_device");
+}
+
 const void *QTensor::device_ptr() const {
   if (!dev_) throw Error("QTensor: not on a HIP device");
   return dev_->ptr();

@@ -87,6 +87,9 @@ class QTensor {
 
   std::vector<uint8_t> data() const;      // the packed bytes (downloaded from a device)
   std::vector<float> dequantize() const;  // on the host, f32
+  // QTensor::dequantize / dequantize_f16 on a HIP device (quantized/cuda.rs:283-334): the elem_count() values into
+  // the device buffer `out` as F32, F16 or BF16, asynchronously on `stream`
+  void dequantize_on_device(void *out, GgmlDType out_dtype, hipStream_t stream) const;
   const void *device_ptr() const;         // the device bytes (device_ptr_with_guard, mod.rs:474-480)
 
  private:

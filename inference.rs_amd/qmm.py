@@ -98,6 +98,12 @@ def _declare(L: ctypes.CDLL) -> None:
         if f is not None:
             f.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
     for t in TYPE_NAME.values():
+        for o in ("f32", "f16", "bf16"):
+            getattr(L, f"launch_dequantize_{t}_{o}").argtypes = [vp, vp, i64, vp]
+        getattr(L, f"launch_get_rows_{t}").argtypes = [vp, vp, vp, i64, i64, i64, vp]
+    for o in ("f32", "bf16"):
+        getattr(L, f"launch_mmvq_gguf_q8_0_{o}_exact").argtypes = [vp, vp, vp, i32, i32, i32, vp]
+    for t in TYPE_NAME.values():
         f = getattr(L, f"launch_mmq_gguf_{t}", None)
         if f is not None:
             f.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i64, i32, i32, vp]
@@ -342,3 +348,40 @@ def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n:
     check()
     return out
 
+
+
+# ------------------------------------------------------------------------------------------------ dequantization
+
+def dequantize(wtype: int, w, n: int, out_dtype=None, out=None):
+    """The n values of the blocks in w (a uint8 tensor) as f32 / f16 / bf16: launch_dequantize_<t>_<dtype>."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty(n, dtype=out_dtype or torch.float32, device=w.device)
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
+    getattr(lib(), f"launch_dequantize_{TYPE_NAME[wtype]}_{oname}")(_ptr(w), _ptr(out), n, _stream())
+    check()
+    return out
+
+
+def get_rows(wtype: int, w, ids, ne00: int, nb01: int, out=None):
+    """Embedding gather: out [len(ids), ne00] f32 = rows ids of the block matrix w (rows nb01 bytes apart)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((ids.numel(), ne00), dtype=torch.float32, device=w.device)
+    getattr(lib(), f"launch_get_rows_{TYPE_NAME[wtype]}")(_ptr(w), _ptr(ids), _ptr(out), ne00, nb01, ids.numel(),
+                                                          _stream())
+    check()
+    return out
+
+
+def q8_0_exact(w, x, n: int, out=None):
+    """x [b, k] (f32 or bf16, b <= 8) -> [b, n] in x's dtype against a Q8_0 weight, activations unquantized:
+    launch_mmvq_gguf_q8_0_<dtype>_exact."""
+    torch = _torch()
+    b, k = x.shape
+    if out is None:
+        out = torch.empty((b, n), dtype=x.dtype, device=x.device)
+    oname = {torch.float32: "f32", torch.bfloat16: "bf16"}[x.dtype]
+    getattr(lib(), f"launch_mmvq_gguf_q8_0_{oname}_exact")(_ptr(w), _ptr(x), _ptr(out), k, n, b, _stream())
+    check()
+    return out

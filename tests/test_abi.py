@@ -59,6 +59,15 @@ def test_bad_arguments_are_rejected_before_any_launch():
     rc = L.launch_moe_weighted_reduce_flat(None, None, None, 1, 1, 0, None)
     assert rc != 0 and "topk" in qmm.last_error()
     L.qmm_clear_error()
+    L.launch_dequantize_q4_k_f32(None, None, 300, None)
+    assert "multiple of 256" in qmm.last_error()
+    L.qmm_clear_error()
+    L.launch_get_rows_q8_0(None, None, None, 40, 34, 1, None)
+    assert "ne00" in qmm.last_error()
+    L.qmm_clear_error()
+    L.launch_mmvq_gguf_q8_0_f32_exact(None, None, None, 64, 4, 9, None)
+    assert "b_size" in qmm.last_error()
+    L.qmm_clear_error()
 
 
 def test_host_library_exports_its_header():
