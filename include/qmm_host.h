@@ -52,6 +52,40 @@ void qmm_moe_free(qmm_moe *m);
 int qmm_moe_forward(const qmm_moe *m, const float *xs, int64_t tokens, const int32_t *ids, const float *weights,
                     int64_t topk, float *out, void *stream, int force_grouped);
 
+/* ------------------------------------------------------------------ GGUF files
+ * The reader and writer of crates/inference-tensor/src/quantized/gguf_file.rs.  qmm_gguf_open runs Content::read
+ * (764-812), or Header::read_summary (603-608) when summary != 0, on the file at `path` and keeps it open for tensor
+ * and large-array reads.  Tensors are listed in the file's table order; dims are outermost first. */
+typedef struct qmm_gguf qmm_gguf;
+int qmm_gguf_open(const char *path, int summary, qmm_gguf **out);
+void qmm_gguf_close(qmm_gguf *g);
+int qmm_gguf_version(const qmm_gguf *g);
+uint64_t qmm_gguf_tensor_data_offset(const qmm_gguf *g);
+int64_t qmm_gguf_tensor_count(const qmm_gguf *g);
+int qmm_gguf_tensor_info(const qmm_gguf *g, int64_t idx, char *name, int64_t name_cap, uint32_t *ggml_dtype,
+                         int64_t *dims, int *n_dims, uint64_t *offset);
+/* metadata keys in sorted order; a value's type id 0..12 (gguf_file.rs:394-435), -1 absent, -2 a large array */
+int64_t qmm_gguf_metadata_count(const qmm_gguf *g);
+int qmm_gguf_metadata_key(const qmm_gguf *g, int64_t idx, char *key, int64_t cap);
+int qmm_gguf_metadata_type(const qmm_gguf *g, const char *key);
+/* Value::to_u64 (upcasts u8 / u16 / u32 / bool); signed integers; f32 or f64; strings (len = full length) */
+int qmm_gguf_metadata_u64(const qmm_gguf *g, const char *key, uint64_t *v);
+int qmm_gguf_metadata_i64(const qmm_gguf *g, const char *key, int64_t *v);
+int qmm_gguf_metadata_f64(const qmm_gguf *g, const char *key, double *v);
+int qmm_gguf_metadata_string(const qmm_gguf *g, const char *key, char *buf, int64_t cap, int64_t *len);
+int qmm_gguf_metadata_array(const qmm_gguf *g, const char *key, int64_t *len, int *elem_type);
+/* read_large_array (707-724): the raw bytes of elements [begin, end) of an array left in the file */
+int qmm_gguf_large_array(const qmm_gguf *g, const char *key, uint64_t begin, uint64_t end, void *out, int64_t cap);
+/* Content::tensor (800-811): the named tensor as a QTensor on the CPU (device_ordinal < 0) or a HIP device; a 1-D
+ * tensor becomes one row */
+int qmm_gguf_load_tensor(const qmm_gguf *g, const char *name, int device_ordinal, qmm_qtensor **out);
+/* peek_architecture (553-572): general.architecture when it is the first key, else "" */
+int qmm_gguf_peek_architecture(const char *path, char *buf, int64_t cap);
+/* write_header + write_tensor_data (826-865): version 2, kv_count entries already serialized as kv_bytes
+ * (metadata_bytes, 867-877), then the tensors in order, 32-byte aligned */
+int qmm_gguf_write(const char *path, uint64_t kv_count, const void *kv_bytes, int64_t kv_len, int64_t n_tensors,
+                   const char *const *names, const qmm_qtensor *const *tensors);
+
 #ifdef __cplusplus
 }
 #endif

@@ -215,8 +215,7 @@ std::shared_ptr<QTensor> QTensor::from_data(const void *bytes, size_t len, const
                                             GgmlDType dtype, Device device) {
   if (dims.size() < 2 || dims.size() > 3) throw Error("QTensor: dims must be [rows, cols] or [experts, rows, cols]");
   const size_t bs = block_size(dtype);
-  if (bs == 0 || dtype == GgmlDType::F32 || dtype == GgmlDType::F16 || dtype == GgmlDType::BF16)
-    throw Error(std::string("QTensor: ") + dtype_name(dtype) + " is not a block type");
+  if (bs == 0) throw Error(std::string("QTensor: ") + dtype_name(dtype) + " has no block size");
   for (int64_t d : dims)
     if (d <= 0) throw Error("QTensor: empty dimension");
   if (dims.back() % (int64_t)bs != 0)

@@ -385,3 +385,158 @@ def q8_0_exact(w, x, n: int, out=None):
     getattr(lib(), f"launch_mmvq_gguf_q8_0_{oname}_exact")(_ptr(w), _ptr(x), _ptr(out), k, n, b, _stream())
     check()
     return out
+
+
+# ------------------------------------------------------------------------------------------------ GGUF files (host)
+
+_host = None
+
+
+def host() -> ctypes.CDLL:
+    """Load libinferencequant_host.so (the QTensor / QMatMul / GGUF host layer, include/qmm_host.h)."""
+    global _host
+    if _host is None:
+        if not os.path.exists(HOST_LIB_PATH):
+            raise QmmError(f"{HOST_LIB_PATH} is missing: run `make -C {HERE}`")
+        H = ctypes.CDLL(HOST_LIB_PATH)
+        vp, i32, i64, u32, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64
+        cp = ctypes.c_char_p
+        H.qmm_host_last_error.restype = cp
+        H.qmm_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
+        H.qmm_gguf_close.argtypes = [vp]
+        H.qmm_gguf_version.argtypes = [vp]
+        H.qmm_gguf_tensor_data_offset.argtypes = [vp]
+        H.qmm_gguf_tensor_data_offset.restype = u64
+        H.qmm_gguf_tensor_count.argtypes = [vp]
+        H.qmm_gguf_tensor_count.restype = i64
+        H.qmm_gguf_tensor_info.argtypes = [vp, i64, cp, i64, ctypes.POINTER(u32), ctypes.POINTER(i64),
+                                           ctypes.POINTER(i32), ctypes.POINTER(u64)]
+        H.qmm_gguf_metadata_count.argtypes = [vp]
+        H.qmm_gguf_metadata_count.restype = i64
+        H.qmm_gguf_metadata_key.argtypes = [vp, i64, cp, i64]
+        H.qmm_gguf_metadata_type.argtypes = [vp, cp]
+        H.qmm_gguf_metadata_u64.argtypes = [vp, cp, ctypes.POINTER(u64)]
+        H.qmm_gguf_metadata_i64.argtypes = [vp, cp, ctypes.POINTER(i64)]
+        H.qmm_gguf_metadata_f64.argtypes = [vp, cp, ctypes.POINTER(ctypes.c_double)]
+        H.qmm_gguf_metadata_string.argtypes = [vp, cp, cp, i64, ctypes.POINTER(i64)]
+        H.qmm_gguf_metadata_array.argtypes = [vp, cp, ctypes.POINTER(i64), ctypes.POINTER(i32)]
+        H.qmm_gguf_large_array.argtypes = [vp, cp, u64, u64, vp, i64]
+        H.qmm_gguf_load_tensor.argtypes = [vp, cp, i32, ctypes.POINTER(vp)]
+        H.qmm_gguf_peek_architecture.argtypes = [cp, cp, i64]
+        H.qmm_gguf_write.argtypes = [cp, u64, vp, i64, i64, ctypes.POINTER(cp), ctypes.POINTER(vp)]
+        H.qmm_qtensor_from_data.argtypes = [u32, vp, i64, i64, i64, i64, i32, ctypes.POINTER(vp)]
+        H.qmm_qtensor_free.argtypes = [vp]
+        H.qmm_qtensor_device_ptr.argtypes = [vp]
+        H.qmm_qtensor_device_ptr.restype = vp
+        H.qmm_qtensor_storage_bytes.argtypes = [vp]
+        H.qmm_qtensor_storage_bytes.restype = i64
+        H.qmm_qmatmul_forward.argtypes = [vp, vp, u32, i64, vp, vp]
+        _host = H
+    return _host
+
+
+def _host_check(rc: int) -> None:
+    if rc != 0:
+        raise QmmError(host().qmm_host_last_error().decode())
+
+
+class GgufFile:
+    """A GGUF file read by the host layer's Content::read (qmm_gguf_open); tensors load into QTensor handles."""
+
+    def __init__(self, path: str, summary: bool = False):
+        H = host()
+        self._h = ctypes.c_void_p()
+        _host_check(H.qmm_gguf_open(path.encode(), int(summary), ctypes.byref(self._h)))
+
+    def close(self) -> None:
+        if self._h:
+            host().qmm_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return host().qmm_gguf_version(self._h)
+
+    @property
+    def tensor_data_offset(self) -> int:
+        return host().qmm_gguf_tensor_data_offset(self._h)
+
+    def tensors(self) -> list:
+        """[(name, ggml type id, dims outermost first, offset)] in the file's table order."""
+        H = host()
+        out = []
+        for i in range(H.qmm_gguf_tensor_count(self._h)):
+            name = ctypes.create_string_buffer(4096)
+            dt, nd, off = ctypes.c_uint32(), ctypes.c_int(), ctypes.c_uint64()
+            dims = (ctypes.c_int64 * 8)()
+            _host_check(H.qmm_gguf_tensor_info(self._h, i, name, 4096, ctypes.byref(dt), dims, ctypes.byref(nd),
+                                               ctypes.byref(off)))
+            out.append((name.value.decode(), dt.value, [dims[d] for d in range(nd.value)], off.value))
+        return out
+
+    def keys(self) -> list:
+        H = host()
+        out = []
+        for i in range(H.qmm_gguf_metadata_count(self._h)):
+            b = ctypes.create_string_buffer(4096)
+            _host_check(H.qmm_gguf_metadata_key(self._h, i, b, 4096))
+            out.append(b.value.decode())
+        return out
+
+    def value_type(self, key: str) -> int:
+        return host().qmm_gguf_metadata_type(self._h, key.encode())
+
+    def u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _host_check(host().qmm_gguf_metadata_u64(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def i64(self, key: str) -> int:
+        v = ctypes.c_int64()
+        _host_check(host().qmm_gguf_metadata_i64(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def f64(self, key: str) -> float:
+        v = ctypes.c_double()
+        _host_check(host().qmm_gguf_metadata_f64(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def string(self, key: str) -> str:
+        n = ctypes.c_int64()
+        _host_check(host().qmm_gguf_metadata_string(self._h, key.encode(), None, 0, ctypes.byref(n)))
+        b = ctypes.create_string_buffer(n.value + 1)
+        _host_check(host().qmm_gguf_metadata_string(self._h, key.encode(), b, n.value + 1, ctypes.byref(n)))
+        return b.raw[:n.value].decode("utf-8", "replace")
+
+    def array(self, key: str):
+        n, t = ctypes.c_int64(), ctypes.c_int()
+        _host_check(host().qmm_gguf_metadata_array(self._h, key.encode(), ctypes.byref(n), ctypes.byref(t)))
+        return n.value, t.value
+
+    def large_array(self, key: str, begin: int, end: int, elem_size: int) -> bytes:
+        buf = ctypes.create_string_buffer(max(1, (end - begin) * elem_size))
+        _host_check(host().qmm_gguf_large_array(self._h, key.encode(), begin, end, buf, len(buf)))
+        return buf.raw[:(end - begin) * elem_size]
+
+    def load_tensor(self, name: str, device_ordinal: int = -1) -> ctypes.c_void_p:
+        """A qmm_qtensor handle (free with host().qmm_qtensor_free) on the CPU or HIP device device_ordinal."""
+        t = ctypes.c_void_p()
+        _host_check(host().qmm_gguf_load_tensor(self._h, name.encode(), device_ordinal, ctypes.byref(t)))
+        return t
+
+
+def gguf_write(path: str, kv_count: int, kv_bytes: bytes, tensors: list) -> None:
+    """qmm_gguf_write: tensors = [(name, qmm_qtensor handle)], the metadata already serialized."""
+    names = (ctypes.c_char_p * max(1, len(tensors)))(*[n.encode() for n, _ in tensors])
+    handles = (ctypes.c_void_p * max(1, len(tensors)))(*[h.value if hasattr(h, "value") else h for _, h in tensors])
+    kv = ctypes.create_string_buffer(kv_bytes, max(1, len(kv_bytes)))
+    _host_check(host().qmm_gguf_write(path.encode(), kv_count, kv, len(kv_bytes), len(tensors), names, handles))
