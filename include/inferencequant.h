@@ -29,6 +29,7 @@
 #ifndef INFERENCEQUANT_H
 #define INFERENCEQUANT_H
 
+#include <stdbool.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -242,6 +243,26 @@ void launch_mmvq_gguf_q8_0_f32_exact(const void *vx, const void *vy, void *dst, 
                                      int b_size, void *stream);
 void launch_mmvq_gguf_q8_0_bf16_exact(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
                                       int b_size, void *stream);
+
+/* ------------------------------------------------------------------ MoE router
+ * moe_router_topk_{f32,bf16,f16} (crates/inference-nn/src/cuda/ffi.rs:1137-1190; kernel
+ * crates/inference-nn/kernels/cuda/sort.cu:1374-1725): logits [n_rows, n_experts] -> weights [n_rows, top_k] f32 and
+ * ids [n_rows, top_k] u32.  score_mode 0 raw, 1 softmax, 2 sigmoid; selection = score + selection_bias (nullable),
+ * ties to the lower expert; weight_mode 0 the score, 1 a softmax over the picked raw logits, 2 their sigmoid;
+ * renormalize divides by max(sum, norm_min); weights are then scaled by output_scale * expert_scale[id] (nullable).
+ * n_experts 1..1024, top_k 1..n_experts.  The stream is a hipStream_t passed as an integer, as the reference's. */
+void moe_router_topk_f32(const float *logits, float *weights, uint32_t *ids, const float *selection_bias,
+                         const float *expert_scale, int n_rows, int n_experts, int top_k, int score_mode,
+                         int weight_mode, bool renormalize, bool clamp_logits, float clamp_min, float clamp_max,
+                         float norm_min, float output_scale, int64_t stream);
+void moe_router_topk_bf16(const void *logits, float *weights, uint32_t *ids, const float *selection_bias,
+                          const float *expert_scale, int n_rows, int n_experts, int top_k, int score_mode,
+                          int weight_mode, bool renormalize, bool clamp_logits, float clamp_min, float clamp_max,
+                          float norm_min, float output_scale, int64_t stream);
+void moe_router_topk_f16(const void *logits, float *weights, uint32_t *ids, const float *selection_bias,
+                         const float *expert_scale, int n_rows, int n_experts, int top_k, int score_mode,
+                         int weight_mode, bool renormalize, bool clamp_logits, float clamp_min, float clamp_max,
+                         float norm_min, float output_scale, int64_t stream);
 
 #ifdef __cplusplus
 }

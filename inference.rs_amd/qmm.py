@@ -53,7 +53,7 @@ def declared_symbols(header: str | None = None) -> list[str]:
         out = subprocess.run(["gcc", "-E", "-P", "-x", "c", "-I", os.path.join(REPO, "include"), h],
                              check=True, capture_output=True, text=True).stdout
         own = out[out.find("extern") if "extern" in out else 0:]
-        for m in re.finditer(r"\b((?:launch|qmm|inference)_\w+)\s*(?:\(|\[)", own):
+        for m in re.finditer(r"\b((?:launch|qmm|inference|moe_router)_\w+)\s*(?:\(|\[)", own):
             if m.group(1) not in names:
                 names.append(m.group(1))
     return names
@@ -372,6 +372,24 @@ def get_rows(wtype: int, w, ids, ne00: int, nb01: int, out=None):
                                                           _stream())
     check()
     return out
+
+
+def router_topk(logits, top_k: int, score_mode: int = 1, weight_mode: int = 0, renormalize: bool = True,
+                bias=None, expert_scale=None, clamp=None, norm_min: float = 0.0, output_scale: float = 1.0):
+    """moe_router_topk_<dtype>: logits [rows, experts] (f32 / bf16 / f16) -> (weights f32, ids int32) [rows, k]."""
+    torch = _torch()
+    rows, n = logits.shape
+    w = torch.empty((rows, top_k), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((rows, top_k), dtype=torch.int32, device=logits.device)
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[logits.dtype]
+    f = getattr(lib(), f"moe_router_topk_{name}")
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 5 + [ctypes.c_bool] * 2 + [ctypes.c_float] * 4 + \
+        [ctypes.c_int64]
+    lo, hi = clamp if clamp is not None else (0.0, 0.0)
+    f(_ptr(logits), _ptr(w), _ptr(ids), _ptr(bias), _ptr(expert_scale), rows, n, top_k, score_mode, weight_mode,
+      renormalize, clamp is not None, lo, hi, norm_min, output_scale, _torch().cuda.current_stream().cuda_stream)
+    check()
+    return w, ids
 
 
 def q8_0_exact(w, x, n: int, out=None):

@@ -169,3 +169,56 @@ def moe_weighted_reduce(inp: np.ndarray, weights: np.ndarray) -> np.ndarray:
     out = np.zeros((tokens, hidden), dtype=np.float32)
     lib().oracle_moe_weighted_reduce(_p(inp), _p(weights), _p(out), tokens, hidden, topk)
     return out
+
+
+def router_topk(logits: np.ndarray, top_k: int, score_mode: int, weight_mode: int, renormalize: bool,
+                bias: np.ndarray | None = None, expert_scale: np.ndarray | None = None, clamp=None,
+                norm_min: float = 0.0, output_scale: float = 1.0):
+    """The MoE router (crates/inference-nn/kernels/cuda/sort.cu:1455-1610, the same steps as the op of
+    crates/inference-nn/src/ops/moe_router.rs:50-79), per row in float32:
+    raw = logit (clamped; NaN -> -inf); score = raw / softmax(raw) / sigmoid(raw) (1490-1494);
+    selection = score + bias (NaN -> -inf, 1496-1508); top_k rounds of the largest selection, ties to the lower
+    expert (1510-1574); weight = score / raw then a softmax over the picks / sigmoid(raw) (1558-1580);
+    renormalize by max(sum, norm_min) (1582-1596); times output_scale * expert_scale[id] (1598-1608).
+    Returns (weights [rows, top_k] f32, ids [rows, top_k] u32)."""
+    f = np.float32
+    lg = np.asarray(logits, dtype=f)
+    rows, n = lg.shape
+    W = np.zeros((rows, top_k), f)
+    I = np.zeros((rows, top_k), np.uint32)
+    for r in range(rows):
+        raw = lg[r].copy()
+        if clamp is not None:
+            raw = np.fmin(np.fmax(raw, f(clamp[0])), f(clamp[1]))  # fmaxf / fminf: a NaN yields the bound
+        raw[np.isnan(raw)] = -np.inf
+        with np.errstate(over="ignore", invalid="ignore"):
+            if score_mode == 1:
+                e = np.exp(raw - raw.max(), dtype=f)
+                score = e * (f(1) / e.sum(dtype=f))
+            elif score_mode == 2:
+                score = f(1) / (f(1) + np.exp(-raw, dtype=f))
+            else:
+                score = raw.copy()
+        sel = score + bias.astype(f) if bias is not None else score.copy()
+        sel[np.isnan(sel)] = -np.inf
+        picks = []
+        for _ in range(top_k):
+            best = max(range(n), key=lambda e: (sel[e], -e))
+            picks.append(best)
+            sel[best] = -np.inf
+        if weight_mode == 1:
+            w = np.array([raw[e] for e in picks], f)
+            w = np.exp(w - w.max(), dtype=f)
+            w = w * (f(1) / w.sum(dtype=f))
+        elif weight_mode == 2:
+            w = np.array([f(1) / (f(1) + np.exp(-raw[e], dtype=f)) for e in picks], f)
+        else:
+            w = np.array([score[e] for e in picks], f)
+        if renormalize:
+            w = w * (f(1) / max(w.sum(dtype=f), f(norm_min)))
+        sc = np.full(top_k, f(output_scale), f)
+        if expert_scale is not None:
+            sc = sc * np.asarray(expert_scale, f)[picks]
+        W[r] = w * sc
+        I[r] = picks
+    return W, I

@@ -360,3 +360,50 @@ def test_moe_dispatch_and_reduce():
     inp2[3, 1] = 0
     want = (inp2.astype(np.float64) * wts[:, :, None]).sum(axis=1)
     np.testing.assert_allclose(out, want, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------- MoE router oracle
+
+def test_router_oracle_softmax_top2_closed_form():
+    # Mixtral's convention: softmax over the experts, the two largest, renormalised to sum to one
+    logits = np.array([[0.5, 2.0, -1.0, 1.0, 2.0]], np.float32)  # a tie at 2.0: expert 1 before expert 4
+    w, ids = O.router_topk(logits, 2, 1, 0, True)
+    assert ids.tolist() == [[1, 4]]
+    assert np.allclose(w, [[0.5, 0.5]], rtol=1e-6)
+    w, ids = O.router_topk(logits, 3, 1, 0, False)
+    p = np.exp(logits[0] - logits[0].max())
+    p /= p.sum()
+    assert ids.tolist() == [[1, 4, 3]] and np.allclose(w[0], p[[1, 4, 3]], rtol=1e-6)
+
+
+def test_router_oracle_matches_a_stable_argsort_and_the_weight_modes():
+    rng = np.random.default_rng(11)
+    logits = rng.standard_normal((20, 64)).astype(np.float32)
+    bias = rng.standard_normal(64).astype(np.float32)
+    for score_mode in (0, 1, 2):
+        w, ids = O.router_topk(logits, 6, score_mode, 0, False, bias=bias)
+        x = logits.astype(np.float64)
+        score = {0: x, 1: np.exp(x - x.max(1, keepdims=True)) / np.exp(x - x.max(1, keepdims=True)).sum(1, keepdims=True),
+                 2: 1 / (1 + np.exp(-x))}[score_mode]
+        want_ids = np.argsort(-(score + bias), axis=1, kind="stable")[:, :6]
+        assert np.array_equal(ids, want_ids)
+        # the bias only selects: the weights are the unbiased scores
+        assert np.allclose(w, np.take_along_axis(score, want_ids, 1), rtol=2e-6, atol=1e-7)
+    w, ids = O.router_topk(logits, 4, 0, 1, False)  # weight mode 1: a softmax over the picked raw logits
+    r = np.take_along_axis(logits.astype(np.float64), ids.astype(np.int64), 1)
+    assert np.allclose(w, np.exp(r - r.max(1, keepdims=True)) / np.exp(r - r.max(1, keepdims=True)).sum(1, keepdims=True),
+                       rtol=2e-6)
+    w2, _ = O.router_topk(logits, 4, 0, 2, True, expert_scale=np.full(64, 2.0, np.float32), output_scale=0.5)
+    s = 1 / (1 + np.exp(-r))
+    assert np.allclose(w2, s / s.sum(1, keepdims=True), rtol=2e-6)  # 0.5 * 2.0 = 1
+
+
+def test_router_oracle_nan_and_clamp():
+    logits = np.array([[np.nan, 1.0, 3.0, 2.0]], np.float32)
+    _, ids = O.router_topk(logits, 3, 0, 0, False)
+    assert ids.tolist() == [[2, 3, 1]]  # NaN is -inf: picked last
+    w, ids = O.router_topk(logits, 3, 0, 0, False, clamp=(0.5, 1.5))
+    # 3 and 2 clamp to 1.5 (ties to the lower index); the clamp takes NaN to its lower bound, as fmaxf does
+    assert ids.tolist() == [[2, 3, 1]] and w.tolist() == [[1.5, 1.5, 1.0]]
+    _, ids = O.router_topk(logits, 4, 0, 0, False, clamp=(1.25, 1.5))
+    assert ids.tolist() == [[2, 3, 0, 1]]  # NaN -> 1.25, 1.0 -> 1.25: a tie, the lower index first
