@@ -75,6 +75,14 @@ void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx
 QMM_DECLARE_MMVQ_PLAIN(q8_0)
 QMM_DECLARE_MMVQ_PLAIN(q4_k)
 QMM_DECLARE_MMVQ_PLAIN(q6_k)
+/* The adjacent GGUF types on the same decode kernels (gguf/ffi.rs:1158-1169 gguf_standard_types q4_0, q5_0, q5_k;
+ * 1265-1267 gguf_iq_types iq4_xs; host fast_mmvq.rs:40-81, 214-298).  Activations: Q8_0 blocks for q4_0 / q5_0
+ * (their CPU VecDotType), Q8_K blocks for q5_k and iq4_xs (k_quants.rs:2145-2232, cpu_dot.rs:416-440).  Weight
+ * pointers: 16-byte aligned for q5_k, 4-byte for iq4_xs, 2-byte for q4_0 / q5_0. */
+QMM_DECLARE_MMVQ_PLAIN(q4_0)
+QMM_DECLARE_MMVQ_PLAIN(q5_0)
+QMM_DECLARE_MMVQ_PLAIN(q5_k)
+QMM_DECLARE_MMVQ_PLAIN(iq4_xs)
 
 /* ------------------------------------------------------------------ decode matvec with its own quantization
  * launch_mmvq_gguf_<t>_{bf16,f16,f32}_quantize_plain: no counterpart in the reference, whose decode makes two
@@ -235,6 +243,16 @@ int launch_moe_weighted_reduce_flat_bf16_input(const void *inputs, const float *
 QMM_DECLARE_DEQUANTIZE(q8_0)
 QMM_DECLARE_DEQUANTIZE(q4_k)
 QMM_DECLARE_DEQUANTIZE(q6_k)
+QMM_DECLARE_DEQUANTIZE(q4_0)
+QMM_DECLARE_DEQUANTIZE(q5_0)
+QMM_DECLARE_DEQUANTIZE(q5_k)
+
+/* launch_dequantize_iq4_xs_{f32,f16,bf16} with the reference's own signature (gguf/ffi.rs:1125-1150, 1265-1267;
+ * kernel mmvq_gguf.cuh:2128-2141, 2167-2174): the nrows * ncols values of contiguous IQ4_XS rows (ncols a multiple
+ * of 256), value = (d * (ls - 32)) * kvalues_iq4nl[q] in f32, rounded to the output type. */
+void launch_dequantize_iq4_xs_f32(const void *vx, void *dst, int64_t nrows, int64_t ncols, void *stream);
+void launch_dequantize_iq4_xs_f16(const void *vx, void *dst, int64_t nrows, int64_t ncols, void *stream);
+void launch_dequantize_iq4_xs_bf16(const void *vx, void *dst, int64_t nrows, int64_t ncols, void *stream);
 
 /* launch_mmvq_gguf_q8_0_{bf16,f32}_exact (gguf/ffi.rs:1001-1022; host fast_mmvq.rs:415-472; kernel
  * mmvq_instance_q8_0.cu:15-146): dst[b][row] = sum_k d q_k x[b][k] with the activations x [b_size, ncols_x] left

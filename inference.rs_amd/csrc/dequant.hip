@@ -8,7 +8,9 @@
 //                                          fast_mmvq.rs:415-472, mmvq_instance_q8_0.cu:15-146)
 //
 // Every value is produced by the same f32 operations, in the same order, as the reference CPU to_float
-// (k_quants.rs:905-921, 2096-2123, 2649-2680): Q8_0 q * d; Q4_K (d * sc) * q - dmin * m; Q6_K (d * sc) * (q - 32).
+// (k_quants.rs:905-921, 2096-2123, 2649-2680, 313-330, 720-743, 2433-2467; raw.rs:794-808): Q8_0 q * d;
+// Q4_K (d * sc) * q - dmin * m; Q6_K (d * sc) * (q - 32); Q4_0 / Q5_0 (q - off) * d; Q5_K as Q4_K with the fifth
+// bit; IQ4_XS (d * (ls - 32)) * table[q].
 // This file is compiled with -ffp-contract=off, so the f32 results are bit-identical to the CPU's, and the f16 / bf16
 // outputs are those f32 values rounded to nearest even.  HBM-bound: a thread decodes 8 consecutive values and writes
 // them with one or two 16-byte stores.
@@ -67,6 +69,80 @@ struct deq_q6k {
     for (int j = 0; j < 8; j++) {
       const int q = ((ql[j] >> lsh) & 0xf) | (((qh[j] >> hsh) & 3) << 4);
       out[j] = ds * (float)(q - 32);
+    }
+  }
+};
+
+struct deq_q4_0 {
+  static constexpr int kBytes = 18, kValues = 32;
+  static __device__ __forceinline__ void chunk(const uint8_t *b, int c, float out[8]) {
+    const float d = f16_bits_to_f32(ld16(b));
+    const uint8_t *q = b + 2 + 8 * (c & 1);
+    const int sh = c >= 2 ? 4 : 0;  // values 16..31 are the high nibbles
+#pragma unroll
+    for (int j = 0; j < 8; j++) out[j] = (float)((int)((q[j] >> sh) & 0xf) - 8) * d;
+  }
+};
+
+struct deq_q5_0 {
+  static constexpr int kBytes = 22, kValues = 32;
+  static __device__ __forceinline__ void chunk(const uint8_t *b, int c, float out[8]) {
+    const float d = f16_bits_to_f32(ld16(b));
+    const uint32_t qh = ld16(b + 2) | (ld16(b + 4) << 16);  // bit v = fifth bit of value v
+    const uint8_t *q = b + 6 + 8 * (c & 1);
+    const int sh = c >= 2 ? 4 : 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int v = ((q[j] >> sh) & 0xf) | (((qh >> (8 * c + j)) & 1) << 4);
+      out[j] = (float)(v - 16) * d;
+    }
+  }
+};
+
+struct deq_q5k {
+  static constexpr int kBytes = 176, kValues = 256;
+  static __device__ __forceinline__ void chunk(const uint8_t *b, int c, float out[8]) {
+    const int g = c >> 3, v = 8 * (c & 7);
+    const int is = 2 * g + (v >= 32);
+    const uint8_t *sc = b + 4;
+    int s, m;
+    if (is < 4) {
+      s = sc[is] & 63;
+      m = sc[is + 4] & 63;
+    } else {
+      s = (sc[is + 4] & 0xf) | ((sc[is - 4] >> 6) << 4);
+      m = (sc[is + 4] >> 4) | ((sc[is] >> 6) << 4);
+    }
+    const float d = f16_bits_to_f32(ld16(b)), dmin = f16_bits_to_f32(ld16(b + 2));
+    const float d1 = d * (float)s, m1 = dmin * (float)m;
+    const uint8_t *qh = b + 16 + (v & 31), *q = b + 48 + 32 * g + (v & 31);
+    const int sh = v >= 32 ? 4 : 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      // (q & 0xf) + 16 * bit in f32 is exact, as the reference's (ql & 0xF) as f32 + to_add
+      const int qv = ((q[j] >> sh) & 0xf) + 16 * ((qh[j] >> is) & 1);
+      out[j] = d1 * (float)qv - m1;
+    }
+  }
+};
+
+// IQ4_XS (raw.rs:794-808 and the reference kernel dequantize_iq4_xs, mmvq_gguf.cuh:2128-2141): value =
+// (d * (ls - 32)) * table[index]
+struct deq_iq4xs {
+  static constexpr int kBytes = 136, kValues = 256;
+  static __device__ __forceinline__ void chunk(const uint8_t *b, int c, float out[8]) {
+    const int ib = c >> 2, part = c & 3;
+    const uint32_t sh = ld16(b + 2), sl = b[4 + ib / 2];
+    const int ls = (int)(((sl >> (4 * (ib & 1))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+    const float scale = f16_bits_to_f32(ld16(b)) * (float)(ls - 32);
+    const uint8_t *q = b + 8 + 16 * ib + 8 * (part & 1);
+    const uint32_t lo = ld16(q) | (ld16(q + 2) << 16), hi = ld16(q + 4) | (ld16(q + 6) << 16);
+    const int nsh = part >= 2 ? 4 : 0;
+    const uint32_t v0 = unit_iq4xs::lookup((lo >> nsh) & 0x0f0f0f0fu), v1 = unit_iq4xs::lookup((hi >> nsh) & 0x0f0f0f0fu);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      out[j] = scale * (float)(int8_t)(v0 >> (8 * j));
+      out[4 + j] = scale * (float)(int8_t)(v1 >> (8 * j));
     }
   }
 };
@@ -283,7 +359,25 @@ extern "C" {
 QMM_DEFINE_DEQ(q8_0, deq_q8_0)
 QMM_DEFINE_DEQ(q4_k, deq_q4k)
 QMM_DEFINE_DEQ(q6_k, deq_q6k)
+QMM_DEFINE_DEQ(q4_0, deq_q4_0)
+QMM_DEFINE_DEQ(q5_0, deq_q5_0)
+QMM_DEFINE_DEQ(q5_k, deq_q5k)
 #undef QMM_DEFINE_DEQ
+
+// IQ4_XS keeps the reference's (nrows, ncols) form of launch_dequantize_iq4_xs_<dt> (gguf/ffi.rs:1125-1150, 1265-1267;
+// mmvq_gguf.cuh:2167-2174): nrows * ncols contiguous values
+#define QMM_DEFINE_DEQ_IQ(t, D, dt, OUT)                                                                           \
+  void launch_dequantize_##t##_##dt(const void *vx, void *dst, int64_t nrows, int64_t ncols, void *stream) {     \
+    if (nrows < 0 || ncols < 0 || (nrows > 0 && ncols > INT64_MAX / nrows)) {                                    \
+      qmm_set_error("dequantize_" #t "_" #dt ": nrows=%lld ncols=%lld", (long long)nrows, (long long)ncols);     \
+      return;                                                                                                      \
+    }                                                                                                              \
+    dequantize<D, OUT>(vx, dst, nrows * ncols, stream, "dequantize_" #t "_" #dt);                                 \
+  }
+QMM_DEFINE_DEQ_IQ(iq4_xs, deq_iq4xs, f32, out_f32)
+QMM_DEFINE_DEQ_IQ(iq4_xs, deq_iq4xs, f16, out_f16)
+QMM_DEFINE_DEQ_IQ(iq4_xs, deq_iq4xs, bf16, out_bf16)
+#undef QMM_DEFINE_DEQ_IQ
 
 void launch_mmvq_gguf_q8_0_f32_exact(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int b_size,
                                      void *stream) {

@@ -1,4 +1,5 @@
-// Decode matvec for GGUF Q8_0 / Q4_K / Q6_K weights against Q8_0 / Q8_K activations (b = 1..16 rows),
+// Decode matvec for GGUF Q8_0 / Q4_K / Q6_K weights (and Q4_0 / Q5_0 / Q5_K / IQ4_XS) against Q8_0 / Q8_K
+// activations (b = 1..16 rows),
 // plus the expert-indexed MoE matvec (optionally fused gate/up with the GLU activation).
 //
 // Replaces mmvq_gguf.cuh:650-759 (mmvq_core_impl) and its launchers (1542-1553, 1647-1702, 1762-1834),
@@ -372,9 +373,19 @@ void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int
 
 // Shape checks shared by the plain and MoE launchers. Returns false (and records why) when the
 // arguments cannot be served.
+// Byte alignment the decode units need of a weight pointer: 16-byte loads for Q4_K / Q5_K, dword loads for IQ4_XS,
+// 16-bit loads (or realigned dwords) for the rest.
+uintptr_t weight_align(int type) {
+  switch (type) {
+    case QMM_TYPE_Q4K: case QMM_TYPE_Q5K: return 16;
+    case QMM_TYPE_IQ4_XS: return 4;
+    default: return 2;
+  }
+}
+
 bool check_mmvq(const char *who, int type, const void *vx, int ncols_x, int nrows_x, int stride_col_y, int b) {
   const int bs = (int)qmm_block_size(type);
-  const int abs_ = type == QMM_TYPE_Q8_0 ? 32 : 256;
+  const int abs_ = (int)qmm_block_size(qmm_vec_dot_type(type));
   if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0) {
     qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x, bs);
     return false;
@@ -387,7 +398,7 @@ bool check_mmvq(const char *who, int type, const void *vx, int ncols_x, int nrow
     qmm_set_error("%s: b_size=%d outside 1..16", who, b);
     return false;
   }
-  const uintptr_t align = type == QMM_TYPE_Q4K ? 16 : (type == QMM_TYPE_Q8_0 ? 2 : 2);
+  const uintptr_t align = weight_align(type);
   if ((uintptr_t)vx % align != 0) {
     qmm_set_error("%s: weight pointer not %zu-byte aligned", who, (size_t)align);
     return false;
@@ -414,6 +425,26 @@ void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int
     case QMM_TYPE_Q6K:
       launch_cols<unit_q6k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
       break;
+    case QMM_TYPE_Q5K:
+      launch_cols<unit_q5k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
+      break;
+    case QMM_TYPE_IQ4_XS:
+      launch_cols<unit_iq4xs, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
+      break;
+    case QMM_TYPE_Q4_0:
+    case QMM_TYPE_Q5_0: {
+      // block pairs as dwords when every pair starts dword aligned, else one block per unit
+      const bool pairs = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0;
+      const int64_t ay = (int64_t)stride_col_y * 34;
+      if (type == QMM_TYPE_Q4_0) {
+        if (pairs) launch_cols<unit_b32<QMM_TYPE_Q4_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+        else launch_cols<unit_b32_odd<QMM_TYPE_Q4_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+      } else {
+        if (pairs) launch_cols<unit_b32<QMM_TYPE_Q5_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+        else launch_cols<unit_b32_odd<QMM_TYPE_Q5_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+      }
+      break;
+    }
     default:  // Q8_0
       if (ncols_x % 64 == 0 && stride_col_y % 2 == 0 && (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0)
         launch_cols<unit_q8_0, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 34, stride_col_dst, b, s);
@@ -587,6 +618,23 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
 
 }  // namespace
 
+#define QMM_DEFINE_PLAIN_ONLY(t, TYPE)                                                                            \
+  void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
+    plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
+                   "mmvq_" #t "_f32");                                                                            \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
+                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
+    plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
+                   "mmvq_" #t "_f16");                                                                            \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,   \
+                                         int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
+    plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
+                    "mmvq_" #t "_bf16");                                                                          \
+  }
+
 #define QMM_DEFINE_PLAIN(t, TYPE)                                                                                 \
   void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
                                         int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
@@ -633,6 +681,10 @@ extern "C" {
 QMM_DEFINE_PLAIN(q8_0, QMM_TYPE_Q8_0)
 QMM_DEFINE_PLAIN(q4_k, QMM_TYPE_Q4K)
 QMM_DEFINE_PLAIN(q6_k, QMM_TYPE_Q6K)
+QMM_DEFINE_PLAIN_ONLY(q4_0, QMM_TYPE_Q4_0)
+QMM_DEFINE_PLAIN_ONLY(q5_0, QMM_TYPE_Q5_0)
+QMM_DEFINE_PLAIN_ONLY(q5_k, QMM_TYPE_Q5K)
+QMM_DEFINE_PLAIN_ONLY(iq4_xs, QMM_TYPE_IQ4_XS)
 
 void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
                                           float *all_outputs, int n, int k, int batch, int topk, int k_padded,

@@ -10,6 +10,11 @@
 //         d; activations with the four matching bsums.           (k_quants.rs:2518-2575)
 //   Q8_0  unit = two consecutive 34 B blocks (68 B, dword aligned when a row holds an even number of blocks)
 //         against two Q8_0 activation blocks.                    (k_quants.rs:982-999)
+//   Q4_0 / Q5_0  unit = a pair of 18 / 22 B blocks against two Q8_0 blocks (one block when rows hold an odd
+//         number).                                               (k_quants.rs:432-449, 615-637)
+//   Q5_K  unit = Q4_K's quarter super-block plus the 32 fifth-bit bytes.  (k_quants.rs:2145-2232)
+//   IQ4_XS unit = two 32-value sub-blocks: 8 B header + 32 B of table indices.
+//                                                   (inference-quant/src/gguf/cpu_dot.rs:416-440)
 #pragma once
 
 #include "common.h"
@@ -293,5 +298,279 @@ struct unit_q8_0_odd {
 #pragma unroll
     for (int i = 0; i < 8; i++) s = sdot4((int)w.q[i], (int)a.q[i], s);
     return (float)s * w.d * a.d;
+  }
+};
+
+// ------------------------------------------------------------------------------------------------ Q4_0 / Q5_0
+// The 32-value types with an offset (Q4_0: q - 8, k_quants.rs:432-449; Q5_0: q - 16, k_quants.rs:615-637) against
+// Q8_0 activation blocks.  A block's integer dot is sum(q * a) - off * sum(a): the nibbles (and fifth bits) are
+// dotted as unsigned bytes and the activation block's sum, taken once when the activation unit is loaded, removes
+// the offset.  Scaling per block as the reference: (float)sumi * d_w * d_a.
+
+// bits 0..3 of h moved to bit 4 of bytes 0..3
+__device__ __forceinline__ uint32_t spread4_bit4(uint32_t h) { return ((h * 0x00204081u) & 0x01010101u) << 4; }
+
+// sum(q * a) over one block: qs = the 16 nibble bytes as 4 dwords, qh = Q5_0's fifth bits (unused for Q4_0)
+template <int T>
+__device__ __forceinline__ int dot_b32(const uint32_t qs[4], uint32_t qh, const uint32_t a[8]) {
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    uint32_t lo = qs[k] & 0x0f0f0f0fu, hi = (qs[k] >> 4) & 0x0f0f0f0fu;
+    if (T == QMM_TYPE_Q5_0) {
+      lo |= spread4_bit4((qh >> (4 * k)) & 15u);
+      hi |= spread4_bit4((qh >> (16 + 4 * k)) & 15u);
+    }
+    s = sdot4((int)lo, (int)a[k], s);
+    s = sdot4((int)hi, (int)a[4 + k], s);
+  }
+  return s;
+}
+
+template <int T>
+struct fmt_b32 {
+  static constexpr int kOff = T == QMM_TYPE_Q5_0 ? 16 : 8;
+  static constexpr int kBytes = T == QMM_TYPE_Q5_0 ? 22 : 18;
+  static constexpr int kPairDwords = kBytes / 2;  // two blocks: 36 or 44 bytes
+};
+
+// Rows of an even number of blocks starting dword aligned: a unit is a block pair (64 values), read as dwords.
+template <int T>
+struct unit_b32 {
+  using F = fmt_b32<T>;
+  static constexpr int kType = T;
+  static constexpr int kValuesPerUnit = 64;
+  static constexpr int kActBlockBytes = 34;
+  static constexpr int kActBlockValues = 32;
+  static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 32 * F::kBytes; }
+  static __host__ __device__ int units(int64_t k) { return (int)(k / 64); }
+
+  struct A {
+    uint32_t qa[8], qb[8];
+    float da, db;
+    int sa, sb;  // sums of the two blocks' values
+  };
+  struct W {
+    uint32_t dw[F::kPairDwords];
+  };
+
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
+    const uint8_t *p = row + (int64_t)u * (2 * F::kBytes);
+#pragma unroll
+    for (int i = 0; i + 4 <= F::kPairDwords; i += 4) {
+      const u32x4 v = ld_a4(p + 4 * i);
+      w.dw[i] = v.x;
+      w.dw[i + 1] = v.y;
+      w.dw[i + 2] = v.z;
+      w.dw[i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = F::kPairDwords / 4 * 4; i < F::kPairDwords; i++) w.dw[i] = ld32(p + 4 * i);
+  }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    typename unit_q8_0::A q;
+    unit_q8_0::load_a(row, u, q);
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      a.qa[i] = q.qa[i];
+      a.qb[i] = q.qb[i];
+      sa = sdot4((int)q.qa[i], 0x01010101, sa);
+      sb = sdot4((int)q.qb[i], 0x01010101, sb);
+    }
+    a.da = q.da;
+    a.db = q.db;
+    a.sa = sa;
+    a.sb = sb;
+  }
+
+  static __device__ __forceinline__ float dot(const W &w, const A &a, int) {
+    uint32_t q0[4], q1[4], h0 = 0, h1 = 0;
+    float d0, d1;
+    if (T == QMM_TYPE_Q5_0) {
+      // block 0: d bytes 0-1, qh 2-5, qs 6-21; block 1: d 22-23, qh 24-27, qs 28-43
+      d0 = f16_bits_to_f32(w.dw[0] & 0xffff);
+      h0 = align_bytes(w.dw[1], w.dw[0], 2);
+#pragma unroll
+      for (int i = 0; i < 4; i++) q0[i] = align_bytes(w.dw[i + 2], w.dw[i + 1], 2);
+      d1 = f16_bits_to_f32(w.dw[5] >> 16);
+      h1 = w.dw[6];
+#pragma unroll
+      for (int i = 0; i < 4; i++) q1[i] = w.dw[7 + i];
+    } else {
+      // block 0: d bytes 0-1, qs 2-17; block 1: d 18-19, qs 20-35
+      d0 = f16_bits_to_f32(w.dw[0] & 0xffff);
+#pragma unroll
+      for (int i = 0; i < 4; i++) q0[i] = align_bytes(w.dw[i + 1], w.dw[i], 2);
+      d1 = f16_bits_to_f32(w.dw[4] >> 16);
+#pragma unroll
+      for (int i = 0; i < 4; i++) q1[i] = w.dw[5 + i];
+    }
+    const int s0 = dot_b32<T>(q0, h0, a.qa) - F::kOff * a.sa;
+    const int s1 = dot_b32<T>(q1, h1, a.qb) - F::kOff * a.sb;
+    return (float)s0 * d0 * a.da + (float)s1 * d1 * a.db;
+  }
+};
+
+// Any other row: one block per unit, read as 16-bit words (blocks are 2-byte aligned).
+template <int T>
+struct unit_b32_odd {
+  using F = fmt_b32<T>;
+  static constexpr int kType = T;
+  static constexpr int kValuesPerUnit = 32;
+  static constexpr int kActBlockBytes = 34;
+  static constexpr int kActBlockValues = 32;
+  static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 32 * F::kBytes; }
+  static __host__ __device__ int units(int64_t k) { return (int)(k / 32); }
+
+  struct A {
+    uint32_t q[8];
+    float d;
+    int s;
+  };
+  struct W {
+    uint32_t h[F::kBytes / 2];
+  };
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
+    const uint8_t *p = row + (int64_t)u * F::kBytes;
+#pragma unroll
+    for (int i = 0; i < F::kBytes / 2; i++) w.h[i] = ld16(p + 2 * i);
+  }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    typename unit_q8_0_odd::A q;
+    unit_q8_0_odd::load_a(row, u, q);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      a.q[i] = q.q[i];
+      s = sdot4((int)q.q[i], 0x01010101, s);
+    }
+    a.d = q.d;
+    a.s = s;
+  }
+  static __device__ __forceinline__ float dot(const W &w, const A &a, int) {
+    constexpr int o = T == QMM_TYPE_Q5_0 ? 3 : 1;  // first 16-bit word of qs
+    uint32_t qs[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) qs[i] = w.h[o + 2 * i] | (w.h[o + 2 * i + 1] << 16);
+    const uint32_t qh = T == QMM_TYPE_Q5_0 ? (w.h[1] | (w.h[2] << 16)) : 0u;
+    const int s = dot_b32<T>(qs, qh, a.q) - F::kOff * a.s;
+    return (float)s * f16_bits_to_f32(w.h[0]) * a.d;
+  }
+};
+
+// ------------------------------------------------------------------------------------------------ Q5_K
+// unit = a quarter super-block as for Q4_K (sub-blocks 2c, 2c+1) plus the 32 qh bytes, whose bits 2c and 2c + 1 are
+// the two sub-blocks' fifth bits (k_quants.rs:2145-2232).  Super-blocks are 176 bytes, so 16-byte aligned rows stay
+// aligned.
+struct unit_q5k {
+  static constexpr int kType = QMM_TYPE_Q5K;
+  static constexpr int kValuesPerUnit = 64;
+  static constexpr int kActBlockBytes = 292;
+  static constexpr int kActBlockValues = 256;
+  static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 256 * 176; }
+  static __host__ __device__ int units(int64_t k) { return (int)(k / 64); }
+
+  struct W {
+    u32x4 hdr, h0, h1, q0, q1;
+  };
+  using A = unit_q4k::A;
+
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * 176;
+    const int c = u & 3;
+    w.hdr = ld_a16(p);
+    w.h0 = ld_a16(p + 16);
+    w.h1 = ld_a16(p + 32);
+    w.q0 = ld_a16(p + 48 + 32 * c);
+    w.q1 = ld_a16(p + 64 + 32 * c);
+  }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k::load_a(row, u, a); }
+
+  static __device__ __forceinline__ float dot(const W &w, const A &a, int u) {
+    const int c = u & 3;
+    int sc0, sc1, m0, m1;
+    unit_q4k::W hw;
+    hw.hdr = w.hdr;
+    unit_q4k::scales(hw, c, sc0, sc1, m0, m1);
+    const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    const uint32_t hb[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t lo = (qw[k] & 0x0f0f0f0fu) | (((hb[k] >> (2 * c)) & 0x01010101u) << 4);
+      const uint32_t hi = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hb[k] >> (2 * c + 1)) & 0x01010101u) << 4);
+      s0 = sdot4((int)lo, (int)a.q[k], s0);
+      s1 = sdot4((int)hi, (int)a.q[8 + k], s1);
+    }
+    const int i1 = sc0 * s0 + sc1 * s1;
+    const int i2 = m0 * a.b0 + m1 * a.b1;
+    const float d = f16_bits_to_f32(w.hdr.x & 0xffff), dmin = f16_bits_to_f32(w.hdr.x >> 16);
+    return a.d * (d * (float)i1 - dmin * (float)i2);
+  }
+};
+
+// ------------------------------------------------------------------------------------------------ IQ4_XS
+// unit = sub-blocks 2c, 2c+1 of a 136-byte super-block: the 8-byte header and 32 bytes of table indices
+// (crates/inference-quant/src/gguf/cpu_dot.rs:416-440).  Four indices at a time become table values with two
+// byte permutes (entries 0-7 and 8-15) and a bitwise select on bit 3.
+struct unit_iq4xs {
+  static constexpr int kType = QMM_TYPE_IQ4_XS;
+  static constexpr int kValuesPerUnit = 64;
+  static constexpr int kActBlockBytes = 292;
+  static constexpr int kActBlockValues = 256;
+  static __host__ __device__ int64_t row_bytes(int64_t k) { return k / 256 * 136; }
+  static __host__ __device__ int units(int64_t k) { return (int)(k / 64); }
+
+  struct W {
+    uint32_t h0, h1;  // d | scales_h << 16, scales_l
+    u32x4 q0, q1;
+  };
+  using A = unit_q4k::A;
+
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * 136;
+    const int c = u & 3;
+    w.h0 = ld32(p);
+    w.h1 = ld32(p + 4);
+    w.q0 = ld_a4(p + 8 + 32 * c);
+    w.q1 = ld_a4(p + 24 + 32 * c);
+  }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k::load_a(row, u, a); }
+
+  // the IQ4_NL table (raw.rs:13-15) as int8 bytes: entries 0-3, 4-7, 8-11, 12-15
+  static constexpr uint32_t kT0 = 0xBFAD9881u, kT1 = 0xF6EADDCFu, kT2 = 0x26190D01u, kT3 = 0x71594535u;
+
+  // four 4-bit indices (one per byte) -> their table values
+  static __device__ __forceinline__ uint32_t lookup(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kT1, kT0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kT3, kT2, sel);
+    // byte selector 4 picks byte 0 of the first operand (0xff), selector 12 gives 0x00
+    const uint32_t mask = __builtin_amdgcn_perm(0xffffffffu, 0u, (n & 0x08080808u) ^ 0x0c0c0c0cu);
+    return (hi & mask) | (lo & ~mask);
+  }
+
+  static __device__ __forceinline__ float dot(const W &w, const A &a, int u) {
+    const int c = u & 3;
+    const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    int s[2] = {0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t q = qw[4 * h + k];
+        s[h] = sdot4((int)lookup(q & 0x0f0f0f0fu), (int)a.q[8 * h + k], s[h]);
+        s[h] = sdot4((int)lookup((q >> 4) & 0x0f0f0f0fu), (int)a.q[8 * h + 4 + k], s[h]);
+      }
+    int ls[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int ib = 2 * c + h;
+      ls[h] = (int)(((w.h1 >> (4 * ib)) & 15u) | (((w.h0 >> (16 + 2 * ib)) & 3u) << 4)) - 32;
+    }
+    // d = d_w * d_a, then d * (ls * sumi) per sub-block (cpu_dot.rs:426, 437)
+    const float d = f16_bits_to_f32(w.h0 & 0xffff) * a.d;
+    return d * (float)(ls[0] * s[0]) + d * (float)(ls[1] * s[1]);
   }
 };

@@ -76,7 +76,7 @@ typedef void (*indexed_fn)(const void *, const void *, const uint32_t *, float *
                            void *);
 
 quant_fn decode_quantizer(GgmlDType w, GgmlDType in) {
-  const bool k = w != GgmlDType::Q8_0;
+  const bool k = qmm_vec_dot_type((int)w) == QMM_TYPE_Q8K;
   switch (in) {
     case GgmlDType::F32: return k ? launch_mmvq_gguf_quantize_q8k_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
     case GgmlDType::F16: return k ? launch_mmvq_gguf_quantize_q8k_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
@@ -96,6 +96,12 @@ mmvq_q_fn decode_matvec_quantize(GgmlDType w) {
   }
 }
 
+// the weight types with kernels: every route (full) or the matvec route and dequantization only
+bool has_all_routes(GgmlDType t) { return t == GgmlDType::Q8_0 || t == GgmlDType::Q4K || t == GgmlDType::Q6K; }
+bool has_matvec(GgmlDType t) {
+  return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0 || t == GgmlDType::Q5K;
+}
+
 mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
 #define QMM_PICK(t)                                                              \
   switch (out) {                                                                 \
@@ -108,6 +114,9 @@ mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
     case GgmlDType::Q8_0: QMM_PICK(q8_0)
     case GgmlDType::Q4K: QMM_PICK(q4_k)
     case GgmlDType::Q6K: QMM_PICK(q6_k)
+    case GgmlDType::Q4_0: QMM_PICK(q4_0)
+    case GgmlDType::Q5_0: QMM_PICK(q5_0)
+    case GgmlDType::Q5K: QMM_PICK(q5_k)
     default: throw Error("QMatMul: unsupported weight type");
   }
 #undef QMM_PICK
@@ -150,14 +159,16 @@ indexed_fn indexed_moe(GgmlDType w) {
 }
 
 // activation block geometry of a weight type (GgmlType::VecDotType)
-int64_t act_block(GgmlDType w) { return w == GgmlDType::Q8_0 ? 32 : 256; }
-int64_t act_block_bytes(GgmlDType w) { return w == GgmlDType::Q8_0 ? 34 : 292; }
+bool act_q8_0(GgmlDType w) { return qmm_vec_dot_type((int)w) == QMM_TYPE_Q8_0; }
+int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
+int64_t act_block_bytes(GgmlDType w) { return act_q8_0(w) ? 34 : 292; }
 int64_t tile_bytes_per_256(GgmlDType w) { return w == GgmlDType::Q8_0 ? 272 : 292; }
 
-void check_weight(const QTensor &w, const char *who) {
+// matvec_only: the route needs the decode matvec alone (QMatMul::forward); else every route
+void check_weight(const QTensor &w, const char *who, bool matvec_only = false) {
   if (!w.device().is_hip()) throw Error(std::string(who) + ": the weight is not on a HIP device");
   const GgmlDType t = w.dtype();
-  if (t != GgmlDType::Q8_0 && t != GgmlDType::Q4K && t != GgmlDType::Q6K)
+  if (!(matvec_only ? has_matvec(t) : has_all_routes(t)))
     throw Error(std::string(who) + ": weight type " + dtype_name(t) + " has no kernels here");
 }
 
@@ -169,8 +180,16 @@ GgmlDType dtype_from_u32(uint32_t u) {
   switch (u) {
     case 0: return GgmlDType::F32;
     case 1: return GgmlDType::F16;
+    case 2: return GgmlDType::Q4_0;
+    case 3: return GgmlDType::Q4_1;
+    case 6: return GgmlDType::Q5_0;
+    case 7: return GgmlDType::Q5_1;
     case 8: return GgmlDType::Q8_0;
+    case 9: return GgmlDType::Q8_1;
+    case 10: return GgmlDType::Q2K;
+    case 11: return GgmlDType::Q3K;
     case 12: return GgmlDType::Q4K;
+    case 13: return GgmlDType::Q5K;
     case 14: return GgmlDType::Q6K;
     case 15: return GgmlDType::Q8K;
     case 30: return GgmlDType::BF16;
@@ -185,8 +204,16 @@ const char *dtype_name(GgmlDType t) {
   switch (t) {
     case GgmlDType::F32: return "F32";
     case GgmlDType::F16: return "F16";
+    case GgmlDType::Q4_0: return "Q4_0";
+    case GgmlDType::Q4_1: return "Q4_1";
+    case GgmlDType::Q5_0: return "Q5_0";
+    case GgmlDType::Q5_1: return "Q5_1";
     case GgmlDType::Q8_0: return "Q8_0";
+    case GgmlDType::Q8_1: return "Q8_1";
+    case GgmlDType::Q2K: return "Q2K";
+    case GgmlDType::Q3K: return "Q3K";
     case GgmlDType::Q4K: return "Q4K";
+    case GgmlDType::Q5K: return "Q5K";
     case GgmlDType::Q6K: return "Q6K";
     case GgmlDType::Q8K: return "Q8K";
     case GgmlDType::BF16: return "BF16";
@@ -266,11 +293,23 @@ std::vector<float> QTensor::dequantize() const {
 
 void QTensor::dequantize_on_device(void *out, GgmlDType out_dtype, hipStream_t stream) const {
   typedef void (*fn)(const void *, void *, int64_t, void *);
-  static const fn table[3][3] = {
+  static const fn table[6][3] = {
       {launch_dequantize_q8_0_f32, launch_dequantize_q8_0_f16, launch_dequantize_q8_0_bf16},
       {launch_dequantize_q4_k_f32, launch_dequantize_q4_k_f16, launch_dequantize_q4_k_bf16},
-      {launch_dequantize_q6_k_f32, launch_dequantize_q6_k_f16, launch_dequantize_q6_k_bf16}};
-  const int ti = dtype_ == GgmlDType::Q8_0 ? 0 : dtype_ == GgmlDType::Q4K ? 1 : dtype_ == GgmlDType::Q6K ? 2 : -1;
+      {launch_dequantize_q6_k_f32, launch_dequantize_q6_k_f16, launch_dequantize_q6_k_bf16},
+      {launch_dequantize_q4_0_f32, launch_dequantize_q4_0_f16, launch_dequantize_q4_0_bf16},
+      {launch_dequantize_q5_0_f32, launch_dequantize_q5_0_f16, launch_dequantize_q5_0_bf16},
+      {launch_dequantize_q5_k_f32, launch_dequantize_q5_k_f16, launch_dequantize_q5_k_bf16}};
+  int ti = -1;
+  switch (dtype_) {
+    case GgmlDType::Q8_0: ti = 0; break;
+    case GgmlDType::Q4K: ti = 1; break;
+    case GgmlDType::Q6K: ti = 2; break;
+    case GgmlDType::Q4_0: ti = 3; break;
+    case GgmlDType::Q5_0: ti = 4; break;
+    case GgmlDType::Q5K: ti = 5; break;
+    default: break;
+  }
   const int oi = out_dtype == GgmlDType::F32 ? 0 : out_dtype == GgmlDType::F16 ? 1 : out_dtype == GgmlDType::BF16 ? 2 : -1;
   if (ti < 0 || oi < 0)
     throw Error(std::string("QTensor::dequantize_on_device: ") + dtype_name(dtype_) + " -> " + dtype_name(out_dtype));
@@ -294,7 +333,7 @@ bool QMatMul::prefers_mmvq(GgmlDType, int64_t rows) { return rows <= kMaxDecodeR
 
 void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys, hipStream_t stream) const {
   const QTensor &w = *w_;
-  check_weight(w, "QMatMul::forward");
+  check_weight(w, "QMatMul::forward", true);
   if (w.shape().size() != 2) throw Error("QMatMul::forward: the weight must be 2-D");
   if (in_dtype != GgmlDType::F32 && in_dtype != GgmlDType::F16 && in_dtype != GgmlDType::BF16)
     throw Error("QMatMul::forward: activations must be F32, F16 or BF16");
@@ -303,19 +342,25 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
   const int64_t k = w.cols(), n = w.rows();
   const GgmlDType t = w.dtype();
   hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
-  if (prefers_mmvq(t, rows) && in_dtype == GgmlDType::F32 && rows <= 2 && k <= 4096 &&
+  if (has_all_routes(t) && prefers_mmvq(t, rows) && in_dtype == GgmlDType::F32 && rows <= 2 && k <= 4096 &&
       (t != GgmlDType::Q8_0 || k % 64 == 0) && (uintptr_t)xs % 4 == 0) {
     // one launch: the matvec quantizes its activations itself (the same bits as the two launches below)
     decode_matvec_quantize(t)(w.device_ptr(), (const float *)xs, ys, (int)k, (int)n, (int)k, (int)n, (int)rows, stream);
     abi_check("QMatMul::forward (matvec)");
-  } else if (prefers_mmvq(t, rows)) {
+  } else if (prefers_mmvq(t, rows) || !has_all_routes(t)) {
+    // the decode matvec; a type without a prefill kernel takes every batch this way, kMaxDecodeRows rows a launch
     const int64_t kp = pad_to(k, act_block(t));
-    void *vy = workspace().get(w.device().ordinal, (size_t)(rows * (kp / act_block(t)) * act_block_bytes(t)), stream);
+    const int64_t row_bytes = (kp / act_block(t)) * act_block_bytes(t);
+    void *vy = workspace().get(w.device().ordinal, (size_t)(rows * row_bytes), stream);
     decode_quantizer(t, in_dtype)(xs, vy, (int)k, (int)kp, (int)rows, stream);
     abi_check("QMatMul::forward (quantize)");
-    decode_matvec(t, in_dtype)(w.device_ptr(), vy, ys, (int)k, (int)n, (int)(kp / act_block(t)), (int)n, (int)rows,
-                               stream);
-    abi_check("QMatMul::forward (matvec)");
+    const size_t out_elem = in_dtype == GgmlDType::F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < rows; r0 += kMaxDecodeRows) {
+      const int64_t b = rows - r0 < kMaxDecodeRows ? rows - r0 : kMaxDecodeRows;
+      decode_matvec(t, in_dtype)(w.device_ptr(), (const uint8_t *)vy + r0 * row_bytes, (uint8_t *)ys + r0 * n * out_elem,
+                                 (int)k, (int)n, (int)(kp / act_block(t)), (int)n, (int)b, stream);
+      abi_check("QMatMul::forward (matvec)");
+    }
   } else {
     const int64_t kp = pad_to(k, 256);
     void *y = workspace().get(w.device().ordinal, (size_t)(rows * kp / 256 * tile_bytes_per_256(t)), stream);

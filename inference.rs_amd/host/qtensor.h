@@ -21,12 +21,21 @@ struct Error : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
 
-// GgmlDType (quantized/mod.rs:481-704) for the types this path serves
+// GgmlDType (quantized/mod.rs:481-704).  Kernels serve Q8_0, Q4K, Q6K (every route) and Q4_0, Q5_0, Q5K (the
+// matvec route and dequantization); Q4_1, Q5_1, Q8_1, Q2K and Q3K are held and saved but have no kernels here.
 enum class GgmlDType : uint32_t {
   F32 = QMM_TYPE_F32,
   F16 = QMM_TYPE_F16,
+  Q4_0 = QMM_TYPE_Q4_0,
+  Q4_1 = QMM_TYPE_Q4_1,
+  Q5_0 = QMM_TYPE_Q5_0,
+  Q5_1 = QMM_TYPE_Q5_1,
   Q8_0 = QMM_TYPE_Q8_0,
+  Q8_1 = QMM_TYPE_Q8_1,
+  Q2K = QMM_TYPE_Q2K,
+  Q3K = QMM_TYPE_Q3K,
   Q4K = QMM_TYPE_Q4K,
+  Q5K = QMM_TYPE_Q5K,
   Q6K = QMM_TYPE_Q6K,
   Q8K = QMM_TYPE_Q8K,
   BF16 = QMM_TYPE_BF16,

@@ -23,10 +23,13 @@ HEADERS = [os.path.join(REPO, "include", "inferencequant.h"), os.path.join(REPO,
 
 # GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603) and block geometry
 F32, F16, Q8_0, Q4K, Q6K, Q8K, BF16 = 0, 1, 8, 12, 14, 15, 30
-BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
-TYPE_SIZE = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
-ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+# the adjacent types served by the decode matvec and the dequantizers (IQ4_XS: inference-quant gguf/kernel.rs:141)
+Q4_0, Q5_0, Q5K, IQ4XS = 2, 6, 13, 23
+BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256, Q4_0: 32, Q5_0: 32, Q5K: 256, IQ4XS: 256}
+TYPE_SIZE = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292, Q4_0: 18, Q5_0: 22, Q5K: 176, IQ4XS: 136}
+ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K, Q4_0: Q8_0, Q5_0: Q8_0, Q5K: Q8K, IQ4XS: Q8K}
 TYPE_NAME = {Q8_0: "q8_0", Q4K: "q4_k", Q6K: "q6_k"}
+ADJ_TYPE_NAME = {Q4_0: "q4_0", Q5_0: "q5_0", Q5K: "q5_k", IQ4XS: "iq4_xs"}
 MOE_NAME = {Q8_0: "q8_0_q8_0", Q4K: "q4k_q8k", Q6K: "q6k_q8k"}
 
 _lib = None
@@ -97,10 +100,15 @@ def _declare(L: ctypes.CDLL) -> None:
         f = getattr(L, f"launch_mmq_quantize_{blk}", None)
         if f is not None:
             f.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
-    for t in TYPE_NAME.values():
+    for t in ADJ_TYPE_NAME.values():
+        for o in ("f32", "f16", "bf16"):
+            getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k"]:
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_dequantize_{t}_{o}").argtypes = [vp, vp, i64, vp]
         getattr(L, f"launch_get_rows_{t}").argtypes = [vp, vp, vp, i64, i64, i64, vp]
+    for o in ("f32", "f16", "bf16"):
+        getattr(L, f"launch_dequantize_iq4_xs_{o}").argtypes = [vp, vp, i64, i64, vp]
     for o in ("f32", "bf16"):
         getattr(L, f"launch_mmvq_gguf_q8_0_{o}_exact").argtypes = [vp, vp, vp, i32, i32, i32, vp]
     for t in TYPE_NAME.values():
@@ -183,7 +191,7 @@ def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out
     if out is None:
         out = torch.empty((b, stride_col_dst or n), dtype=out_dtype, device=w.device)
     oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_plain")(
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_{oname}_plain")(
         _ptr(w), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], stride_col_dst or n, b, _stream())
     check()
     return out
@@ -358,7 +366,11 @@ def dequantize(wtype: int, w, n: int, out_dtype=None, out=None):
     if out is None:
         out = torch.empty(n, dtype=out_dtype or torch.float32, device=w.device)
     oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
-    getattr(lib(), f"launch_dequantize_{TYPE_NAME[wtype]}_{oname}")(_ptr(w), _ptr(out), n, _stream())
+    if wtype == IQ4XS:  # the reference's (nrows, ncols) form
+        getattr(lib(), f"launch_dequantize_iq4_xs_{oname}")(_ptr(w), _ptr(out), 1, n, _stream())
+    else:
+        getattr(lib(), f"launch_dequantize_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_{oname}")(
+            _ptr(w), _ptr(out), n, _stream())
     check()
     return out
 
@@ -368,8 +380,8 @@ def get_rows(wtype: int, w, ids, ne00: int, nb01: int, out=None):
     torch = _torch()
     if out is None:
         out = torch.empty((ids.numel(), ne00), dtype=torch.float32, device=w.device)
-    getattr(lib(), f"launch_get_rows_{TYPE_NAME[wtype]}")(_ptr(w), _ptr(ids), _ptr(out), ne00, nb01, ids.numel(),
-                                                          _stream())
+    getattr(lib(), f"launch_get_rows_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}")(
+        _ptr(w), _ptr(ids), _ptr(out), ne00, nb01, ids.numel(), _stream())
     check()
     return out
 

@@ -78,20 +78,27 @@ float oracle_f16_to_f32(uint16_t h) {
 
 /* ---------------------------------------------------------------- type table */
 
+/* the IQ4_NL / IQ4_XS value table (crates/inference-quant/src/gguf/raw.rs:13-15) */
+const int8_t oracle_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
 size_t oracle_type_size(int type) {
     switch (type) {
     case OR_Q8_0: return sizeof(or_block_q8_0);
     case OR_Q4K: return sizeof(or_block_q4k);
     case OR_Q6K: return sizeof(or_block_q6k);
     case OR_Q8K: return sizeof(or_block_q8k);
+    case OR_Q4_0: return sizeof(or_block_q4_0);
+    case OR_Q5_0: return sizeof(or_block_q5_0);
+    case OR_Q5K: return sizeof(or_block_q5k);
+    case OR_IQ4XS: return sizeof(or_block_iq4xs);
     default: return 0;
     }
 }
 
 size_t oracle_block_size(int type) {
     switch (type) {
-    case OR_Q8_0: return 32;
-    case OR_Q4K: case OR_Q6K: case OR_Q8K: return 256;
+    case OR_Q8_0: case OR_Q4_0: case OR_Q5_0: return 32;
+    case OR_Q4K: case OR_Q6K: case OR_Q8K: case OR_Q5K: case OR_IQ4XS: return 256;
     default: return 0;
     }
 }
@@ -118,6 +125,13 @@ static int8_t sat_i8(float v) {
     if (v >= 127.0f) return 127;
     if (v <= -128.0f) return -128;
     return (int8_t)v;
+}
+
+/* Rust's `f32 as u8`: saturating, truncating toward zero, NaN -> 0 */
+static uint8_t sat_u8(float v) {
+    if (!(v > 0.0f)) return 0;
+    if (v >= 255.0f) return 255;
+    return (uint8_t)v;
 }
 
 /* ---------------------------------------------------------------- Q8_0 (mod.rs:41-56, k_quants.rs:899-1000) */
@@ -407,6 +421,119 @@ void oracle_quantize_q6k(const float *x, int64_t n, or_block_q6k *y) {
     for (int64_t b = 0; b < nb; b++) quantize_q6k_block(x + 256 * b, y + b);
 }
 
+/* ---------------------------------------------------------------- Q5_K weights */
+
+/* k_quants.rs:2256-2334 (the plain, no-imatrix branch): Q4_K's search with 31 levels and Q5K_SEARCH
+ * {rmin -0.5, rdelta 0.1, nstep 15, mad false} (k_quants.rs:254-259), the fifth bits moved to qh */
+static void quantize_q5k_block(const float *x, or_block_q5k *blk) {
+    uint8_t l[256];
+    float mins[8], scales[8];
+    memset(blk, 0, sizeof *blk);
+    for (int j = 0; j < 8; j++) {
+        const float *xs = x + 32 * j;
+        float ss = 0.0f;
+        for (int i = 0; i < 32; i++) ss = ss + xs[i] * xs[i];
+        float av_x = sqrtf(ss / 32.0f);
+        float w[32];
+        for (int i = 0; i < 32; i++) w[i] = av_x + fabsf(xs[i]);
+        scales[j] = make_qkx2_quants(31, xs, w, -0.5f, 0.1f, 15, 0, l + 32 * j, &mins[j]);
+    }
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        max_scale = fmaxf(scales[j], max_scale);
+        max_min = fmaxf(mins[j], max_min);
+    }
+    float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    for (int j = 0; j < 8; j++) {
+        int32_t lsi = nearest_int_mul(inv_scale, scales[j]);
+        int32_t lmi = nearest_int_mul(inv_min, mins[j]);
+        uint8_t ls = (uint8_t)(lsi < 63 ? lsi : 63);
+        uint8_t lm = (uint8_t)(lmi < 63 ? lmi : 63);
+        if (j < 4) {
+            blk->scales[j] = ls;
+            blk->scales[j + 4] = lm;
+        } else {
+            blk->scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            blk->scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            blk->scales[j] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    blk->d = oracle_f32_to_f16(max_scale / 63.0f);
+    blk->dmin = oracle_f32_to_f16(max_min / 63.0f);
+    for (int j = 0; j < 8; j++) {
+        uint8_t sc, m;
+        get_scale_min_k4(j, blk->scales, &sc, &m);
+        float d = oracle_f16_to_f32(blk->d) * (float)sc;
+        if (d == 0.0f) continue;
+        float dm = oracle_f16_to_f32(blk->dmin) * (float)m;
+        for (int ii = 0; ii < 32; ii++) l[32 * j + ii] = (uint8_t)clampi(nearest_int((x[32 * j + ii] + dm) / d), 0, 31);
+    }
+    uint8_t m1 = 1, m2 = 2;
+    for (int nn = 0; nn < 256; nn += 64) {
+        const int off = nn / 64 * 32;
+        for (int j = 0; j < 32; j++) {
+            uint8_t l1 = l[nn + j], l2 = l[nn + j + 32];
+            if (l1 > 15) { l1 -= 16; blk->qh[j] |= m1; }
+            if (l2 > 15) { l2 -= 16; blk->qh[j] |= m2; }
+            blk->qs[off + j] = (uint8_t)(l1 | (l2 << 4));
+        }
+        m1 <<= 2;
+        m2 <<= 2;
+    }
+}
+
+void oracle_quantize_q5k(const float *x, int64_t n, or_block_q5k *y) {
+    int64_t nb = n / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < nb; b++) quantize_q5k_block(x + 256 * b, y + b);
+}
+
+/* ---------------------------------------------------------------- Q4_0 / Q5_0 weights */
+
+/* the signed value of largest magnitude, the first one on a tie (k_quants.rs:393-401, 694-701) */
+static float signed_absmax32(const float *x) {
+    float amax = 0.0f, max = 0.0f;
+    for (int i = 0; i < 32; i++)
+        if (amax < fabsf(x[i])) { amax = fabsf(x[i]); max = x[i]; }
+    return max;
+}
+
+/* k_quants.rs:380-418: d = max / -8, q = min(15, (x / d + 8.5) as u8) */
+void oracle_quantize_q4_0(const float *x, int64_t n, or_block_q4_0 *y) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        const float *xs = x + 32 * b;
+        float d = signed_absmax32(xs) / -8.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[b].d = oracle_f32_to_f16(d);
+        for (int j = 0; j < 16; j++) {
+            uint8_t q0 = sat_u8(xs[j] * id + 8.5f), q1 = sat_u8(xs[16 + j] * id + 8.5f);
+            q0 = q0 < 15 ? q0 : 15;
+            q1 = q1 < 15 ? q1 : 15;
+            y[b].qs[j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+/* k_quants.rs:681-717: d = max / -16, q = min(31, (x / d + 16.5) as i8) as u8, fifth bits into qh */
+void oracle_quantize_q5_0(const float *x, int64_t n, or_block_q5_0 *y) {
+    for (int64_t b = 0; b < n / 32; b++) {
+        const float *xs = x + 32 * b;
+        float d = signed_absmax32(xs) / -16.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[b].d = oracle_f32_to_f16(d);
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; j++) {
+            int8_t a = sat_i8(xs[j] * id + 16.5f), c = sat_i8(xs[16 + j] * id + 16.5f);
+            uint8_t q0 = (uint8_t)(a < 31 ? a : 31), q1 = (uint8_t)(c < 31 ? c : 31);
+            y[b].qs[j] = (uint8_t)((q0 & 0x0F) | ((q1 & 0x0F) << 4));
+            qh |= (uint32_t)((q0 & 0x10) >> 4) << j;
+            qh |= (uint32_t)((q1 & 0x10) >> 4) << (j + 16);
+        }
+        memcpy(y[b].qh, &qh, 4); /* little-endian */
+    }
+}
+
 int oracle_quantize(int type, const float *x, int64_t n, void *out) {
     size_t bs = oracle_block_size(type);
     if (bs == 0 || n % (int64_t)bs != 0) return -1;
@@ -415,13 +542,17 @@ int oracle_quantize(int type, const float *x, int64_t n, void *out) {
     case OR_Q4K: oracle_quantize_q4k(x, n, (or_block_q4k *)out); return 0;
     case OR_Q6K: oracle_quantize_q6k(x, n, (or_block_q6k *)out); return 0;
     case OR_Q8K: oracle_quantize_q8k(x, n, (or_block_q8k *)out); return 0;
+    case OR_Q4_0: oracle_quantize_q4_0(x, n, (or_block_q4_0 *)out); return 0;
+    case OR_Q5_0: oracle_quantize_q5_0(x, n, (or_block_q5_0 *)out); return 0;
+    case OR_Q5K: oracle_quantize_q5k(x, n, (or_block_q5k *)out); return 0;
     default: return -1;
     }
 }
 
 /* ---------------------------------------------------------------- dequantize */
 
-/* Q8_0: k_quants.rs:905-921; Q4_K: 2096-2123; Q6_K: 2649-2680; Q8_K: 2762-2773 */
+/* Q8_0: k_quants.rs:905-921; Q4_K: 2096-2123; Q6_K: 2649-2680; Q8_K: 2762-2773; Q4_0: 313-330; Q5_0: 720-743;
+ * Q5_K: 2433-2467; IQ4_XS: crates/inference-quant/src/gguf/raw.rs:773-808 */
 void oracle_dequantize(int type, const void *blocks, int64_t n, float *y) {
     if (type == OR_Q8_0) {
         const or_block_q8_0 *b = (const or_block_q8_0 *)blocks;
@@ -474,6 +605,63 @@ void oracle_dequantize(int type, const void *blocks, int64_t n, float *y) {
         const or_block_q8k *b = (const or_block_q8k *)blocks;
         for (int64_t i = 0; i < n / 256; i++)
             for (int j = 0; j < 256; j++) y[256 * i + j] = b[i].d * (float)b[i].qs[j];
+    } else if (type == OR_Q4_0) {
+        const or_block_q4_0 *b = (const or_block_q4_0 *)blocks;
+        for (int64_t i = 0; i < n / 32; i++) {
+            float d = oracle_f16_to_f32(b[i].d);
+            for (int j = 0; j < 16; j++) {
+                y[32 * i + j] = (float)((int)(b[i].qs[j] & 0x0F) - 8) * d;
+                y[32 * i + j + 16] = (float)((int)(b[i].qs[j] >> 4) - 8) * d;
+            }
+        }
+    } else if (type == OR_Q5_0) {
+        const or_block_q5_0 *b = (const or_block_q5_0 *)blocks;
+        for (int64_t i = 0; i < n / 32; i++) {
+            float d = oracle_f16_to_f32(b[i].d);
+            uint32_t qh;
+            memcpy(&qh, b[i].qh, 4);
+            for (int j = 0; j < 16; j++) {
+                int h0 = (int)(((qh >> j) << 4) & 0x10), h1 = (int)((qh >> (j + 12)) & 0x10);
+                y[32 * i + j] = (float)(((int)(b[i].qs[j] & 0x0F) | h0) - 16) * d;
+                y[32 * i + j + 16] = (float)(((int)(b[i].qs[j] >> 4) | h1) - 16) * d;
+            }
+        }
+    } else if (type == OR_Q5K) {
+        const or_block_q5k *b = (const or_block_q5k *)blocks;
+        for (int64_t i = 0; i < n / 256; i++) {
+            float d = oracle_f16_to_f32(b[i].d), min = oracle_f16_to_f32(b[i].dmin);
+            float *out = y + 256 * i;
+            uint8_t u1 = 1, u2 = 2;
+            for (int j = 0, is = 0; j < 256; j += 64, is += 2) {
+                const uint8_t *ql = b[i].qs + j / 2;
+                uint8_t sc, m;
+                get_scale_min_k4(is, b[i].scales, &sc, &m);
+                float d1 = d * (float)sc, m1 = min * (float)m;
+                get_scale_min_k4(is + 1, b[i].scales, &sc, &m);
+                float d2 = d * (float)sc, m2 = min * (float)m;
+                for (int l = 0; l < 32; l++)
+                    out[j + l] = d1 * ((float)(ql[l] & 0xF) + ((b[i].qh[l] & u1) ? 16.0f : 0.0f)) - m1;
+                for (int l = 0; l < 32; l++)
+                    out[j + 32 + l] = d2 * ((float)(ql[l] >> 4) + ((b[i].qh[l] & u2) ? 16.0f : 0.0f)) - m2;
+                u1 <<= 2;
+                u2 <<= 2;
+            }
+        }
+    } else if (type == OR_IQ4XS) {
+        const or_block_iq4xs *b = (const or_block_iq4xs *)blocks;
+        for (int64_t i = 0; i < n / 256; i++) {
+            float d = oracle_f16_to_f32(b[i].d);
+            for (int ib = 0; ib < 8; ib++) {
+                int ls = ((b[i].scales_l[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((b[i].scales_h >> (2 * ib)) & 3) << 4);
+                float scale = d * (float)(ls - 32);
+                const uint8_t *qs = b[i].qs + 16 * ib;
+                float *out = y + 256 * i + 32 * ib;
+                for (int j = 0; j < 16; j++) {
+                    out[j] = scale * (float)oracle_kvalues_iq4nl[qs[j] & 0xF];
+                    out[j + 16] = scale * (float)oracle_kvalues_iq4nl[qs[j] >> 4];
+                }
+            }
+        }
     }
 }
 
@@ -567,15 +755,117 @@ float oracle_vec_dot_q6k_q8k(int64_t n, const or_block_q6k *xs, const or_block_q
     return s;
 }
 
+float oracle_vec_dot_q4_0_q8_0(int64_t n, const or_block_q4_0 *x, const or_block_q8_0 *y) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < n / 32; b++) {
+        int32_t sum_i = 0;
+        for (int j = 0; j < 16; j++)
+            sum_i += ((int32_t)(x[b].qs[j] & 0x0F) - 8) * y[b].qs[j] + ((int32_t)(x[b].qs[j] >> 4) - 8) * y[b].qs[j + 16];
+        sumf += (float)sum_i * oracle_f16_to_f32(x[b].d) * oracle_f16_to_f32(y[b].d);
+    }
+    return sumf;
+}
+
+float oracle_vec_dot_q5_0_q8_0(int64_t n, const or_block_q5_0 *x, const or_block_q8_0 *y) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < n / 32; b++) {
+        uint32_t qh;
+        memcpy(&qh, x[b].qh, 4);
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            int32_t h0 = (int32_t)(((qh & (1u << j)) >> j) << 4);
+            int32_t h1 = (int32_t)((qh & (1u << (j + 16))) >> (j + 12));
+            int32_t x0 = ((int32_t)(x[b].qs[j] & 0x0F) | h0) - 16;
+            int32_t x1 = ((int32_t)(x[b].qs[j] >> 4) | h1) - 16;
+            sumi += x0 * y[b].qs[j] + x1 * y[b].qs[j + 16];
+        }
+        sumf += (float)sumi * oracle_f16_to_f32(x[b].d) * oracle_f16_to_f32(y[b].d);
+    }
+    return sumf;
+}
+
+float oracle_vec_dot_q5k_q8k(int64_t n, const or_block_q5k *xs, const or_block_q8k *ys) {
+    const uint32_t kmask1 = 0x3f3f3f3fu, kmask2 = 0x0f0f0f0fu, kmask3 = 0x03030303u;
+    float sums[8] = {0};
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < n / 256; b++) {
+        const or_block_q5k *x = xs + b;
+        const or_block_q8k *y = ys + b;
+        int8_t aux8[256];
+        int32_t aux32[8] = {0};
+        uint8_t m = 1;
+        for (int c = 0; c < 4; c++) {
+            const uint8_t *q5 = x->qs + 32 * c;
+            for (int l = 0; l < 32; l++) aux8[64 * c + l] = (int8_t)((q5[l] & 0xF) + ((x->qh[l] & m) ? 16 : 0));
+            m <<= 1;
+            for (int l = 0; l < 32; l++) aux8[64 * c + 32 + l] = (int8_t)((q5[l] >> 4) + ((x->qh[l] & m) ? 16 : 0));
+            m <<= 1;
+        }
+        uint32_t utmp[4];
+        memcpy(utmp, x->scales, 12);
+        utmp[3] = ((utmp[2] >> 4) & kmask2) | (((utmp[1] >> 6) & kmask3) << 4);
+        uint32_t uaux = utmp[1] & kmask1;
+        utmp[1] = (utmp[2] & kmask2) | (((utmp[0] >> 6) & kmask3) << 4);
+        utmp[2] = uaux;
+        utmp[0] &= kmask1;
+        uint8_t scales[8], mins[8];
+        memcpy(scales, utmp, 8);
+        memcpy(mins, utmp + 2, 8);
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++) sumi += (int32_t)y->bsums[j] * (int32_t)mins[j / 2];
+        const int8_t *a = aux8;
+        const int8_t *q8 = y->qs;
+        for (int s = 0; s < 8; s++) {
+            int32_t scale = scales[s];
+            for (int r = 0; r < 4; r++) {
+                for (int l = 0; l < 8; l++) aux32[l] += scale * (int32_t)(int16_t)((int16_t)q8[l] * (int16_t)a[l]);
+                q8 += 8;
+                a += 8;
+            }
+        }
+        float d = oracle_f16_to_f32(x->d) * y->d;
+        for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
+        float dmin = oracle_f16_to_f32(x->dmin) * y->d;
+        sumf -= dmin * (float)sumi;
+    }
+    float s = 0.0f;
+    for (int l = 0; l < 8; l++) s += sums[l];
+    return sumf + s;
+}
+
+float oracle_vec_dot_iq4xs_q8k(int64_t n, const or_block_iq4xs *xs, const or_block_q8k *ys) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < n / 256; b++) {
+        const or_block_iq4xs *x = xs + b;
+        const or_block_q8k *y = ys + b;
+        float d = oracle_f16_to_f32(x->d) * y->d;
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t *qs = x->qs + 16 * ib;
+            const int8_t *q8 = y->qs + 32 * ib;
+            int32_t sumi = 0;
+            for (int j = 0; j < 16; j++)
+                sumi += (int32_t)q8[j] * oracle_kvalues_iq4nl[qs[j] & 0xF] + (int32_t)q8[j + 16] * oracle_kvalues_iq4nl[qs[j] >> 4];
+            int32_t ls = (int32_t)(((x->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((x->scales_h >> (2 * ib)) & 3) << 4)) - 32;
+            sumf += d * (float)(ls * sumi);
+        }
+    }
+    return sumf;
+}
+
 /* ---------------------------------------------------------------- matmul (k_quants.rs:2776-2894) */
 
-static int vec_dot_type(int type) { return type == OR_Q8_0 ? OR_Q8_0 : OR_Q8K; }
+/* GgmlType::VecDotType: Q8_0 for the 32-value types, Q8_K for the super-block types (IQ4_XS: cpu_dot.rs:67-68) */
+static int vec_dot_type(int type) { return oracle_block_size(type) == 32 ? OR_Q8_0 : OR_Q8K; }
 
 static float vec_dot_any(int type, int64_t k, const void *w_row, const void *a_row) {
     switch (type) {
     case OR_Q8_0: return oracle_vec_dot_q8_0_q8_0(k, (const or_block_q8_0 *)w_row, (const or_block_q8_0 *)a_row);
     case OR_Q4K: return oracle_vec_dot_q4k_q8k(k, (const or_block_q4k *)w_row, (const or_block_q8k *)a_row);
     case OR_Q6K: return oracle_vec_dot_q6k_q8k(k, (const or_block_q6k *)w_row, (const or_block_q8k *)a_row);
+    case OR_Q4_0: return oracle_vec_dot_q4_0_q8_0(k, (const or_block_q4_0 *)w_row, (const or_block_q8_0 *)a_row);
+    case OR_Q5_0: return oracle_vec_dot_q5_0_q8_0(k, (const or_block_q5_0 *)w_row, (const or_block_q8_0 *)a_row);
+    case OR_Q5K: return oracle_vec_dot_q5k_q8k(k, (const or_block_q5k *)w_row, (const or_block_q8k *)a_row);
+    case OR_IQ4XS: return oracle_vec_dot_iq4xs_q8k(k, (const or_block_iq4xs *)w_row, (const or_block_q8k *)a_row);
     default: return 0.0f;
     }
 }

@@ -29,9 +29,23 @@ typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128];
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } or_block_q6k;
 /* k_quants.rs:217-223 */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } or_block_q8k;
+/* k_quants.rs:116-120: value j in qs[j] low nibble, value j + 16 in its high nibble, both offset by 8 */
+typedef struct { uint16_t d; uint8_t qs[16]; } or_block_q4_0;
+/* k_quants.rs:133-138: as Q4_0 with a fifth bit per value in the little-endian word qh (bit j = value j), offset 16 */
+typedef struct { uint16_t d; uint8_t qh[4]; uint8_t qs[16]; } or_block_q5_0;
+/* k_quants.rs:200-206: Q4_K's header and nibbles plus qh[32]; bit 2c of qh[l] is the fifth bit of value 64c + l,
+ * bit 2c + 1 that of value 64c + 32 + l */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } or_block_q5k;
+/* IQ4_XS, 136 bytes per 256 values (crates/inference-quant/src/gguf/cpu_dot.rs:15-18, raw.rs:794-808): f16 d,
+ * 6-bit sub-block scales (low 4 bits in scales_l nibbles, high 2 bits in scales_h), then per 32 values 16 bytes of
+ * 4-bit indices into the IQ4_NL table (low nibbles the first 16 values, high nibbles the next 16) */
+typedef struct { uint16_t d; uint16_t scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } or_block_iq4xs;
 
-/* GGUF type ids, crates/inference-tensor/src/quantized/mod.rs:582-603 */
-enum { OR_Q8_0 = 8, OR_Q4K = 12, OR_Q6K = 14, OR_Q8K = 15 };
+/* GGUF type ids, crates/inference-tensor/src/quantized/mod.rs:582-603; IQ4_XS: inference-quant/src/gguf/kernel.rs:141 */
+enum { OR_Q4_0 = 2, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4K = 12, OR_Q5K = 13, OR_Q6K = 14, OR_Q8K = 15, OR_IQ4XS = 23 };
+
+/* the IQ4_NL / IQ4_XS value table (crates/inference-quant/src/gguf/raw.rs:13-15) */
+extern const int8_t oracle_kvalues_iq4nl[16];
 
 /* IEEE binary16 conversions, round to nearest even (the `half` crate 2.7.1's f16::from_f32 / to_f32) */
 uint16_t oracle_f32_to_f16(float f);
@@ -47,7 +61,10 @@ void oracle_quantize_q8_0(const float *x, int64_t n, or_block_q8_0 *y);     /* k
 void oracle_quantize_q8k(const float *x, int64_t n, or_block_q8k *y);       /* k_quants.rs:2721-2760 */
 void oracle_quantize_q4k(const float *x, int64_t n, or_block_q4k *y);       /* k_quants.rs:1930-2001 */
 void oracle_quantize_q6k(const float *x, int64_t n, or_block_q6k *y);       /* k_quants.rs:2590-2646 */
-/* generic: quantize n values (multiple of the block size) of `type` into `out` */
+void oracle_quantize_q4_0(const float *x, int64_t n, or_block_q4_0 *y);     /* k_quants.rs:380-418 */
+void oracle_quantize_q5_0(const float *x, int64_t n, or_block_q5_0 *y);     /* k_quants.rs:681-717 */
+void oracle_quantize_q5k(const float *x, int64_t n, or_block_q5k *y);       /* k_quants.rs:2256-2334 */
+/* generic: quantize n values (multiple of the block size) of `type` into `out` (IQ4_XS has no quantizer: -1) */
 int oracle_quantize(int type, const float *x, int64_t n, void *out);
 
 /* dequantizers */
@@ -57,6 +74,11 @@ void oracle_dequantize(int type, const void *blocks, int64_t n, float *y);
 float oracle_vec_dot_q8_0_q8_0(int64_t n, const or_block_q8_0 *x, const or_block_q8_0 *y); /* k_quants.rs:982-999 */
 float oracle_vec_dot_q4k_q8k(int64_t n, const or_block_q4k *x, const or_block_q8k *y);     /* k_quants.rs:1848-1928 */
 float oracle_vec_dot_q6k_q8k(int64_t n, const or_block_q6k *x, const or_block_q8k *y);     /* k_quants.rs:2518-2575 */
+float oracle_vec_dot_q4_0_q8_0(int64_t n, const or_block_q4_0 *x, const or_block_q8_0 *y); /* k_quants.rs:432-449 */
+float oracle_vec_dot_q5_0_q8_0(int64_t n, const or_block_q5_0 *x, const or_block_q8_0 *y); /* k_quants.rs:615-637 */
+float oracle_vec_dot_q5k_q8k(int64_t n, const or_block_q5k *x, const or_block_q8k *y);     /* k_quants.rs:2145-2232 */
+/* crates/inference-quant/src/gguf/cpu_dot.rs:416-440 (iq4_xs_sub_scale, iq4_xs_generic) */
+float oracle_vec_dot_iq4xs_q8k(int64_t n, const or_block_iq4xs *x, const or_block_q8k *y);
 
 /* k_quants::matmul (k_quants.rs:2776-2894): dst[m][n] = vec_dot(W row n, Q8(lhs row m)).
  * `threads` <= 0 uses every available thread. Returns 0, or -1 on a bad type/shape. */

@@ -16,8 +16,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-# GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603)
+# GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603; IQ4_XS: inference-quant/src/gguf/kernel.rs:141)
 Q8_0, Q4K, Q6K, Q8K = 8, 12, 14, 15
+Q4_0, Q5_0, Q5K, IQ4XS = 2, 6, 13, 23
 
 # block layouts (k_quants.rs:152-223), as numpy structured dtypes
 BLOCK_DTYPES = {
@@ -25,10 +26,19 @@ BLOCK_DTYPES = {
     Q4K: np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", 12), ("qs", "u1", 128)]),
     Q6K: np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("scales", "i1", 16), ("d", "<u2")]),
     Q8K: np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)]),
+    Q4_0: np.dtype([("d", "<u2"), ("qs", "u1", 16)]),
+    Q5_0: np.dtype([("d", "<u2"), ("qh", "u1", 4), ("qs", "u1", 16)]),
+    Q5K: np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", 12), ("qh", "u1", 32), ("qs", "u1", 128)]),
+    IQ4XS: np.dtype([("d", "<u2"), ("scales_h", "<u2"), ("scales_l", "u1", 4), ("qs", "u1", 128)]),
 }
-BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+BLOCK_SIZE = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256, Q4_0: 32, Q5_0: 32, Q5K: 256, IQ4XS: 256}
 TYPE_SIZE = {t: d.itemsize for t, d in BLOCK_DTYPES.items()}
-ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K, Q4_0: Q8_0, Q5_0: Q8_0, Q5K: Q8K, IQ4XS: Q8K}
+# the IQ4_NL value table (crates/inference-quant/src/gguf/raw.rs:13-15)
+KVALUES_IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int8)
+VEC_DOT = {Q8_0: "oracle_vec_dot_q8_0_q8_0", Q4K: "oracle_vec_dot_q4k_q8k", Q6K: "oracle_vec_dot_q6k_q8k",
+           Q4_0: "oracle_vec_dot_q4_0_q8_0", Q5_0: "oracle_vec_dot_q5_0_q8_0", Q5K: "oracle_vec_dot_q5k_q8k",
+           IQ4XS: "oracle_vec_dot_iq4xs_q8k"}
 
 _lib = None
 
@@ -57,7 +67,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_indexed_moe.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, i64, i64, i64, vp, vp, ctypes.c_int]
         L.oracle_moe_dispatch.argtypes = [vp, i32, i32, i32, vp, vp, vp]
         L.oracle_moe_weighted_reduce.argtypes = [vp, vp, vp, i32, i32, i32]
-        for name in ("oracle_vec_dot_q8_0_q8_0", "oracle_vec_dot_q4k_q8k", "oracle_vec_dot_q6k_q8k"):
+        for name in VEC_DOT.values():
             getattr(L, name).argtypes = [i64, vp, vp]
             getattr(L, name).restype = ctypes.c_float
         _lib = L
@@ -97,6 +107,18 @@ def quantize(gtype: int, x: np.ndarray) -> np.ndarray:
     return out.reshape(x.shape[:-1] + (x.shape[-1] // bs * TYPE_SIZE[gtype],))
 
 
+def random_blocks(gtype: int, n_values: int, rng: np.random.Generator, scale: float = 0.01) -> np.ndarray:
+    """Random bytes of n_values / block-size blocks of gtype with finite f16 scales near `scale` (every byte pattern of
+    the quantized fields is a valid block); for a type without a quantizer (IQ4_XS) and for edge patterns."""
+    nb = n_values // BLOCK_SIZE[gtype]
+    raw = rng.integers(0, 256, nb * TYPE_SIZE[gtype], dtype=np.uint8)
+    b = raw.view(BLOCK_DTYPES[gtype])
+    for f in ("d", "dmin"):
+        if f in b.dtype.names:
+            b[f] = (rng.uniform(0.5, 1.5, nb) * scale * rng.choice([-1, 1], nb)).astype(np.float16).view(np.uint16)
+    return raw
+
+
 def blocks(gtype: int, data: np.ndarray) -> np.ndarray:
     """View quantized bytes as structured blocks."""
     return np.ascontiguousarray(data).reshape(-1).view(BLOCK_DTYPES[gtype])
@@ -110,7 +132,7 @@ def dequantize(gtype: int, data: np.ndarray, n: int) -> np.ndarray:
 
 
 def vec_dot(gtype: int, k: int, w_row: np.ndarray, a_row: np.ndarray) -> float:
-    name = {Q8_0: "oracle_vec_dot_q8_0_q8_0", Q4K: "oracle_vec_dot_q4k_q8k", Q6K: "oracle_vec_dot_q6k_q8k"}[gtype]
+    name = VEC_DOT[gtype]
     w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
     a_row = np.ascontiguousarray(a_row, dtype=np.uint8)
     return float(getattr(lib(), name)(k, _p(w_row), _p(a_row)))

@@ -1,0 +1,142 @@
+"""GPU parity of the adjacent GGUF types (Q4_0, Q5_0, Q5_K, IQ4_XS) through the C ABI: the decode matvec
+launch_mmvq_gguf_<t>_<dtype>_plain against the oracle's CPU QMatMul on the same bytes and the same (bit-exact)
+activation blocks, max rel. error <= 1e-3 and per element <= 1e-5 * sum|terms|; the dequantizers bit-exact with the
+oracle's to_float (f16 / bf16 outputs: the f32 values rounded to nearest even)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import qmm
+from helpers import acts, assert_parity, weights
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TYPES = [O.Q4_0, O.Q5_0, O.Q5K, O.IQ4XS]
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def weight_bytes(gtype, n, k, rng, random_bytes=False):
+    if gtype == O.IQ4XS or random_bytes:
+        return O.random_blocks(gtype, n * k, rng, 0.002).reshape(n, -1)
+    return O.quantize(gtype, weights(rng, n, k))
+
+
+def terms(gtype, aq, wq, m, n, k):
+    import test_oracle as T
+    a = T.NP_DEQUANT[O.ACT_TYPE[gtype]](aq).reshape(m, -1)[:, :k]
+    w = T.NP_DEQUANT[gtype](wq).reshape(n, k)
+    return np.abs(a) @ np.abs(w).T
+
+
+def run_matvec(gtype, wq, x, n, out_dtype=torch.float32):
+    m, k = x.shape
+    w = to_dev(wq.reshape(-1))
+    vy, kp = qmm.quantize_decode(gtype, to_dev(x))
+    got = qmm.mmvq(gtype, w, vy, k, n, m, kp, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    aq = vy.cpu().numpy()
+    assert kp == k  # K is whole weight blocks, and a weight block is as long as its activation block
+    # the oracle on the activation blocks the GPU made (bit-exact with the oracle's own quantizer, checked below)
+    want = O.matmul_preq(gtype, aq, m, k, wq, n)
+    return got.float().cpu().numpy(), want, aq
+
+
+def _k_cases(gtype):
+    # 32-value types: even and odd block counts (the block-pair and the one-block unit); super-block types: one to
+    # many super-blocks, including counts that leave a wave's lanes partly idle
+    return [32, 96, 512, 1056, 4096, 14336] if O.BLOCK_SIZE[gtype] == 32 else [256, 768, 4096, 5120, 14336]
+
+
+@pytest.mark.parametrize("gtype", TYPES)
+@pytest.mark.parametrize("kidx", range(5))
+@pytest.mark.parametrize("b", [1, 2, 5, 8, 16])
+def test_adjacent_matvec_matches_the_oracle(gtype, kidx, b):
+    k = _k_cases(gtype)[kidx]
+    rng = np.random.default_rng(1000 * gtype + 10 * kidx + b)
+    n = 37 if k > 4096 else 300
+    wq = weight_bytes(gtype, n, k, rng)
+    x = acts(rng, b, k)
+    x[:, ::64] *= 30.0
+    got, want, aq = run_matvec(gtype, wq, x, n)
+    kp = qmm.pad_to(k, O.BLOCK_SIZE[O.ACT_TYPE[gtype]])
+    xp = np.zeros((b, kp), np.float32)
+    xp[:, :k] = x
+    assert np.array_equal(aq, O.quantize(O.ACT_TYPE[gtype], xp).reshape(-1))
+    assert_parity(got, want, terms(gtype, aq, wq, b, n, k), what=f"type {gtype} k={k} b={b}")
+
+
+@pytest.mark.parametrize("gtype", TYPES)
+@pytest.mark.parametrize("out", ["f16", "bf16"])
+def test_adjacent_matvec_half_outputs(gtype, out):
+    rng = np.random.default_rng(77 + gtype)
+    k = 4096
+    n = 513
+    wq = weight_bytes(gtype, n, k, rng, random_bytes=True)
+    x = acts(rng, 3, k)
+    odt = {"f16": torch.float16, "bf16": torch.bfloat16}[out]
+    got, want, _ = run_matvec(gtype, wq, x, n, out_dtype=odt)
+    # the f32 result rounded once to the output type
+    assert_parity(got, want, rel=1e-2 if out == "bf16" else 2e-3, what=f"type {gtype} {out}")
+
+
+@pytest.mark.parametrize("gtype", [O.Q4_0, O.Q5_0])
+def test_odd_block_rows_and_unaligned_weights(gtype):
+    """Rows of an odd number of 32-value blocks and a weight pointer that is only 2-byte aligned take the one-block
+    unit; the result is the same arithmetic."""
+    rng = np.random.default_rng(5 + gtype)
+    k, n = 160, 77
+    wq = weight_bytes(gtype, n, k, rng)
+    x = acts(rng, 4, k)
+    buf = torch.zeros(wq.size + 2, dtype=torch.uint8, device=DEV)
+    buf[2:] = to_dev(wq.reshape(-1))
+    vy, kp = qmm.quantize_decode(gtype, to_dev(x))
+    got = qmm.mmvq(gtype, buf[2:], vy, k, n, 4, kp).cpu().numpy()
+    want = O.matmul(gtype, x, wq, n)
+    assert_parity(got, want, what="odd/unaligned")
+    # a 64-multiple K through the same 2-byte-aligned pointer
+    k = 256
+    wq = weight_bytes(gtype, n, k, rng)
+    x = acts(rng, 2, k)
+    buf = torch.zeros(wq.size + 2, dtype=torch.uint8, device=DEV)
+    buf[2:] = to_dev(wq.reshape(-1))
+    vy, kp = qmm.quantize_decode(gtype, to_dev(x))
+    got = qmm.mmvq(gtype, buf[2:], vy, k, n, 2, kp).cpu().numpy()
+    assert_parity(got, O.matmul(gtype, x, wq, n), what="aligned-K, unaligned pointer")
+
+
+def test_q5k_and_iq4xs_reject_misaligned_weights():
+    w = torch.zeros(176 * 4 + 16, dtype=torch.uint8, device=DEV)
+    vy, kp = qmm.quantize_decode(qmm.Q5K, torch.zeros((1, 256), device=DEV))
+    with pytest.raises(qmm.QmmError, match="aligned"):
+        qmm.mmvq(qmm.Q5K, w[4:], vy, 256, 4, 1, kp)
+    with pytest.raises(qmm.QmmError, match="aligned"):
+        qmm.mmvq(qmm.IQ4XS, w[2:], vy, 256, 4, 1, kp)
+
+
+@pytest.mark.parametrize("gtype", TYPES)
+@pytest.mark.parametrize("out", ["f32", "f16", "bf16"])
+def test_adjacent_dequantize_is_bit_exact(gtype, out):
+    rng = np.random.default_rng(31 + gtype)
+    n = 256 * 37
+    wq = weight_bytes(gtype, 1, n, rng, random_bytes=True).reshape(-1)
+    odt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[out]
+    got = qmm.dequantize(gtype, to_dev(wq), n, out_dtype=odt)
+    torch.cuda.synchronize()
+    want = torch.from_numpy(O.dequantize(gtype, wq, n)).to(odt)  # torch's f32 -> f16 / bf16 casts round to nearest even
+    assert torch.equal(got.cpu().view(torch.int16 if out != "f32" else torch.int32),
+                       want.view(torch.int16 if out != "f32" else torch.int32))
+
+
+@pytest.mark.parametrize("gtype", [O.Q4_0, O.Q5_0, O.Q5K])
+def test_adjacent_get_rows(gtype):
+    rng = np.random.default_rng(41 + gtype)
+    rows, k = 50, 512
+    wq = weight_bytes(gtype, rows, k, rng)
+    ids = np.array([3, 0, 49, 3, 17], np.uint32)
+    got = qmm.get_rows(gtype, to_dev(wq.reshape(-1)), to_dev(ids), k, wq.shape[1]).cpu().numpy()
+    want = O.dequantize(gtype, wq, rows * k).reshape(rows, k)[ids]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

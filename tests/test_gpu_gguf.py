@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("gtype,n,k,rows", [(O.Q4K, 96, 1024, 1), (O.Q6K, 64, 512, 5), (O.Q8_0, 48, 256, 40),
-                                            (O.Q4K, 130, 2048, 100)])
+                                            (O.Q4K, 130, 2048, 100), (O.Q5K, 64, 512, 40), (O.Q4_0, 48, 256, 3),
+                                            (O.Q5_0, 40, 96, 17)])
 def test_gguf_weight_runs_through_qmatmul(tmp_path, gtype, n, k, rows):
     rng = np.random.default_rng(n + k + rows)
     wq = O.quantize(gtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32)).reshape(-1)

@@ -189,20 +189,83 @@ def np_dequant_q8k(data):
     return (b["qs"].astype(np.float64) * b["d"].astype(np.float64)[:, None]).reshape(-1)
 
 
-NP_DEQUANT = {O.Q4K: np_dequant_q4k, O.Q6K: np_dequant_q6k, O.Q8_0: np_dequant_q8_0, O.Q8K: np_dequant_q8k}
+def _f16(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q8K])
+def np_dequant_q4_0(data):
+    """Q4_0 (k_quants.rs:116-120, 313-330): qs[j] low nibble = value j, high nibble = value j + 16, minus 8."""
+    b = O.blocks(O.Q4_0, data)
+    q = np.concatenate([b["qs"] & 0xF, b["qs"] >> 4], axis=1).astype(np.float64) - 8
+    return (q * _f16(b["d"])[:, None]).reshape(-1)
+
+
+def np_dequant_q5_0(data):
+    """Q5_0 (k_quants.rs:133-138, 720-743): the fifth bit of value i is bit i of the little-endian qh word."""
+    b = O.blocks(O.Q5_0, data)
+    qh = b["qh"].copy().view("<u4")[:, 0]
+    bits = (qh[:, None] >> np.arange(32, dtype=np.uint32)) & 1
+    q = np.concatenate([b["qs"] & 0xF, b["qs"] >> 4], axis=1).astype(np.int64) + 16 * bits - 16
+    return (q.astype(np.float64) * _f16(b["d"])[:, None]).reshape(-1)
+
+
+def np_dequant_q5k(data):
+    """Q5_K (k_quants.rs:200-206, 2433-2467): Q4_K's fields; bit 2c (2c + 1) of qh[l] adds 16 to value 64c + l
+    (64c + 32 + l)."""
+    out = []
+    for blk in O.blocks(O.Q5K, data):
+        d, dmin = _f16(blk["d"]), _f16(blk["dmin"])
+        s, m = _q4k_fields(blk)
+        qs = blk["qs"].reshape(4, 32).astype(np.int64)
+        qh = blk["qh"].astype(np.int64)
+        vals = np.empty(256, np.float64)
+        for c in range(4):
+            lo = (qs[c] & 0xF) + 16 * ((qh >> (2 * c)) & 1)
+            hi = (qs[c] >> 4) + 16 * ((qh >> (2 * c + 1)) & 1)
+            vals[64 * c:64 * c + 32] = d * s[2 * c] * lo - dmin * m[2 * c]
+            vals[64 * c + 32:64 * c + 64] = d * s[2 * c + 1] * hi - dmin * m[2 * c + 1]
+        out.append(vals)
+    return np.concatenate(out)
+
+
+def np_dequant_iq4xs(data):
+    """IQ4_XS (crates/inference-quant/src/gguf/raw.rs:794-808): sub-block ib's 6-bit scale is nibble ib of scales_l
+    plus bits 2ib..2ib+1 of scales_h, minus 32; values index the IQ4_NL table."""
+    out = []
+    for blk in O.blocks(O.IQ4XS, data):
+        d = _f16(blk["d"])
+        lo_nib = np.stack([blk["scales_l"] & 0xF, blk["scales_l"] >> 4], axis=1).reshape(8).astype(np.int64)
+        hi = (int(blk["scales_h"]) >> (2 * np.arange(8))) & 3
+        ls = lo_nib | (hi << 4)
+        qs = blk["qs"].reshape(8, 16)
+        idx = np.concatenate([qs & 0xF, qs >> 4], axis=1)
+        out.append((d * (ls - 32)[:, None] * O.KVALUES_IQ4NL[idx].astype(np.float64)).reshape(-1))
+    return np.concatenate(out)
+
+
+NP_DEQUANT = {O.Q4K: np_dequant_q4k, O.Q6K: np_dequant_q6k, O.Q8_0: np_dequant_q8_0, O.Q8K: np_dequant_q8k,
+              O.Q4_0: np_dequant_q4_0, O.Q5_0: np_dequant_q5_0, O.Q5K: np_dequant_q5k, O.IQ4XS: np_dequant_iq4xs}
+
+
+def weight_bytes(gtype, w, rng):
+    """Quantized bytes of w, or random blocks of its size for a type the reference has no quantizer for."""
+    if gtype == O.IQ4XS:
+        return O.random_blocks(gtype, w.size, rng, 0.002).reshape(w.shape[0], -1)
+    return O.quantize(gtype, w)
+
+
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q8K, O.Q4_0, O.Q5_0, O.Q5K, O.IQ4XS])
 def test_dequantize_matches_independent_decoder(gtype):
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((4, 512)) * 0.02).astype(np.float32)
-    q = O.quantize(gtype, x)
+    q = weight_bytes(gtype, x, rng)
     got = O.dequantize(gtype, q, x.size).astype(np.float64)
     want = NP_DEQUANT[gtype](q)
     np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-9)
 
 
-@pytest.mark.parametrize("gtype,tol", [(O.Q8_0, 0.006), (O.Q4K, 0.12), (O.Q6K, 0.03), (O.Q8K, 0.012)])
+@pytest.mark.parametrize("gtype,tol", [(O.Q8_0, 0.006), (O.Q4K, 0.12), (O.Q6K, 0.03), (O.Q8K, 0.012), (O.Q4_0, 0.12),
+                                      (O.Q5_0, 0.06), (O.Q5K, 0.06)])
 def test_quantize_round_trip_error(gtype, tol):
     rng = np.random.default_rng(5)
     x = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
@@ -232,7 +295,95 @@ def test_q6k_weight_invariants():
         assert np.uint16(blk["d"]).view(np.float16) != 0
 
 
-@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K])
+def test_q4_0_and_q5_0_quantize_exact_grids_exactly():
+    """Values on the quantization grid (d a power of two, the block's extreme at the grid's negative end) come back
+    as the very integers they were built from (k_quants.rs:380-418, 681-717)."""
+    rng = np.random.default_rng(14)
+    for gtype, levels, off in ((O.Q4_0, 16, 8), (O.Q5_0, 32, 16)):
+        q = rng.integers(0, levels, (6, 32))
+        q[:, 5] = 0                       # max |x| = off * d at a negative value: d = max / -off exactly
+        q[:, 6:][q[:, 6:] == 0] = 1       # and the first such value is the only one
+        d = 2.0 ** -rng.integers(3, 9, 6)
+        x = ((q - off) * d[:, None] * -1.0).astype(np.float32) * -1.0
+        got = O.blocks(gtype, O.quantize(gtype, x.reshape(1, -1)))
+        assert np.array_equal(_f16(got["d"]), d)
+        vals = np.concatenate([got["qs"] & 0xF, got["qs"] >> 4], axis=1).astype(np.int64)
+        if gtype == O.Q5_0:
+            qh = got["qh"].copy().view("<u4")[:, 0]
+            vals += 16 * ((qh[:, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(np.int64)
+        assert np.array_equal(vals, q)
+
+
+def test_q4_0_and_q5_0_quantizer_clamps_the_positive_end():
+    """The value of largest magnitude sets d = max / -8 (-16); a positive extreme lands on q = 0 and the other sign's
+    values saturate at 15 (31), the `min` of the reference's cast."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1] = 1.0, -1.0      # tie: the first (positive) wins, d = -1/8
+    b = O.blocks(O.Q4_0, O.quantize(O.Q4_0, x[None]))[0]
+    assert _f16(b["d"]) == -0.125 and (b["qs"][0] & 0xF) == 0 and (b["qs"][1] & 0xF) == 15
+    b = O.blocks(O.Q5_0, O.quantize(O.Q5_0, x[None]))[0]
+    assert _f16(b["d"]) == -1 / 16 and (b["qs"][0] & 0xF) == 0 and (b["qs"][1] & 0xF) == 15
+    assert b["qh"].copy().view("<u4")[0] & 0b11 == 0b10  # value 1 = 31 has its fifth bit, value 0 = 0 not
+    z = O.blocks(O.Q5_0, O.quantize(O.Q5_0, np.zeros((1, 32), np.float32)))[0]
+    # 0 / -16 = -0.0, so d is f16 -0; id = 0 and every value (0 * 0 + 16.5) -> 16: low nibble 0, fifth bit set
+    assert z["d"] == 0x8000 and (z["qs"] == 0x00).all()
+    assert z["qh"].copy().view("<u4")[0] == 0xFFFFFFFF
+
+
+def test_q5k_is_q4k_plus_the_fifth_bit():
+    """A Q5_K block with qh = 0 dequantizes exactly as the Q4_K block of the same header and nibbles (pinned above),
+    and each qh bit adds 16 * d * scale to its value."""
+    rng = np.random.default_rng(15)
+    raw = O.random_blocks(O.Q5K, 4 * 256, rng)
+    b = O.blocks(O.Q5K, raw)
+    q4 = np.zeros(4, O.BLOCK_DTYPES[O.Q4K])
+    for f in ("d", "dmin", "scales", "qs"):
+        q4[f] = b[f]
+    b0 = b.copy()
+    b0["qh"] = 0
+    assert np.array_equal(O.dequantize(O.Q5K, b0.view(np.uint8), 1024).view(np.uint32),
+                          O.dequantize(O.Q4K, q4.view(np.uint8), 1024).view(np.uint32))
+    full = O.dequantize(O.Q5K, raw, 1024).astype(np.float64)
+    zero = O.dequantize(O.Q5K, b0.view(np.uint8), 1024).astype(np.float64)
+    for i, blk in enumerate(b):
+        s, _ = _q4k_fields(blk)
+        for c in range(4):
+            for half in range(2):
+                bit = (blk["qh"].astype(np.int64) >> (2 * c + half)) & 1
+                idx = 256 * i + 64 * c + 32 * half + np.arange(32)
+                step = _f16(blk["d"]) * s[2 * c + half] * 16
+                np.testing.assert_allclose(full[idx] - zero[idx], bit * step, rtol=1e-6, atol=1e-6 * abs(step) + 1e-30)
+
+
+def test_q5k_weight_invariants():
+    rng = np.random.default_rng(16)
+    x = (rng.standard_normal((8, 1024)) * 0.02).astype(np.float32)
+    b = O.blocks(O.Q5K, O.quantize(O.Q5K, x))
+    for blk in b:
+        s, m = _q4k_fields(blk)
+        assert s.max() == 63 and (m <= 63).all() and _f16(blk["d"]) > 0
+
+
+def test_iq4xs_closed_form():
+    """A hand-built IQ4_XS block: d = 0.5, sub-block ib's scale code 32 + ib + 1 (so ls - 32 = ib + 1; codes above 15
+    use scales_h), value j of sub-block ib = index (j + ib) % 16 of the IQ4_NL table."""
+    blk = np.zeros(1, O.BLOCK_DTYPES[O.IQ4XS])
+    blk["d"] = np.float16(0.5).view(np.uint16)
+    codes = 33 + np.arange(8)
+    sl = np.zeros(4, np.uint8)
+    sh = 0
+    for ib, c in enumerate(codes):
+        sl[ib // 2] |= (c & 0xF) << (4 * (ib % 2))
+        sh |= (int(c) >> 4) << (2 * ib)
+    blk["scales_l"], blk["scales_h"] = sl, sh
+    idx = (np.arange(32)[None, :] + np.arange(8)[:, None]) % 16
+    blk["qs"] = (idx[:, :16] | (idx[:, 16:] << 4)).reshape(-1)
+    got = O.dequantize(O.IQ4XS, blk.view(np.uint8), 256).reshape(8, 32)
+    want = 0.5 * (np.arange(8) + 1)[:, None] * O.KVALUES_IQ4NL[idx]
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q4_0, O.Q5_0, O.Q5K])
 def test_tensor_quantizes_to_its_rows_quantized_alone(gtype):
     """quantized/mod.rs:1720-1765: a whole tensor's bytes equal its rows quantized one at a time."""
     rng = np.random.default_rng(8)
@@ -253,7 +404,7 @@ def brute(gtype, x, wq, n):
     return a @ w.T, np.abs(a) @ np.abs(w).T
 
 
-@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q4_0, O.Q5_0, O.Q5K, O.IQ4XS])
 @pytest.mark.parametrize("k", [256, 512, 1024, 4096])
 def test_matmul_matches_float64_brute_force(gtype, k):
     rng = np.random.default_rng(9 + k)
@@ -261,7 +412,7 @@ def test_matmul_matches_float64_brute_force(gtype, k):
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[:, ::64] *= 60.0  # the outlier pattern of quantized/mod.rs:1775-1850
-    wq = O.quantize(gtype, w)
+    wq = weight_bytes(gtype, w, rng)
     got = O.matmul(gtype, x, wq, n)
     want, terms = brute(gtype, x, wq, n)
     assert np.all(np.abs(got - want) <= 1e-5 * terms + 1e-12)
@@ -293,7 +444,7 @@ def test_brute_force_check_catches_a_planted_min_sign_error():
     assert not np.all(np.abs(got - wrong) <= 1e-5 * terms + 1e-12)
 
 
-@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("gtype", [O.Q4_0, O.Q5_0, O.Q4K, O.Q6K, O.Q8_0, O.Q5K])
 def test_quantized_matmuls_match_their_dequantized_weights(gtype):
     """quantized/mod.rs:1882-1918: Frobenius relative error < 0.02 against the f32 matmul of the dequantized weight."""
     rng = np.random.default_rng(11)
@@ -311,10 +462,10 @@ def test_quantized_matmuls_match_their_dequantized_weights(gtype):
 def test_vec_dot_is_the_matmul_entry():
     rng = np.random.default_rng(12)
     k, n = 1024, 5
-    for gtype in (O.Q4K, O.Q6K, O.Q8_0):
+    for gtype in (O.Q4K, O.Q6K, O.Q8_0, O.Q4_0, O.Q5_0, O.Q5K, O.IQ4XS):
         w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
         x = rng.standard_normal((1, k)).astype(np.float32)
-        wq = O.quantize(gtype, w)
+        wq = weight_bytes(gtype, w, rng)
         aq = O.quantize(O.ACT_TYPE[gtype], x)
         mm = O.matmul(gtype, x, wq, n)
         for c in range(n):
