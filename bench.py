@@ -32,8 +32,9 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published (POP/s)
 SEED = 20261201
 
 Q8_0, Q4K, Q6K = 8, 12, 14
-BS = {Q8_0: 32, Q4K: 256, Q6K: 256}
-TS = {Q8_0: 34, Q4K: 144, Q6K: 210}
+Q4_0, Q5_0, Q5K, IQ4XS = 2, 6, 13, 23
+BS = {Q8_0: 32, Q4K: 256, Q6K: 256, Q4_0: 32, Q5_0: 32, Q5K: 256, IQ4XS: 256}
+TS = {Q8_0: 34, Q4K: 144, Q6K: 210, Q4_0: 18, Q5_0: 22, Q5K: 176, IQ4XS: 136}
 
 
 def log(*a):
@@ -65,8 +66,14 @@ def host_lib():
 
 
 def quantized_weight(gtype, n, k, seed):
-    """N(0, 0.02) f32 weights quantized on the host by the library's QTensor quantizer."""
+    """N(0, 0.02) f32 weights quantized on the host by the library's QTensor quantizer (IQ4_XS, which has no
+    quantizer in the reference: random indices and scale codes under f16 scales of 0.002)."""
     rng = np.random.default_rng(seed)
+    if gtype == IQ4XS:
+        raw = rng.integers(0, 256, n * k // 256 * 136, dtype=np.uint8)
+        d = (rng.uniform(0.5, 1.5, n * k // 256) * 0.002).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        raw.reshape(-1, 136)[:, :2] = d
+        return raw
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
     out = np.empty(n * k // BS[gtype] * TS[gtype], dtype=np.uint8)
     rc = host_lib().qmm_quantize_cpu(gtype, w.ctypes.data, w.size, out.ctypes.data)
@@ -162,7 +169,7 @@ def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
         "kernel_gb_s": kernel_bytes / (t_kernel / steps) / 1e9, "kernel_bytes": kernel_bytes,
         "weights": wq, "x": x.cpu().numpy(), "y": y,
     }
-    if b <= 2 and k <= 4096:
+    if b <= 2 and k <= 4096 and gtype in (Q8_0, Q4K, Q6K):
         t1 = graph_time(torch, one_launch, steps, warmup)
         if not np.array_equal(out.cpu().numpy().view(np.uint32), y.view(np.uint32)):
             raise RuntimeError("one-launch decode differs from the two-launch result")
@@ -343,7 +350,8 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 # ------------------------------------------------------------------------------------------------ main
 
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
-               "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2"}
+               "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
+               "iq4_xs_decode", "q6_k_decode"}
 
 
 def decode_summary(r):
@@ -406,6 +414,17 @@ def main():
                                                       max(20, args.steps // 20), 5, SEED + 11),
         "llama3_8b_linear_stack": lambda: stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20),
         "moe_8x_q4_k_64tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30),
+        # the other weight types at the headline shape, b = 1: the two-launch step and the matvec alone
+        "q6_k_decode": lambda: decode_summary(decode_workload(torch, qmm, Q6K, n, k, 1, 12, args.steps // 2,
+                                                              args.warmup // 2, SEED + 40)),
+        "q4_0_decode": lambda: decode_summary(decode_workload(torch, qmm, Q4_0, n, k, 1, 16, args.steps // 2,
+                                                              args.warmup // 2, SEED + 41)),
+        "q5_0_decode": lambda: decode_summary(decode_workload(torch, qmm, Q5_0, n, k, 1, 16, args.steps // 2,
+                                                              args.warmup // 2, SEED + 42)),
+        "q5_k_decode": lambda: decode_summary(decode_workload(torch, qmm, Q5K, n, k, 1, 16, args.steps // 2,
+                                                              args.warmup // 2, SEED + 43)),
+        "iq4_xs_decode": lambda: decode_summary(decode_workload(torch, qmm, IQ4XS, n, k, 1, 16, args.steps // 2,
+                                                                args.warmup // 2, SEED + 44)),
     }
     assert set(extra_runs) == EXTRA_NAMES
     if args.only:

@@ -6,6 +6,8 @@
 //   Q8_K  k_quants.rs:2721-2760
 //   Q4_K  k_quants.rs:1930-2001 (no imatrix) with utils.rs:268-361 (make_qkx2_quants)
 //   Q6_K  k_quants.rs:2590-2646 (no imatrix) with utils.rs:135-264 (make_qx_quants)
+//   Q5_K  k_quants.rs:2256-2334 (no imatrix): Q4_K's fit with 31 levels and Q5K_SEARCH, fifth bits in qh
+//   Q4_0  k_quants.rs:380-418;  Q5_0  k_quants.rs:681-717
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -152,8 +154,12 @@ float qx16(const float *x, int8_t *ls) {
   return scale;
 }
 
-void q4k_block(const float *x, qmm_block_q4k &b) {
-  std::array<uint8_t, 256> L{};
+// The shared part of Q4_K and Q5_K: per-sub-block affine fits onto 0..nmax, 6-bit scales and mins packed into
+// scales[12] (the inverse of get_scale_min_k4, k_quants.rs:1979-1990), f16 d / dmin, and the final levels L
+// re-quantized against the stored scales.
+template <int NMAX>
+void kquant_levels(const float *x, float rmin, int nstep, uint16_t &d16, uint16_t &dmin16, uint8_t scales[12],
+                   std::array<uint8_t, 256> &L) {
   std::array<float, 8> sc{}, mn{};
   for (int j = 0; j < 8; ++j) {
     const float *xs = x + 32 * j;
@@ -162,7 +168,7 @@ void q4k_block(const float *x, qmm_block_q4k &b) {
     const float rms = std::sqrt(ss / 32.0f);
     float w[32];
     for (int i = 0; i < 32; ++i) w[i] = rms + std::fabs(xs[i]);  // qkx2_weights, k_quants.rs:302-305
-    const Fit<32> f = qkx2(xs, w, 15, -1.0f, 0.1f, 20);        // Q4K_SEARCH, k_quants.rs:245-250
+    const Fit<32> f = qkx2(xs, w, NMAX, rmin, 0.1f, nstep);
     std::copy(f.l.begin(), f.l.end(), L.begin() + 32 * j);
     sc[j] = f.scale;
     mn[j] = f.neg_min;
@@ -174,32 +180,89 @@ void q4k_block(const float *x, qmm_block_q4k &b) {
   }
   const float inv_sc = max_sc > 0.0f ? 63.0f / max_sc : 0.0f;
   const float inv_mn = max_mn > 0.0f ? 63.0f / max_mn : 0.0f;
-  std::memset(&b, 0, sizeof b);
   std::array<uint8_t, 8> ls, lm;
   for (int j = 0; j < 8; ++j) {
     ls[j] = static_cast<uint8_t>(std::min(nearest_int_mul(inv_sc, sc[j]), 63));
     lm[j] = static_cast<uint8_t>(std::min(nearest_int_mul(inv_mn, mn[j]), 63));
   }
-  // 6-bit scale/min packing, the inverse of get_scale_min_k4 (k_quants.rs:1979-1990)
   for (int j = 0; j < 4; ++j) {
-    b.scales[j] = static_cast<uint8_t>(ls[j] | ((ls[j + 4] >> 4) << 6));
-    b.scales[j + 4] = static_cast<uint8_t>(lm[j] | ((lm[j + 4] >> 4) << 6));
-    b.scales[j + 8] = static_cast<uint8_t>((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
+    scales[j] = static_cast<uint8_t>(ls[j] | ((ls[j + 4] >> 4) << 6));
+    scales[j + 4] = static_cast<uint8_t>(lm[j] | ((lm[j + 4] >> 4) << 6));
+    scales[j + 8] = static_cast<uint8_t>((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
   }
-  b.d = f32_to_f16(max_sc / 63.0f);
-  b.dmin = f32_to_f16(max_mn / 63.0f);
-  const float d = f16_to_f32(b.d), dmin = f16_to_f32(b.dmin);
+  d16 = f32_to_f16(max_sc / 63.0f);
+  dmin16 = f32_to_f16(max_mn / 63.0f);
+  const float d = f16_to_f32(d16), dmin = f16_to_f32(dmin16);
   for (int j = 0; j < 8; ++j) {
-    const int s = j < 4 ? (b.scales[j] & 63) : ((b.scales[j + 4] & 0xF) | ((b.scales[j - 4] >> 6) << 4));
-    const int m = j < 4 ? (b.scales[j + 4] & 63) : ((b.scales[j + 4] >> 4) | ((b.scales[j] >> 6) << 4));
+    const int s = j < 4 ? (scales[j] & 63) : ((scales[j + 4] & 0xF) | ((scales[j - 4] >> 6) << 4));
+    const int m = j < 4 ? (scales[j + 4] & 63) : ((scales[j + 4] >> 4) | ((scales[j] >> 6) << 4));
     const float dj = d * static_cast<float>(s);
     if (dj == 0.0f) continue;  // keeps the fit's levels
     const float dm = dmin * static_cast<float>(m);
     for (int i = 0; i < 32; ++i)
-      L[32 * j + i] = static_cast<uint8_t>(std::clamp(nearest_int((x[32 * j + i] + dm) / dj), 0, 15));
+      L[32 * j + i] = static_cast<uint8_t>(std::clamp(nearest_int((x[32 * j + i] + dm) / dj), 0, NMAX));
   }
+}
+
+void q4k_block(const float *x, qmm_block_q4k &b) {
+  std::array<uint8_t, 256> L{};
+  std::memset(&b, 0, sizeof b);
+  kquant_levels<15>(x, -1.0f, 20, b.d, b.dmin, b.scales, L);  // Q4K_SEARCH, k_quants.rs:248-253
   for (int c = 0; c < 4; ++c)
     for (int l = 0; l < 32; ++l) b.qs[32 * c + l] = static_cast<uint8_t>(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+}
+
+void q5k_block(const float *x, qmm_block_q5k &b) {
+  std::array<uint8_t, 256> L{};
+  std::memset(&b, 0, sizeof b);
+  kquant_levels<31>(x, -0.5f, 15, b.d, b.dmin, b.scales, L);  // Q5K_SEARCH, k_quants.rs:254-259
+  for (int c = 0; c < 4; ++c)
+    for (int l = 0; l < 32; ++l) {
+      const uint8_t lo = L[64 * c + l], hi = L[64 * c + 32 + l];
+      b.qs[32 * c + l] = static_cast<uint8_t>((lo & 15) | ((hi & 15) << 4));
+      b.qh[l] |= static_cast<uint8_t>(((lo >> 4) << (2 * c)) | ((hi >> 4) << (2 * c + 1)));
+    }
+}
+
+// Q4_0 / Q5_0: d = (the signed value of largest magnitude, first on a tie) / -levels/2, q = clamp(x / d + off + 0.5)
+// truncated (Rust's saturating casts)
+float absmax_signed32(const float *x) {
+  float amax = 0.0f, mx = 0.0f;
+  for (int i = 0; i < 32; ++i)
+    if (amax < std::fabs(x[i])) {
+      amax = std::fabs(x[i]);
+      mx = x[i];
+    }
+  return mx;
+}
+
+void q4_0_block(const float *x, qmm_block_q4_0 &b) {
+  const float d = absmax_signed32(x) / -8.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  b.d = f32_to_f16(d);
+  auto q = [&](float v) {  // (v * id + 8.5) as u8, then min 15
+    const float t = v * id + 8.5f;
+    const int u = std::isnan(t) || t <= 0.0f ? 0 : t >= 255.0f ? 255 : static_cast<int>(t);
+    return static_cast<uint8_t>(std::min(u, 15));
+  };
+  for (int j = 0; j < 16; ++j) b.qs[j] = static_cast<uint8_t>(q(x[j]) | (q(x[16 + j]) << 4));
+}
+
+void q5_0_block(const float *x, qmm_block_q5_0 &b) {
+  const float d = absmax_signed32(x) / -16.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  b.d = f32_to_f16(d);
+  auto q = [&](float v) {  // ((v * id + 16.5) as i8).min(31) as u8
+    return static_cast<uint8_t>(std::min<int>(as_i8(v * id + 16.5f), 31));
+  };
+  uint32_t qh = 0;
+  for (int j = 0; j < 16; ++j) {
+    const uint8_t a = q(x[j]), c = q(x[16 + j]);
+    b.qs[j] = static_cast<uint8_t>((a & 15) | ((c & 15) << 4));
+    qh |= static_cast<uint32_t>((a >> 4) & 1) << j;
+    qh |= static_cast<uint32_t>((c >> 4) & 1) << (16 + j);
+  }
+  std::memcpy(b.qh, &qh, 4);
 }
 
 void q6k_block(const float *x, qmm_block_q6k &b) {
@@ -331,6 +394,18 @@ bool quantize(GgmlDType t, const float *x, int64_t n, void *out) {
       if (n % 256) return false;
       for_blocks<qmm_block_q8k>(x, n, 256, out, q8k_block);
       return true;
+    case GgmlDType::Q5K:
+      if (n % 256) return false;
+      for_blocks<qmm_block_q5k>(x, n, 256, out, q5k_block);
+      return true;
+    case GgmlDType::Q4_0:
+      if (n % 32) return false;
+      for_blocks<qmm_block_q4_0>(x, n, 32, out, q4_0_block);
+      return true;
+    case GgmlDType::Q5_0:
+      if (n % 32) return false;
+      for_blocks<qmm_block_q5_0>(x, n, 32, out, q5_0_block);
+      return true;
     default: return false;
   }
 }
@@ -381,6 +456,45 @@ bool dequantize(GgmlDType t, const void *blocks, int64_t n, float *y) {
       const auto *b = static_cast<const qmm_block_q8k *>(blocks);
       for (int64_t i = 0; i < n / 256; ++i)
         for (int j = 0; j < 256; ++j) y[256 * i + j] = b[i].d * static_cast<float>(b[i].qs[j]);
+      return true;
+    }
+    case GgmlDType::Q5K: {  // k_quants.rs:2433-2467
+      const auto *b = static_cast<const qmm_block_q5k *>(blocks);
+      for (int64_t i = 0; i < n / 256; ++i) {
+        const float d = f16_to_f32(b[i].d), dmin = f16_to_f32(b[i].dmin);
+        for (int j = 0; j < 8; ++j) {
+          const uint8_t *s = b[i].scales;
+          const int sc = j < 4 ? (s[j] & 63) : ((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+          const int m = j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+          const float d1 = d * static_cast<float>(sc), m1 = dmin * static_cast<float>(m);
+          const int c = j / 2, hi = j & 1;
+          for (int l = 0; l < 32; ++l) {
+            const uint8_t q = b[i].qs[32 * c + l];
+            const int v = (hi ? (q >> 4) : (q & 0xF)) + 16 * ((b[i].qh[l] >> j) & 1);
+            y[256 * i + 32 * j + l] = d1 * static_cast<float>(v) - m1;
+          }
+        }
+      }
+      return true;
+    }
+    case GgmlDType::Q4_0:  // k_quants.rs:313-330
+    case GgmlDType::Q5_0: {  // k_quants.rs:720-743
+      const bool five = t == GgmlDType::Q5_0;
+      const size_t bytes = five ? 22 : 18;
+      const uint8_t *p = static_cast<const uint8_t *>(blocks);
+      for (int64_t i = 0; i < n / 32; ++i, p += bytes) {
+        uint16_t dh;
+        std::memcpy(&dh, p, 2);
+        const float d = f16_to_f32(dh);
+        uint32_t qh = 0;
+        if (five) std::memcpy(&qh, p + 2, 4);
+        const uint8_t *qs = p + (five ? 6 : 2);
+        for (int v = 0; v < 32; ++v) {
+          int q = v < 16 ? (qs[v] & 0xF) : (qs[v - 16] >> 4);
+          if (five) q |= static_cast<int>((qh >> v) & 1) << 4;
+          y[32 * i + v] = static_cast<float>(q - (five ? 16 : 8)) * d;
+        }
+      }
       return true;
     }
     default: return false;

@@ -35,7 +35,7 @@ def quantize(gtype, x):
     return out
 
 
-@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q8K])
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q8K, O.Q4_0, O.Q5_0, O.Q5K])
 @pytest.mark.parametrize("sigma", [0.02, 1.0])
 def test_host_quantizer_matches_the_oracle_bytes(gtype, sigma):
     rng = np.random.default_rng(31 + gtype)
@@ -54,7 +54,7 @@ def test_host_f16_matches_numpy_through_q8_0_scales():
     assert np.array_equal(q["d"], want)
 
 
-@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K])
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4K, O.Q6K, O.Q4_0, O.Q5_0, O.Q5K])
 def test_host_dequantize_matches_the_oracle(gtype):
     rng = np.random.default_rng(33)
     x = (rng.standard_normal(4096) * 0.02).astype(np.float32)
