@@ -62,6 +62,85 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t *__restrict__ vx, co
 
 // ------------------------------------------------------------------------------------------------ persistent form
 
+// Pieces of the one-launch kernel's row loop.  A wave holds two rows' weights, in two buffers that are loaded and
+// used in place: the loop is unrolled by two so that no buffer is ever copied, because a copy of a register that a
+// load is still filling waits for that load, and the wait the compiler places at a loop-carried copy covers every
+// load in flight, the next row's included.  Loads are unconditional, so each wait covers exactly the row about to be
+// used: a row past the end is read through an empty buffer resource (zeros, no memory traffic), and lanes past the
+// last unit re-read the row's last unit.
+template <class U, int S, bool FULL>
+__device__ __forceinline__ void load_row(const uint8_t *vx, int64_t row_bytes, int nunits, int nrows, int r, int lane,
+                                         typename U::W (&w)[S]) {
+  r = __builtin_amdgcn_readfirstlane(r);  // one row per wave: a scalar buffer resource
+  const bool live = r < nrows;
+  const row_buf src = make_row_buf(vx + (int64_t)(live ? r : 0) * row_bytes, live ? row_bytes : 0);
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    const int u = (FULL || lane + 64 * s < nunits) ? lane + 64 * s : nunits - 1;
+    U::load_w(src, u, w[s]);
+  }
+}
+
+// One row's dot products against NC activation rows (held in registers when kRegs, else read from act), per lane.
+template <class U, int NC, int S, bool FULL, bool kRegs>
+__device__ __forceinline__ void row_dots(const typename U::W (&w)[S], const typename U::A *areg, const uint8_t *act,
+                                         int64_t act_row_bytes, int nunits, int lane, float (&acc)[NC]) {
+#pragma unroll
+  for (int j = 0; j < NC; j++) acc[j] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    if (!(FULL || lane + 64 * s < nunits)) continue;
+    const int u = lane + 64 * s;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      if (kRegs) {
+        acc[j] += U::dot(w[s], areg[s * NC + j], u);
+      } else {
+        typename U::A a;
+        U::load_a(act + j * act_row_bytes, u, a);
+        acc[j] += U::dot(w[s], a, u);
+      }
+    }
+  }
+}
+
+// The wave sums of acc.  Every lane stores the same value to the same address (one write): a store under
+// `lane == 63` would sit behind a branch, and the compiler's wait counts after a conditional store assume the
+// worst of both paths, which makes the next row's math wait for loads that are still in flight.
+template <class Out, int NC>
+__device__ __forceinline__ void row_store(const float (&acc)[NC], int lane, typename Out::T *dst, int stride_col_dst,
+                                          int row) {
+  (void)lane;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const float v = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc[j])), 63));
+    Out::store(dst, (int64_t)j * stride_col_dst + row, v);
+  }
+}
+
+// Rows row, row + tw, ... (row < nrows) of one wave with two rows in flight: buffer a holds row r and buffer b row
+// r + tw, both requested before this is called.  Each buffer is reloaded between its row's dot products and the
+// row's store, so no stored value shares a register with a load in flight.
+template <class U, class Out, int NC, int S, bool FULL, bool kRegs>
+__device__ __forceinline__ void row_pairs(const uint8_t *vx, int64_t row_bytes, int nunits, int nrows, int row, int tw,
+                                          int lane, typename U::W (&wa)[S], typename U::W (&wb)[S],
+                                          const typename U::A *areg, const uint8_t *act, int64_t act_row_bytes,
+                                          typename Out::T *dst, int stride_col_dst) {
+  float acc[NC];
+  for (;;) {
+    row_dots<U, NC, S, FULL, kRegs>(wa, areg, act, act_row_bytes, nunits, lane, acc);
+    load_row<U, S, FULL>(vx, row_bytes, nunits, nrows, row + 2 * tw, lane, wa);
+    row_store<Out, NC>(acc, lane, dst, stride_col_dst, row);
+    if (row + tw >= nrows) break;
+    row_dots<U, NC, S, FULL, kRegs>(wb, areg, act, act_row_bytes, nunits, lane, acc);
+    load_row<U, S, FULL>(vx, row_bytes, nunits, nrows, row + 3 * tw, lane, wb);
+    row_store<Out, NC>(acc, lane, dst, stride_col_dst, row + tw);
+    row += 2 * tw;
+    if (row >= nrows) break;
+  }
+}
+
 // Persistent decode matvec: wave w of the grid takes rows w, w + T, w + 2T, ... (T waves in the grid), so a few
 // thousand resident waves keep the HBM queues full, and each wave requests its next row's weights before it
 // does the current row's math.  Lane l owns units l + 64 s (s < S) of every row, so with NC * S <= 2 its
@@ -168,21 +247,13 @@ __global__ __launch_bounds__(64 * NW) void k_mmvq_pq(const uint8_t *__restrict__
     __builtin_memcpy(&f, __builtin_assume_aligned(x + j * stride_x + k0, 4), 16);
     v[t][0] = f.x, v[t][1] = f.y, v[t][2] = f.z, v[t][3] = f.w;
   }
-  // 2. the first two rows' weights, without branches (a row or unit past the end is clamped to the last one and
-  // never used), so the quantization below waits for the f32 loads only
+  // 2. the first two rows' weights, so the quantization below waits for the f32 loads only
   auto has = [&](int s) { return FULL || lane + 64 * s < nunits; };
   const int tw = gridDim.x * NW;
   int row = blockIdx.x * NW + wave;
-  typename U::W w[S], wn[S];
-  {
-    const int64_t r0 = row < nrows ? row : nrows - 1, r1 = row + tw < nrows ? row + tw : nrows - 1;
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-      const int u = has(s) ? lane + 64 * s : nunits - 1;
-      U::load_w(vx + r0 * row_bytes, u, w[s]);
-      U::load_w(vx + r1 * row_bytes, u, wn[s]);
-    }
-  }
+  typename U::W wa[S], wb[S];
+  load_row<U, S, FULL>(vx, row_bytes, nunits, nrows, row, lane, wa);  // a wave with no row reads zeros
+  load_row<U, S, FULL>(vx, row_bytes, nunits, nrows, row + tw, lane, wb);
   __builtin_amdgcn_sched_barrier(0);
   // 3. quantize into LDS
   if constexpr (kQ8K) {
@@ -213,37 +284,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmvq_pq(const uint8_t *__restrict__
       for (int j = 0; j < NC; j++)
         if (has(s)) U::load_a(s_act + j * act_row_bytes, lane + 64 * s, areg[kRegs ? s * NC + j : 0]);
   }
-  // 4. rows row, row + tw, ...; the row after next is requested before each row's math
-  for (; row < nrows; row += tw) {
-    float acc[NC];
-#pragma unroll
-    for (int j = 0; j < NC; j++) acc[j] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-      if (!has(s)) continue;
-      const int u = lane + 64 * s;
-#pragma unroll
-      for (int j = 0; j < NC; j++) {
-        if (kRegs) {
-          acc[j] += U::dot(w[s], areg[s * NC + j], u);
-        } else {
-          typename U::A a;
-          U::load_a(s_act + j * act_row_bytes, u, a);
-          acc[j] += U::dot(w[s], a, u);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NC; j++) {
-      const float r = wave_sum_to_lane63(acc[j]);
-      if (lane == 63) Out::store(dst, (int64_t)j * stride_col_dst + row, r);
-    }
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-      w[s] = wn[s];
-      if (row + 2 * tw < nrows && has(s)) U::load_w(vx + (int64_t)(row + 2 * tw) * row_bytes, lane + 64 * s, wn[s]);
-    }
-  }
+  // 4. rows row, row + tw, ... with two in flight
+  row_pairs<U, Out, NC, S, FULL, kRegs>(vx, row_bytes, nunits, nrows, row, tw, lane, wa, wb, areg, s_act,
+                                        act_row_bytes, dst, stride_col_dst);
 }
 
 // MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's

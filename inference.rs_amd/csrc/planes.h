@@ -11,14 +11,6 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef short s2 __attribute__((ext_vector_type(2)));
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// Buffer resource over [base, base + bytes) (gfx9 raw buffer, dword format): loads past the end return zero.
-__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
-  const int n = bytes > 0x7ffffff0 ? 0x7ffffff0 : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
-}
-
 __device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
 __device__ __forceinline__ v16f mfma_f16(v8h a, v8h b, v16f c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
 

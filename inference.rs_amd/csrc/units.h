@@ -33,6 +33,47 @@ __device__ __forceinline__ u32x4 ld_a4(const uint8_t *p) {
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)__builtin_assume_aligned(p, 4); }
 __device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *(const uint16_t *)__builtin_assume_aligned(p, 2); }
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Buffer resource over [base, base + bytes) (gfx9 raw buffer, dword format): loads past the end return zero.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int n = bytes > 0x7ffffff0 ? 0x7ffffff0 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+// Where a unit's weight loads read: byte offsets o (>= -3) from the start of one weight row.
+//   row_ptr  plain global loads from a row pointer
+//   row_buf  raw buffer loads over the row; an empty buffer (a row past the end) reads zeros with no memory
+//            traffic, so a persistent wave can request "the row after next" unconditionally
+struct row_ptr {
+  const uint8_t *p;
+  __device__ __forceinline__ u32x4 a16(int o) const { return ld_a16(p + o); }
+  __device__ __forceinline__ u32x4 a4x16(int o) const { return ld_a4(p + o); }
+  __device__ __forceinline__ uint32_t x4(int o) const { return ld32(p + o); }
+  __device__ __forceinline__ uint32_t x2(int o) const { return ld16(p + o); }
+  __device__ __forceinline__ uint32_t mis(int o) const { return (uint32_t)((uintptr_t)(p + o) & 3); }
+};
+struct row_buf {
+  rsrc_t r;
+  uint32_t m;  // the row start's address mod 4: the buffer starts m bytes earlier, dword aligned
+  __device__ __forceinline__ u32x4 a16(int o) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(o + (int)m), 0, 0);
+  }
+  __device__ __forceinline__ u32x4 a4x16(int o) const { return a16(o); }
+  __device__ __forceinline__ uint32_t x4(int o) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)(o + (int)m), 0, 0);
+  }
+  __device__ __forceinline__ uint32_t x2(int o) const {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)(o + (int)m), 0, 0);
+  }
+  __device__ __forceinline__ uint32_t mis(int o) const { return (m + (uint32_t)o) & 3; }
+};
+// row: a wave-uniform pointer; bytes 0 for a row that does not exist
+__device__ __forceinline__ row_buf make_row_buf(const uint8_t *row, int64_t bytes) {
+  const uint32_t m = (uint32_t)((uintptr_t)row & 3);
+  return {make_rsrc(row - m, bytes > 0 ? bytes + m : 0), m};
+}
+
 // ------------------------------------------------------------------------------------------------ Q4_K
 struct unit_q4k {
   static constexpr int kType = QMM_TYPE_Q4K;
@@ -51,13 +92,14 @@ struct unit_q4k {
     float d;
   };
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *p = row + (int64_t)(u >> 2) * 144;
-    const int c = u & 3;
-    w.hdr = ld_a16(p);
-    w.q0 = ld_a16(p + 16 + 32 * c);
-    w.q1 = ld_a16(p + 32 + 32 * c);
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int o = (u >> 2) * 144, c = u & 3;
+    w.hdr = r.a16(o);
+    w.q0 = r.a16(o + 16 + 32 * c);
+    w.q1 = r.a16(o + 32 + 32 * c);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
 
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     const uint8_t *p = row + (int64_t)(u >> 2) * 292;
@@ -141,21 +183,23 @@ struct unit_q6k {
     out[3] = align_bytes(e, v.w, off);
   }
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *sb = row + (int64_t)(u >> 2) * 210;
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int sb = (u >> 2) * 210;
     const int h = (u >> 1) & 1, p = u & 1;
-    w.off = (uint32_t)((uintptr_t)sb & 3);
-    const uint8_t *a4 = sb - w.off;
-    w.qa = ld_a4(a4 + 64 * h + 16 * p);
-    w.ea = ld32(a4 + 64 * h + 16 * p + 16);
-    w.qb = ld_a4(a4 + 64 * h + 32 + 16 * p);
-    w.eb = ld32(a4 + 64 * h + 32 + 16 * p + 16);
-    w.qh = ld_a4(a4 + 128 + 32 * h + 16 * p);
-    w.eh = ld32(a4 + 128 + 32 * h + 16 * p + 16);
+    w.off = r.mis(sb);
+    const int a4 = sb - (int)w.off;
+    w.qa = r.a4x16(a4 + 64 * h + 16 * p);
+    w.ea = r.x4(a4 + 64 * h + 16 * p + 16);
+    w.qb = r.a4x16(a4 + 64 * h + 32 + 16 * p);
+    w.eb = r.x4(a4 + 64 * h + 32 + 16 * p + 16);
+    w.qh = r.a4x16(a4 + 128 + 32 * h + 16 * p);
+    w.eh = r.x4(a4 + 128 + 32 * h + 16 * p + 16);
 #pragma unroll
-    for (int q = 0; q < 4; q++) w.sc[q] = ld16(sb + 192 + 8 * h + 2 * q);
-    w.d = ld16(sb + 208);
+    for (int q = 0; q < 4; q++) w.sc[q] = r.x2(sb + 192 + 8 * h + 2 * q);
+    w.d = r.x2(sb + 208);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
 
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     const uint8_t *p0 = row + (int64_t)(u >> 2) * 292;
@@ -238,7 +282,20 @@ struct unit_q8_0 {
     for (int i = 0; i < 8; i++) a.qb[i] = dw[9 + i];
   }
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_raw(row + (int64_t)u * 68, w.dw); }
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int o = u * 68;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const u32x4 v = r.a4x16(o + 16 * i);
+      w.dw[4 * i] = v.x;
+      w.dw[4 * i + 1] = v.y;
+      w.dw[4 * i + 2] = v.z;
+      w.dw[4 * i + 3] = v.w;
+    }
+    w.dw[16] = r.x4(o + 64);
+  }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     uint32_t dw[17];
     load_raw(row + (int64_t)u * 68, dw);
@@ -285,7 +342,12 @@ struct unit_q8_0_odd {
 #pragma unroll
     for (int i = 0; i < 8; i++) a.q[i] = h[1 + 2 * i] | (h[2 + 2 * i] << 16);
   }
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_raw(row + (int64_t)u * 34, w.h); }
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+#pragma unroll
+    for (int i = 0; i < 17; i++) w.h[i] = r.x2(u * 34 + 2 * i);
+  }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     uint32_t h[17];
     load_raw(row + (int64_t)u * 34, h);
@@ -354,19 +416,21 @@ struct unit_b32 {
     uint32_t dw[F::kPairDwords];
   };
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *p = row + (int64_t)u * (2 * F::kBytes);
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int o = u * (2 * F::kBytes);
 #pragma unroll
     for (int i = 0; i + 4 <= F::kPairDwords; i += 4) {
-      const u32x4 v = ld_a4(p + 4 * i);
+      const u32x4 v = r.a4x16(o + 4 * i);
       w.dw[i] = v.x;
       w.dw[i + 1] = v.y;
       w.dw[i + 2] = v.z;
       w.dw[i + 3] = v.w;
     }
 #pragma unroll
-    for (int i = F::kPairDwords / 4 * 4; i < F::kPairDwords; i++) w.dw[i] = ld32(p + 4 * i);
+    for (int i = F::kPairDwords / 4 * 4; i < F::kPairDwords; i++) w.dw[i] = r.x4(o + 4 * i);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     typename unit_q8_0::A q;
     unit_q8_0::load_a(row, u, q);
@@ -431,11 +495,12 @@ struct unit_b32_odd {
   struct W {
     uint32_t h[F::kBytes / 2];
   };
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *p = row + (int64_t)u * F::kBytes;
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
 #pragma unroll
-    for (int i = 0; i < F::kBytes / 2; i++) w.h[i] = ld16(p + 2 * i);
+    for (int i = 0; i < F::kBytes / 2; i++) w.h[i] = r.x2(u * F::kBytes + 2 * i);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
     typename unit_q8_0_odd::A q;
     unit_q8_0_odd::load_a(row, u, q);
@@ -476,15 +541,16 @@ struct unit_q5k {
   };
   using A = unit_q4k::A;
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *p = row + (int64_t)(u >> 2) * 176;
-    const int c = u & 3;
-    w.hdr = ld_a16(p);
-    w.h0 = ld_a16(p + 16);
-    w.h1 = ld_a16(p + 32);
-    w.q0 = ld_a16(p + 48 + 32 * c);
-    w.q1 = ld_a16(p + 64 + 32 * c);
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int o = (u >> 2) * 176, c = u & 3;
+    w.hdr = r.a16(o);
+    w.h0 = r.a16(o + 16);
+    w.h1 = r.a16(o + 32);
+    w.q0 = r.a16(o + 48 + 32 * c);
+    w.q1 = r.a16(o + 64 + 32 * c);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k::load_a(row, u, a); }
 
   static __device__ __forceinline__ float dot(const W &w, const A &a, int u) {
@@ -528,14 +594,15 @@ struct unit_iq4xs {
   };
   using A = unit_q4k::A;
 
-  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) {
-    const uint8_t *p = row + (int64_t)(u >> 2) * 136;
-    const int c = u & 3;
-    w.h0 = ld32(p);
-    w.h1 = ld32(p + 4);
-    w.q0 = ld_a4(p + 8 + 32 * c);
-    w.q1 = ld_a4(p + 24 + 32 * c);
+  template <class Src>
+  static __device__ __forceinline__ void load_w(const Src &r, int u, W &w) {
+    const int o = (u >> 2) * 136, c = u & 3;
+    w.h0 = r.x4(o);
+    w.h1 = r.x4(o + 4);
+    w.q0 = r.a4x16(o + 8 + 32 * c);
+    w.q1 = r.a4x16(o + 24 + 32 * c);
   }
+  static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
   static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k::load_a(row, u, a); }
 
   // the IQ4_NL table (raw.rs:13-15) as int8 bytes: entries 0-3, 4-7, 8-11, 12-15
