@@ -510,9 +510,12 @@ void launch_pq_nw(const uint8_t *vx, const float *x, int64_t stride_x, typename 
   const int64_t wgs = qmm_ceil_div(nrows, NW);
   const size_t lds = (size_t)NC * nblk * U::kActBlockBytes;
   const int64_t rb = U::row_bytes(k);
-  // at most two resident workgroups per CU (fewer when the kernel's registers allow only one)
+  // Resident workgroups per CU: one for the 8-wave form (tall weights: 7 rows per wave at 14336 rows, so the two-row
+  // pipeline of each wave runs long; two measured 3% slower on MI355X), two for the 16-wave form (short weights),
+  // fewer when the kernel's registers allow only one.
+  const int kCap = NW == 8 ? 1 : 2;
   auto grid = [&](int per_cu) {
-    const int64_t cap = (int64_t)(per_cu < 2 ? per_cu : 2) * qmm_device_cus();
+    const int64_t cap = (int64_t)(per_cu < kCap ? per_cu : kCap) * qmm_device_cus();
     return dim3((unsigned)(wgs < cap ? wgs : cap));
   };
 #define QMM_PQ_F(FF, GG)                                                                                            \
