@@ -145,6 +145,12 @@ QMM_DECLARE_MMVQ_FUSED(q6_k)
 QMM_DECLARE_MMVQ_MOE(q8_0)
 QMM_DECLARE_MMVQ_MOE(q4_k)
 QMM_DECLARE_MMVQ_MOE(q6_k)
+/* the adjacent types (the reference's gguf_type_library! blocks, gguf/ffi.rs:879-893), activations as for their
+ * _plain launchers */
+QMM_DECLARE_MMVQ_MOE(q4_0)
+QMM_DECLARE_MMVQ_MOE(q5_0)
+QMM_DECLARE_MMVQ_MOE(q5_k)
+QMM_DECLARE_MMVQ_MOE(iq4_xs)
 
 /* ------------------------------------------------------------------ prefill activation quantizers
  * Replace launch_mmq_quantize_q8_1_{D4,DS4,D2S6} (gguf/ffi.rs:657-700; kernel mmq_gguf/mmq_quantize.cu:
@@ -203,6 +209,17 @@ void launch_indexed_moe_forward_q4k_q8k(const void *all_weights, const void *all
                                         float *all_outputs, int n, int k, int batch, int topk, int k_padded,
                                         int input_dim1, void *stream);
 void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream);
+/* launch_indexed_moe_forward_{q4_0,q5_0,q5k}_q8_1 (gguf/ffi.rs:105-119, 150-164, 180-194), likewise, with Q8_0
+ * activations for q4_0 / q5_0 and Q8_K for q5k */
+void launch_indexed_moe_forward_q4_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream);
+void launch_indexed_moe_forward_q5_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream);
+void launch_indexed_moe_forward_q5k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
                                         float *all_outputs, int n, int k, int batch, int topk, int k_padded,
                                         int input_dim1, void *stream);
 

@@ -633,6 +633,44 @@ void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride
       moe_launch<unit_q6k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
                            (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
       break;
+    case QMM_TYPE_Q5K:
+      if (expert_stride % 16 != 0 || (vx_up && (uintptr_t)vx_up % 16 != 0)) {
+        qmm_set_error("%s: Q5_K expert_stride / vx_up not 16-byte aligned", who);
+        return;
+      }
+      moe_launch<unit_q5k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
+      break;
+    case QMM_TYPE_IQ4_XS:
+      if (expert_stride % 4 != 0 || (vx_up && (uintptr_t)vx_up % 4 != 0)) {
+        qmm_set_error("%s: IQ4_XS expert_stride / vx_up not 4-byte aligned", who);
+        return;
+      }
+      moe_launch<unit_iq4xs>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
+                             (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
+      break;
+    case QMM_TYPE_Q4_0:
+    case QMM_TYPE_Q5_0: {
+      const bool pairs = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
+                         (uintptr_t)vx_gate % 4 == 0 && (!vx_up || (uintptr_t)vx_up % 4 == 0) && (uintptr_t)vy % 4 == 0;
+      const int64_t ay = (int64_t)stride_col_y * 34;
+      if (type == QMM_TYPE_Q4_0) {
+        if (pairs)
+          moe_launch<unit_b32<QMM_TYPE_Q4_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div,
+                                              n_pairs, activation, s);
+        else
+          moe_launch<unit_b32_odd<QMM_TYPE_Q4_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay,
+                                                  y_div, n_pairs, activation, s);
+      } else {
+        if (pairs)
+          moe_launch<unit_b32<QMM_TYPE_Q5_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div,
+                                              n_pairs, activation, s);
+        else
+          moe_launch<unit_b32_odd<QMM_TYPE_Q5_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay,
+                                                  y_div, n_pairs, activation, s);
+      }
+      break;
+    }
     default: {
       const bool fast = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
                         (uintptr_t)vx_gate % 4 == 0 && (!vx_up || (uintptr_t)vx_up % 4 == 0) && (uintptr_t)vy % 4 == 0;
@@ -652,7 +690,7 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
     qmm_set_error("%s: batch=%d topk=%d input_dim1=%d k=%d k_padded=%d", who, batch, topk, input_dim1, k, k_padded);
     return;
   }
-  const int abs_ = type == QMM_TYPE_Q8_0 ? 32 : 256;
+  const int abs_ = (int)qmm_block_size(qmm_vec_dot_type(type));
   if (k_padded % abs_ != 0) {
     qmm_set_error("%s: k_padded=%d not a multiple of %d", who, k_padded, abs_);
     return;
@@ -679,6 +717,15 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
                                          int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
     plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
                     "mmvq_" #t "_bf16");                                                                          \
+  }
+
+#define QMM_DEFINE_MOE(t, TYPE)                                                                                   \
+  void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy,  \
+                                  const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \
+                                  int y_div, int n_pairs, int activation, int grouped, void *stream) {            \
+    (void)grouped;                                                                                                \
+    moe(TYPE, vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, stride_col_y, y_div, n_pairs,        \
+        activation, stream, "mmvq_" #t "_moe");                                                                   \
   }
 
 #define QMM_DEFINE_PLAIN(t, TYPE)                                                                                 \
@@ -731,6 +778,10 @@ QMM_DEFINE_PLAIN_ONLY(q4_0, QMM_TYPE_Q4_0)
 QMM_DEFINE_PLAIN_ONLY(q5_0, QMM_TYPE_Q5_0)
 QMM_DEFINE_PLAIN_ONLY(q5_k, QMM_TYPE_Q5K)
 QMM_DEFINE_PLAIN_ONLY(iq4_xs, QMM_TYPE_IQ4_XS)
+QMM_DEFINE_MOE(q4_0, QMM_TYPE_Q4_0)
+QMM_DEFINE_MOE(q5_0, QMM_TYPE_Q5_0)
+QMM_DEFINE_MOE(q5_k, QMM_TYPE_Q5K)
+QMM_DEFINE_MOE(iq4_xs, QMM_TYPE_IQ4_XS)
 
 void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
                                           float *all_outputs, int n, int k, int batch, int topk, int k_padded,
@@ -749,6 +800,24 @@ void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all
                                         int input_dim1, void *stream) {
   indexed(QMM_TYPE_Q6K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
           stream, "indexed_moe_q6k");
+}
+void launch_indexed_moe_forward_q4_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q4_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q4_0");
+}
+void launch_indexed_moe_forward_q5_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                          int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q5_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q5_0");
+}
+void launch_indexed_moe_forward_q5k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
+                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
+                                        int input_dim1, void *stream) {
+  indexed(QMM_TYPE_Q5K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
+          stream, "indexed_moe_q5k");
 }
 }
 

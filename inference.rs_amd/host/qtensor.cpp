@@ -154,6 +154,9 @@ indexed_fn indexed_moe(GgmlDType w) {
     case GgmlDType::Q8_0: return launch_indexed_moe_forward_q8_0_q8_0;
     case GgmlDType::Q4K: return launch_indexed_moe_forward_q4k_q8k;
     case GgmlDType::Q6K: return launch_indexed_moe_forward_q6k_q8k;
+    case GgmlDType::Q4_0: return launch_indexed_moe_forward_q4_0_q8_0;
+    case GgmlDType::Q5_0: return launch_indexed_moe_forward_q5_0_q8_0;
+    case GgmlDType::Q5K: return launch_indexed_moe_forward_q5k_q8k;
     default: throw Error("gather_forward: unsupported weight type");
   }
 }
@@ -164,7 +167,7 @@ int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
 int64_t act_block_bytes(GgmlDType w) { return act_q8_0(w) ? 34 : 292; }
 int64_t tile_bytes_per_256(GgmlDType w) { return w == GgmlDType::Q8_0 ? 272 : 292; }
 
-// matvec_only: the route needs the decode matvec alone (QMatMul::forward); else every route
+// matvec_only: the route needs the decode matvec kernels alone (QMatMul::forward, gather_forward); else every route
 void check_weight(const QTensor &w, const char *who, bool matvec_only = false) {
   if (!w.device().is_hip()) throw Error(std::string(who) + ": the weight is not on a HIP device");
   const GgmlDType t = w.dtype();
@@ -376,7 +379,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
 void QMatMul::gather_forward(const float *xs, int64_t batch, int64_t xdim1, const uint32_t *ids, int64_t topk,
                              float *ys, hipStream_t stream) const {
   const QTensor &w = *w_;
-  check_weight(w, "QMatMul::gather_forward");
+  check_weight(w, "QMatMul::gather_forward", true);
   if (w.shape().size() != 3) throw Error("gather_forward: the weight must be [experts, rows, cols]");
   if (xdim1 != 1 && xdim1 != topk) throw Error("gather_forward: x's second dim must be 1 or topk");
   if (batch <= 0 || topk <= 0) return;

@@ -30,7 +30,7 @@ TYPE_SIZE = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292, Q4_0: 18, Q5_0: 22, Q5K: 17
 ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K, Q4_0: Q8_0, Q5_0: Q8_0, Q5K: Q8K, IQ4XS: Q8K}
 TYPE_NAME = {Q8_0: "q8_0", Q4K: "q4_k", Q6K: "q6_k"}
 ADJ_TYPE_NAME = {Q4_0: "q4_0", Q5_0: "q5_0", Q5K: "q5_k", IQ4XS: "iq4_xs"}
-MOE_NAME = {Q8_0: "q8_0_q8_0", Q4K: "q4k_q8k", Q6K: "q6k_q8k"}
+MOE_NAME = {Q8_0: "q8_0_q8_0", Q4K: "q4k_q8k", Q6K: "q6k_q8k", Q4_0: "q4_0_q8_0", Q5_0: "q5_0_q8_0", Q5K: "q5k_q8k"}
 
 _lib = None
 
@@ -103,6 +103,8 @@ def _declare(L: ctypes.CDLL) -> None:
     for t in ADJ_TYPE_NAME.values():
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+        getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                                            i32, vp]
     for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k"]:
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_dequantize_{t}_{o}").argtypes = [vp, vp, i64, vp]
@@ -251,7 +253,7 @@ def mmvq_moe(wtype: int, w_gate, w_up, expert_stride: int, vy, ids, k: int, n: i
     torch = _torch()
     if out is None:
         out = torch.empty((n_pairs, n), dtype=torch.float32, device=w_gate.device)
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_moe")(
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
         _ptr(w_gate), _ptr(w_up), expert_stride, _ptr(vy), _ptr(ids), _ptr(out), k, n,
         kp // BLOCK_SIZE[ACT_TYPE[wtype]], y_div, n_pairs, activation, 1, _stream())
     check()

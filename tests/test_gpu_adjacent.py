@@ -140,3 +140,40 @@ def test_adjacent_get_rows(gtype):
     got = qmm.get_rows(gtype, to_dev(wq.reshape(-1)), to_dev(ids), k, wq.shape[1]).cpu().numpy()
     want = O.dequantize(gtype, wq, rows * k).reshape(rows, k)[ids]
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("gtype", TYPES)
+@pytest.mark.parametrize("glu", [False, True])
+def test_adjacent_moe_matvec(gtype, glu):
+    """launch_mmvq_gguf_<t>_moe: routed pairs against the oracle's per-route matmul (and the GLU form)."""
+    rng = np.random.default_rng(51 + gtype + 7 * glu)
+    E, n, k, tokens, topk = 4, 96, 512, 3, 2
+    wg = weight_bytes(gtype, E * n, k, rng).reshape(E, -1)
+    wu = weight_bytes(gtype, E * n, k, rng).reshape(E, -1)
+    x = acts(rng, tokens, k)
+    ids = np.array([[0, 3], [2, 2], [1, 0]], np.uint32)
+    vy, kp = qmm.quantize_decode(gtype, to_dev(x))
+    out = qmm.mmvq_moe(gtype, to_dev(wg), to_dev(wu) if glu else None, wg.shape[1], vy, to_dev(ids.reshape(-1)), k,
+                       n, kp, topk, tokens * topk, 0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(tokens, topk, n)
+    g = O.indexed_moe(gtype, wg, E, n, k, x[:, None, :], ids)
+    if glu:
+        u = O.indexed_moe(gtype, wu, E, n, k, x[:, None, :], ids)
+        want = g / (1 + np.exp(-g.astype(np.float64))) * u  # SiLU(gate) * up
+        assert_parity(got, want, rel=1e-4, what=f"moe glu type {gtype}")
+    else:
+        assert_parity(got, g, what=f"moe type {gtype}")
+
+
+@pytest.mark.parametrize("gtype", [O.Q4_0, O.Q5_0, O.Q5K])
+@pytest.mark.parametrize("xdim1", [1, 2])
+def test_adjacent_indexed_moe(gtype, xdim1):
+    rng = np.random.default_rng(61 + gtype + xdim1)
+    E, n, k, batch, topk = 3, 64, 768 if gtype == O.Q5K else 160, 4, 2
+    w = weight_bytes(gtype, E * n, k, rng).reshape(E, -1)
+    x = acts(rng, batch * xdim1, k).reshape(batch, xdim1, k)
+    ids = rng.integers(0, E, (batch, topk)).astype(np.uint32)
+    got = qmm.indexed_moe(gtype, to_dev(w), to_dev(x), to_dev(ids), n).cpu().numpy()
+    want = O.indexed_moe(gtype, w, E, n, k, x, ids)
+    assert_parity(got, want, what=f"indexed type {gtype} xdim1={xdim1}")
