@@ -267,10 +267,11 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     return res
 
 
-def moe_workload(torch, qmm, steps, warmup, seed):
-    """8 experts, gate/up Q4_K 14336x4096 and down Q4_K 4096x14336; 64 tokens, top-2 from softmax(N(0,1) logits)
-    (Mixtral renormalisation); the grouped prefill path of the MoE experts block."""
-    E, hidden, inter, tokens, topk = 8, 4096, 14336, 64, 2
+def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
+    """8 experts, gate/up Q4_K 14336x4096 and down Q4_K 4096x14336; `tokens` tokens, top-2 from softmax(N(0,1)
+    logits) (Mixtral renormalisation): the grouped prefill path of the MoE experts block at 64 tokens, the indexed
+    decode path (gate/up GLU matvec, then down with the weighted sum folded in) at 8 or fewer."""
+    E, hidden, inter, topk = 8, 4096, 14336, 2
     H = host_lib()
     gate = quantized_weight(Q4K, inter, hidden, seed)
     up = quantized_weight(Q4K, inter, hidden, seed + 1)
@@ -305,7 +306,8 @@ def moe_workload(torch, qmm, steps, warmup, seed):
     st = max(4, steps // 10)
     t = graph_time(torch, step, st, 2)
     per = t / st
-    wbytes = 3 * E * gate.size
+    # weight bytes the step must read: every expert at 64 tokens; at decode sizes only the experts routed to
+    wbytes = 3 * len(np.unique(ids)) * gate.size
     ops = 2.0 * tokens * topk * 3 * inter * hidden
     return {"ms_per_step": per * 1e3, "weight_bytes": wbytes, "gb_s": wbytes / per / 1e9,
             "frac_hbm_peak": wbytes / per / 1e9 / HBM_PEAK_GBS, "tops": ops / per / 1e12}
@@ -351,7 +353,7 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
                "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
-               "iq4_xs_decode", "q6_k_decode"}
+               "iq4_xs_decode", "q6_k_decode", "moe_8x_q4_k_4tok_top2"}
 
 
 def decode_summary(r):
@@ -414,6 +416,7 @@ def main():
                                                       max(20, args.steps // 20), 5, SEED + 11),
         "llama3_8b_linear_stack": lambda: stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20),
         "moe_8x_q4_k_64tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30),
+        "moe_8x_q4_k_4tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 31, tokens=4),
         # the other weight types at the headline shape, b = 1: the two-launch step and the matvec alone
         "q6_k_decode": lambda: decode_summary(decode_workload(torch, qmm, Q6K, n, k, 1, 12, args.steps // 2,
                                                               args.warmup // 2, SEED + 40)),

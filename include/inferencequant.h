@@ -152,6 +152,20 @@ QMM_DECLARE_MMVQ_MOE(q5_0)
 QMM_DECLARE_MMVQ_MOE(q5_k)
 QMM_DECLARE_MMVQ_MOE(iq4_xs)
 
+/* launch_mmvq_gguf_<t>_moe_wsum: no counterpart in the reference, whose MoE decode runs the down projection
+ * (launch_mmvq_gguf_<t>_moe) and then the weighted sum over a token's routes (launch_moe_weighted_reduce_flat;
+ * inference-nn/src/moe/experts/backends.rs:2418, gguf/cuda.rs:627-1000) as two launches.  This is the two in one:
+ * dst[t * nrows_x + row] = sum over s < topk, in order, of weights[t * topk + s] * (W[ids[t * topk + s]][row] .
+ * y[t * topk + s]) for t < n_tokens, with the same arithmetic as the two launches; a route of weight zero is not
+ * read.  vy holds n_tokens * topk activation rows (stride_col_y blocks apart), ids u32. */
+#define QMM_DECLARE_MMVQ_MOE_WSUM(t)                                                                          \
+  void launch_mmvq_gguf_##t##_moe_wsum(const void *vx, int64_t expert_stride, const void *vy, const void *ids, \
+                                       const float *weights, float *dst, int ncols_x, int nrows_x,             \
+                                       int stride_col_y, int n_tokens, int topk, void *stream);
+QMM_DECLARE_MMVQ_MOE_WSUM(q8_0)
+QMM_DECLARE_MMVQ_MOE_WSUM(q4_k)
+QMM_DECLARE_MMVQ_MOE_WSUM(q6_k)
+
 /* ------------------------------------------------------------------ prefill activation quantizers
  * Replace launch_mmq_quantize_q8_1_{D4,DS4,D2S6} (gguf/ffi.rs:657-700; kernel mmq_gguf/mmq_quantize.cu:
  * 98-195, 395-415), same arguments: x of type_x (0 f32, 1 f16, 30 bf16); output row i1 < ne1 of channel

@@ -333,6 +333,50 @@ __global__ __launch_bounds__(256) void k_mmvq_moe(const uint8_t *__restrict__ vx
   }
 }
 
+// The MoE down projection with the weighted sum over a token's routes folded in: grid (tokens, row groups);
+// dst[t * nrows + row] = sum over s < topk, in order, of w[t, s] * (W[ids[t, s]] . y[t * topk + s]).  Each route's
+// dot is the same per-lane sum and wave reduction as k_mmvq_moe's, and the sum over routes is the same expression,
+// in the same order, as the standalone weighted reduce, so the result equals the two-kernel sequence's.  A route of
+// weight zero is skipped, as the reduce skips reading it.
+template <class U, int R>
+__global__ __launch_bounds__(256) void k_mmvq_moe_wsum(const uint8_t *__restrict__ vx, int64_t expert_stride,
+                                                       const uint8_t *__restrict__ vy, const uint32_t *__restrict__ ids,
+                                                       const float *__restrict__ weights, float *__restrict__ dst,
+                                                       int nrows, int64_t row_bytes, int nunits, int64_t act_row_bytes,
+                                                       int topk) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  const int row0 = (blockIdx.y * kWaves + (threadIdx.x >> 6)) * R;
+  if (row0 >= nrows) return;
+  float out[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) out[r] = 0.0f;
+  for (int sl = 0; sl < topk; sl++) {
+    const int64_t pair = (int64_t)t * topk + sl;
+    const float ws = weights[pair];
+    if (ws == 0.0f) continue;  // uniform over the workgroup
+    const uint8_t *w = vx + (int64_t)ids[pair] * expert_stride;
+    const uint8_t *act = vy + pair * act_row_bytes;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int u = lane; u < nunits; u += QMM_WAVE) {
+      typename U::W wr[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) U::load_w(w + (int64_t)min(row0 + r, nrows - 1) * row_bytes, u, wr[r]);
+      typename U::A a;
+      U::load_a(act, u, a);
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r] += U::dot(wr[r], a, u);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) out[r] += wave_sum_to_lane63(acc[r]) * ws;
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if (lane == 63 && row0 + r < nrows) dst[(int64_t)t * nrows + row0 + r] = out[r];
+}
+
 template <class U, class Out, int NC>
 void launch_nc(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
                int stride_col_dst, hipStream_t s) {
@@ -684,6 +728,54 @@ void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride
   }
 }
 
+template <class U>
+void moe_wsum_launch(const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
+                     float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int n_tokens, int topk,
+                     hipStream_t s) {
+  constexpr int R = 2;  // as moe_launch, so each route's dot is the same sum
+  const dim3 grid((unsigned)n_tokens, (unsigned)qmm_ceil_div(nrows_x, kWaves * R));
+  k_mmvq_moe_wsum<U, R><<<grid, 256, 0, s>>>((const uint8_t *)vx, expert_stride, (const uint8_t *)vy,
+                                             (const uint32_t *)ids, weights, dst, nrows_x, U::row_bytes(ncols_x),
+                                             U::units(ncols_x), act_row_bytes, topk);
+}
+
+void moe_wsum(int type, const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
+              float *dst, int ncols_x, int nrows_x, int stride_col_y, int n_tokens, int topk, void *stream,
+              const char *who) {
+  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, stride_col_y, 1)) return;
+  if (n_tokens < 0 || n_tokens > 65535 * 1024 || topk <= 0 || expert_stride < 0 || !weights) {
+    qmm_set_error("%s: n_tokens=%d topk=%d expert_stride=%lld weights=%p", who, n_tokens, topk,
+                  (long long)expert_stride, (const void *)weights);
+    return;
+  }
+  if (n_tokens == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  switch (type) {
+    case QMM_TYPE_Q4K:
+      if (expert_stride % 16 != 0) {
+        qmm_set_error("%s: Q4_K expert_stride not 16-byte aligned", who);
+        return;
+      }
+      moe_wsum_launch<unit_q4k>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
+                                (int64_t)stride_col_y * 292, n_tokens, topk, s);
+      break;
+    case QMM_TYPE_Q6K:
+      moe_wsum_launch<unit_q6k>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
+                                (int64_t)stride_col_y * 292, n_tokens, topk, s);
+      break;
+    default: {  // Q8_0
+      const bool fast = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
+                        (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0;
+      if (fast)
+        moe_wsum_launch<unit_q8_0>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
+                                   (int64_t)stride_col_y * 34, n_tokens, topk, s);
+      else
+        moe_wsum_launch<unit_q8_0_odd>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
+                                       (int64_t)stride_col_y * 34, n_tokens, topk, s);
+    }
+  }
+}
+
 void indexed(int type, const void *w, const void *x, const uint32_t *ids, float *out, int n, int k, int batch,
              int topk, int k_padded, int input_dim1, void *stream, const char *who) {
   if (batch < 0 || topk <= 0 || (input_dim1 != 1 && input_dim1 != topk) || k_padded < k) {
@@ -782,6 +874,18 @@ QMM_DEFINE_MOE(q4_0, QMM_TYPE_Q4_0)
 QMM_DEFINE_MOE(q5_0, QMM_TYPE_Q5_0)
 QMM_DEFINE_MOE(q5_k, QMM_TYPE_Q5K)
 QMM_DEFINE_MOE(iq4_xs, QMM_TYPE_IQ4_XS)
+
+#define QMM_DEFINE_MOE_WSUM(t, TYPE)                                                                              \
+  void launch_mmvq_gguf_##t##_moe_wsum(const void *vx, int64_t expert_stride, const void *vy, const void *ids,    \
+                                       const float *weights, float *dst, int ncols_x, int nrows_x,                \
+                                       int stride_col_y, int n_tokens, int topk, void *stream) {                  \
+    moe_wsum(TYPE, vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x, stride_col_y, n_tokens, topk,      \
+             stream, "mmvq_" #t "_moe_wsum");                                                                     \
+  }
+QMM_DEFINE_MOE_WSUM(q8_0, QMM_TYPE_Q8_0)
+QMM_DEFINE_MOE_WSUM(q4_k, QMM_TYPE_Q4K)
+QMM_DEFINE_MOE_WSUM(q6_k, QMM_TYPE_Q6K)
+#undef QMM_DEFINE_MOE_WSUM
 
 void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
                                           float *all_outputs, int n, int k, int batch, int topk, int k_padded,

@@ -149,6 +149,17 @@ mmvq_moe_fn decode_matvec_moe(GgmlDType w) {
   }
 }
 
+typedef void (*mmvq_moe_wsum_fn)(const void *, int64_t, const void *, const void *, const float *, float *, int, int,
+                                 int, int, int, void *);
+mmvq_moe_wsum_fn decode_matvec_moe_wsum(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe_wsum;
+    case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_moe_wsum;
+    case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_moe_wsum;
+    default: throw Error("MoE: unsupported weight type");
+  }
+}
+
 indexed_fn indexed_moe(GgmlDType w) {
   switch (w) {
     case GgmlDType::Q8_0: return launch_indexed_moe_forward_q8_0_q8_0;
@@ -423,13 +434,12 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   const GgmlDType tg = gate_->dtype(), td = down_->dtype();
   const bool grouped = force_grouped || tokens > kIndexedMaxTokens;
   if (!grouped) {
-    // decode: fused gate/up matvec per routed pair, then down, then the weighted sum over slots
+    // decode: fused gate/up matvec per routed pair, then down with the weighted sum over slots folded in
     const int64_t kp1 = pad_to(hidden, act_block(tg)), kp2 = pad_to(inter, act_block(td));
     Carver c;
     const size_t o_x = c.add((size_t)(tokens * (kp1 / act_block(tg)) * act_block_bytes(tg)));
     const size_t o_mid = c.add((size_t)(pairs * inter * 4));
     const size_t o_midq = c.add((size_t)(pairs * (kp2 / act_block(td)) * act_block_bytes(td)));
-    const size_t o_y = c.add((size_t)(pairs * hidden * 4));
     uint8_t *ws = (uint8_t *)workspace().get(ordinal, c.total, stream);
     decode_quantizer(tg, GgmlDType::F32)(xs, ws + o_x, (int)hidden, (int)kp1, (int)tokens, stream);
     abi_check("MoE decode (quantize x)");
@@ -439,12 +449,11 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
     abi_check("MoE decode (gate/up)");
     decode_quantizer(td, GgmlDType::F32)(ws + o_mid, ws + o_midq, (int)inter, (int)kp2, (int)pairs, stream);
     abi_check("MoE decode (quantize mid)");
-    decode_matvec_moe(td)(down_->device_ptr(), nullptr, (int64_t)(hidden * down_->row_bytes()), ws + o_midq, ids,
-                          (float *)(ws + o_y), (int)inter, (int)hidden, (int)(kp2 / act_block(td)), 1, (int)pairs, 0,
-                          1, stream);
-    abi_check("MoE decode (down)");
-    launch_moe_weighted_reduce_flat(ws + o_y, weights, out, (int)tokens, (int)hidden, (int)topk, stream);
-    abi_check("MoE decode (reduce)");
+    // down projection and the weighted sum over each token's routes in one launch
+    decode_matvec_moe_wsum(td)(down_->device_ptr(), (int64_t)(hidden * down_->row_bytes()), ws + o_midq, ids, weights,
+                               out, (int)inter, (int)hidden, (int)(kp2 / act_block(td)), (int)tokens, (int)topk,
+                               stream);
+    abi_check("MoE decode (down + weighted sum)");
     return;
   }
   // grouped prefill: dispatch tables, gate and up as expert-grouped matmuls over the gathered rows, the GLU

@@ -89,6 +89,8 @@ def _declare(L: ctypes.CDLL) -> None:
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
         getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
                                                             i32, vp]
+    for t in TYPE_NAME.values():
+        getattr(L, f"launch_mmvq_gguf_{t}_moe_wsum").argtypes = [vp, i64, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
     for name in MOE_NAME.values():
         getattr(L, f"launch_indexed_moe_forward_{name}").argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
     L.launch_moe_dispatch.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]
@@ -256,6 +258,20 @@ def mmvq_moe(wtype: int, w_gate, w_up, expert_stride: int, vy, ids, k: int, n: i
     getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
         _ptr(w_gate), _ptr(w_up), expert_stride, _ptr(vy), _ptr(ids), _ptr(out), k, n,
         kp // BLOCK_SIZE[ACT_TYPE[wtype]], y_div, n_pairs, activation, 1, _stream())
+    check()
+    return out
+
+
+def mmvq_moe_wsum(wtype: int, w, expert_stride: int, vy, ids, weights, k: int, n: int, kp: int, n_tokens: int,
+                  topk: int, out=None):
+    """MoE down projection with the weighted sum over each token's routes: launch_mmvq_gguf_<t>_moe_wsum.
+    vy: n_tokens * topk activation rows; ids u32 and weights f32 [n_tokens, topk] -> out [n_tokens, n] f32."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((n_tokens, n), dtype=torch.float32, device=w.device)
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_moe_wsum")(
+        _ptr(w), expert_stride, _ptr(vy), _ptr(ids), _ptr(weights), _ptr(out), k, n,
+        kp // BLOCK_SIZE[ACT_TYPE[wtype]], n_tokens, topk, _stream())
     check()
     return out
 
@@ -463,6 +479,9 @@ def host() -> ctypes.CDLL:
         H.qmm_qtensor_storage_bytes.argtypes = [vp]
         H.qmm_qtensor_storage_bytes.restype = i64
         H.qmm_qmatmul_forward.argtypes = [vp, vp, u32, i64, vp, vp]
+        H.qmm_moe_new.argtypes = [vp, vp, vp, i32, ctypes.POINTER(vp)]
+        H.qmm_moe_free.argtypes = [vp]
+        H.qmm_moe_forward.argtypes = [vp, vp, i64, vp, vp, i64, vp, vp, i32]
         _host = H
     return _host
 

@@ -140,3 +140,70 @@ def test_weighted_reduce(kind):
     got = qmm.moe_weighted_reduce(t, to_dev(w), out_dtype=torch.bfloat16 if kind == "bf16_out" else None)
     tol = 1e-6 if kind == "f32" else 2e-2
     np.testing.assert_allclose(got.float().cpu().numpy(), want, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("tokens,topk", [(1, 2), (5, 4), (8, 8)])
+def test_moe_down_with_weighted_sum(gtype, tokens, topk):
+    """launch_mmvq_gguf_<t>_moe_wsum equals the two launches it replaces (the down projection per route, then the
+    weighted reduce), and both match the oracle's per-route matmul and reduce; zero-weight routes drop out."""
+    rng = np.random.default_rng(100 * gtype + 10 * tokens + topk)
+    E, hidden, inter = 8, 256, 512 if gtype != O.Q8_0 else 160
+    down = experts(rng, gtype, E, hidden, inter)
+    ids, w = routing(rng, tokens, E, topk)
+    w[0, -1] = 0.0  # a route that contributes nothing
+    mid = acts(rng, tokens * topk, inter)
+    vy, kp = qmm.quantize_decode(gtype, to_dev(mid))
+    ids_d, w_d = to_dev(ids.astype(np.uint32).reshape(-1)), to_dev(w.reshape(-1))
+    got = qmm.mmvq_moe_wsum(gtype, to_dev(down), down.shape[1], vy, ids_d, w_d, inter, hidden, kp, tokens,
+                            topk).cpu().numpy()
+    per_route = qmm.mmvq_moe(gtype, to_dev(down), None, down.shape[1], vy, ids_d, inter, hidden, kp, 1,
+                             tokens * topk)
+    two = qmm.moe_weighted_reduce(per_route.reshape(tokens, topk, hidden), w_d).cpu().numpy()
+    np.testing.assert_allclose(got, two, rtol=1e-6, atol=1e-6 * np.abs(two).max())
+    routes = O.indexed_moe(gtype, down, E, hidden, inter, mid.reshape(tokens, topk, inter),
+                           ids.astype(np.uint32)).reshape(tokens, topk, hidden)
+    assert_parity(got, O.moe_weighted_reduce(routes, w), what=f"moe wsum type {gtype}")
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("tokens,grouped", [(3, 0), (8, 0), (3, 1), (40, 0)])
+def test_moe_experts_block(gtype, tokens, grouped):
+    """The host MoE block (qmm_moe_forward): out[t] = sum_s w[t, s] * down_e(SiLU(gate_e(x_t)) * up_e(x_t)), on the
+    indexed decode route (the down projection with the weighted sum folded in) and the grouped prefill route,
+    against the oracle's matmuls per route and its weighted reduce."""
+    import ctypes
+    rng = np.random.default_rng(7 * gtype + tokens + 100 * grouped)
+    E, hidden, inter, topk = 4, 256, 512, 2
+    mats = [experts(rng, gtype, E, inter, hidden), experts(rng, gtype, E, inter, hidden),
+            experts(rng, gtype, E, hidden, inter)]
+    H = qmm.host()
+    handles = []
+    try:
+        for m, (rows, cols) in zip(mats, ((inter, hidden), (inter, hidden), (hidden, inter))):
+            h = ctypes.c_void_p()
+            rc = H.qmm_qtensor_from_data(gtype, m.ctypes.data, m.size, E, rows, cols, 0, ctypes.byref(h))
+            assert rc == 0, H.qmm_host_last_error()
+            handles.append(h)
+        moe = ctypes.c_void_p()
+        assert H.qmm_moe_new(handles[0], handles[1], handles[2], 0, ctypes.byref(moe)) == 0, H.qmm_host_last_error()
+        ids, w = routing(rng, tokens, E, topk)
+        x = acts(rng, tokens, hidden)
+        out = torch.empty((tokens, hidden), dtype=torch.float32, device=DEV)
+        xd, idd, wd = to_dev(x), to_dev(ids), to_dev(w)
+        rc = H.qmm_moe_forward(moe, xd.data_ptr(), tokens, idd.data_ptr(), wd.data_ptr(), topk, out.data_ptr(),
+                               torch.cuda.current_stream().cuda_stream, grouped)
+        assert rc == 0, H.qmm_host_last_error()
+        torch.cuda.synchronize()
+        H.qmm_moe_free(moe)
+        got = out.cpu().numpy()
+    finally:
+        for h in handles:
+            H.qmm_qtensor_free(h)
+    u32 = ids.astype(np.uint32)
+    g = O.indexed_moe(gtype, mats[0], E, inter, hidden, x[:, None], u32).astype(np.float64)
+    u = O.indexed_moe(gtype, mats[1], E, inter, hidden, x[:, None], u32).astype(np.float64)
+    mid = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+    routes = O.indexed_moe(gtype, mats[2], E, hidden, inter, mid, u32)
+    # the intermediate is rounded to f32 by different exp implementations before its Q8 requantization
+    assert_parity(got, O.moe_weighted_reduce(routes, w), rel=2e-3, what=f"moe block type {gtype} tokens={tokens}")
