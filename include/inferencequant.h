@@ -205,6 +205,10 @@ void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const 
 QMM_DECLARE_MMQ(q8_0)
 QMM_DECLARE_MMQ(q4_k)
 QMM_DECLARE_MMQ(q6_k)
+/* Q4_0 and Q5_0 (gguf/ffi.rs:906-955 gguf_mmq_type_library, gguf_standard_types): the Q8_0 kernel with their block
+ * decoders, on Q8_0-layout activations (launch_mmq_quantize_q8_0) */
+QMM_DECLARE_MMQ(q4_0)
+QMM_DECLARE_MMQ(q5_0)
 /* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
  * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
  * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by

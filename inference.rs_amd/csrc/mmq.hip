@@ -331,7 +331,56 @@ void zero_rows(float *dst, int64_t rows, int64_t cols, int64_t ldd, const int32_
 
 // Q8_0 weights against Q8_0 activations: one MFMA per 32-value block, scaled in f32 per block as
 // k_quants.rs:982-999 does ((sum as f32 * d_w) * d_a, summed over blocks).
-template <class Out>
+// The 32-value weight blocks of the Q8_0-layout prefill: lane half g of a weight row takes values 16g .. 16g + 15 of
+// each block as 16 signed bytes, and the block's f32 scale.
+//   Q8_0  34 B {f16 d; i8 q[32]}                      (k_quants.rs:152-157)
+//   Q4_0  18 B {f16 d; u8 qs[16]}, value q - 8         (k_quants.rs:116-120): half g = nibble g of qs[0..15]
+//   Q5_0  22 B {f16 d; u8 qh[4]; u8 qs[16]}, q - 16    (k_quants.rs:133-138): fifth bit of value v = bit v of qh
+// q - 8 is the 4-bit two's complement of q ^ 8, and q - 16 the 5-bit one of q ^ 16; their sign bits spread to the
+// byte's top bits by one multiply per dword (no carry crosses a byte).
+struct wb_q8_0 {
+  static constexpr int kBytes = 34;
+  static __device__ __forceinline__ void load(const uint8_t *p, int g, uint32_t (&wq)[4], float &d) {
+    d = f16_bits_to_f32(ld16(p));
+    const uint8_t *q = p + 2 + 16 * g;
+    const uint32_t off = (uint32_t)((uintptr_t)q & 3);
+    unit_q6k::realign(ld_a4(q - off), ld32(q - off + 16), off, wq);
+  }
+};
+struct wb_q4_0 {
+  static constexpr int kBytes = 18;
+  static __device__ __forceinline__ void load(const uint8_t *p, int g, uint32_t (&wq)[4], float &d) {
+    d = f16_bits_to_f32(ld16(p));
+    const uint8_t *q = p + 2;
+    const uint32_t off = (uint32_t)((uintptr_t)q & 3);
+    uint32_t raw[4];
+    unit_q6k::realign(ld_a4(q - off), ld32(q - off + 16), off, raw);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t v = ((raw[i] >> (4 * g)) & 0x0f0f0f0fu) ^ 0x08080808u;
+      wq[i] = v | ((v & 0x08080808u) * 0x1eu);
+    }
+  }
+};
+struct wb_q5_0 {
+  static constexpr int kBytes = 22;
+  static __device__ __forceinline__ void load(const uint8_t *p, int g, uint32_t (&wq)[4], float &d) {
+    d = f16_bits_to_f32(ld16(p));
+    const uint32_t qh = ld16(p + 2) | (ld16(p + 4) << 16);
+    const uint8_t *q = p + 6;
+    const uint32_t off = (uint32_t)((uintptr_t)q & 3);
+    uint32_t raw[4];
+    unit_q6k::realign(ld_a4(q - off), ld32(q - off + 16), off, raw);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t hb = (((qh >> (16 * g + 4 * i)) & 15u) * 0x00204081u & 0x01010101u) << 4;
+      const uint32_t v = (((raw[i] >> (4 * g)) & 0x0f0f0f0fu) | hb) ^ 0x10101010u;
+      wq[i] = v | ((v & 0x10101010u) * 0x0fu);
+    }
+  }
+};
+
+template <class WB, class Out>
 __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                               int64_t nblk_w, const ActTile &a, int64_t m0, int64_t mrows, int64_t n0,
                                               int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
@@ -355,11 +404,7 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
     for (int j = 0; j < 8; j++) {
       const int64_t blk = sb * 8 + j;
       if (blk < nblk_w) {
-        const uint8_t *p = wrow + blk * 34;
-        dw[j] = f16_bits_to_f32(ld16(p));
-        const uint8_t *q = p + 2 + 16 * g;
-        const uint32_t off = (uint32_t)((uintptr_t)q & 3);
-        unit_q6k::realign(ld_a4(q - off), ld32(q - off + 16), off, wq[j]);
+        WB::load(wrow + blk * WB::kBytes, g, wq[j], dw[j]);
       } else {
         dw[j] = 0.0f;
         wq[j][0] = wq[j][1] = wq[j][2] = wq[j][3] = 0;
@@ -455,13 +500,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
                             splits > 1);
 }
 
-template <class Out>
+template <class WB, class Out>
 __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                                   int64_t nblk_w, ActTile a, int64_t mrows, int64_t nsb,
                                                   typename Out::T *__restrict__ dst, int64_t ldd) {
   int64_t mt, nt, split;
   tile_of((mrows + BM - 1) / BM, (nrows_w + BN - 1) / BN, 1, mt, nt, split);
-  mmq_q8_0_tile<Out>(W, nrows_w, w_row_bytes, nblk_w, a, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
+  mmq_q8_0_tile<WB, Out>(W, nrows_w, w_row_bytes, nblk_w, a, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
 }
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
@@ -482,6 +527,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
 }
 
+template <class WB>
 __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                       int64_t nrows_w, int64_t w_row_bytes, int64_t nblk_w, ActTile a,
                                                       const int32_t *__restrict__ bounds,
@@ -490,8 +536,8 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict_
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * BM, m1 = bounds[e + 1];
   if (m0 >= m1) return;
-  mmq_q8_0_tile<out_f32>(W + e * expert_bytes, nrows_w, w_row_bytes, nblk_w, a, m0, m1, (int64_t)blockIdx.x * BN, nsb,
-                         dst, ldd, ids_dst);
+  mmq_q8_0_tile<WB, out_f32>(W + e * expert_bytes, nrows_w, w_row_bytes, nblk_w, a, m0, m1, (int64_t)blockIdx.x * BN,
+                             nsb, dst, ldd, ids_dst);
 }
 
 bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_t nrows_x, int64_t stride_row_x) {
@@ -555,7 +601,12 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
     case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
     default: {
       const dim3 grid((unsigned)(((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN)));
-      k_mmq_q8_0<Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+      if (type == QMM_TYPE_Q4_0)
+        k_mmq_q8_0<wb_q4_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+      else if (type == QMM_TYPE_Q5_0)
+        k_mmq_q8_0<wb_q5_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+      else
+        k_mmq_q8_0<wb_q8_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
     }
   }
 }
@@ -605,7 +656,8 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   const dim3 grid((unsigned)((nrows_x + BN - 1) / BN), (unsigned)((ncols_max + BM - 1) / BM), (unsigned)num_experts);
   hipStream_t s = (hipStream_t)stream;
   // a few rows per expert: the few-row kernel streams each expert's weights once, without 64-row tiles of padding
-  if (type != QMM_TYPE_Q8_0 && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
+  const bool b32 = qmm_block_size(type) == 32;  // Q8_0, Q4_0, Q5_0: the Q8_0-layout kernel
+  if (!b32 && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
                                               ncols_dst, stride_col_dst, num_experts, s))
     return;
   const uint8_t *w = (const uint8_t *)x;
@@ -615,7 +667,7 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
   // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
   const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
-  const int64_t splits = type == QMM_TYPE_Q8_0 ? 1 : k_splits(busy, nsb, true);
+  const int64_t splits = b32 ? 1 : k_splits(busy, nsb, true);
   if (splits > 1)
     zero_rows(d, ncols_dst, nrows_x, stride_col_dst, ids_dst, s);
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
@@ -636,9 +688,17 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
         k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                     splits, d, stride_col_dst);
       break;
+    case QMM_TYPE_Q4_0:
+      k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+                                                   ids_dst, nsb, d, stride_col_dst);
+      break;
+    case QMM_TYPE_Q5_0:
+      k_mmq_q8_0_moe<wb_q5_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+                                                   ids_dst, nsb, d, stride_col_dst);
+      break;
     default:
-      k_mmq_q8_0_moe<<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds, ids_dst, nsb,
-                                          d, stride_col_dst);
+      k_mmq_q8_0_moe<wb_q8_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+                                                   ids_dst, nsb, d, stride_col_dst);
   }
 }
 
@@ -666,4 +726,6 @@ extern "C" {
 QMM_DEFINE_MMQ(q8_0, QMM_TYPE_Q8_0)
 QMM_DEFINE_MMQ(q4_k, QMM_TYPE_Q4K)
 QMM_DEFINE_MMQ(q6_k, QMM_TYPE_Q6K)
+QMM_DEFINE_MMQ(q4_0, QMM_TYPE_Q4_0)
+QMM_DEFINE_MMQ(q5_0, QMM_TYPE_Q5_0)
 }

@@ -96,8 +96,10 @@ mmvq_q_fn decode_matvec_quantize(GgmlDType w) {
   }
 }
 
-// the weight types with kernels: every route (full) or the matvec route and dequantization only
+// the weight types with kernels: every route (full), the prefill matmul besides the matvec, or the matvec route and
+// dequantization only
 bool has_all_routes(GgmlDType t) { return t == GgmlDType::Q8_0 || t == GgmlDType::Q4K || t == GgmlDType::Q6K; }
+bool has_prefill(GgmlDType t) { return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0; }
 bool has_matvec(GgmlDType t) {
   return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0 || t == GgmlDType::Q5K;
 }
@@ -125,6 +127,8 @@ mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
 mmq_fn prefill_matmul(GgmlDType w) {
   switch (w) {
     case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0;
+    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0;
+    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k;
     default: throw Error("QMatMul: unsupported weight type");
@@ -134,6 +138,8 @@ mmq_fn prefill_matmul(GgmlDType w) {
 mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
   switch (w) {
     case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_moe;
+    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_moe;
+    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_moe;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k_moe;
     default: throw Error("MoE: unsupported weight type");
@@ -176,7 +182,7 @@ indexed_fn indexed_moe(GgmlDType w) {
 bool act_q8_0(GgmlDType w) { return qmm_vec_dot_type((int)w) == QMM_TYPE_Q8_0; }
 int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
 int64_t act_block_bytes(GgmlDType w) { return act_q8_0(w) ? 34 : 292; }
-int64_t tile_bytes_per_256(GgmlDType w) { return w == GgmlDType::Q8_0 ? 272 : 292; }
+int64_t tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : 292; }
 
 // matvec_only: the route needs the decode matvec kernels alone (QMatMul::forward, gather_forward); else every route
 void check_weight(const QTensor &w, const char *who, bool matvec_only = false) {
@@ -361,7 +367,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     // one launch: the matvec quantizes its activations itself (the same bits as the two launches below)
     decode_matvec_quantize(t)(w.device_ptr(), (const float *)xs, ys, (int)k, (int)n, (int)k, (int)n, (int)rows, stream);
     abi_check("QMatMul::forward (matvec)");
-  } else if (prefers_mmvq(t, rows) || !has_all_routes(t)) {
+  } else if (prefers_mmvq(t, rows) || !has_prefill(t)) {
     // the decode matvec; a type without a prefill kernel takes every batch this way, kMaxDecodeRows rows a launch
     const int64_t kp = pad_to(k, act_block(t));
     const int64_t row_bytes = (kp / act_block(t)) * act_block_bytes(t);
@@ -378,7 +384,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
   } else {
     const int64_t kp = pad_to(k, 256);
     void *y = workspace().get(w.device().ordinal, (size_t)(rows * kp / 256 * tile_bytes_per_256(t)), stream);
-    (t == GgmlDType::Q8_0 ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
+    (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
         xs, nullptr, y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
     abi_check("QMatMul::forward (quantize)");
     prefill_matmul(t)(nullptr, w.device_ptr(), y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, 256, 160 * 1024,

@@ -115,7 +115,7 @@ def _declare(L: ctypes.CDLL) -> None:
         getattr(L, f"launch_dequantize_iq4_xs_{o}").argtypes = [vp, vp, i64, i64, vp]
     for o in ("f32", "bf16"):
         getattr(L, f"launch_mmvq_gguf_q8_0_{o}_exact").argtypes = [vp, vp, vp, i32, i32, i32, vp]
-    for t in TYPE_NAME.values():
+    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0"]:
         f = getattr(L, f"launch_mmq_gguf_{t}", None)
         if f is not None:
             f.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i64, i32, i32, vp]
@@ -354,7 +354,7 @@ def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None):
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=w.device)
     type_dst = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[out.dtype]
-    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME[wtype]}")(
+    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}")(
         None, _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, 256, 160 * 1024, 64, type_dst,
         _stream())
     check()
@@ -368,7 +368,7 @@ def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None):
 
 def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
             ncols_max: int, out):
-    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME[wtype]}_moe")(
+    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
         None, _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
         k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, 256, 160 * 1024, 64, _stream())
     check()

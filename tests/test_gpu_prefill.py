@@ -1,5 +1,6 @@
 """GPU parity of the prefill path through the C ABI: the tile-layout Q8_K / Q8_0 quantizers (bit-exact) and the
-int8-MFMA matmul for Q4_K / Q6_K / Q8_0 (max rel. error <= 1e-3 against the oracle's CPU QMatMul)."""
+int8-MFMA matmul for Q4_K / Q6_K / Q8_0 and, on the Q8_0 kernel, Q4_0 / Q5_0 (max rel. error <= 1e-3 against the
+oracle's CPU QMatMul)."""
 import numpy as np
 import pytest
 
@@ -69,6 +70,8 @@ CASES = [
     (O.Q4K, 512, 256, 4096), (O.Q4K, 17, 33, 2048),
     (O.Q6K, 40, 64, 512), (O.Q6K, 130, 200, 1024), (O.Q6K, 64, 96, 14336), (O.Q6K, 255, 129, 256),
     (O.Q8_0, 40, 64, 512), (O.Q8_0, 33, 48, 1056), (O.Q8_0, 130, 200, 1024), (O.Q8_0, 9, 32, 2688),
+    (O.Q4_0, 40, 64, 512), (O.Q4_0, 33, 48, 1056), (O.Q4_0, 130, 200, 4096), (O.Q4_0, 9, 32, 2720),
+    (O.Q5_0, 40, 64, 512), (O.Q5_0, 33, 48, 1056), (O.Q5_0, 130, 200, 4096), (O.Q5_0, 9, 32, 2720),
 ]
 
 
