@@ -453,6 +453,277 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
     }
 }
 
+// ------------------------------------------------------------------------------------------ 32-value blocks, runs
+
+// The pipelined kernel for Q8_0 / Q4_0 / Q5_0 weights (rows a whole number of superblocks, dword-aligned).  Each
+// superblock of a weight row is read as two dword-aligned runs of four blocks: lane half g of the row's lane pair
+// loads blocks 4g .. 4g + 3 with 16-byte loads, decodes both 16-value halves of each, and one v_permlane32_swap per
+// dword trades halves with the partner lane, so that half g of all eight blocks ends in lane half g (the MFMA B
+// layout used by the Q8_0 kernel above).  Per block, the scale products da * dw (exact in f32: two f16 factors)
+// come from an f32 outer-product MFMA in the accumulator layout, leaving one convert and one FMA per output.
+__device__ __forceinline__ uint32_t run_dw(const uint32_t *R, int o) {  // dword at byte offset o of the run
+  return o % 4 == 0 ? R[o / 4] : __builtin_amdgcn_alignbyte(R[o / 4 + 1], R[o / 4], (uint32_t)(o % 4));
+}
+__device__ __forceinline__ uint32_t run_u16(const uint32_t *R, int o) { return (R[o / 4] >> (8 * (o % 4))) & 0xffffu; }
+
+// decode(R, i, d, h0, h1): block i of the run: f16 scale bits d, values 0..15 (h0) and 16..31 (h1) as signed bytes
+struct wr_q8_0 {
+  static constexpr int kBytes = 34, kDwords = 34;  // run: 136 bytes
+  static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
+                                                uint32_t (&h1)[4]) {
+    const int o = 34 * i;
+    d = run_u16(R, o);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      h0[q] = run_dw(R, o + 2 + 4 * q);
+      h1[q] = run_dw(R, o + 18 + 4 * q);
+    }
+  }
+};
+struct wr_q4_0 {
+  static constexpr int kBytes = 18, kDwords = 18;  // run: 72 bytes
+  static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
+                                                uint32_t (&h1)[4]) {
+    const int o = 18 * i;
+    d = run_u16(R, o);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t Q = run_dw(R, o + 2 + 4 * q);
+      const uint32_t v0 = (Q & 0x0f0f0f0fu) ^ 0x08080808u, v1 = ((Q >> 4) & 0x0f0f0f0fu) ^ 0x08080808u;
+      h0[q] = v0 | ((v0 & 0x08080808u) * 0x1eu);
+      h1[q] = v1 | ((v1 & 0x08080808u) * 0x1eu);
+    }
+  }
+};
+struct wr_q5_0 {
+  static constexpr int kBytes = 22, kDwords = 22;  // run: 88 bytes
+  static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
+                                                uint32_t (&h1)[4]) {
+    const int o = 22 * i;
+    d = run_u16(R, o);
+    const uint32_t qh = run_dw(R, o + 2);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t Q = run_dw(R, o + 6 + 4 * q);
+      const uint32_t b0 = ((((qh >> (4 * q)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+      const uint32_t b1 = ((((qh >> (16 + 4 * q)) & 15u) * 0x00204081u) & 0x01010101u) << 4;
+      const uint32_t v0 = ((Q & 0x0f0f0f0fu) | b0) ^ 0x10101010u, v1 = (((Q >> 4) & 0x0f0f0f0fu) | b1) ^ 0x10101010u;
+      h0[q] = v0 | ((v0 & 0x10101010u) * 0x0fu);
+      h1[q] = v1 | ((v1 & 0x10101010u) * 0x0fu);
+    }
+  }
+};
+
+// The lane's run of superblock sb: kDwords / 4 16-byte loads and one 8-byte load (every run is 4k + 2 dwords).
+template <class WR>
+struct RunLoad {
+  static_assert(WR::kDwords % 4 == 2, "run of 4k + 2 dwords");
+  static constexpr int kLoads = WR::kDwords / 4 + 1;
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t off, uint32_t (&R)[WR::kDwords]) {
+#pragma unroll
+    for (int k = 0; k < WR::kDwords / 4; k++) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * k, 0, 0);
+      R[4 * k] = v[0], R[4 * k + 1] = v[1], R[4 * k + 2] = v[2], R[4 * k + 3] = v[3];
+    }
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off + 16 * (WR::kDwords / 4), 0, 0);
+    R[WR::kDwords - 2] = v[0], R[WR::kDwords - 1] = v[1];
+  }
+};
+
+// Activation superblock of the Q8_0 prefill layout (int8 qs, f16 d per 32 values) by DMA into an LDS slot: qs as
+// in ActDma (swizzled 256-byte rows), then the rows' 16-byte scale groups in row order.
+template <int BMt>
+struct ActDma8 {
+  static constexpr int QS = BMt * 256;
+  static constexpr int STAGE = QS + BMt * 16;
+  static constexpr int NQ = BMt / 16;  // 1 KB qs pieces per wave
+  static constexpr int ND = BMt / 4;   // lanes of each wave that load one row's 16 bytes of scales
+  static constexpr int kLoads = NQ + 1;
+  uint32_t oq[NQ], od;
+
+  __device__ __forceinline__ void init(int wave, int lane, int64_t m0, int64_t rows, int64_t nsb) {
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+      const int L = 64 * (4 * i + wave) + lane, r = L >> 4, c = (L & 15) ^ (r & 15);
+      oq[i] = (uint32_t)((m0 + r) * 256 + 16 * c);
+    }
+    od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 16);
+  }
+  // (device pass only: the host pass rejects the gfx950 16-byte LDS load inside this template)
+  __device__ __forceinline__ void issue(rsrc_t r, uint8_t *slot, int wave, int lane, uint32_t sb_rows) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+    for (int i = 0; i < NQ; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (4 * i + wave)),
+                                               16, oq[i] + 256 * sb_rows, 0, 0, 0);
+    if (lane < ND)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void *)(slot + QS + 16 * ND * wave), 16, od + 16 * sb_rows, 0, 0, 0);
+#endif
+  }
+};
+
+// v_permlane32_swap_b32 (gfx950): lanes 32..63 of lo trade places with lanes 0..31 of hi, so that afterwards lo
+// holds lane half 0's lo in both halves of each lane pair and hi lane half 1's hi (device pass only: the builtin
+// needs the gfx950 target)
+__device__ __forceinline__ void swap_lane_halves(uint32_t &lo, uint32_t &hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+  lo = r[0];
+  hi = r[1];
+#endif
+}
+
+// An empty volatile asm statement on v: the compiler keeps such statements in order, and v's producers before it
+// (device pass only: the host pass has no VGPR constraint and never runs this code)
+template <class T>
+__device__ __forceinline__ void order_point(T &v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __asm__ volatile("" : "+v"(v));
+#endif
+}
+
+__device__ __forceinline__ v16f mfma_f32x2(float a, float b) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, (v16f){}, 0, 0, 0);
+}
+
+// Group k = (tile k / 8, block j = k % 8): the integer block dot and the scale outer product.  Block j's scales
+// live in lane half j / 4; the other half contributes 0 * 0 at k = 1.
+__device__ __forceinline__ void b32_group(const uint8_t *slot, const uint32_t (&qoff)[8], const v4i (&b)[8],
+                                          const float (&da)[4], const float (&dw)[4], int g, int k, v16i &acc,
+                                          v16f &sc) {
+  const int t = k >> 3, j = k & 7, i = j & 3;
+  const bool mine = g == (j >> 2);
+  v4i av = *(const v4i *)(slot + 8192 * t + qoff[j]);
+  order_point(av);
+  acc = mfma_i8(av, b[j], (v16i){});
+  sc = mfma_f32x2(mine ? da[i] : 0.0f, mine ? dw[i] : 0.0f);
+}
+
+// One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows, superblocks [sb0, sb1).
+// Three LDS slots and three weight register sets rotate as in mmq_kq_tile: the activations and weights of s + 2 are
+// in flight while s is computed.
+template <class WR, class Out, int TM>
+__device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
+                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
+                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
+                                             const int32_t *__restrict__ dst_rows, bool accumulate) {
+  constexpr int BMt = 32 * TM;
+  typedef ActDma8<BMt> AD;
+  typedef RunLoad<WR> RL;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AD::STAGE];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int64_t n = n0 + 32 * wave + li;
+  const int64_t nlast = (nrows_w - n0 < BN ? nrows_w - n0 : BN) - 1;
+  const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;
+
+  const int64_t rows = a.rows, nsb = a.nsb;
+  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 272);
+  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, (nlast + 1) * w_row_bytes);
+  const uint32_t wrun = (uint32_t)(nl * w_row_bytes + 4 * WR::kBytes * g);
+
+  uint32_t qoff[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) qoff[j] = 256 * li + 16 * ((2 * j + g) ^ (li & 15));
+
+  v16f fa[TM];
+#pragma unroll
+  for (int t = 0; t < TM; t++) fa[t] = (v16f){};
+
+  AD dma;
+  dma.init(wave, lane, m0, rows, nsb);
+  // two weight register sets: step s decodes set s % 2 into B operands, then reloads it with superblock s + 2
+  uint32_t raw[2][WR::kDwords];
+  auto issue = [&](int64_t sb, int u, int v) {
+    __builtin_amdgcn_sched_barrier(0);
+    dma.issue(ra, lds + u * AD::STAGE, wave, lane, (uint32_t)(sb * rows));
+    RL::load(rw, wrun + (uint32_t)(sb * 8 * WR::kBytes), raw[v]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  v4i b[8];
+  float dw[4];
+  auto decode = [&](const uint32_t (&R)[WR::kDwords]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t d, h0[4], h1[4];
+      WR::decode(R, i, d, h0, h1);
+      dw[i] = f16_bits_to_f32(d);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        swap_lane_halves(h0[q], h1[q]);
+        b[i][q] = (int)h0[q];
+        b[4 + i][q] = (int)h1[q];
+      }
+    }
+  };
+
+  // Groups (t, j) = activation tile t x block j run in order, software-pipelined by one: the two MFMAs of group
+  // k + 1 (integer dot, scale outer product) are issued before the 16 converts and 16 FMAs of group k.  Empty
+  // volatile asm statements (which keep their order) pin that sequence: group k + 2's A fragment passes one after
+  // group k's accumulator update, so no MFMA is hoisted further ahead (the compiler would otherwise issue every
+  // group's MFMAs first and spill their results).
+  auto compute = [&](const uint8_t *slot) {
+    // this lane's activation rows 32t + li: scales of blocks 4g .. 4g + 3
+    float da[TM][4];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      const uint2 d4 = *(const uint2 *)(slot + AD::QS + 16 * (32 * t + li) + 8 * g);
+      da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
+      da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
+    }
+    v16i acc[2];
+    v16f sc[2];
+    b32_group(slot, qoff, b, da[0], dw, g, 0, acc[0], sc[0]);
+#pragma unroll
+    for (int k = 0; k < 8 * TM; k++) {
+      if (k + 1 < 8 * TM) b32_group(slot, qoff, b, da[(k + 1) >> 3], dw, g, k + 1, acc[(k + 1) & 1], sc[(k + 1) & 1]);
+      const int t = k >> 3;
+#pragma unroll
+      for (int r = 0; r < 16; r++) fa[t][r] = __builtin_fmaf((float)acc[k & 1][r], sc[k & 1][r], fa[t][r]);
+      order_point(fa[t]);
+    }
+  };
+
+  // u = (s - sb0) % 3 selects the LDS slot, v = (s - sb0) % 2 the weight set; both constant after unrolling
+  auto step = [&](int64_t s, int u, int v) {
+    __builtin_amdgcn_sched_barrier(0);
+    dma_barrier<AD::kLoads + RL::kLoads>();
+    decode(raw[v]);
+    const int64_t sn = s + 2 < sb1 ? s + 2 : sb1 - 1;
+    issue(sn, (u + 2) % 3, v);
+    if (s < sb1) compute(lds + u * AD::STAGE);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(sb0, 0, 0);
+  issue(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1, 1);
+  for (int64_t sb = sb0; sb < sb1; sb += 6) {
+    step(sb, 0, 0);
+    step(sb + 1, 1, 1);
+    step(sb + 2, 2, 0);
+    step(sb + 3, 0, 1);
+    step(sb + 4, 1, 0);
+    step(sb + 5, 2, 1);
+  }
+
+  if (n >= nrows_w) return;
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int64_t m = m0 + 32 * t + out_row(r, g);
+      if (m < mrows) {
+        const int64_t drow = dst_rows ? dst_rows[m] : m;
+        if (accumulate)
+          __hip_atomic_fetch_add((float *)dst + drow * ldd + n, fa[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          Out::store(dst, drow * ldd + n, fa[t][r]);
+      }
+    }
+}
+
 // ------------------------------------------------------------------------------------------ kernels
 
 // Workgroups are numbered so that the BM-row tiles sharing one weight tile are consecutive, then spread over
@@ -540,6 +811,39 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict_
                              nsb, dst, ldd, ids_dst);
 }
 
+// The pipelined 32-value-block kernels: 32 or 64 activation rows per workgroup, two waves per SIMD.
+template <int TMv>
+constexpr int b32_waves() { return 2; }
+
+template <class WR, class Out, int TMv>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32(
+    const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
+    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
+  constexpr int BMt = 32 * TMv;
+  int64_t mt, nt, split;
+  tile_of((mrows + BMt - 1) / BMt, (nrows_w + BN - 1) / BN, splits, mt, nt, split);
+  const int64_t per = (nsb + splits - 1) / splits;
+  const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
+  if (sb0 >= sb1) return;
+  mmq_b32_tile<WR, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
+                             splits > 1);
+}
+
+template <class WR, int TMv>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32_moe(
+    const uint8_t *__restrict__ W, int64_t expert_bytes, int64_t nrows_w, int64_t w_row_bytes, ActTile a,
+    const int32_t *__restrict__ bounds, const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
+    float *__restrict__ dst, int64_t ldd) {
+  const int64_t e = blockIdx.z;
+  const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
+  if (m0 >= m1) return;  // uniform over the workgroup
+  const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
+  const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
+  if (sb0 >= sb1) return;
+  mmq_b32_tile<WR, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
+                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
+}
+
 bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_t nrows_x, int64_t stride_row_x) {
   const int64_t bs = (int64_t)qmm_block_size(type);
   if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0 || stride_row_x < ncols_x / bs) {
@@ -588,6 +892,48 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
   }
 }
 
+// The pipelined 32-value-block kernel takes rows of whole superblocks that start on dword boundaries; other
+// shapes take the Q8_0 kernel.
+bool b32_runs(const void *x, int64_t ncols_x, int64_t w_row_bytes) {
+  return ncols_x % 256 == 0 && w_row_bytes % 4 == 0 && (uintptr_t)x % 4 == 0;
+}
+
+template <class WR, class Out>
+void launch_b32(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y,
+                int64_t nsb, typename Out::T *d, int64_t ldd, hipStream_t s) {
+  const int64_t ntiles = (nrows_x + BN - 1) / BN;
+  const int tm = ncols_y <= 32 ? 1 : 2;
+  const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
+  const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
+  if (splits > 1)
+    zero_rows((float *)d, ncols_y, nrows_x, ldd, nullptr, s);
+  const dim3 grid((unsigned)(tiles * splits));
+  if (tm == 1)
+    k_mmq_b32<WR, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+  else
+    k_mmq_b32<WR, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+}
+
+template <class WR>
+void launch_b32_moe(const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a,
+                    const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, float *d, int64_t ldd,
+                    int64_t ncols_dst, int64_t ncols_max, int64_t num_experts, hipStream_t s) {
+  const int64_t ntiles = (nrows_x + BN - 1) / BN;
+  const int tm = ncols_max <= 32 ? 1 : 2;
+  const int64_t bm = 32 * tm;
+  // expected work: about ncols_dst / bm row tiles per n tile over all experts
+  const int64_t splits = k_splits(ntiles * ((ncols_dst + bm - 1) / bm), nsb, true);
+  if (splits > 1)
+    zero_rows(d, ncols_dst, nrows_x, ldd, ids_dst, s);
+  const dim3 grid((unsigned)(ntiles * splits), (unsigned)((ncols_max + bm - 1) / bm), (unsigned)num_experts);
+  if (tm == 1)
+    k_mmq_b32_moe<WR, 1><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                               splits, d, ldd);
+  else
+    k_mmq_b32_moe<WR, 2><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                               splits, d, ldd);
+}
+
 template <class Out>
 void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_y,
                int64_t stride_row_x, int64_t ldd, hipStream_t s) {
@@ -600,6 +946,15 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
     case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
     case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
     default: {
+      if (b32_runs(w, ncols_x, w_row_bytes)) {
+        if (type == QMM_TYPE_Q4_0)
+          launch_b32<wr_q4_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+        else if (type == QMM_TYPE_Q5_0)
+          launch_b32<wr_q5_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+        else
+          launch_b32<wr_q8_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+        break;
+      }
       const dim3 grid((unsigned)(((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN)));
       if (type == QMM_TYPE_Q4_0)
         k_mmq_q8_0<wb_q4_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
@@ -662,6 +1017,18 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
     return;
   const uint8_t *w = (const uint8_t *)x;
   float *d = (float *)dst;
+  if (b32 && b32_runs(w, ncols_x, w_row_bytes)) {
+    if (type == QMM_TYPE_Q4_0)
+      launch_b32_moe<wr_q4_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+                              ncols_dst, ncols_max, num_experts, s);
+    else if (type == QMM_TYPE_Q5_0)
+      launch_b32_moe<wr_q5_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+                              ncols_dst, ncols_max, num_experts, s);
+    else
+      launch_b32_moe<wr_q8_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+                              ncols_dst, ncols_max, num_experts, s);
+    return;
+  }
   const bool small = ncols_max <= 32;
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
