@@ -354,7 +354,7 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
                "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
                "iq4_xs_decode", "q6_k_decode", "moe_8x_q4_k_4tok_top2", "q4_0_prefill_m512", "q8_0_prefill_m512",
-               "q5_0_prefill_m512"}
+               "q5_0_prefill_m512", "q5_k_prefill_m512"}
 
 
 def decode_summary(r):
@@ -424,6 +424,8 @@ def main():
                                                       max(20, args.steps // 20), 5, SEED + 46),
         "q5_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q5_0, 14336, 4096, 512, 4,
                                                       max(20, args.steps // 20), 5, SEED + 47),
+        "q5_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q5K, 14336, 4096, 512, 4,
+                                                      max(20, args.steps // 20), 5, SEED + 48),
         # the other weight types at the headline shape, b = 1: the two-launch step and the matvec alone
         "q6_k_decode": lambda: decode_summary(decode_workload(torch, qmm, Q6K, n, k, 1, 12, args.steps // 2,
                                                               args.warmup // 2, SEED + 40)),

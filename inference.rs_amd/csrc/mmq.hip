@@ -106,7 +106,9 @@ struct ActDma {
     }
     od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 4);
   }
+  // (device pass only: the host pass rejects the gfx950 16-byte LDS load inside this template)
   __device__ __forceinline__ void issue(rsrc_t r, uint8_t *slot, int wave, int lane, uint32_t sb_rows) const {
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
     for (int i = 0; i < NQ; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (4 * i + wave)),
@@ -120,6 +122,7 @@ struct ActDma {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           r, (__attribute__((address_space(3))) void *)(slot + QS + BSB + 4 * ND * wave), 4, od + 4 * sb_rows, 0, 0,
           0);
+#endif
   }
 };
 
@@ -208,9 +211,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   auto compute = [&](const uint8_t *slot, const typename WT::Raw &rr) {
     typename WT::Prep p;
     WT::prepare(rr, g, p);
-    v16i acc1[TM], acc2[TM];
+    v16i acc1[TM], acc2[TM], acc3[TM];  // acc3: Q5_K's fifth-bit plane
 #pragma unroll
-    for (int t = 0; t < TM; t++) acc1[t] = acc2[t] = (v16i){};
+    for (int t = 0; t < TM; t++) acc1[t] = acc2[t] = acc3[t] = (v16i){};
     // (Q4_K at TM = 2 runs at 2 waves per SIMD, where the extra registers would spill: it reads just in time)
     constexpr bool kAhead = !(WT::kMin && TM == 2);
     v4i av[2][TM];
@@ -222,13 +225,17 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
         for (int t = 0; t < TM; t++) av[(j + 1) & 1][t] = *(const v4i *)(slot + 8192 * t + qoff[j + 1]);
       }
-      v4i b1, b2;
-      WT::planes(rr, p, j, b1, b2);
+      v4i b1, b2, b3;
+      if constexpr (WT::kPlanes == 3)
+        WT::planes(rr, p, j, b1, b2, b3);
+      else
+        WT::planes(rr, p, j, b1, b2);
 #pragma unroll
       for (int t = 0; t < TM; t++) {
         const v4i a = kAhead ? av[j & 1][t] : *(const v4i *)(slot + 8192 * t + qoff[j]);
         acc1[t] = mfma_i8(a, b1, acc1[t]);
         acc2[t] = mfma_i8(a, b2, acc2[t]);
+        if constexpr (WT::kPlanes == 3) acc3[t] = mfma_i8(a, b3, acc3[t]);
       }
     }
 #pragma unroll
@@ -244,7 +251,8 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int r = 4 * q + i;
-          const int iv = (acc1[t][r] << WT::kShift) + acc2[t][r];
+          int iv = (acc1[t][r] << WT::kShift) + acc2[t][r];
+          if constexpr (WT::kPlanes == 3) iv += acc3[t][r] << 4;
           float v = p.d * (float)iv;
           if (WT::kMin) v -= p.dmin * fmin[r];
           fa[t][r] += dy4[i] * v;
@@ -587,14 +595,12 @@ __device__ __forceinline__ v16f mfma_f32x2(float a, float b) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, (v16f){}, 0, 0, 0);
 }
 
-// Group k = (tile k / 8, block j = k % 8): the integer block dot and the scale outer product.  Block j's scales
-// live in lane half j / 4; the other half contributes 0 * 0 at k = 1.
-__device__ __forceinline__ void b32_group(const uint8_t *slot, const uint32_t (&qoff)[8], const v4i (&b)[8],
-                                          const float (&da)[4], const float (&dw)[4], int g, int k, v16i &acc,
-                                          v16f &sc) {
-  const int t = k >> 3, j = k & 7, i = j & 3;
+// Group k = (tile k / 8, block j = k % 8): the integer block dot and the scale outer product on A fragment av.
+// Block j's scales live in lane half j / 4; the other half contributes 0 * 0 at k = 1.
+__device__ __forceinline__ void b32_group(v4i av, const v4i (&b)[8], const float (&da)[4], const float (&dw)[4],
+                                          int g, int k, v16i &acc, v16f &sc) {
+  const int j = k & 7, i = j & 3;
   const bool mine = g == (j >> 2);
-  v4i av = *(const v4i *)(slot + 8192 * t + qoff[j]);
   order_point(av);
   acc = mfma_i8(av, b[j], (v16i){});
   sc = mfma_f32x2(mine ? da[i] : 0.0f, mine ? dw[i] : 0.0f);
@@ -659,11 +665,12 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
     }
   };
 
-  // Groups (t, j) = activation tile t x block j run in order, software-pipelined by one: the two MFMAs of group
-  // k + 1 (integer dot, scale outer product) are issued before the 16 converts and 16 FMAs of group k.  Empty
-  // volatile asm statements (which keep their order) pin that sequence: group k + 2's A fragment passes one after
-  // group k's accumulator update, so no MFMA is hoisted further ahead (the compiler would otherwise issue every
-  // group's MFMAs first and spill their results).
+  // Groups (t, j) = activation tile t x block j run in order, software-pipelined: the two MFMAs of group k + 1
+  // (integer dot, scale outer product) are issued before the 16 converts and 16 FMAs of group k, and the A fragment
+  // of group k + 2 is read from LDS meanwhile.  Empty volatile asm statements (which keep their order) pin that
+  // sequence: group k + 2's A fragment passes one after group k's accumulator update, so no MFMA is hoisted further
+  // ahead (the compiler would otherwise issue every group's MFMAs first and spill their results), and by then the
+  // fragment has arrived.
   auto compute = [&](const uint8_t *slot) {
     // this lane's activation rows 32t + li: scales of blocks 4g .. 4g + 3
     float da[TM][4];
@@ -673,12 +680,17 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
       da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
       da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
     }
+    auto frag = [&](int k) { return *(const v4i *)(slot + 8192 * (k >> 3) + qoff[k & 7]); };
     v16i acc[2];
     v16f sc[2];
-    b32_group(slot, qoff, b, da[0], dw, g, 0, acc[0], sc[0]);
+    v4i av[2];
+    av[0] = frag(0);
+    av[1] = frag(1);
+    b32_group(av[0], b, da[0], dw, g, 0, acc[0], sc[0]);
 #pragma unroll
     for (int k = 0; k < 8 * TM; k++) {
-      if (k + 1 < 8 * TM) b32_group(slot, qoff, b, da[(k + 1) >> 3], dw, g, k + 1, acc[(k + 1) & 1], sc[(k + 1) & 1]);
+      if (k + 1 < 8 * TM) b32_group(av[(k + 1) & 1], b, da[(k + 1) >> 3], dw, g, k + 1, acc[(k + 1) & 1], sc[(k + 1) & 1]);
+      if (k + 2 < 8 * TM) av[k & 1] = frag(k + 2);
       const int t = k >> 3;
 #pragma unroll
       for (int r = 0; r < 16; r++) fa[t][r] = __builtin_fmaf((float)acc[k & 1][r], sc[k & 1][r], fa[t][r]);
@@ -754,7 +766,7 @@ ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
 template <class WT>
 constexpr int kq_tm_max() { return WT::kMin ? 2 : 4; }
 template <class WT, int TMv>
-constexpr int kq_waves() { return WT::kMin && TMv <= 2 ? 2 : 1; }
+constexpr int kq_waves() { return WT::kMin && TMv <= (WT::kPlanes == 3 ? 1 : 2) ? 2 : 1; }
 
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst
 template <class WT, class Out, int TMv>
@@ -851,8 +863,8 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
                   (long long)stride_row_x);
     return false;
   }
-  if (type == QMM_TYPE_Q4K && ((uintptr_t)x % 16 != 0)) {
-    qmm_set_error("%s: Q4_K weights must be 16-byte aligned", who);
+  if ((type == QMM_TYPE_Q4K || type == QMM_TYPE_Q5K) && ((uintptr_t)x % 16 != 0)) {
+    qmm_set_error("%s: Q4_K / Q5_K weights must be 16-byte aligned", who);
     return false;
   }
   if ((uintptr_t)x % 2 != 0) {
@@ -945,6 +957,7 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
   switch (type) {
     case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
     case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
+    case QMM_TYPE_Q5K: launch_kq<wq5k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
     default: {
       if (b32_runs(w, ncols_x, w_row_bytes)) {
         if (type == QMM_TYPE_Q4_0)
@@ -1047,6 +1060,14 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
         k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                     splits, d, stride_col_dst);
       break;
+    case QMM_TYPE_Q5K:
+      if (small)
+        k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
+      else
+        k_mmq_kq_moe<wq5k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                    splits, d, stride_col_dst);
+      break;
     case QMM_TYPE_Q6K:
       if (small)
         k_mmq_kq_moe<wq6k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
@@ -1093,6 +1114,7 @@ extern "C" {
 QMM_DEFINE_MMQ(q8_0, QMM_TYPE_Q8_0)
 QMM_DEFINE_MMQ(q4_k, QMM_TYPE_Q4K)
 QMM_DEFINE_MMQ(q6_k, QMM_TYPE_Q6K)
+QMM_DEFINE_MMQ(q5_k, QMM_TYPE_Q5K)
 QMM_DEFINE_MMQ(q4_0, QMM_TYPE_Q4_0)
 QMM_DEFINE_MMQ(q5_0, QMM_TYPE_Q5_0)
 }

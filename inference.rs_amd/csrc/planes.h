@@ -29,6 +29,7 @@ __device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 *
 // (qs[32c + 16g .. +16], c = 0..3) -> sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles).
 struct wq4k {
   static constexpr int kBytes = 144;
+  static constexpr int kPlanes = 2;
   static constexpr int kShift = 3;  // I1 = 8 * plane1 + plane2
   static constexpr bool kMin = true;
   static constexpr bool kDma = true;  // prefill stages activations by DMA (see mmq.hip)
@@ -83,10 +84,54 @@ struct wq4k {
   }
 };
 
+// Q5_K (k_quants.rs:200-206, 2145-2232): Q4_K's header and nibbles plus qh[32], whose bit j of byte l is the fifth
+// bit of value l of sub-block j's low or high half (32 j + l for j's nibble half).  q5 = nib + 16 h, so
+// sc * q5 = 8 (sh * nib) + (sl * nib) + 16 (h * sc): the two Q4_K planes plus a third, h * sc <= 63.
+struct wq5k {
+  static constexpr int kBytes = 176;
+  static constexpr int kPlanes = 3;
+  static constexpr int kShift = 3;
+  static constexpr bool kMin = true;
+  static constexpr bool kDma = true;
+  static constexpr int kLoads = 6;  // header, this lane's 16 qh bytes, four 16-byte nibble chunks
+  struct Raw {
+    u32x4 hdr, qh, q[4];
+  };
+  typedef wq4k::Prep Prep;
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
+    const uint32_t o = row + sb * kBytes;
+    r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+    r.qh = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 16 * g, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 48 + 32 * c + 16 * g, 0, 0);
+  }
+  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
+    wq4k::Raw h;
+    h.hdr = r.hdr;
+    wq4k::prepare(h, g, p);
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2, v4i &b3) {
+    (void)p;
+    wq4k::Raw h;
+    h.hdr = r.hdr;
+    const u32x4 q = r.q[j >> 1];
+    const uint32_t sc = wq4k::scale(h, j), sh = sc >> 3, sl = sc & 7;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w}, qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t nib = (j & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
+      b1[i] = (int)mul_bytes(nib, sh);
+      b2[i] = (int)mul_bytes(nib, sl);
+      b3[i] = (int)mul_bytes((qh[i] >> j) & 0x01010101u, sc);
+    }
+  }
+};
+
 // Q6_K: per lane, per superblock: ql[64h + 32p + 16g ..+16], qh[32h + 16g ..+16] (h, p in {0,1}), the 8 scales
 // sc[2j + g] and d.  Chunk j (32 values 32j..32j+31) covers h = j / 4, q = j % 4, l = 16g + (0..15).
 struct wq6k {
   static constexpr int kBytes = 210;
+  static constexpr int kPlanes = 2;
   static constexpr int kShift = 6;  // I = 64 * wh + wl
   static constexpr bool kMin = false;
   static constexpr bool kDma = false;

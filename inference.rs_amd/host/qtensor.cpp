@@ -99,7 +99,9 @@ mmvq_q_fn decode_matvec_quantize(GgmlDType w) {
 // the weight types with kernels: every route (full), the prefill matmul besides the matvec, or the matvec route and
 // dequantization only
 bool has_all_routes(GgmlDType t) { return t == GgmlDType::Q8_0 || t == GgmlDType::Q4K || t == GgmlDType::Q6K; }
-bool has_prefill(GgmlDType t) { return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0; }
+bool has_prefill(GgmlDType t) {
+  return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0 || t == GgmlDType::Q5K;
+}
 bool has_matvec(GgmlDType t) {
   return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0 || t == GgmlDType::Q5K;
 }
@@ -131,6 +133,7 @@ mmq_fn prefill_matmul(GgmlDType w) {
     case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k;
+    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k;
     default: throw Error("QMatMul: unsupported weight type");
   }
 }
@@ -142,6 +145,7 @@ mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
     case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_moe;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k_moe;
+    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k_moe;
     default: throw Error("MoE: unsupported weight type");
   }
 }

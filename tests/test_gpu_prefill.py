@@ -75,6 +75,8 @@ CASES = [
     # 32-value types with K a multiple of 256: the run-loading kernel, 32-row tiles with K split across
     # workgroups (f32 atomics), 64-row tiles, a ragged last weight tile
     (O.Q8_0, 17, 300, 4096), (O.Q4_0, 20, 130, 2048), (O.Q5_0, 64, 257, 1280), (O.Q8_0, 300, 129, 768),
+    # Q5_K: the K-quant kernel with the fifth-bit plane (32-row tiles with split K, 64-row tiles, ragged edges)
+    (O.Q5K, 40, 64, 512), (O.Q5K, 130, 200, 1024), (O.Q5K, 17, 300, 4096), (O.Q5K, 255, 129, 256),
 ]
 
 
@@ -102,7 +104,8 @@ def test_mmq_half_outputs(out):
     np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max())
 
 
-@pytest.mark.parametrize("gtype,n,k", [(O.Q4K, 14336, 4096), (O.Q6K, 4096, 14336), (O.Q8_0, 14336, 4096)])
+@pytest.mark.parametrize("gtype,n,k", [(O.Q4K, 14336, 4096), (O.Q6K, 4096, 14336), (O.Q8_0, 14336, 4096),
+                                       (O.Q5K, 14336, 4096)])
 def test_mmq_config_shapes(gtype, n, k):
     """[512, K] activations; checked against the oracle on 24 sampled activation rows."""
     rng = np.random.default_rng(20261203 + gtype)
