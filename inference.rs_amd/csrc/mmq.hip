@@ -764,7 +764,7 @@ ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
 // Q4_K (measured on MI355X): 64 activation rows per wave at 2 waves per SIMD beats 128 rows at 1 wave; Q6_K, whose
 // plane building needs more registers, runs 1 wave per SIMD and takes 128 rows.
 template <class WT>
-constexpr int kq_tm_max() { return WT::kMin ? 2 : 4; }
+constexpr int kq_tm_max() { return WT::kPlanes == 3 ? 1 : WT::kMin ? 2 : 4; }
 template <class WT, int TMv>
 constexpr int kq_waves() { return WT::kMin && TMv <= (WT::kPlanes == 3 ? 1 : 2) ? 2 : 1; }
 
@@ -889,7 +889,7 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
                typename Out::T *d, int64_t ldd, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
-  const int tm = ncols_y <= 32 ? 1 : ncols_y <= 64 || kq_tm_max<WT>() < 4 ? 2 : 4;
+  const int tm = ncols_y <= 32 || kq_tm_max<WT>() < 2 ? 1 : ncols_y <= 64 || kq_tm_max<WT>() < 4 ? 2 : 4;
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
   const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
   if (splits > 1)
