@@ -191,8 +191,16 @@ void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const 
  * launch_mmq_gguf_<t> (gguf/ffi.rs:902-918; host fast_mmq.rs:446-524, 604-715; kernel mmq_instance.cuh:
  * 217-256, mmq_gguf.cuh:3533-3875).  dst[col * stride_col_dst + row] for row < nrows_x (weight rows),
  * col < ncols_y (activation rows); x = weight rows of stride_row_x blocks; y = prefill-layout activations
- * with ne0 = ncols_x padded to 256 and ne1 = ncols_y.  type_dst 0 f32, 1 f16, 30 bf16.  tmp_fixup, cc,
- * nsm, smpbo and warp_size are the reference's device hints: accepted, unused (tmp_fixup may be NULL). */
+ * with ne0 = ncols_x padded to 256 and ne1 = ncols_y.  type_dst 0 f32, 1 f16, 30 bf16.
+ * Weight buffers: as in the reference, whose QTensor device allocations carry MATRIX_ROW_PADDING = 512 values of
+ * padding (quantized/cuda.rs:25, 246-248), a kernel may read a few bytes past the last block -- here at most 4, by the
+ * Q8_0 / Q4_0 / Q5_0 kernel for rows that are not whole 4-byte aligned superblocks -- so the buffer must extend at
+ * least 4 bytes beyond the last row (the host QTensor pads by 512 values).
+ * tmp_fixup: the caller's split-K workspace of nsm * 128 * 128 f32, as the reference sizes it (fast_mmq.rs:442-444;
+ * nsm = the device's compute-unit count).  When the tile grid alone would leave compute units idle, the K range is
+ * split, each split writes its partial sums to its own f32 plane there, and a second kernel adds the planes in split
+ * order and stores dst: results are the same bits on every run, as with the reference's fixed-order stream-k fixup
+ * (mmq_gguf.cuh:3610-3611, 3877-3930).  tmp_fixup NULL: no split.  cc, smpbo and warp_size are accepted, unused. */
 #define QMM_DECLARE_MMQ(t)                                                                                     \
   void launch_mmq_gguf_##t(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,          \
                            int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc, \

@@ -154,7 +154,7 @@ template <class WT, class Out, int TM>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
-                                            const int32_t *__restrict__ dst_rows, bool accumulate) {
+                                            const int32_t *__restrict__ dst_rows, float *__restrict__ part) {
   constexpr int BMt = 32 * TM;
   // Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a register
   // ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
@@ -304,35 +304,49 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     for (int r = 0; r < 16; r++) {
       const int64_t m = m0 + 32 * t + out_row(r, g);
       if (m < mrows) {
-        const int64_t drow = dst_rows ? dst_rows[m] : m;
-        if (accumulate)  // split K: f32 partial sums meet in dst (zeroed first)
-          __hip_atomic_fetch_add((float *)dst + drow * ldd + n, fa[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (part)  // split K: this split's partial sum, row m of the activation order (summed by k_split_sum)
+          part[m * nrows_w + n] = fa[t][r];
         else
-          Out::store(dst, drow * ldd + n, fa[t][r]);
+          Out::store(dst, (dst_rows ? dst_rows[m] : m) * ldd + n, fa[t][r]);
       }
     }
 }
 
-// Zero rows of an f32 matrix before split-K partial sums land in it (a kernel, not a memset node, so the
-// launch sequence can sit in a HIP graph).  rows_map != nullptr: zero rows rows_map[0..rows).
-__global__ __launch_bounds__(256) void k_zero_rows(float *__restrict__ dst, int64_t rows, int64_t cols, int64_t ldd,
+// Split K: split s of a tile writes its partial sums to plane s of the caller's fixup buffer (planes of rows x cols
+// f32, row m of the activation order); this kernel adds the planes in split order, so the result does not depend on
+// which split finished first, and stores them in the output type (dst row rows_map ? rows_map[m] : m).  Workgroup
+// (x, y) takes 1024 columns of rows y, y + gridDim.y, ...; 4 columns per thread.  A kernel, so that the launch
+// sequence can sit in a HIP graph.
+template <class Out>
+__global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int64_t splits, int64_t rows,
+                                                   int64_t cols, typename Out::T *__restrict__ dst, int64_t ldd,
                                                    const int32_t *__restrict__ rows_map) {
-  // workgroup (x, y) clears 1024 columns of rows y, y + gridDim.y, ...; 4 columns per thread
   const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= cols) return;
+  const int64_t plane = rows * cols;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    float *p = dst + (rows_map ? rows_map[r] : r) * ldd + c;
-    if (c + 4 <= cols && ((uintptr_t)p & 15) == 0) {
-      *(v4f *)p = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    const float *p = part + r * cols + c;
+    const int64_t o = (rows_map ? rows_map[r] : r) * ldd + c;
+    if (c + 4 <= cols && cols % 4 == 0) {
+      v4f v = *(const v4f *)p;
+      for (int64_t sp = 1; sp < splits; sp++) v += *(const v4f *)(p + sp * plane);
+#pragma unroll
+      for (int i = 0; i < 4; i++) Out::store(dst, o + i, v[i]);
     } else {
-      for (int64_t i = 0; i < 4 && c + i < cols; i++) p[i] = 0.0f;
+      for (int64_t i = 0; i < 4 && c + i < cols; i++) {
+        float v = p[i];
+        for (int64_t sp = 1; sp < splits; sp++) v += p[sp * plane + i];
+        Out::store(dst, o + i, v);
+      }
     }
   }
 }
 
-void zero_rows(float *dst, int64_t rows, int64_t cols, int64_t ldd, const int32_t *rows_map, hipStream_t s) {
+template <class Out>
+void split_sum(const float *part, int64_t splits, int64_t rows, int64_t cols, typename Out::T *dst, int64_t ldd,
+               const int32_t *rows_map, hipStream_t s) {
   const dim3 grid((unsigned)qmm_ceil_div(cols, 1024), (unsigned)(rows < 64 ? rows : 64));
-  k_zero_rows<<<grid, 256, 0, s>>>(dst, rows, cols, ldd, rows_map);
+  k_split_sum<Out><<<grid, 256, 0, s>>>(part, splits, rows, cols, dst, ldd, rows_map);
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 kernel
@@ -613,7 +627,7 @@ template <class WR, class Out, int TM>
 __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                              const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                              int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
-                                             const int32_t *__restrict__ dst_rows, bool accumulate) {
+                                             const int32_t *__restrict__ dst_rows, float *__restrict__ part) {
   constexpr int BMt = 32 * TM;
   typedef ActDma8<BMt> AD;
   typedef RunLoad<WR> RL;
@@ -727,11 +741,10 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
     for (int r = 0; r < 16; r++) {
       const int64_t m = m0 + 32 * t + out_row(r, g);
       if (m < mrows) {
-        const int64_t drow = dst_rows ? dst_rows[m] : m;
-        if (accumulate)
-          __hip_atomic_fetch_add((float *)dst + drow * ldd + n, fa[t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (part)
+          part[m * nrows_w + n] = fa[t][r];
         else
-          Out::store(dst, drow * ldd + n, fa[t][r]);
+          Out::store(dst, (dst_rows ? dst_rows[m] : m) * ldd + n, fa[t][r]);
       }
     }
 }
@@ -768,11 +781,12 @@ constexpr int kq_tm_max() { return WT::kPlanes == 3 ? 1 : WT::kMin ? 2 : 4; }
 template <class WT, int TMv>
 constexpr int kq_waves() { return WT::kMin && TMv <= (WT::kPlanes == 3 ? 1 : 2) ? 2 : 1; }
 
-// grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst
+// grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst, or with more
+// than one split into plane s of `part` (mrows x nrows_w f32 per plane)
 template <class WT, class Out, int TMv>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
-    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
+    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd, float *__restrict__ part) {
   constexpr int BMt = 32 * TMv;
   int64_t mt, nt, split;
   tile_of((mrows + BMt - 1) / BMt, (nrows_w + BN - 1) / BN, splits, mt, nt, split);
@@ -780,7 +794,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
   mmq_kq_tile<WT, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
-                            splits > 1);
+                            part ? part + split * mrows * nrows_w : nullptr);
 }
 
 template <class WB, class Out>
@@ -799,7 +813,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
                                                     const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
-                                                    float *__restrict__ dst, int64_t ldd) {
+                                                    float *__restrict__ dst, int64_t ldd, float *__restrict__ part,
+                                                    int64_t ncols_dst) {
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
   if (m0 >= m1) return;  // uniform over the workgroup
@@ -807,7 +822,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
   mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
-                                (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
+                                (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
+                                part ? part + split * ncols_dst * nrows_w : nullptr);
 }
 
 template <class WB>
@@ -830,7 +846,7 @@ constexpr int b32_waves() { return 2; }
 template <class WR, class Out, int TMv>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
-    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd) {
+    int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd, float *__restrict__ part) {
   constexpr int BMt = 32 * TMv;
   int64_t mt, nt, split;
   tile_of((mrows + BMt - 1) / BMt, (nrows_w + BN - 1) / BN, splits, mt, nt, split);
@@ -838,14 +854,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<T
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
   mmq_b32_tile<WR, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
-                             splits > 1);
+                             part ? part + split * mrows * nrows_w : nullptr);
 }
 
 template <class WR, int TMv>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32_moe(
     const uint8_t *__restrict__ W, int64_t expert_bytes, int64_t nrows_w, int64_t w_row_bytes, ActTile a,
     const int32_t *__restrict__ bounds, const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
-    float *__restrict__ dst, int64_t ldd) {
+    float *__restrict__ dst, int64_t ldd, float *__restrict__ part, int64_t ncols_dst) {
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
   if (m0 >= m1) return;  // uniform over the workgroup
@@ -853,7 +869,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<T
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
   mmq_b32_tile<WR, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
-                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst, splits > 1);
+                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
+                                 part ? part + split * ncols_dst * nrows_w : nullptr);
 }
 
 bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_t nrows_x, int64_t stride_row_x) {
@@ -874,34 +891,38 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
   return true;
 }
 
-// K splits so that tiles x splits fills every CU once over, each split keeping at least 4 superblocks;
-// only for f32 outputs (the partial sums meet through f32 atomics).
-int64_t k_splits(int64_t tiles, int64_t nsb, bool f32_out) {
-  if (!f32_out) return 1;
+// K splits so that tiles x splits fills every CU once over, each split keeping at least 4 superblocks, as long as the
+// caller's fixup buffer holds one rows x cols f32 plane per split.  The reference sizes that buffer (tmp_fixup) as
+// nsm * 128 * 128 f32 (fast_mmq.rs:442-444); without one there is no split.  Every split gets at least one
+// superblock, since each writes its whole plane.
+int64_t k_splits(int64_t tiles, int64_t nsb, int64_t rows, int64_t cols, const void *fixup, int nsm) {
+  if (!fixup || (uintptr_t)fixup % 16 != 0) return 1;
+  const int64_t cap = (int64_t)(nsm > 0 ? nsm : qmm_device_cus()) * 128 * 128 * 4;
   const int64_t want = qmm_device_cus();
   int64_t s = 1;
-  while (tiles * s < want && nsb / (s * 2) >= 4) s *= 2;
+  while (tiles * s < want && nsb / (s * 2) >= 4 && 2 * s * rows * cols * 4 <= cap) s *= 2;
+  while (s > 1 && (s - 1) * ((nsb + s - 1) / s) >= nsb) s--;
   return s;
 }
 
 template <class WT, class Out>
 void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y, int64_t nsb,
-               typename Out::T *d, int64_t ldd, hipStream_t s) {
+               typename Out::T *d, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
   const int tm = ncols_y <= 32 || kq_tm_max<WT>() < 2 ? 1 : ncols_y <= 64 || kq_tm_max<WT>() < 4 ? 2 : 4;
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
-  const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
-  if (splits > 1)
-    zero_rows((float *)d, ncols_y, nrows_x, ldd, nullptr, s);
+  const int64_t splits = k_splits(tiles, nsb, ncols_y, nrows_x, fixup, nsm);
+  float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1) {
-    k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+    k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   } else if (tm == 2) {
-    k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+    k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   } else if constexpr (kq_tm_max<WT>() >= 4) {  // (not instantiated where it cannot be chosen)
-    k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+    k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   }
+  if (part) split_sum<Out>(part, splits, ncols_y, nrows_x, d, ldd, nullptr, s);
 }
 
 // The pipelined 32-value-block kernel takes rows of whole superblocks that start on dword boundaries; other
@@ -912,60 +933,60 @@ bool b32_runs(const void *x, int64_t ncols_x, int64_t w_row_bytes) {
 
 template <class WR, class Out>
 void launch_b32(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y,
-                int64_t nsb, typename Out::T *d, int64_t ldd, hipStream_t s) {
+                int64_t nsb, typename Out::T *d, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   const int tm = ncols_y <= 32 ? 1 : 2;
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
-  const int64_t splits = k_splits(tiles, nsb, sizeof(typename Out::T) == 4);
-  if (splits > 1)
-    zero_rows((float *)d, ncols_y, nrows_x, ldd, nullptr, s);
+  const int64_t splits = k_splits(tiles, nsb, ncols_y, nrows_x, fixup, nsm);
+  float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1)
-    k_mmq_b32<WR, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+    k_mmq_b32<WR, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   else
-    k_mmq_b32<WR, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd);
+    k_mmq_b32<WR, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+  if (part) split_sum<Out>(part, splits, ncols_y, nrows_x, d, ldd, nullptr, s);
 }
 
 template <class WR>
 void launch_b32_moe(const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a,
                     const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, float *d, int64_t ldd,
-                    int64_t ncols_dst, int64_t ncols_max, int64_t num_experts, hipStream_t s) {
+                    int64_t ncols_dst, int64_t ncols_max, int64_t num_experts, void *fixup, int nsm, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   const int tm = ncols_max <= 32 ? 1 : 2;
   const int64_t bm = 32 * tm;
   // expected work: about ncols_dst / bm row tiles per n tile over all experts
-  const int64_t splits = k_splits(ntiles * ((ncols_dst + bm - 1) / bm), nsb, true);
-  if (splits > 1)
-    zero_rows(d, ncols_dst, nrows_x, ldd, ids_dst, s);
+  const int64_t splits = k_splits(ntiles * ((ncols_dst + bm - 1) / bm), nsb, ncols_dst, nrows_x, fixup, nsm);
+  float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(ntiles * splits), (unsigned)((ncols_max + bm - 1) / bm), (unsigned)num_experts);
   if (tm == 1)
     k_mmq_b32_moe<WR, 1><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                               splits, d, ldd);
+                                               splits, d, ldd, part, ncols_dst);
   else
     k_mmq_b32_moe<WR, 2><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                               splits, d, ldd);
+                                               splits, d, ldd, part, ncols_dst);
+  if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, ldd, ids_dst, s);
 }
 
 template <class Out>
 void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_y,
-               int64_t stride_row_x, int64_t ldd, hipStream_t s) {
+               int64_t stride_row_x, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   const int64_t nsb = (ncols_x + 255) / 256;
   const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
   const ActTile a = act_tile(y, ncols_y, nsb);
   typename Out::T *d = (typename Out::T *)dst;
   const uint8_t *w = (const uint8_t *)x;
   switch (type) {
-    case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
-    case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
-    case QMM_TYPE_Q5K: launch_kq<wq5k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s); break;
+    case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
+    case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
+    case QMM_TYPE_Q5K: launch_kq<wq5k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     default: {
       if (b32_runs(w, ncols_x, w_row_bytes)) {
         if (type == QMM_TYPE_Q4_0)
-          launch_b32<wr_q4_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+          launch_b32<wr_q4_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         else if (type == QMM_TYPE_Q5_0)
-          launch_b32<wr_q5_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+          launch_b32<wr_q5_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         else
-          launch_b32<wr_q8_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, s);
+          launch_b32<wr_q8_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         break;
       }
       const dim3 grid((unsigned)(((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN)));
@@ -990,8 +1011,8 @@ bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows) {
 }
 
 void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x,
-         int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int type_dst, void *stream, const char *who) {
-  (void)tmp_fixup;
+         int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int nsm, int type_dst, void *stream,
+         const char *who) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_y)) return;
   if (ncols_y < 0 || stride_col_dst < nrows_x) {
     qmm_set_error("%s: ncols_y=%lld stride_col_dst=%lld", who, (long long)ncols_y, (long long)stride_col_dst);
@@ -1000,16 +1021,16 @@ void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int
   if (ncols_y == 0) return;
   hipStream_t s = (hipStream_t)stream;
   switch (type_dst) {
-    case QMM_TYPE_F32: mmq_plain<out_f32>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, s); break;
-    case QMM_TYPE_F16: mmq_plain<out_f16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, s); break;
-    case QMM_TYPE_BF16: mmq_plain<out_bf16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, s); break;
+    case QMM_TYPE_F32: mmq_plain<out_f32>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
+    case QMM_TYPE_F16: mmq_plain<out_f16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
+    case QMM_TYPE_BF16: mmq_plain<out_bf16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
     default: qmm_set_error("%s: type_dst=%d (0 f32, 1 f16, 30 bf16)", who, type_dst);
   }
 }
 
-void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, void *dst,
-             int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,
-             int64_t num_experts, int64_t ncols_max, void *stream, const char *who) {
+void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
+             void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
+             int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst)) return;
   if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
     qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
@@ -1033,48 +1054,49 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   if (b32 && b32_runs(w, ncols_x, w_row_bytes)) {
     if (type == QMM_TYPE_Q4_0)
       launch_b32_moe<wr_q4_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
-                              ncols_dst, ncols_max, num_experts, s);
+                              ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     else if (type == QMM_TYPE_Q5_0)
       launch_b32_moe<wr_q5_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
-                              ncols_dst, ncols_max, num_experts, s);
+                              ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     else
       launch_b32_moe<wr_q8_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
-                              ncols_dst, ncols_max, num_experts, s);
+                              ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     return;
   }
-  const bool small = ncols_max <= 32;
+  // 32-row tiles for a few rows per expert, and always for Q5_K (its third plane does not fit two waves per SIMD at
+  // 64 rows, the form the plain prefill measured slower)
+  const bool small = ncols_max <= 32 || type == QMM_TYPE_Q5K;
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
   // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
   const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
-  const int64_t splits = b32 ? 1 : k_splits(busy, nsb, true);
-  if (splits > 1)
-    zero_rows(d, ncols_dst, nrows_x, stride_col_dst, ids_dst, s);
+  const int64_t splits = b32 ? 1 : k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
+  float *part = splits > 1 ? (float *)tmp_fixup : nullptr;
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
   switch (type) {
     case QMM_TYPE_Q4K:
       if (small)
         k_mmq_kq_moe<wq4k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       else
         k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q5K:
       if (small)
         k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       else
         k_mmq_kq_moe<wq5k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q6K:
       if (small)
         k_mmq_kq_moe<wq6k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       else
         k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q4_0:
       k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
@@ -1088,6 +1110,7 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
       k_mmq_q8_0_moe<wb_q8_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
                                                    ids_dst, nsb, d, stride_col_dst);
   }
+  if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, stride_col_dst, ids_dst, s);
 }
 
 }  // namespace
@@ -1096,18 +1119,18 @@ void mmq_moe(int type, const void *x, const void *y, const int32_t *ids_dst, con
   void launch_mmq_gguf_##t(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,             \
                            int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc, \
                            int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream) {                    \
-    (void)cc, (void)nsm, (void)smpbo, (void)warp_size;                                                             \
-    mmq(TYPE, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, type_dst, stream,     \
-        "mmq_" #t);                                                                                                \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq(TYPE, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, nsm, type_dst,        \
+        stream, "mmq_" #t);                                                                                        \
   }                                                                                                                \
   void launch_mmq_gguf_##t##_moe(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,           \
                                  const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,        \
                                  int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,                  \
                                  int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,           \
                                  int warp_size, void *stream) {                                                    \
-    (void)tmp_fixup, (void)cc, (void)nsm, (void)smpbo, (void)warp_size;                                            \
-    mmq_moe(TYPE, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x, stride_col_dst,    \
-            num_experts, ncols_max, stream, "mmq_" #t "_moe");                                                     \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq_moe(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,         \
+            stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe");                                \
   }
 
 extern "C" {

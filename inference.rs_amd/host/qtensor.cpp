@@ -17,6 +17,8 @@ void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// A launcher's argument error (qmm_last_error), then a launch the runtime refused (hipGetLastError: an invalid
+// configuration or a missing code object), which would otherwise leave the output unwritten without a word.
 void abi_check(const char *what) {
   const char *msg = qmm_last_error();
   if (msg && msg[0]) {
@@ -24,7 +26,18 @@ void abi_check(const char *what) {
     qmm_clear_error();
     throw Error(m);
   }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) throw Error(std::string(what) + ": launch failed: " + hipGetErrorString(e));
 }
+
+// Compute units of a device: the reference's `nsm` device hint (fast_mmq.rs:397-440)
+int device_cus(int ordinal) {
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, ordinal) != hipSuccess || v <= 0) v = 256;
+  return v;
+}
+// The split-K fixup workspace of one MMQ launch, nsm * 128 * 128 f32 (fast_mmq.rs:442-444)
+size_t fixup_bytes(int nsm) { return (size_t)nsm * 128 * 128 * 4; }
 
 int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
@@ -387,12 +400,16 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     }
   } else {
     const int64_t kp = pad_to(k, 256);
-    void *y = workspace().get(w.device().ordinal, (size_t)(rows * kp / 256 * tile_bytes_per_256(t)), stream);
+    const int nsm = device_cus(w.device().ordinal);
+    Carver c;
+    const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+    const size_t o_fix = c.add(fixup_bytes(nsm));
+    uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
     (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
-        xs, nullptr, y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
+        xs, nullptr, ws + o_y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
     abi_check("QMatMul::forward (quantize)");
-    prefill_matmul(t)(nullptr, w.device_ptr(), y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, 256, 160 * 1024,
-                      64, (int)in_dtype, stream);
+    prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
+                      160 * 1024, 64, (int)in_dtype, stream);
     abi_check("QMatMul::forward (matmul)");
   }
 }
@@ -480,6 +497,8 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   const size_t o_u = c.add((size_t)(pairs * inter * 4));
   const size_t o_mq = c.add((size_t)(pairs * kp2 / 256 * tile_bytes_per_256(td)));
   const size_t o_y = c.add((size_t)(pairs * hidden * 4));
+  const int nsm = device_cus(ordinal);
+  const size_t o_fix = c.add(fixup_bytes(nsm));
   uint8_t *ws = (uint8_t *)workspace().get(ordinal, c.total, stream);
   int32_t *bounds = (int32_t *)(ws + o_bounds), *tok = (int32_t *)(ws + o_tok), *src = (int32_t *)(ws + o_src);
   launch_moe_dispatch(ids, bounds, tok, src, (int)pairs, (int)E, (int)topk, (int32_t *)(ws + o_cnt),
@@ -490,8 +509,8 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   abi_check("MoE grouped (quantize x)");
   for (int which = 0; which < 2; which++) {
     const QTensor &w = which == 0 ? *gate_ : *up_;
-    prefill_matmul_moe(tg)(nullptr, w.device_ptr(), ws + o_x, tok, bounds, ws + (which == 0 ? o_g : o_u), hidden,
-                           inter, pairs, hidden / (int64_t)block_size(tg), inter, E, pairs, 0, 256, 160 * 1024, 64,
+    prefill_matmul_moe(tg)(ws + o_fix, w.device_ptr(), ws + o_x, tok, bounds, ws + (which == 0 ? o_g : o_u), hidden,
+                           inter, pairs, hidden / (int64_t)block_size(tg), inter, E, pairs, 0, nsm, 160 * 1024, 64,
                            stream);
     abi_check("MoE grouped (gate/up)");
   }
@@ -499,8 +518,8 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
       (const float *)(ws + o_g), (const float *)(ws + o_u), tok, ws + o_mq, inter, inter, kp2, pairs, activation_,
       stream);
   abi_check("MoE grouped (GLU + quantize)");
-  prefill_matmul_moe(td)(nullptr, down_->device_ptr(), ws + o_mq, tok, bounds, ws + o_y, inter, hidden, pairs,
-                         inter / (int64_t)block_size(td), hidden, E, pairs, 0, 256, 160 * 1024, 64, stream);
+  prefill_matmul_moe(td)(ws + o_fix, down_->device_ptr(), ws + o_mq, tok, bounds, ws + o_y, inter, hidden, pairs,
+                         inter / (int64_t)block_size(td), hidden, E, pairs, 0, nsm, 160 * 1024, 64, stream);
   abi_check("MoE grouped (down)");
   launch_moe_weighted_reduce_flat(ws + o_y, weights, out, (int)tokens, (int)hidden, (int)topk, stream);
   abi_check("MoE grouped (reduce)");

@@ -102,6 +102,8 @@ def _declare(L: ctypes.CDLL) -> None:
         f = getattr(L, f"launch_mmq_quantize_{blk}", None)
         if f is not None:
             f.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
+    for blk in ("q8k", "q8_0"):
+        getattr(L, f"launch_mmq_quantize_glu_{blk}_f32").argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
     for t in ADJ_TYPE_NAME.values():
         for o in ("f32", "f16", "bf16"):
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
@@ -347,15 +349,46 @@ def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None)
     return out, kp
 
 
-def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None):
-    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t>."""
+_fixups = {}
+
+
+def fixup(device):
+    """(buffer, nsm): the split-K fixup workspace the reference hands every MMQ launch (tmp_fixup, sized
+    nsm * 128 * 128 f32 in fast_mmq.rs:442-444), one per device, with the device's CU count as nsm."""
+    torch = _torch()
+    idx = torch.device(device).index or 0
+    if idx not in _fixups:
+        nsm = torch.cuda.get_device_properties(idx).multi_processor_count
+        _fixups[idx] = (torch.empty(nsm * 128 * 128 * 4, dtype=torch.uint8, device=f"cuda:{idx}"), nsm)
+    return _fixups[idx]
+
+
+def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, out=None):
+    """act(gate[r]) * up[r] for r = ids[i] (or i), f32 [rows, k] inputs, quantized into the prefill tile layout
+    through launch_mmq_quantize_glu_{q8k,q8_0}_f32.  Returns (uint8 tensor, kp)."""
+    torch = _torch()
+    k = gate.shape[-1]
+    kp = pad_to(k, 256)
+    ne1 = ids.numel() if ids is not None else gate.shape[0]
+    if out is None:
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp), 1), dtype=torch.uint8, device=gate.device)
+    blk = "q8k" if ACT_TYPE[wtype] == Q8K else "q8_0"
+    getattr(lib(), f"launch_mmq_quantize_glu_{blk}_f32")(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0),
+                                                         kp, ne1, activation, _stream())
+    check()
+    return out, kp
+
+
+def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None, tmp_fixup=True):
+    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t>.  tmp_fixup=False passes no fixup buffer (no split-K)."""
     torch = _torch()
     out_dtype = out_dtype or torch.float32
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=w.device)
     type_dst = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[out.dtype]
+    fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
     getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}")(
-        None, _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, 256, 160 * 1024, 64, type_dst,
+        _ptr(fx), _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, nsm, 160 * 1024, 64, type_dst,
         _stream())
     check()
     return out
@@ -367,10 +400,11 @@ def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None):
 
 
 def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
-            ncols_max: int, out):
+            ncols_max: int, out, tmp_fixup=True):
+    fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
     getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
-        None, _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
-        k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, 256, 160 * 1024, 64, _stream())
+        _ptr(fx), _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
+        k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, nsm, 160 * 1024, 64, _stream())
     check()
     return out
 

@@ -40,7 +40,7 @@ def test_fused_glu(gtype, b):
     vy, kp = qmm.quantize_decode(gtype, dev(x))
     for act, f in ACTS.items():
         got = qmm.mmvq_fused_glu(gtype, dev(wg), dev(wu), vy, k, n, b, kp, activation=act).cpu().numpy()
-        assert_parity(got, f(g) * u, rel=2e-3, what=f"t{gtype} b{b} act{act}")
+        assert_parity(got, f(g) * u, what=f"t{gtype} b{b} act{act}")
 
 
 def test_fused_glu_half_output():

@@ -59,7 +59,7 @@ def test_moe_decode_fused_glu(gtype):
     for act, f in ((0, lambda v: v / (1 + np.exp(-v))), (2, lambda v: np.maximum(v, 0))):
         got = qmm.mmvq_moe(gtype, to_dev(gate), to_dev(up), stride, vy, to_dev(ids.reshape(-1)), hidden, inter, kp,
                            topk, tokens * topk, activation=act).cpu().numpy()
-        assert_parity(got, f(g.astype(np.float64)) * u, rel=2e-3)
+        assert_parity(got, f(g.astype(np.float64)) * u)
     got = qmm.mmvq_moe(gtype, to_dev(gate), None, stride, vy, to_dev(ids.reshape(-1)), hidden, inter, kp, topk,
                        tokens * topk).cpu().numpy()
     assert_parity(got, g)
@@ -205,5 +205,6 @@ def test_moe_experts_block(gtype, tokens, grouped):
     u = O.indexed_moe(gtype, mats[1], E, inter, hidden, x[:, None], u32).astype(np.float64)
     mid = (g / (1 + np.exp(-g)) * u).astype(np.float32)
     routes = O.indexed_moe(gtype, mats[2], E, hidden, inter, mid, u32)
-    # the intermediate is rounded to f32 by different exp implementations before its Q8 requantization
-    assert_parity(got, O.moe_weighted_reduce(routes, w), rel=2e-3, what=f"moe block type {gtype} tokens={tokens}")
+    # the intermediate is rounded to f32 by different exp implementations before its Q8 requantization: a value may
+    # land on the other side of a rounding step, which moves the output far less than the north-star bound
+    assert_parity(got, O.moe_weighted_reduce(routes, w), what=f"moe block type {gtype} tokens={tokens}")
