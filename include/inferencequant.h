@@ -328,6 +328,21 @@ void moe_router_topk_f16(const void *logits, float *weights, uint32_t *ids, cons
                          int weight_mode, bool renormalize, bool clamp_logits, float clamp_min, float clamp_max,
                          float norm_min, float output_scale, int64_t stream);
 
+/* ------------------------------------------------------------------ QMatMul::forward that allocates nothing
+ * qmm_qmatmul_forward_noalloc: no counterpart in the reference.  For callers that cannot allocate device memory --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc -- the host layer's
+ * QMatMul::forward (qmm_qmatmul_forward in qmm_host.h, whose per-thread workspace grows with hipMalloc) with the same
+ * routes and kernels: ys[rows, n] = xs[rows, k] . W^T, W = n rows of GGUF blocks of type wtype (8 q8_0, 12 q4_k,
+ * 14 q6_k, 2 q4_0, 6 q5_0, 13 q5_k, 23 iq4_xs) padded as QTensor pads them; xs and ys device pointers of in_dtype
+ * (0 f32, 1 f16, 30 bf16).  Quantized activations and split-K planes live in one 32 MiB device array of the library,
+ * held by each device it runs on until the process ends; the quantized activations must fit in its 16 MiB
+ * activation part (rows * ceil(k / 256) * 292 bytes, 272 for the 32-value block types, above 16 rows; rows * k / 256 *
+ * 292 or rows * k / 32 * 34 bytes at 16 rows or fewer), else nothing is launched and the call returns -1 with
+ * qmm_last_error() set.  Every call on a device shares that device's array: calls that overlap on one device race.
+ * Returns 0, or -1 with the error recorded. */
+int qmm_qmatmul_forward_noalloc(const void *w, uint32_t wtype, int64_t n, int64_t k, const void *xs, uint32_t in_dtype,
+                                int64_t rows, void *ys, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
