@@ -103,6 +103,22 @@ size_t oracle_block_size(int type) {
     }
 }
 
+/* ---------------------------------------------------------------- planted mistakes
+ * Built with -DORACLE_PLANT=n (tests/test_weight_quantizers.py only, into a temporary library), the weight quantizers
+ * carry one deliberate mistake each, so the tests can show that their checks catch it:
+ *   1 make_qkx2_quants fuses its multiply-adds (the ik_llama.cpp build's madd, not the LlamaCpp one)
+ *   2 Q4_K searches from rmin -0.5 instead of -1
+ *   3 Q4_K stores dmin = max_min / 64
+ *   4 make_qx_quants tries candidate scales around nmax - 1
+ *   5 Q6_K scales its sub-block scales by -127 / max_scale
+ *   6 Q5_K searches 20 steps instead of 15
+ *   7 make_qkx2_quants scores candidates by absolute error
+ *   8 make_qkx2_quants refits a positive min as sum_xl / sum_l
+ * The default build (ORACLE_PLANT undefined) is the restatement. */
+#ifndef ORACLE_PLANT
+#define ORACLE_PLANT 0
+#endif
+
 /* ---------------------------------------------------------------- rounding helpers (utils.rs) */
 
 /* utils.rs:3-4, 32-35: add 1.5*2^23, read the low mantissa bits: round to nearest, ties to even */
@@ -211,6 +227,7 @@ static float make_qkx2_quants(int nmax, const float *x, const float *weights, fl
         *neg_min = -min;
         return 0.0f;
     }
+    if (ORACLE_PLANT == 7) use_mad = 1;
     float iscale = (float)nmax / (max - min);
     float scale = 1.0f / iscale;
     float best_error = 0.0f;
@@ -219,7 +236,7 @@ static float make_qkx2_quants(int nmax, const float *x, const float *weights, fl
         l[i] = (uint8_t)li;
         float diff = scale * (float)li + min - x[i];
         float e = use_mad ? fabsf(diff) : diff * diff;
-        best_error = weights[i] * e + best_error;
+        best_error = ORACLE_PLANT == 1 ? fmaf(weights[i], e, best_error) : weights[i] * e + best_error;
     }
     if (nstep == 0) { *neg_min = -min; return scale; }
     int32_t laux[32];
@@ -232,8 +249,8 @@ static float make_qkx2_quants(int nmax, const float *x, const float *weights, fl
             float w = weights[i], lf = (float)li;
             float wl = w * lf;
             sum_l += wl;
-            sum_l2 = wl * lf + sum_l2;
-            sum_xl = wl * x[i] + sum_xl;
+            sum_l2 = ORACLE_PLANT == 1 ? fmaf(wl, lf, sum_l2) : wl * lf + sum_l2;
+            sum_xl = ORACLE_PLANT == 1 ? fmaf(wl, x[i], sum_xl) : wl * x[i] + sum_xl;
         }
         float d = sum_w * sum_l2 - sum_l * sum_l;
         if (d > 0.0f) {
@@ -241,13 +258,13 @@ static float make_qkx2_quants(int nmax, const float *x, const float *weights, fl
             float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / d;
             if (this_min > 0.0f) {
                 this_min = 0.0f;
-                this_scale = sum_xl / sum_l2;
+                this_scale = ORACLE_PLANT == 8 ? sum_xl / sum_l : sum_xl / sum_l2;
             }
             float cur_error = 0.0f;
             for (int i = 0; i < n; i++) {
                 float diff = this_scale * (float)laux[i] + this_min - x[i];
                 float e = use_mad ? fabsf(diff) : diff * diff;
-                cur_error = weights[i] * e + cur_error;
+                cur_error = ORACLE_PLANT == 1 ? fmaf(weights[i], e, cur_error) : weights[i] * e + cur_error;
             }
             if (cur_error < best_error) {
                 for (int i = 0; i < n; i++) l[i] = (uint8_t)laux[i];
@@ -273,7 +290,7 @@ static void quantize_q4k_block(const float *x, or_block_q4k *blk) {
         float av_x = sqrtf(ss / 32.0f);
         float w[32];
         for (int i = 0; i < 32; i++) w[i] = av_x + fabsf(xs[i]);
-        scales[j] = make_qkx2_quants(15, xs, w, -1.0f, 0.1f, 20, 0, l + 32 * j, &mins[j]);
+        scales[j] = make_qkx2_quants(15, xs, w, ORACLE_PLANT == 2 ? -0.5f : -1.0f, 0.1f, 20, 0, l + 32 * j, &mins[j]);
     }
     float max_scale = 0.0f, max_min = 0.0f;
     for (int j = 0; j < 8; j++) {
@@ -297,7 +314,7 @@ static void quantize_q4k_block(const float *x, or_block_q4k *blk) {
         }
     }
     blk->d = oracle_f32_to_f16(max_scale / 63.0f);
-    blk->dmin = oracle_f32_to_f16(max_min / 63.0f);
+    blk->dmin = oracle_f32_to_f16(max_min / (ORACLE_PLANT == 3 ? 64.0f : 63.0f));
     for (int j = 0; j < 8; j++) {
         uint8_t sc, m;
         get_scale_min_k4(j, blk->scales, &sc, &m);
@@ -362,7 +379,7 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *ls, int rms
     for (int is = -9; is <= 9; is++) {
         if (is == 0) continue;
         float tenths = (float)is;
-        iscale = -(0.1f * tenths + (float)nmax) / max;
+        iscale = -(0.1f * tenths + (float)(ORACLE_PLANT == 4 ? nmax - 1 : nmax)) / max;
         sumlx = 0.0f;
         suml2 = 0.0f;
         for (int i = 0; i < n; i++) {
@@ -391,7 +408,7 @@ static void quantize_q6k_block(const float *x, or_block_q6k *y) {
         scales[ib] = scale;
         if (fabsf(scale) > max_abs_scale) { max_abs_scale = fabsf(scale); max_scale = scale; }
     }
-    float iscale = -128.0f / max_scale;
+    float iscale = (ORACLE_PLANT == 5 ? -127.0f : -128.0f) / max_scale;
     y->d = oracle_f32_to_f16(1.0f / iscale);
     for (int j = 0; j < 16; j++) {
         int32_t v = nearest_int_mul(iscale, scales[j]);
@@ -421,6 +438,16 @@ void oracle_quantize_q6k(const float *x, int64_t n, or_block_q6k *y) {
     for (int64_t b = 0; b < nb; b++) quantize_q6k_block(x + 256 * b, y + b);
 }
 
+/* The sub-block searches on their own, for the tests that pin them: make_qkx2_quants over 32 values (returns the
+ * scale, *neg_min = the subtracted min negated, as the reference returns it) and make_qx_quants over n <= 32. */
+float oracle_make_qkx2_quants(int nmax, const float *x, const float *weights, float rmin, float rdelta, int nstep,
+                              int use_mad, uint8_t *l, float *neg_min) {
+    return make_qkx2_quants(nmax, x, weights, rmin, rdelta, nstep, use_mad, l, neg_min);
+}
+float oracle_make_qx_quants(int n, int nmax, const float *x, int8_t *ls, int rmse_type) {
+    return n >= 1 && n <= 32 ? make_qx_quants(n, nmax, x, ls, rmse_type) : 0.0f;
+}
+
 /* ---------------------------------------------------------------- Q5_K weights */
 
 /* k_quants.rs:2256-2334 (the plain, no-imatrix branch): Q4_K's search with 31 levels and Q5K_SEARCH
@@ -436,7 +463,7 @@ static void quantize_q5k_block(const float *x, or_block_q5k *blk) {
         float av_x = sqrtf(ss / 32.0f);
         float w[32];
         for (int i = 0; i < 32; i++) w[i] = av_x + fabsf(xs[i]);
-        scales[j] = make_qkx2_quants(31, xs, w, -0.5f, 0.1f, 15, 0, l + 32 * j, &mins[j]);
+        scales[j] = make_qkx2_quants(31, xs, w, -0.5f, 0.1f, ORACLE_PLANT == 6 ? 20 : 15, 0, l + 32 * j, &mins[j]);
     }
     float max_scale = 0.0f, max_min = 0.0f;
     for (int j = 0; j < 8; j++) {

@@ -61,6 +61,10 @@ void oracle_quantize_q8_0(const float *x, int64_t n, or_block_q8_0 *y);     /* k
 void oracle_quantize_q8k(const float *x, int64_t n, or_block_q8k *y);       /* k_quants.rs:2721-2760 */
 void oracle_quantize_q4k(const float *x, int64_t n, or_block_q4k *y);       /* k_quants.rs:1930-2001 */
 void oracle_quantize_q6k(const float *x, int64_t n, or_block_q6k *y);       /* k_quants.rs:2590-2646 */
+/* the sub-block searches alone (utils.rs:268-361, 135-264), for the tests that pin them */
+float oracle_make_qkx2_quants(int nmax, const float *x, const float *weights, float rmin, float rdelta, int nstep,
+                              int use_mad, uint8_t *l, float *neg_min);
+float oracle_make_qx_quants(int n, int nmax, const float *x, int8_t *ls, int rmse_type);
 void oracle_quantize_q4_0(const float *x, int64_t n, or_block_q4_0 *y);     /* k_quants.rs:380-418 */
 void oracle_quantize_q5_0(const float *x, int64_t n, or_block_q5_0 *y);     /* k_quants.rs:681-717 */
 void oracle_quantize_q5k(const float *x, int64_t n, or_block_q5k *y);       /* k_quants.rs:2256-2334 */
