@@ -11,7 +11,7 @@ One step = one pass of the hot path over one batch of synthetic input, with ever
   replayed once between a synchronize on both sides; `value` = algorithmic bytes per step / time per step.
 Extra lines in "extra": Q4_K decode at b = 4 and 16, Q8_0 4096^2 decode, the M = 512 prefill (Q4_K and Q6_K,
 int8 TOPS), the Llama-3-8B linear stack (tokens/s) and the 8-expert MoE (64 tokens, top-2).
-`roofline` is the step's one kernel, `cpu_baseline` the oracle's CPU QMatMul (oracle/, a C restatement of the
+`roofline` is the step's one kernel, `cpu_baseline` the reference's x86 CPU QMatMul route (oracle/x86.c, a C restatement of the
 reference's) on the box's host cores over a bounded sample.
 """
 import argparse
@@ -315,38 +315,70 @@ def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
 
-def cpu_baseline(wq, n, k, seconds=10.0):
-    """The oracle's CPU QMatMul (a C restatement of the reference's, oracle/) on the headline workload: Q4_K
-    14336x4096 at b = 1, rotating 8 weight copies (264 MB, beyond any host L3) for about `seconds`."""
-    sys.path.insert(0, os.path.join(REPO, "oracle"))
-    import oracle as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
-    rng = np.random.default_rng(SEED + 7)
-    x = rng.standard_normal((1, k), dtype=np.float32)
-    copies = [wq] + [wq.copy() for _ in range(7)]
-    O.matmul(O.Q4K, x, copies[0], n, threads)
+def _timed(fn, seconds, min_reps):
+    fn(0)
     reps, t0 = 0, time.perf_counter()
     while True:
-        O.matmul(O.Q4K, x, copies[reps % 8], n, threads)
+        fn(reps)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= seconds and reps >= 8:
-            break
-    per = el / reps
+        if el >= seconds and reps >= min_reps:
+            return el / reps, reps, el
+
+
+def cpu_baseline(wq, n, k, seconds=10.0):
+    """The reference's CPU QMatMul on this box's host, as the reference runs it on x86-64: repacked 16-row tiles
+    with vpdpbusd at the level repack_x86::level() picks (AVX-512 VNNI / AVX-VNNI / AVX2), AMX for Q4_K at
+    m >= 32 where the CPU has it, threads = physical cores (oracle/x86.c, a C restatement of repack_x86.rs /
+    avx.rs).  Headline: Q4_K 14336x4096 at b = 1 over 8 rotating weight copies for about `seconds`.  Also, for
+    about a third of that each: config 1 (Q8_0 4096x4096, m = 1, 32 rotating copies), the Q4_K prefill at
+    M = 512, and the scalar vec_dot_unopt restatement (oracle/oracle.c) on the headline."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    cores = O.x86_physical_cores()
+    rng = np.random.default_rng(SEED + 7)
+    x = rng.standard_normal((1, k), dtype=np.float32)
     step_bytes = wq.size + k * 4 + n * 4
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} Q4_K 14336x4096 b=1 matvecs (8 rotating weight copies) in {el:.1f} s; "
-                      f"oracle/oracle.c vec_dot_unopt + matmul, OpenMP over output rows; host CPU: {cpu}",
-            "ms_per_step": per * 1e3}
+
+    ws = [O.X86Weight(O.Q4K, wq if i == 0 else wq.copy(), n, k) for i in range(8)]
+    out = np.zeros((1, n), np.float32)
+    paths = set()
+    per, reps, el = _timed(lambda i: paths.add(ws[i % 8].matmul(x, cores, out)[1]), seconds, 8)
+    head_path = "/".join(sorted(paths))
+    del ws
+
+    extra = {}
+    # config 1: Q8_0 4096x4096 QMatMul at m = 1 (17.8 MB per weight; 32 copies, 570 MB, beyond any host L3)
+    w8 = quantized_weight(Q8_0, 4096, 4096, SEED + 5)
+    x8 = rng.standard_normal((1, 4096), dtype=np.float32)
+    w8s = [O.X86Weight(O.Q8_0, w8 if i == 0 else w8.copy(), 4096, 4096) for i in range(32)]
+    o8 = np.zeros((1, 4096), np.float32)
+    p8 = set()
+    t8, r8, e8 = _timed(lambda i: p8.add(w8s[i % 32].matmul(x8, cores, o8)[1]), seconds / 3, 32)
+    del w8s
+    b8 = w8.size + 4096 * 8
+    extra["q8_0_4096x4096_m1"] = {"ms_per_step": t8 * 1e3, "gb_s": b8 / t8 / 1e9, "path": "/".join(sorted(p8)),
+                                  "sample": f"{r8} calls in {e8:.1f} s, 32 rotating copies"}
+    # Q4_K prefill, M = 512 (the weight stays resident: compute-bound on the CPU)
+    xp = rng.standard_normal((512, k), dtype=np.float32)
+    wp = O.X86Weight(O.Q4K, wq, n, k)
+    op = np.zeros((512, n), np.float32)
+    pp = set()
+    tp, rp, ep = _timed(lambda i: pp.add(wp.matmul(xp, cores, op)[1]), seconds / 3, 2)
+    del wp
+    extra["q4_k_prefill_m512"] = {"ms_per_step": tp * 1e3, "tops": 2 * 512 * n * k / tp / 1e12,
+                                  "path": "/".join(sorted(pp)), "sample": f"{rp} calls in {ep:.1f} s"}
+    # the scalar restatement (k_quants.rs vec_dot_unopt + matmul), same headline workload
+    copies = [wq] + [wq.copy() for _ in range(7)]
+    ts, rs, es = _timed(lambda i: O.matmul(O.Q4K, x, copies[i % 8], n, cores), seconds / 3, 8)
+    extra["scalar_vec_dot_unopt_headline"] = {"ms_per_step": ts * 1e3, "gb_s": step_bytes / ts / 1e9,
+                                              "sample": f"{rs} calls in {es:.1f} s, 8 rotating copies"}
+    return {"value": step_bytes / per / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "variant": f"x86 repacked path ({head_path})",
+            "sample": f"{reps} Q4_K 14336x4096 b=1 QMatMul calls (quantize + {head_path}, 8 rotating weight "
+                      f"copies) in {el:.1f} s; oracle/x86.c, a restatement of repack_x86.rs at the level "
+                      f"repack_x86::level() picks; host CPU: {O.x86_describe()}, {cores} physical cores",
+            "ms_per_step": per * 1e3, "extra": extra}
 
 
 # ------------------------------------------------------------------------------------------------ main
@@ -463,7 +495,7 @@ def main():
 
     base = None
     if not args.quick:
-        log("CPU baseline (oracle)")
+        log("CPU baseline (the reference's x86 route, oracle/x86.c)")
         base = cpu_baseline(head["weights"], n, k, args.cpu_seconds)
 
     # the step is one launch: its kernel moves the step's bytes (weights, f32 activation, f32 output)

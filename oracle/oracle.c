@@ -14,8 +14,8 @@
  *   f16 conversion       numpy's IEEE binary16 cast on every f16 bit pattern and random floats
  *   quantize_block32     the reference's own known-answer blocks (quantized/mod.rs:1650-1686)
  *   Q8_K quantizer       closed form on special blocks (zero, tied maxima, signs); bsums == sums of qs
- *   Q4_K / Q6_K weights  invariants only (ranges, scale pack/unpack, round-trip error, row independence);
- *                        the exact bits are "parity unpinned": no reference build or golden vector exists here
+ *   Q4_K / Q5_K / Q6_K   exact-grid known answers, float64 re-derivations of the candidate-scale searches, a
+ *   weights              byte-identical second float32 reading in numpy, planted mistakes (tests/test_weight_quantizers.py)
  *   dequantize           closed forms against hand-built blocks
  *   vec_dot / matmul     float64 brute force over the dequantized operands; a planted-error check
  *   MoE                  brute force per route over oracle_matmul

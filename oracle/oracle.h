@@ -110,6 +110,20 @@ int oracle_moe_dispatch(const int32_t *topk_ids, int32_t total, int32_t n_expert
 void oracle_moe_weighted_reduce(const float *in, const float *w, float *out, int32_t tokens, int32_t hidden,
                                 int32_t topk);
 
+/* x86.c: the path the reference's CPU QMatMul takes on x86-64 (repack_x86.rs, repack.rs:219-262, avx.rs), the
+ * timed CPU baseline.  Levels: 0 none, 1 AVX2, 2 AVX-VNNI, 3 AVX-512 VNNI (repack_x86.rs:1318-1342). */
+int oracle_x86_level(void);
+int oracle_x86_amx(void);                                           /* repack_x86.rs:985-1024 */
+int oracle_x86_select(int type, int64_t m, int64_t n, int64_t k);   /* repack_x86.rs:100-121 */
+/* the weight with the tile forms the reference caches (repack.rs:35-70); `blocks` must outlive the handle */
+void *oracle_x86_prepare(int type, const void *blocks, int64_t n, int64_t k);
+void oracle_x86_release(void *handle);
+/* dst [m][n] = lhs [m][k] x W^T on the reference's x86 route; returns 1 AMX, 2 tiles, 3 compact AVX2,
+ * 4 scalar, -1 error */
+int oracle_x86_matmul(const void *handle, int64_t m, const float *lhs, float *dst, int threads);
+int oracle_x86_physical_cores(void);
+int oracle_x86_describe(char *buf, int len);
+
 #ifdef __cplusplus
 }
 #endif

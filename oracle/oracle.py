@@ -70,6 +70,12 @@ def lib() -> ctypes.CDLL:
         for name in VEC_DOT.values():
             getattr(L, name).argtypes = [i64, vp, vp]
             getattr(L, name).restype = ctypes.c_float
+        L.oracle_x86_select.argtypes = [ctypes.c_int, i64, i64, i64]
+        L.oracle_x86_prepare.argtypes = [ctypes.c_int, vp, i64, i64]
+        L.oracle_x86_prepare.restype = vp
+        L.oracle_x86_release.argtypes = [vp]
+        L.oracle_x86_matmul.argtypes = [vp, i64, vp, vp, ctypes.c_int]
+        L.oracle_x86_describe.argtypes = [ctypes.c_char_p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -244,3 +250,54 @@ def router_topk(logits: np.ndarray, top_k: int, score_mode: int, weight_mode: in
         W[r] = w * sc
         I[r] = picks
     return W, I
+
+
+# ------------------------------------------------------------------ the reference's x86 CPU path (x86.c)
+
+X86_PATHS = {1: "amx", 2: "tiles", 3: "compact_avx2", 4: "scalar"}
+
+
+def x86_level() -> int:
+    """repack_x86::level(): 0 none, 1 AVX2, 2 AVX-VNNI, 3 AVX-512 VNNI (the reference's MISTRALRS_FORCE_AVX2 /
+    MISTRALRS_FORCE_AVXVNNI environment switches are read on every call)."""
+    return int(lib().oracle_x86_level())
+
+
+def x86_amx() -> bool:
+    return bool(lib().oracle_x86_amx())
+
+
+def x86_physical_cores() -> int:
+    return int(lib().oracle_x86_physical_cores())
+
+
+def x86_describe() -> str:
+    buf = ctypes.create_string_buffer(512)
+    lib().oracle_x86_describe(buf, 512)
+    return buf.value.decode(errors="replace")
+
+
+class X86Weight:
+    """A quantized weight prepared as the reference's CPU QMatMul caches it on x86 (tiles, AMX tiles)."""
+
+    def __init__(self, gtype: int, w: np.ndarray, n: int, k: int):
+        self.w = np.ascontiguousarray(w, dtype=np.uint8)  # the handle points into these bytes
+        assert self.w.size == n * k // BLOCK_SIZE[gtype] * TYPE_SIZE[gtype]
+        self.gtype, self.n, self.k = gtype, n, k
+        self.h = lib().oracle_x86_prepare(gtype, _p(self.w), n, k)
+        assert self.h, f"type {gtype} has no x86 path"
+
+    def matmul(self, x: np.ndarray, threads: int = 0, out: np.ndarray | None = None):
+        """x [m, k] f32 -> ([m, n] f32, path name)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m, k = x.shape
+        assert k == self.k
+        dst = out if out is not None else np.zeros((m, self.n), dtype=np.float32)
+        path = lib().oracle_x86_matmul(self.h, m, _p(x), _p(dst), threads)
+        assert path > 0
+        return dst, X86_PATHS[path]
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oracle_x86_release(self.h)
+            self.h = None
