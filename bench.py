@@ -207,8 +207,9 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     Per layer, as the reference's decode path runs them: the attention input is quantized once and q, k, v read
     that one activation; o and down quantize their own inputs (at b <= 2, o in one launch with its quantization,
     launch_mmvq_gguf_q4_k_f32_quantize_plain); gate and up are one fused-GLU launch
-    (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  Rows > 16 take the prefill matmul, one quantized
-    activation per distinct input.  The inputs are synthetic, one per projection group."""
+    (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  Each input takes QMatMul's route: the decode
+    launcher up to 32 rows, except the Q6_K down projection (K = 14336) above 16 rows, which takes the prefill
+    matmul; one quantized activation per distinct input.  The inputs are synthetic, one per projection group."""
     shapes = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
               ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
     layers = 32
@@ -217,16 +218,19 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
     res = {"weight_bytes_per_step": total_bytes,
            "launches_per_layer": "decode b <= 2: 3 quantize + q, k, v, o (quantizing its input), gate/up (fused GLU), "
-                                 "down = 9; b 3..16: 4 quantize + 6 = 10; prefill: 4 quantize + 7 matmuls"}
+                                 "down = 9; b 3..16: 4 quantize + 6 = 10; b 17..32: the same with down on the "
+                                 "prefill matmul = 10; prefill: 4 quantize + 7 matmuls"}
     import qmm as Q
     for b in batches:
         rng = np.random.default_rng(seed + 100 + b)
         xs = {g: torch.from_numpy(rng.standard_normal((b, kk), dtype=np.float32)).cuda()
               for g, kk in (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
         outs = {name: torch.empty((b, n), dtype=torch.float32, device="cuda") for name, _, n, _ in shapes}
-        decode = b <= 16
+        # QMatMul's route (QMatMul::max_decode_rows): the decode launcher up to 32 rows for Q4_K and for Q6_K with
+        # K <= 8192, up to 16 for the Q6_K down projection (K = 14336); the prefill matmul above
+        dec_of = {"attn": b <= 32, "o": b <= 32, "ffn": b <= 32, "down": b <= 16}
         # all seven types here quantize activations to Q8_K, so one buffer per input serves every projection on it
-        bufs = {g: (Q.quantize_decode(Q4K, x) if decode else Q.quantize_prefill(Q4K, x)) for g, x in xs.items()}
+        bufs = {g: (Q.quantize_decode(Q4K, x) if dec_of[g] else Q.quantize_prefill(Q4K, x)) for g, x in xs.items()}
         group = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "ffn", "up": "ffn", "down": "down"}
         kdim = {name: k for name, _, _, k in shapes}
         tdim = {name: t for name, t, _, _ in shapes}
@@ -238,15 +242,16 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
             for layer in range(layers):
                 for g, x in xs.items():
                     vy, kp = bufs[g]
-                    if decode and g == "o" and one_launch_o:
+                    if g == "o" and one_launch_o:
                         continue
-                    if decode:
+                    if dec_of[g]:
                         Q.quantize_decode(Q4K, x, kp=kp, out=vy)
                     else:
                         Q.quantize_prefill(Q4K, x, out=vy)
                 for name in ("q", "k", "v", "o", "gate", "down"):
                     vy, kp = bufs[group[name]]
                     t, n, k = tdim[name], ndim[name], kdim[name]
+                    decode = dec_of[group[name]]
                     if decode and name == "o" and one_launch_o:
                         Q.mmvq_quantize(t, dev["o"][layer], xs["o"], n, out=outs["o"])
                     elif decode and name == "gate":

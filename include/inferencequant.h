@@ -64,7 +64,7 @@ void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx
  * 1762-1834).  dst[j * stride_col_dst + row] = sum_k W[row, k] * Q(y_j)[k] for j < b_size, row < nrows_x;
  * vx = nrows_x rows of ncols_x / block values (GGUF bytes); vy = b_size activation rows from the
  * decode quantizer above, stride_col_y blocks apart.  The dtype suffix is dst's element type.
- * b_size 1..16 (the reference's plain launcher takes 1..8, its tensor-core one up to 16). */
+ * b_size 1..16, 1..32 for q4_k and q6_k (the reference's plain launcher takes 1..8, its tensor-core one up to 16). */
 #define QMM_DECLARE_MMVQ_PLAIN(t)                                                                                 \
   void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
                                         int stride_col_y, int stride_col_dst, int b_size, void *stream);         \
@@ -75,6 +75,28 @@ void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx
 QMM_DECLARE_MMVQ_PLAIN(q8_0)
 QMM_DECLARE_MMVQ_PLAIN(q4_k)
 QMM_DECLARE_MMVQ_PLAIN(q6_k)
+/* ------------------------------------------------------------------ tensor-core matvec entries
+ * launch_mmvq_tc_quantize_{bf16,f16,f32} (gguf/ffi.rs:632-652) and launch_mmvq_tc_gguf_{q4_k,q6_k}_<dt>_plain
+ * (gguf/ffi.rs:966-998), the pair fast_mmvq::plain routes 1..16 rows of a Q4_K / Q6_K weight to
+ * (fast_mmvq.rs:505-513, 1897-1930).  The quantizer writes num_rows rows of kx values (kx a multiple of 256) as
+ * kx / 256 blocks {f32 d; int8 qs[256]} of 260 bytes each: BlockQ8K::from_float's d and qs, bit-exact, without
+ * the bsums, so b rows fit the reference's scratch of (kx / 32) * 288 bytes per 8-row half
+ * (fast_mmvq.rs:92-93, 1903-1908).  The matvec reads b_size (1..16) such rows and writes
+ * dst[j * stride_col_dst + row] as the _plain entries do; it sums the int8 values itself, so the integer dots are
+ * those of the decode layout.  cfg (the reference's CUDA tile shape) is accepted and unused. */
+void launch_mmvq_tc_quantize_f32(const void *x, void *vy, int kx, int num_rows, void *stream);
+void launch_mmvq_tc_quantize_f16(const void *x, void *vy, int kx, int num_rows, void *stream);
+void launch_mmvq_tc_quantize_bf16(const void *x, void *vy, int kx, int num_rows, void *stream);
+#define QMM_DECLARE_MMVQ_TC(t)                                                                                    \
+  void launch_mmvq_tc_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
+                                           int stride_col_dst, int b_size, int cfg, void *stream);              \
+  void launch_mmvq_tc_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
+                                           int stride_col_dst, int b_size, int cfg, void *stream);              \
+  void launch_mmvq_tc_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,\
+                                            int stride_col_dst, int b_size, int cfg, void *stream);
+QMM_DECLARE_MMVQ_TC(q4_k)
+QMM_DECLARE_MMVQ_TC(q6_k)
+
 /* The adjacent GGUF types on the same decode kernels (gguf/ffi.rs:1158-1169 gguf_standard_types q4_0, q5_0, q5_k;
  * 1265-1267 gguf_iq_types iq4_xs; host fast_mmvq.rs:40-81, 214-298).  Activations: Q8_0 blocks for q4_0 / q5_0
  * (their CPU VecDotType), Q8_K blocks for q5_k and iq4_xs (k_quants.rs:2145-2232, cpu_dot.rs:416-440).  Weight

@@ -158,7 +158,8 @@ bool check_weights(const char *who, int type, int ncols_x, int stride_col_y, int
                    std::initializer_list<int> rows) {
   const int bs = (int)qmm_block_size(type);
   const int abs_ = type == QMM_TYPE_Q8_0 ? 32 : 256;
-  if (ncols_x <= 0 || ncols_x % bs != 0 || (int64_t)stride_col_y * abs_ < ncols_x || b < 0 || b > 16) {
+  const int bmax = type == QMM_TYPE_Q4K || type == QMM_TYPE_Q6K ? 32 : 16;  // as the plain launcher
+  if (ncols_x <= 0 || ncols_x % bs != 0 || (int64_t)stride_col_y * abs_ < ncols_x || b < 0 || b > bmax) {
     qmm_set_error("%s: ncols_x=%d stride_col_y=%d b_size=%d", who, ncols_x, stride_col_y, b);
     return false;
   }

@@ -585,17 +585,6 @@ struct ActDma8 {
   }
 };
 
-// v_permlane32_swap_b32 (gfx950): lanes 32..63 of lo trade places with lanes 0..31 of hi, so that afterwards lo
-// holds lane half 0's lo in both halves of each lane pair and hi lane half 1's hi (device pass only: the builtin
-// needs the gfx950 target)
-__device__ __forceinline__ void swap_lane_halves(uint32_t &lo, uint32_t &hi) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
-  lo = r[0];
-  hi = r[1];
-#endif
-}
-
 // An empty volatile asm statement on v: the compiler keeps such statements in order, and v's producers before it
 // (device pass only: the host pass has no VGPR constraint and never runs this code)
 template <class T>
@@ -1082,13 +1071,9 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
         k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                     splits, d, stride_col_dst, part, ncols_dst);
       break;
-    case QMM_TYPE_Q5K:
-      if (small)
-        k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
-      else
-        k_mmq_kq_moe<wq5k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
+    case QMM_TYPE_Q5K:  // always 32-row tiles (small)
+      k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                  splits, d, stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q6K:
       if (small)

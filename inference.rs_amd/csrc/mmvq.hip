@@ -481,8 +481,10 @@ bool check_mmvq(const char *who, int type, const void *vx, int ncols_x, int nrow
     qmm_set_error("%s: stride_col_y=%d blocks holds fewer than ncols_x=%d values", who, stride_col_y, ncols_x);
     return false;
   }
-  if (b < 0 || b > 16) {
-    qmm_set_error("%s: b_size=%d outside 1..16", who, b);
+  // Q4_K / Q6_K take up to 32 rows (the few-row MFMA kernel holds 32 activation rows in one tile); the rest 16
+  const int bmax = type == QMM_TYPE_Q4K || type == QMM_TYPE_Q6K ? 32 : 16;
+  if (b < 0 || b > bmax) {
+    qmm_set_error("%s: b_size=%d outside 1..%d", who, b, bmax);
     return false;
   }
   const uintptr_t align = weight_align(type);
@@ -792,7 +794,46 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
       0, stream, who);
 }
 
+// The reference's tensor-core matvec entries (launch_mmvq_tc_gguf_<t>_<dt>_plain, crates/inference-quant/src/gguf/
+// ffi.rs:966-998; routed by fast_mmvq.rs:505-513 for 1..16 rows) over the tensor-core entries' activation layout
+// (launch_mmvq_tc_quantize_*: rows of ncols_x / 256 blocks {f32 d; int8 qs[256]}, units.h): the persistent matvec
+// below the few-row threshold, the few-row MFMA kernel from it, with the same integer dots as the plain entries.
+// cfg names one of the reference's CUDA tile shapes (fast_mmvq.rs:1845-1881); it is accepted and has no meaning here.
+template <class Out>
+void tc_plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_dst,
+              int b, int cfg, void *stream, const char *who) {
+  (void)cfg;
+  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, ncols_x / 256, b)) return;
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  if (b >= qmm_skinny_min_rows(type) &&
+      qmm_skinny_tc(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s))
+    return;
+  const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+  typename Out::T *d = (typename Out::T *)dst;
+  const int64_t ay = (int64_t)(ncols_x / 256) * 260;
+  if (type == QMM_TYPE_Q4K)
+    launch_cols<unit_q4k_tc, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+  else
+    launch_cols<unit_q6k_tc, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+}
+
 }  // namespace
+
+#define QMM_DEFINE_TC(t, TYPE)                                                                                    \
+  void launch_mmvq_tc_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
+                                           int stride_col_dst, int b_size, int cfg, void *stream) {             \
+    tc_plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream, "mmvq_tc_" #t "_f32"); \
+  }                                                                                                               \
+  void launch_mmvq_tc_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
+                                           int stride_col_dst, int b_size, int cfg, void *stream) {             \
+    tc_plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream, "mmvq_tc_" #t "_f16"); \
+  }                                                                                                               \
+  void launch_mmvq_tc_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,\
+                                            int stride_col_dst, int b_size, int cfg, void *stream) {            \
+    tc_plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream,                  \
+                       "mmvq_tc_" #t "_bf16");                                                                    \
+  }
 
 #define QMM_DEFINE_PLAIN_ONLY(t, TYPE)                                                                            \
   void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
@@ -863,6 +904,8 @@ void indexed(int type, const void *w, const void *x, const uint32_t *ids, float 
   }
 
 extern "C" {
+QMM_DEFINE_TC(q4_k, QMM_TYPE_Q4K)
+QMM_DEFINE_TC(q6_k, QMM_TYPE_Q6K)
 QMM_DEFINE_PLAIN(q8_0, QMM_TYPE_Q8_0)
 QMM_DEFINE_PLAIN(q4_k, QMM_TYPE_Q4K)
 QMM_DEFINE_PLAIN(q6_k, QMM_TYPE_Q6K)

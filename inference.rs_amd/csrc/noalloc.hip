@@ -19,7 +19,11 @@ constexpr size_t kActBytes = (size_t)16 << 20;
 constexpr size_t kFixupBytes = (size_t)16 << 20;
 constexpr size_t kScratchBytes = kActBytes + kFixupBytes;
 constexpr int kMaxDevices = 64;
-constexpr int64_t kDecodeRows = 16;  // the host QMatMul's decode / prefill boundary (QMatMul::kMaxDecodeRows)
+// the host QMatMul's decode / prefill boundary (QMatMul::max_decode_rows): 32 rows for Q4_K and for Q6_K rows of
+// at most 8192 values (the few-row MFMA kernel), 16 otherwise
+int64_t decode_rows(int type, int64_t k) {
+  return type == QMM_TYPE_Q4K || (type == QMM_TYPE_Q6K && k <= 8192) ? 32 : 16;
+}
 }  // namespace
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
@@ -141,7 +145,8 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
   }
   uint8_t *ptr = scratch_ptr();
   if (!ptr) return -1;
-  if (rows <= kDecodeRows || !mm) {
+  const int64_t per = decode_rows(wtype, k);
+  if (rows <= per || !mm) {
     const int64_t kp = pad_to(k, act_block(wtype));
     const int64_t row_bytes = kp / act_block(wtype) * act_block_bytes(wtype);
     if (rows * row_bytes > (int64_t)kActBytes) {
@@ -151,8 +156,8 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
     }
     decode_quantizer(wtype, in_dtype)(xs, ptr, (int)k, (int)kp, (int)rows, stream);
     const int64_t out_elem = in_dtype == QMM_TYPE_F32 ? 4 : 2;
-    for (int64_t r0 = 0; r0 < rows; r0 += kDecodeRows) {
-      const int64_t b = rows - r0 < kDecodeRows ? rows - r0 : kDecodeRows;
+    for (int64_t r0 = 0; r0 < rows; r0 += per) {
+      const int64_t b = rows - r0 < per ? rows - r0 : per;
       decode_matvec(wtype, in_dtype)(w, ptr + r0 * row_bytes, (uint8_t *)ys + r0 * n * out_elem, (int)k, (int)n,
                                      (int)(kp / act_block(wtype)), (int)n, (int)b, stream);
     }

@@ -20,6 +20,17 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t v, uint32_t s) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// v_permlane32_swap_b32 (gfx950): lanes 32..63 of lo trade places with lanes 0..31 of hi, so that afterwards lo
+// holds lane half 0's lo in both halves of each lane pair and hi lane half 1's hi (device pass only: the builtin
+// needs the gfx950 target)
+__device__ __forceinline__ void swap_lane_halves(uint32_t &lo, uint32_t &hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+  lo = r[0];
+  hi = r[1];
+#endif
+}
+
 // Row of 32x32 output register r of lane group g (v_mfma 32x32 D layout): 8 (r / 4) + 4 g + r % 4
 __device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 

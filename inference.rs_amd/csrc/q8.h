@@ -10,8 +10,8 @@
 
 namespace qmm_q8 {
 
-// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k, bsums int16) or the
-// prefill tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16] as f16, which holds every
+// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k, bsums int16), the
+// tensor-core entries' layout (no bsums) or the prefill tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16] as f16, which holds every
 // bsum exactly: |bsum| <= 16 * 128 = 2048).
 struct q8k_dst {
   uint8_t *qs;
@@ -23,6 +23,12 @@ struct q8k_dst {
 __device__ __forceinline__ q8k_dst q8k_decode_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8k);
   return {b + 4, (float *)b, (uint16_t *)(b + 260), false};
+}
+
+// tensor-core entry layout: {f32 d; int8 qs[256]} blocks of 260 bytes, no bsums
+__device__ __forceinline__ q8k_dst q8k_tc_dst(uint8_t *vy, int64_t block) {
+  uint8_t *b = vy + block * 260;
+  return {b + 4, (float *)b, nullptr, false};
 }
 
 __device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
@@ -81,7 +87,7 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
     const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *(uint32_t *)(dst[t].qs + 4 * lane) = packed;
-    if ((lane & 3) == 0) dst[t].bsums[lane >> 2] = bsum_bits(s, dst[t].bsums_f16);  // +0 for a zero block
+    if ((lane & 3) == 0 && dst[t].bsums) dst[t].bsums[lane >> 2] = bsum_bits(s, dst[t].bsums_f16);  // +0 for a zero block
     if (lane == 0) *dst[t].d = nz ? 1.0f / iscale : 0.0f;
   }
 }

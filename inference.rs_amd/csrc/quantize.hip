@@ -28,6 +28,20 @@ __global__ __launch_bounds__(256) void k_quantize_q8k_rows(const typename In::T 
   q8k_wave(v, lane, q8k_decode_dst(vy, blk));
 }
 
+// the tensor-core entries' layout: rows of kx / 256 blocks {f32 d; int8 qs[256]}
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_q8k_tc_rows(const typename In::T *__restrict__ x,
+                                                              uint8_t *__restrict__ vy, int kx, int num_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nsb = kx / 256;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nsb * num_rows) return;  // whole wave
+  const int64_t row = blk / nsb, sb = blk % nsb;
+  float v[4];
+  load4<In>(x + row * (int64_t)kx, sb * 256 + lane * 4, kx, v);
+  q8k_wave(v, lane, q8k_tc_dst(vy, blk));
+}
+
 template <class In>
 __global__ __launch_bounds__(256) void k_quantize_q8_0_rows(const typename In::T *__restrict__ x,
                                                             uint8_t *__restrict__ vy, int kx, int kx_padded,
@@ -148,6 +162,18 @@ void decode_q8k(const void *x, void *vy, int kx, int kx_padded, int num_rows, vo
 }
 
 template <class In>
+void tc_q8k(const void *x, void *vy, int kx, int num_rows, void *stream) {
+  if (kx <= 0 || num_rows < 0 || kx % 256 != 0) {
+    qmm_set_error("mmvq_tc_quantize: kx=%d num_rows=%d (kx must be a positive multiple of 256)", kx, num_rows);
+    return;
+  }
+  const int64_t blocks = (int64_t)kx / 256 * num_rows;
+  if (blocks == 0) return;
+  k_quantize_q8k_tc_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
+      (const typename In::T *)x, (uint8_t *)vy, kx, num_rows);
+}
+
+template <class In>
 void decode_q8_0(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
   if (kx < 0 || num_rows < 0 || kx_padded % 32 != 0 || kx_padded < kx) {
     qmm_set_error("quantize_q8_0: kx=%d kx_padded=%d num_rows=%d (kx_padded must be a multiple of 32, >= kx)", kx,
@@ -181,6 +207,15 @@ void launch_mmvq_gguf_quantize_q8k_f16(const void *x, void *vy, int kx, int kx_p
 }
 void launch_mmvq_gguf_quantize_q8k_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
   decode_q8k<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
+}
+void launch_mmvq_tc_quantize_f32(const void *x, void *vy, int kx, int num_rows, void *stream) {
+  tc_q8k<in_f32>(x, vy, kx, num_rows, stream);
+}
+void launch_mmvq_tc_quantize_f16(const void *x, void *vy, int kx, int num_rows, void *stream) {
+  tc_q8k<in_f16>(x, vy, kx, num_rows, stream);
+}
+void launch_mmvq_tc_quantize_bf16(const void *x, void *vy, int kx, int num_rows, void *stream) {
+  tc_q8k<in_bf16>(x, vy, kx, num_rows, stream);
 }
 void launch_mmvq_gguf_quantize_q8_0_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
   decode_q8_0<in_f32>(x, vy, kx, kx_padded, num_rows, stream);

@@ -20,6 +20,11 @@ bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_
                     int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation,
                     hipStream_t s);
 
+// The same over the tensor-core entries' activation layout (rows of ncols_x / 256 blocks {f32 d; int8 qs[256]},
+// units.h), for launch_mmvq_tc_gguf_<t>_*_plain.
+bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                   int stride_col_dst, int b, hipStream_t s);
+
 // Expert-grouped matmul (launch_mmq_gguf_<t>_moe) over prefill-layout activations when the experts receive few
 // rows each: at most QMM_SKINNY_MOE_ROWS on average.  dst[ids_dst[m] * ldd + n], f32.  Returns false, launching
 // nothing, for a case it does not serve.

@@ -69,6 +69,44 @@ struct act_decode {
   }
 };
 
+// Tensor-core entry layout (units.h): row m = K / 256 blocks of 260 bytes {f32 d; int8 qs[256]}, no bsums.  Lane
+// (li, g) sums its own fragments -- q[j] is values 32 j + 16 g .. +16, bsum index 2 j + g -- and trades half of
+// them with its partner lane so that it ends with bsums 8 g .. 8 g + 7, the order act_decode loads them in.
+struct act_tc {
+  const uint8_t *base;
+  int64_t bytes;
+  uint32_t row_bytes;
+  __device__ __forceinline__ rsrc_t rsrc() const { return make_rsrc(base, bytes); }
+  __device__ __forceinline__ uint32_t handle(int64_t m, bool valid) const {
+    return valid ? (uint32_t)m * row_bytes : 0x80000000u;
+  }
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t row_off, int64_t sb, int g, bool min, ActFrag &f) const {
+    const uint32_t o = row_off + (uint32_t)sb * 260;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, o + 4 + 32 * j + 16 * g, 0, 0));
+    if (min) {
+      uint32_t s[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc = sdot4(f.q[j][i], 0x01010101, acc);
+        s[j] = (uint32_t)acc;
+      }
+      // lo = own bsum 2i + g, hi = own bsum 2 (i + 4) + g; after the swap lane half g holds 8 g + 2i in lo and
+      // 8 g + 2i + 1 in hi
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        swap_lane_halves(s[i], s[i + 4]);
+        f.bs[2 * i] = (_Float16)(float)(int)s[i];  // exact: |bsum| <= 2048
+        f.bs[2 * i + 1] = (_Float16)(float)(int)s[i + 4];
+      }
+    }
+    f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
+  }
+};
+
 // Prefill layout of one channel (include/inferencequant.h): qs[nsb][rows][256] int8, then d[nsb][rows] f32, then
 // bsums[nsb][rows][16] f16.  The handle is the lane's offset 256 m of row m inside one superblock's qs slab, with
 // bit 31 set for a row that reads as zero; the superblock's part of every offset is uniform and goes in the
@@ -382,6 +420,29 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
 }
 
+// The tensor-core entries: the 32x32 form over act_tc, 4 waves splitting K (8 for long rows).
+template <class WT, class Out>
+void launch_tc(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_dst, int b,
+               hipStream_t s) {
+  const int64_t nsb = ncols_x / 256;
+  act_tc ap;
+  ap.row_bytes = (uint32_t)(nsb * 260);
+  ap.base = (const uint8_t *)vy;
+  ap.bytes = (int64_t)b * ap.row_bytes;
+  const uint8_t *w = (const uint8_t *)vx;
+  typename Out::T *d = (typename Out::T *)dst;
+  const int64_t wrb = nsb * WT::kBytes;
+  if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
+    k_skinny<WT, act_tc, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
+  else if (nsb >= 32)
+    k_skinny<WT, act_tc, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
+  else
+    k_skinny<WT, act_tc, Out, 4, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
+        w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
+}
+
 template <class WT>
 void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                 int64_t nrows_x, int64_t w_row_bytes, int64_t nsb, int64_t ncols_dst, int64_t ldd, int64_t num_experts,
@@ -438,6 +499,25 @@ bool qmm_skinny_glu(int type, int out_type, const void *vx_gate, const void *vx_
                     hipStream_t s) {
   return dispatch(type, out_type, vx_gate, vx_up, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b,
                   activation, s);
+}
+
+bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,
+                   int stride_col_dst, int b, hipStream_t s) {
+  if (b < 1 || b > 32 || ncols_x % 256 != 0 || (int64_t)b * (ncols_x / 256) * 260 > 0x7ffffff0) return false;
+  if (type != QMM_TYPE_Q4K && type != QMM_TYPE_Q6K) return false;
+#define QMM_TC(WT)                                                                                   \
+  switch (out_type) {                                                                                \
+    case QMM_TYPE_F16: launch_tc<WT, out_f16>(vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s); break;   \
+    case QMM_TYPE_BF16: launch_tc<WT, out_bf16>(vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s); break; \
+    default: launch_tc<WT, out_f32>(vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s);            \
+  }
+  if (type == QMM_TYPE_Q4K) {
+    QMM_TC(wq4k)
+  } else {
+    QMM_TC(wq6k)
+  }
+#undef QMM_TC
+  return true;
 }
 
 bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,

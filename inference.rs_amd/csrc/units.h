@@ -641,3 +641,53 @@ struct unit_iq4xs {
     return d * (float)(ls[0] * s[0]) + d * (float)(ls[1] * s[1]);
   }
 };
+
+// ------------------------------------------------------------------------------------------------ tensor-core layout
+// Activations of the tensor-core matvec entries (launch_mmvq_tc_quantize_*, launch_mmvq_tc_gguf_<t>_*_plain):
+// Q8_K blocks without their bsums, {f32 d; int8 qs[256]}, 260 bytes per 256 values and rows K / 256 blocks apart,
+// so b rows fit the reference's tensor-core scratch of 288 bytes per 256 values and 8-row half
+// (crates/inference-quant/src/gguf/fast_mmvq.rs:92-93, 1903-1908).  The units sum the int8 values they need
+// themselves (one v_dot4 against ones per 4 values, once per launch), so the integer dots are those of the
+// decode layout.
+__device__ __forceinline__ int byte_sum(const uint32_t *q, int n, int acc) {
+  for (int i = 0; i < n; i++) acc = sdot4((int)q[i], 0x01010101, acc);
+  return acc;
+}
+
+struct unit_q4k_tc : unit_q4k {
+  static constexpr int kActBlockBytes = 260;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * 260;
+    const int c = u & 3;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const u32x4 v = ld_a4(p + 4 + 64 * c + 16 * i);
+      a.q[4 * i + 0] = v.x;
+      a.q[4 * i + 1] = v.y;
+      a.q[4 * i + 2] = v.z;
+      a.q[4 * i + 3] = v.w;
+    }
+    a.b0 = byte_sum(a.q, 8, 0);      // sub-block 2c: bsums[4c] + bsums[4c + 1]
+    a.b1 = byte_sum(a.q + 8, 8, 0);  // sub-block 2c + 1
+    a.d = __builtin_bit_cast(float, ld32(p));
+  }
+};
+
+struct unit_q6k_tc : unit_q6k {
+  static constexpr int kActBlockBytes = 260;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p0 = row + (int64_t)(u >> 2) * 260;
+    const int h = (u >> 1) & 1, p = u & 1;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const u32x4 v = ld_a4(p0 + 4 + 128 * h + 32 * q + 16 * p);
+      a.q[4 * q + 0] = v.x;
+      a.q[4 * q + 1] = v.y;
+      a.q[4 * q + 2] = v.z;
+      a.q[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) a.bs[q] = byte_sum(a.q + 4 * q, 4, 0);  // bsums[8h + 2q + p]
+    a.d = __builtin_bit_cast(float, ld32(p0));
+  }
+};

@@ -366,7 +366,12 @@ QMatMul::QMatMul(std::shared_ptr<QTensor> w) : w_(std::move(w)) {
   if (!w_) throw Error("QMatMul: null weight");
 }
 
-bool QMatMul::prefers_mmvq(GgmlDType, int64_t rows) { return rows <= kMaxDecodeRows; }
+int64_t QMatMul::max_decode_rows(GgmlDType dtype, int64_t k) {
+  if (dtype == GgmlDType::Q4K || (dtype == GgmlDType::Q6K && k <= kMaxFewRowK)) return kMaxFewRows;
+  return kMaxDecodeRows;
+}
+
+bool QMatMul::prefers_mmvq(GgmlDType dtype, int64_t rows, int64_t k) { return rows <= max_decode_rows(dtype, k); }
 
 void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys, hipStream_t stream) const {
   const QTensor &w = *w_;
@@ -379,21 +384,22 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
   const int64_t k = w.cols(), n = w.rows();
   const GgmlDType t = w.dtype();
   hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
-  if (has_all_routes(t) && prefers_mmvq(t, rows) && in_dtype == GgmlDType::F32 && rows <= 2 && k <= 4096 &&
+  if (has_all_routes(t) && in_dtype == GgmlDType::F32 && rows <= 2 && k <= 4096 &&
       (t != GgmlDType::Q8_0 || k % 64 == 0) && (uintptr_t)xs % 4 == 0) {
     // one launch: the matvec quantizes its activations itself (the same bits as the two launches below)
     decode_matvec_quantize(t)(w.device_ptr(), (const float *)xs, ys, (int)k, (int)n, (int)k, (int)n, (int)rows, stream);
     abi_check("QMatMul::forward (matvec)");
-  } else if (prefers_mmvq(t, rows) || !has_prefill(t)) {
-    // the decode matvec; a type without a prefill kernel takes every batch this way, kMaxDecodeRows rows a launch
+  } else if (prefers_mmvq(t, rows, k) || !has_prefill(t)) {
+    // the decode matvec; a type without a prefill kernel takes every batch this way, max_decode_rows rows a launch
+    const int64_t per = max_decode_rows(t, k);
     const int64_t kp = pad_to(k, act_block(t));
     const int64_t row_bytes = (kp / act_block(t)) * act_block_bytes(t);
     void *vy = workspace().get(w.device().ordinal, (size_t)(rows * row_bytes), stream);
     decode_quantizer(t, in_dtype)(xs, vy, (int)k, (int)kp, (int)rows, stream);
     abi_check("QMatMul::forward (quantize)");
     const size_t out_elem = in_dtype == GgmlDType::F32 ? 4 : 2;
-    for (int64_t r0 = 0; r0 < rows; r0 += kMaxDecodeRows) {
-      const int64_t b = rows - r0 < kMaxDecodeRows ? rows - r0 : kMaxDecodeRows;
+    for (int64_t r0 = 0; r0 < rows; r0 += per) {
+      const int64_t b = rows - r0 < per ? rows - r0 : per;
       decode_matvec(t, in_dtype)(w.device_ptr(), (const uint8_t *)vy + r0 * row_bytes, (uint8_t *)ys + r0 * n * out_elem,
                                  (int)k, (int)n, (int)(kp / act_block(t)), (int)n, (int)b, stream);
       abi_check("QMatMul::forward (matvec)");

@@ -111,16 +111,23 @@ class QTensor {
 };
 
 // QMatMul (mod.rs:1117-1187, 1625-1648) over a quantized weight, with the GPU route choice of
-// gguf/mod.rs:434-452: decode matvec (launch_mmvq_gguf_*) for a flat batch of at most kMaxDecodeRows rows,
+// gguf/mod.rs:434-452: decode matvec (launch_mmvq_gguf_*) for a flat batch of at most max_decode_rows rows,
 // the prefill matmul (launch_mmq_gguf_*) above it.
 class QMatMul {
  public:
   static constexpr int64_t kMaxDecodeRows = 16;  // fast_mmvq.rs TENSOR_CORE_MAX_ROWS, re-derived for gfx950
+  // Q4_K, and Q6_K with rows of at most kMaxFewRowK values, stay on the decode launcher up to 32 rows: its few-row
+  // MFMA kernel streams the weight once for all of them and measured faster than the prefill tile there on MI355X
+  // (Q4_K 4096x4096 at 32 rows 10.4 against 13.2 us; Q6_K 4096x14336 is the exception, 34.6 against 31.7 us, as
+  // the reference keeps Q6_K's widest rows on MMQ, fast_mmvq.rs:1838-1881)
+  static constexpr int64_t kMaxFewRows = 32;
+  static constexpr int64_t kMaxFewRowK = 8192;
 
   explicit QMatMul(std::shared_ptr<QTensor> w);
   const QTensor &weight() const { return *w_; }
 
-  static bool prefers_mmvq(GgmlDType dtype, int64_t rows);
+  static int64_t max_decode_rows(GgmlDType dtype, int64_t k);
+  static bool prefers_mmvq(GgmlDType dtype, int64_t rows, int64_t k);
 
   // ys[rows, N] = xs[rows, K] . W^T on the weight's device; xs / ys device pointers of in_dtype
   // (F32, F16 or BF16), as QMatMul::forward keeps the activation dtype (gguf/mod.rs:656-661).

@@ -89,6 +89,11 @@ def _declare(L: ctypes.CDLL) -> None:
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
         getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
                                                             i32, vp]
+    for src in ("f32", "f16", "bf16"):
+        getattr(L, f"launch_mmvq_tc_quantize_{src}").argtypes = [vp, vp, i32, i32, vp]
+    for t in ("q4_k", "q6_k"):
+        for o in ("f32", "f16", "bf16"):
+            getattr(L, f"launch_mmvq_tc_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
     for t in TYPE_NAME.values():
         getattr(L, f"launch_mmvq_gguf_{t}_moe_wsum").argtypes = [vp, i64, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
     for name in MOE_NAME.values():
@@ -244,6 +249,36 @@ def mmvq_fused_qkv(wtype: int, wq, wk, wv, vy, k: int, nq: int, nk: int, nv: int
         kp // BLOCK_SIZE[ACT_TYPE[wtype]], b, _stream())
     check()
     return outs
+
+
+def tc_scratch_bytes(k: int, rows: int) -> int:
+    """The reference's tensor-core activation scratch: (k / 32) * 288 bytes per 8-row half
+    (crates/inference-quant/src/gguf/fast_mmvq.rs:92-93, 1903-1908)."""
+    return k // 32 * (32 * 8 + 8 * 2 + 8 * 2) * ((rows + 7) // 8)
+
+
+def tc_quantize(x, out=None):
+    """x [rows, k] (k a multiple of 256) -> the tensor-core entries' layout (rows of k / 256 blocks {f32 d; i8 qs[256]})
+    through launch_mmvq_tc_quantize_<src>; out defaults to the reference's scratch size."""
+    torch = _torch()
+    rows, k = x.shape
+    if out is None:
+        out = torch.empty(tc_scratch_bytes(k, rows), dtype=torch.uint8, device=x.device)
+    getattr(lib(), f"launch_mmvq_tc_quantize_{_src_name(x)}")(_ptr(x), _ptr(out), k, rows, _stream())
+    check()
+    return out
+
+
+def mmvq_tc(wtype: int, w, vy, k: int, n: int, b: int, cfg: int = 0, out_dtype=None, out=None):
+    """dst [b, n] through launch_mmvq_tc_gguf_<t>_<dtype>_plain over tc_quantize's layout."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((b, n), dtype=out_dtype or torch.float32, device=w.device)
+    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
+    getattr(lib(), f"launch_mmvq_tc_gguf_{TYPE_NAME[wtype]}_{oname}_plain")(
+        _ptr(w), _ptr(vy), _ptr(out), k, n, out.stride(0), b, cfg, _stream())
+    check()
+    return out
 
 
 def qmatmul_decode(wtype: int, w, x, n: int, out_dtype=None):

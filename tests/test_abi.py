@@ -50,7 +50,7 @@ def test_bad_arguments_are_rejected_before_any_launch():
     L.launch_mmvq_gguf_q4_k_f32_plain(None, None, None, 100, 8, 1, 8, 1, None)
     assert "ncols_x" in qmm.last_error()
     L.qmm_clear_error()
-    L.launch_mmvq_gguf_q4_k_f32_plain(None, None, None, 256, 8, 1, 8, 17, None)
+    L.launch_mmvq_gguf_q4_k_f32_plain(None, None, None, 256, 8, 1, 8, 33, None)  # Q4_K takes up to 32 rows
     assert "b_size" in qmm.last_error()
     L.qmm_clear_error()
     L.launch_indexed_moe_forward_q4k_q8k(None, None, None, None, 8, 256, 2, 2, 256, 3, None)

@@ -40,11 +40,12 @@ def stack():
     return ws, {name: dev(w) for name, w in ws.items()}
 
 
-@pytest.mark.parametrize("b", [1, 8, 32])
+@pytest.mark.parametrize("b", [1, 8, 24, 32])
 def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
-    """Each projection of one layer through the launch sequence bench.py's stack workload times: at b <= 16 the
-    decode quantizer once per input and the matvec (o in one launch with its own quantization at b <= 2; gate and
-    up as one fused-GLU launch, SiLU); above 16 rows the prefill quantizer and matmul."""
+    """Each projection of one layer through the launch sequence bench.py's stack workload times, on QMatMul's route:
+    the decode quantizer once per input and the matvec up to 32 rows (o in one launch with its own quantization at
+    b <= 2; gate and up as one fused-GLU launch, SiLU), except the Q6_K down projection (K = 14336), which takes
+    the prefill quantizer and matmul above 16 rows."""
     ws, wd = stack
     rng = np.random.default_rng(40 + b)
     x = {"attn": acts(rng, b, 4096), "o": acts(rng, b, 4096), "ffn": acts(rng, b, 4096), "down": acts(rng, b, 14336)}
@@ -52,11 +53,12 @@ def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
     spec = {name: (t, n, k) for name, t, n, k in STACK}
     want = {name: O.matmul(t, x[group[name]], ws[name], n) for name, (t, n, k) in spec.items()}
     xd = {g: dev(v) for g, v in x.items()}
-    decode = b <= 16
-    bufs = {g: (qmm.quantize_decode(O.Q4K, v) if decode else qmm.quantize_prefill(O.Q4K, v)) for g, v in xd.items()}
+    dec_of = {"attn": b <= 32, "o": b <= 32, "ffn": b <= 32, "down": b <= 16}
+    bufs = {g: (qmm.quantize_decode(O.Q4K, v) if dec_of[g] else qmm.quantize_prefill(O.Q4K, v)) for g, v in xd.items()}
     for name in ("q", "k", "v", "o", "down"):
         t, n, k = spec[name]
         vy, kp = bufs[group[name]]
+        decode = dec_of[group[name]]
         if decode and name == "o" and b <= 2:
             got = qmm.mmvq_quantize(t, wd[name], xd["o"], n)
         elif decode:
@@ -66,7 +68,7 @@ def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
         assert_parity(got.cpu().numpy(), want[name], what=f"b={b} {name}")
     t, n, k = spec["gate"]
     vy, kp = bufs["ffn"]
-    if decode:
+    if dec_of["ffn"]:
         got = qmm.mmvq_fused_glu(t, wd["gate"], wd["up"], vy, k, n, b, kp, activation=0).cpu().numpy()
         assert_parity(got, silu(want["gate"]) * want["up"], what=f"b={b} fused gate/up")
     else:
@@ -75,7 +77,7 @@ def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
             assert_parity(got, want[name], what=f"b={b} {name}")
 
 
-@pytest.mark.parametrize("b", [1, 8, 32])
+@pytest.mark.parametrize("b", [1, 8, 24, 32, 40])
 def test_llama3_stack_through_qmatmul_forward(stack, b):
     """The same projections through the host operator QMatMul::forward (qmm_qmatmul_forward), which picks the route
     for the row count itself."""

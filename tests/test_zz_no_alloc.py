@@ -34,9 +34,9 @@ def host_forward(h, x, n):
 
 
 # (weight type, n, k, activation dtype, row counts of consecutive calls): the prefill route with split K (300 and 40
-# rows: planes in the scratch's fixup part), the decode route through the scratch (9 rows), the one-launch matvec
+# rows: planes in the scratch's fixup part), the decode route through the scratch (24 rows on the few-row kernel, 9), the one-launch matvec
 # (2 rows, no scratch); Q6_K at K = 14336 with bf16 activations; Q8_0 and Q5_K with f16
-CASES = [(O.Q4K, 4096, 4096, torch.float32, (300, 40, 9, 2)),
+CASES = [(O.Q4K, 4096, 4096, torch.float32, (300, 40, 24, 9, 2)),
          (O.Q6K, 1024, 14336, torch.bfloat16, (64, 5)),
          (O.Q8_0, 2048, 4096, torch.float16, (20, 3)),
          (O.Q5K, 512, 2048, torch.float32, (33, 17))]
