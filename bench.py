@@ -318,6 +318,41 @@ def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
             "frac_hbm_peak": wbytes / per / 1e9 / HBM_PEAK_GBS, "tops": ops / per / 1e12}
 
 
+def read_floor_workload(torch, qmm, steps, warmup, seed):
+    """The HBM read floor for the headline: one launch streaming 33,030,144 bytes (the Q4_K 14336x4096 weight) over 16
+    rotating copies, as qmm_hbm_read_probe's grid-stride walk (depth x per-CU workgroups swept) and as the decode
+    matvec's walk over Q4_K rows; the best of the sweep is the floor a one-launch decode step can reach."""
+    nbytes = 33030144
+    copies = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(16)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(16 * cus * 256, dtype=torch.int32, device="cuda")
+    res = {"bytes": nbytes, "copies": 16}
+    L = qmm.lib()
+
+    def run(pattern, per_cu, depth):
+        def fn(i):
+            rc = L.qmm_hbm_read_probe(qmm._ptr(copies[i % 16]), nbytes, pattern, per_cu, depth, qmm._ptr(out),
+                                      qmm._stream())
+            if rc != 0:
+                raise RuntimeError(qmm.last_error())
+        return graph_time(torch, fn, steps, warmup) / steps
+
+    best = None
+    for per_cu in (1, 2, 4, 8):
+        for depth in (1, 2, 4, 8):
+            t = run(0, per_cu, depth)
+            res[f"stride_wg{per_cu}_d{depth}_us"] = t * 1e6
+            if best is None or t < best[0]:
+                best = (t, f"stride wg{per_cu} d{depth}")
+    t = run(1, 8, 1)
+    res["matvec_rows_wg8_us"] = t * 1e6
+    res["floor_us"] = best[0] * 1e6
+    res["floor_gb_s"] = nbytes / best[0] / 1e9
+    res["floor_form"] = best[1]
+    res["matvec_rows_gb_s"] = nbytes / t / 1e9
+    return res
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 
 def _timed(fn, seconds, min_reps):
@@ -391,7 +426,7 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
                "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
                "iq4_xs_decode", "q6_k_decode", "moe_8x_q4_k_4tok_top2", "q4_0_prefill_m512", "q8_0_prefill_m512",
-               "q5_0_prefill_m512", "q5_k_prefill_m512"}
+               "q5_0_prefill_m512", "q5_k_prefill_m512", "read_floor"}
 
 
 def decode_summary(r):
@@ -474,6 +509,7 @@ def main():
                                                               args.warmup // 2, SEED + 43)),
         "iq4_xs_decode": lambda: decode_summary(decode_workload(torch, qmm, IQ4XS, n, k, 1, 16, args.steps // 2,
                                                                 args.warmup // 2, SEED + 44)),
+        "read_floor": lambda: read_floor_workload(torch, qmm, args.steps // 4, args.warmup // 4, SEED),
     }
     assert set(extra_runs) == EXTRA_NAMES
     if args.only:

@@ -89,6 +89,8 @@ def _declare(L: ctypes.CDLL) -> None:
             getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
         getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
                                                             i32, vp]
+    L.qmm_hbm_read_probe.argtypes = [vp, i64, i32, i32, i32, vp, vp]
+    L.qmm_hbm_read_probe.restype = i32
     for src in ("f32", "f16", "bf16"):
         getattr(L, f"launch_mmvq_tc_quantize_{src}").argtypes = [vp, vp, i32, i32, vp]
     for t in ("q4_k", "q6_k"):
