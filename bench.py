@@ -320,8 +320,9 @@ def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
 
 def read_floor_workload(torch, qmm, steps, warmup, seed):
     """The HBM read floor for the headline: one launch streaming 33,030,144 bytes (the Q4_K 14336x4096 weight) over 16
-    rotating copies, as qmm_hbm_read_probe's grid-stride walk (depth x per-CU workgroups swept) and as the decode
-    matvec's walk over Q4_K rows; the best of the sweep is the floor a one-launch decode step can reach."""
+    rotating copies, as qmm_hbm_read_probe's grid-stride walk (depth x per-CU workgroups swept) and as walks over Q4_K
+    rows (the decode units' loads, contiguous chunks, contiguous chunks plus headers; 1 or 2 rows in flight per wave);
+    the best grid-stride time is the floor a one-launch decode step can reach."""
     nbytes = 33030144
     copies = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(16)]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -344,12 +345,18 @@ def read_floor_workload(torch, qmm, steps, warmup, seed):
             res[f"stride_wg{per_cu}_d{depth}_us"] = t * 1e6
             if best is None or t < best[0]:
                 best = (t, f"stride wg{per_cu} d{depth}")
-    t = run(1, 8, 1)
-    res["matvec_rows_wg8_us"] = t * 1e6
+    rows = None
+    for pattern, name in ((1, "units"), (2, "contig"), (3, "contig_hdr")):
+        for per_cu in (2, 4, 8):
+            for depth in (1, 2):
+                t = run(pattern, per_cu, depth)
+                res[f"rows_{name}_wg{per_cu}_d{depth}_us"] = t * 1e6
+                if pattern == 1 and (rows is None or t < rows):
+                    rows = t
     res["floor_us"] = best[0] * 1e6
     res["floor_gb_s"] = nbytes / best[0] / 1e9
     res["floor_form"] = best[1]
-    res["matvec_rows_gb_s"] = nbytes / t / 1e9
+    res["matvec_rows_gb_s"] = nbytes / rows / 1e9
     return res
 
 

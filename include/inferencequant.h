@@ -48,8 +48,9 @@ void qmm_clear_error(void);
  * qmm_hbm_read_probe (no counterpart in the reference): one launch that streams `bytes` of `src` (16-byte aligned)
  * and writes per-thread XORs to out (per_cu * CUs * 256 u32), the floor the decode matvec's HBM rate is measured
  * against.  pattern 0: a grid-stride walk of 16-byte chunks with `depth` (1, 2, 4 or 8) loads in flight per lane;
- * pattern 1: the decode matvec's walk over Q4_K rows of K = 4096 (header and two nibble chunks per lane, two rows in
- * flight).  per_cu workgroups of 256 threads per CU (1..16).  Returns 0, or -1 with qmm_last_error() set. */
+ * patterns 1-3: walks over Q4_K rows of K = 4096 with `depth` (1..3) rows in flight per wave, each lane loading the
+ * decode unit's header and two nibble chunks (1), contiguous 16-byte chunks (2), or those plus its superblock header
+ * (3).  per_cu workgroups of 256 threads per CU (1..16).  Returns 0, or -1 with qmm_last_error() set. */
 int qmm_hbm_read_probe(const void *src, int64_t bytes, int pattern, int per_cu, int depth, uint32_t *out,
                        void *stream);
 

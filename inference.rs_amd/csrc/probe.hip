@@ -4,7 +4,9 @@
 //   pattern 0  grid stride: wave slot s of the persistent grid reads 16-byte chunks s * 64 + lane, s + S, ... with
 //              `depth` loads in flight per lane
 //   pattern 1  the decode matvec's walk over Q4_K rows (k_mmvq_p): row r of wave slot s = r mod S, each lane loading
-//              the 16-byte header and two 16-byte nibble chunks of its quarter superblock, two rows in flight
+//              the 16-byte header and two 16-byte nibble chunks of its quarter superblock, `depth` rows in flight
+//   pattern 2  the same rows read as contiguous 16-byte chunks per lane (1 KB per wave instruction)
+//   pattern 3  pattern 2 plus each lane's 16-byte superblock header
 #include "common.h"
 #include "inferencequant.h"
 #include "units.h"
@@ -28,26 +30,44 @@ __global__ __launch_bounds__(256) void k_read_stride(const u32x4 *__restrict__ s
   out[(int64_t)blockIdx.x * 256 + threadIdx.x] = x;
 }
 
-// rows of row_bytes (a multiple of 144): lane l of a wave loads unit l of the row (the unit_q4k loads), units past
-// the row skipped; two rows in flight
+// rows of row_bytes (a multiple of 144), D rows in flight per wave.  Scattered (the decode units): lane l loads unit l
+// of the row (the unit_q4k loads, units past the row skipped).  Contiguous: lane l loads 16-byte chunks l, l + 64, ...
+// of the row (1 KB per wave instruction), plus, with HDR, the 16-byte header of its first chunk's superblock.
+template <bool CONTIG, bool HDR, int D>
 __global__ __launch_bounds__(256) void k_read_rows(const uint8_t *__restrict__ w, int64_t nrows, int64_t row_bytes,
                                                    uint32_t *__restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t S = (int64_t)gridDim.x * 4;
   const int nunits = (int)(row_bytes / 144 * 4);
+  const int nchunks = (int)(row_bytes / 16);
   uint32_t x = 0;
   int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  unit_q4k::W a, b;
-  auto load = [&](int64_t row, unit_q4k::W &u) {
-    if (row < nrows && lane < nunits) unit_q4k::load_w(w + row * row_bytes, lane, u);
+  struct buf {
+    u32x4 v[3];
   };
-  load(r, a);
-  load(r + S, b);
-  for (; r < nrows; r += 2 * S) {
-    x ^= a.hdr.x ^ a.q0.y ^ a.q1.z;
-    load(r + 2 * S, a);
-    x ^= b.hdr.x ^ b.q0.y ^ b.q1.z;
-    load(r + 3 * S, b);
+  auto load = [&](int64_t row, buf &u) {
+    if (row >= nrows) return;
+    const uint8_t *p = w + row * row_bytes;
+    if (CONTIG) {
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+        if (64 * i + lane < nchunks) u.v[i] = ld_a16(p + 16 * (64 * i + lane));
+      if (HDR) u.v[2].x ^= ld_a16(p + 144 * (lane / 9)).y;
+    } else if (lane < nunits) {
+      unit_q4k::W t;
+      unit_q4k::load_w(p, lane, t);
+      u.v[0] = t.hdr, u.v[1] = t.q0, u.v[2] = t.q1;
+    }
+  };
+  buf b[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) load(r + i * S, b[i]);
+  for (; r < nrows; r += D * S) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      x ^= b[i].v[0].x ^ b[i].v[1].y ^ b[i].v[2].z;
+      load(r + (D + i) * S, b[i]);
+    }
   }
   out[(int64_t)blockIdx.x * 256 + threadIdx.x] = x;
 }
@@ -72,7 +92,18 @@ extern "C" int qmm_hbm_read_probe(const void *src, int64_t bytes, int pattern, i
     }
   } else {
     const int64_t row_bytes = 2304;  // Q4_K, K = 4096
-    k_read_rows<<<grid, 256, 0, s>>>((const uint8_t *)src, bytes / row_bytes, row_bytes, out);
+    const int64_t nrows = bytes / row_bytes;
+    const uint8_t *w = (const uint8_t *)src;
+#define QMM_RR(C, H)                                                                               \
+  do {                                                                                             \
+    if (depth <= 1) k_read_rows<C, H, 1><<<grid, 256, 0, s>>>(w, nrows, row_bytes, out);           \
+    else if (depth == 2) k_read_rows<C, H, 2><<<grid, 256, 0, s>>>(w, nrows, row_bytes, out);      \
+    else k_read_rows<C, H, 3><<<grid, 256, 0, s>>>(w, nrows, row_bytes, out);                      \
+  } while (0)
+    if (pattern == 1) QMM_RR(false, false);
+    else if (pattern == 2) QMM_RR(true, false);
+    else QMM_RR(true, true);
+#undef QMM_RR
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
