@@ -433,7 +433,7 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
                "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
                "iq4_xs_decode", "q6_k_decode", "moe_8x_q4_k_4tok_top2", "q4_0_prefill_m512", "q8_0_prefill_m512",
-               "q5_0_prefill_m512", "q5_k_prefill_m512", "read_floor"}
+               "q5_0_prefill_m512", "q5_k_prefill_m512", "iq4_xs_prefill_m512", "read_floor"}
 
 
 def decode_summary(r):
@@ -490,21 +490,23 @@ def main():
                                                                   args.warmup // 2, SEED)),
         "q8_0_decode_4096": lambda: decode_summary(decode_workload(torch, qmm, Q8_0, 4096, 4096, 1, 32, args.steps,
                                                                    args.warmup, SEED + 5)),
-        "q4_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q4K, 14336, 4096, 512, 4,
+        "q4_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q4K, 14336, 4096, 512, 10,
                                                       max(20, args.steps // 20), 5, SEED + 9),
-        "q6_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q6K, 4096, 14336, 512, 4,
+        "q6_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q6K, 4096, 14336, 512, 8,
                                                       max(20, args.steps // 20), 5, SEED + 11),
         "llama3_8b_linear_stack": lambda: stack_workload(torch, qmm, (1, 8, 32), args.steps, args.warmup, SEED + 20),
         "moe_8x_q4_k_64tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 30),
         "moe_8x_q4_k_4tok_top2": lambda: moe_workload(torch, qmm, args.steps // 10, 2, SEED + 31, tokens=4),
-        "q4_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q4_0, 14336, 4096, 512, 4,
+        "q4_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q4_0, 14336, 4096, 512, 10,
                                                       max(20, args.steps // 20), 5, SEED + 45),
-        "q8_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q8_0, 14336, 4096, 512, 4,
+        "q8_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q8_0, 14336, 4096, 512, 10,
                                                       max(20, args.steps // 20), 5, SEED + 46),
-        "q5_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q5_0, 14336, 4096, 512, 4,
+        "q5_0_prefill_m512": lambda: prefill_workload(torch, qmm, Q5_0, 14336, 4096, 512, 10,
                                                       max(20, args.steps // 20), 5, SEED + 47),
-        "q5_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q5K, 14336, 4096, 512, 4,
+        "q5_k_prefill_m512": lambda: prefill_workload(torch, qmm, Q5K, 14336, 4096, 512, 10,
                                                       max(20, args.steps // 20), 5, SEED + 48),
+        "iq4_xs_prefill_m512": lambda: prefill_workload(torch, qmm, IQ4XS, 14336, 4096, 512, 10,
+                                                        max(20, args.steps // 20), 5, SEED + 49),
         # the other weight types at the headline shape, b = 1: the two-launch step and the matvec alone
         "q6_k_decode": lambda: decode_summary(decode_workload(torch, qmm, Q6K, n, k, 1, 12, args.steps // 2,
                                                               args.warmup // 2, SEED + 40)),

@@ -252,6 +252,10 @@ QMM_DECLARE_MMQ(q5_0)
 /* Q5_K (gguf/ffi.rs:906-955 gguf_mmq_type_library; block k_quants.rs:200-206): the K-quant kernel with a third
  * weight plane for the fifth bit, on Q8_K-layout activations (launch_mmq_quantize_q8k); weights 16-byte aligned */
 QMM_DECLARE_MMQ(q5_k)
+/* IQ4_XS (gguf/ffi.rs:906-952 gguf_mmq_type_library through gguf_iq_types, :1265-1267; mmq_instance_iq4_xs.cu): the
+ * K-quant kernel with table values times (ls - 32) split into two int8 planes as Q6_K's, on Q8_K-layout activations
+ * (launch_mmq_quantize_q8k); weights 4-byte aligned */
+QMM_DECLARE_MMQ(iq4_xs)
 /* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
  * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
  * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by

@@ -179,10 +179,11 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, (nlast + 1) * w_row_bytes);
   const uint32_t wrow = (uint32_t)(nl * w_row_bytes);
 
-  // LDS read offsets of this lane's A fragments: row 32t + li, chunk 2j + g, swizzled
+  // LDS read offsets of this lane's A fragments: row 32t + li, chunk WT::chunk(j, g) (2j + g but for IQ4_XS),
+  // swizzled
   uint32_t qoff[8];
 #pragma unroll
-  for (int j = 0; j < 8; j++) qoff[j] = 256 * li + 16 * ((2 * j + g) ^ (li & 15));
+  for (int j = 0; j < 8; j++) qoff[j] = 256 * li + 16 * (WT::chunk(j, g) ^ (li & 15));
 
   v16f fa[TM];
 #pragma unroll
@@ -873,6 +874,10 @@ bool check_mmq(const char *who, int type, const void *x, int64_t ncols_x, int64_
     qmm_set_error("%s: Q4_K / Q5_K weights must be 16-byte aligned", who);
     return false;
   }
+  if (type == QMM_TYPE_IQ4_XS && ((uintptr_t)x % 4 != 0)) {
+    qmm_set_error("%s: IQ4_XS weights must be 4-byte aligned", who);
+    return false;
+  }
   if ((uintptr_t)x % 2 != 0) {
     qmm_set_error("%s: weights must be 2-byte aligned", who);
     return false;
@@ -968,6 +973,7 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
     case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     case QMM_TYPE_Q5K: launch_kq<wq5k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
+    case QMM_TYPE_IQ4_XS: launch_kq<wiq4xs, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     default: {
       if (b32_runs(w, ncols_x, w_row_bytes)) {
         if (type == QMM_TYPE_Q4_0)
@@ -1083,6 +1089,14 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
         k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                     splits, d, stride_col_dst, part, ncols_dst);
       break;
+    case QMM_TYPE_IQ4_XS:
+      if (small)
+        k_mmq_kq_moe<wiq4xs, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                      splits, d, stride_col_dst, part, ncols_dst);
+      else
+        k_mmq_kq_moe<wiq4xs, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                      splits, d, stride_col_dst, part, ncols_dst);
+      break;
     case QMM_TYPE_Q4_0:
       k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
                                                    ids_dst, nsb, d, stride_col_dst);
@@ -1125,4 +1139,5 @@ QMM_DEFINE_MMQ(q6_k, QMM_TYPE_Q6K)
 QMM_DEFINE_MMQ(q5_k, QMM_TYPE_Q5K)
 QMM_DEFINE_MMQ(q4_0, QMM_TYPE_Q4_0)
 QMM_DEFINE_MMQ(q5_0, QMM_TYPE_Q5_0)
+QMM_DEFINE_MMQ(iq4_xs, QMM_TYPE_IQ4_XS)
 }

@@ -10,6 +10,7 @@
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef short s2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
 __device__ __forceinline__ v16f mfma_f16(v8h a, v8h b, v16f c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
@@ -45,6 +46,8 @@ struct wq4k {
   static constexpr bool kMin = true;
   static constexpr bool kDma = true;  // prefill stages activations by DMA (see mmq.hip)
   static constexpr int kLoads = 5;    // load() issues five 16-byte loads
+  // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
+  static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   struct Raw {
     u32x4 hdr, q[4];
   };
@@ -105,6 +108,8 @@ struct wq5k {
   static constexpr bool kMin = true;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 6;  // header, this lane's 16 qh bytes, four 16-byte nibble chunks
+  // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
+  static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   struct Raw {
     u32x4 hdr, qh, q[4];
   };
@@ -147,6 +152,8 @@ struct wq6k {
   static constexpr bool kMin = false;
   static constexpr bool kDma = false;
   static constexpr int kLoads = 6;  // at least six loads (16-byte ones; the 4-byte ones may merge)
+  // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
+  static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   // 16 bytes at a 2-byte aligned offset, kept as the five dwords that cover them: realigned only when used, so a
   // prefetch does not wait for its data at issue time
   struct Chunk {
@@ -218,6 +225,65 @@ struct wq6k {
       // bytes 0,2 and 1,3 in 16-bit lanes, minus 32, times the scale: w in [-4096, 4064]
       const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
       const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
+      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
+      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
+      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
+      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+    }
+  }
+};
+
+// IQ4_XS (gguf/cpu_dot.rs:416-440): 136-byte superblock {f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128]}; sub-block
+// ib holds qs[16 ib .. +16], values 0..15 in the low nibbles and 16..31 in the high ones, each value
+// kvalues_iq4nl[q] (int8) times the sub-block scale ls - 32 in [-32, 31].  w = (ls - 32) * kv in [-4064, 4032] splits
+// as Q6_K's: 64 wh + wl, wl in [0, 63], wh in [-64, 63].
+// The scale is folded into every weight byte, so an MFMA step may mix sub-blocks across lane halves: lane half g
+// loads qs[64 g .. +64] (sub-blocks 4g .. 4g + 3) and step j takes nibble half j % 2 of sub-block 4g + j / 2, i.e.
+// values 128 g + 16 j .. +16 -- activation chunk 8g + j instead of the other types' 2j + g.
+struct wiq4xs {
+  static constexpr int kBytes = 136;
+  static constexpr int kPlanes = 2;
+  static constexpr int kShift = 6;
+  static constexpr bool kMin = false;
+  static constexpr bool kDma = true;
+  static constexpr int kLoads = 5;  // one 8-byte header load and four 16-byte loads (none adjacent to another)
+  static __device__ __forceinline__ int chunk(int j, int g) { return 8 * g + j; }
+  struct Raw {
+    u32x2 h;  // d | scales_h << 16, scales_l
+    u32x4 q[4];
+  };
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
+    const uint32_t o = row + sb * kBytes;
+    r.h = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 64 * g + 16 * c, 0, 0);
+  }
+  struct Prep {
+    int sc[4];  // ls - 32 of sub-blocks 4g .. 4g + 3
+    float d, dmin;
+    v8h bmin;
+  };
+  static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // iq4_xs_sub_scale (cpu_dot.rs:416-420)
+      const int ib = 4 * g + i;
+      p.sc[i] = (int)(((r.h.y >> (4 * ib)) & 15u) | (((r.h.x >> (16 + 2 * ib)) & 3u) << 4)) - 32;
+    }
+    p.d = f16_bits_to_f32(r.h.x & 0xffff);
+    p.dmin = 0.0f;
+    p.bmin = (v8h){};
+  }
+  static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
+    const u32x4 q = r.q[j >> 1];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const s2 sc2 = {(short)p.sc[j >> 1], (short)p.sc[j >> 1]};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t nib = (j & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
+      const uint32_t v = unit_iq4xs::lookup(nib);  // four int8 table values
+      // bytes 0,2 and 1,3 sign-extended into 16-bit lanes, times the scale
+      const s2 lo = (__builtin_bit_cast(s2, v << 8) >> (s2){8, 8}) * sc2;
+      const s2 hi = (__builtin_bit_cast(s2, v) >> (s2){8, 8}) * sc2;
       const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
       b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
       const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});

@@ -321,7 +321,6 @@ __global__ __launch_bounds__(64 * NW) void k_skinny16(const uint8_t *__restrict_
     for (int t = 0; t < 4; t++)
       af[u].q[t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, o + 4 + WT::act_offset(t, kg), 0, 0));
     if (WT::kMin) {
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(ra, o + 260 + 8 * kg, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; i++)  // int16 -> f16, exact

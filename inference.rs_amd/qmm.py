@@ -124,7 +124,7 @@ def _declare(L: ctypes.CDLL) -> None:
         getattr(L, f"launch_dequantize_iq4_xs_{o}").argtypes = [vp, vp, i64, i64, vp]
     for o in ("f32", "bf16"):
         getattr(L, f"launch_mmvq_gguf_q8_0_{o}_exact").argtypes = [vp, vp, vp, i32, i32, i32, vp]
-    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k"]:
+    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k", "iq4_xs"]:
         f = getattr(L, f"launch_mmq_gguf_{t}", None)
         if f is not None:
             f.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i64, i32, i32, vp]

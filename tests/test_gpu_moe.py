@@ -17,6 +17,8 @@ def to_dev(a):
 
 
 def experts(rng, gtype, E, n, k):
+    if gtype == O.IQ4XS:  # no quantizer on this path: random blocks (every byte pattern is a valid block)
+        return O.random_blocks(O.IQ4XS, E * n * k, rng, 0.002).reshape(E, -1)
     w = weights(rng, E * n, k)
     return O.quantize(gtype, w).reshape(E, -1)
 
@@ -104,7 +106,7 @@ def skewed_routing(rng, tokens, E, topk):
 # 64 tokens x top-2 over 8 experts (16 rows each on average) and the skewed case take the few-row route of the
 # K-quant grouped matmul; 400 tokens (100 rows per expert) take the 128-row tile route.
 @pytest.mark.parametrize("case", ["uniform64", "skewed64", "uniform400"])
-@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0, O.Q4_0, O.Q5_0, O.Q5K])
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0, O.Q4_0, O.Q5_0, O.Q5K, O.IQ4XS])
 def test_grouped_prefill_matches_the_oracle(gtype, case):
     rng = np.random.default_rng(8 + gtype)
     E, n, k, topk = 8, 160, 1024, 2

@@ -201,3 +201,61 @@ def test_mmq_config_shapes(gtype, n, k):
     want = O.matmul(gtype, x, wq, n)
     r = assert_parity(got, want, what=f"t{gtype}")
     print(f"type {gtype} [{m},{k}]x[{n},{k}]: max rel err {r:.2e}")
+
+
+def iq4xs_weight(rng, n, k):
+    """IQ4_XS weight bytes: random blocks (every byte pattern is a valid block; the reference has no IQ4_XS
+    quantizer on this path), f16 scales near 0.002 of both signs."""
+    return O.random_blocks(O.IQ4XS, n * k, rng, 0.002).reshape(n, -1)
+
+
+# IQ4_XS on the K-quant kernel: 32-, 64- and 128-row activation tiles, split K (17 rows), ragged weight tiles, the
+# FFN-down shape
+IQ4XS_CASES = [(40, 64, 512), (130, 200, 1024), (17, 300, 4096), (255, 129, 256), (512, 256, 4096), (64, 96, 14336),
+               (1, 128, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", IQ4XS_CASES)
+def test_mmq_iq4_xs_matches_the_cpu_qmatmul(m, n, k):
+    rng = np.random.default_rng(23000 + m + n + k)
+    wq = iq4xs_weight(rng, n, k)
+    x = acts(rng, m, k)
+    x[:, ::64] *= 60.0
+    want = O.matmul(O.IQ4XS, x, wq, n)
+    got = qmm.qmatmul_prefill(O.IQ4XS, to_dev(wq), to_dev(x), n).cpu().numpy()
+    assert_parity(got, want, terms(O.IQ4XS, x, wq, n), what=f"iq4_xs m{m} n{n} k{k}")
+
+
+@pytest.mark.parametrize("out", ["f16", "bf16"])
+def test_mmq_iq4_xs_half_outputs(out):
+    rng = np.random.default_rng(29)
+    n, k, m = 128, 1024, 64
+    wq = iq4xs_weight(rng, n, k)
+    x = acts(rng, m, k)
+    want = O.matmul(O.IQ4XS, x, wq, n).astype(np.float64)
+    tdt, ulp = {"f16": (torch.float16, 2.0 ** -11), "bf16": (torch.bfloat16, 2.0 ** -8)}[out]
+    got = qmm.qmatmul_prefill(O.IQ4XS, to_dev(wq), to_dev(x), n, out_dtype=tdt).float().cpu().numpy()
+    assert np.all(np.abs(got - want) <= 1e-3 * np.abs(want).max() + ulp * np.abs(want))
+
+
+def test_mmq_iq4_xs_split_k_is_deterministic():
+    rng = np.random.default_rng(37)
+    m, n, k = 17, 4096, 4096
+    wq = iq4xs_weight(rng, n, k)
+    x = acts(rng, m, k)
+    wd = to_dev(wq)
+    y, _ = qmm.quantize_prefill(O.IQ4XS, to_dev(x))
+    a = qmm.mmq(O.IQ4XS, wd, y, k, n, m).cpu().numpy()
+    b = qmm.mmq(O.IQ4XS, wd, y, k, n, m).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert_parity(a, O.matmul(O.IQ4XS, x, wq, n), what="iq4_xs split")
+
+
+def test_mmq_iq4_xs_rejects_misaligned_weights():
+    rng = np.random.default_rng(41)
+    wq = iq4xs_weight(rng, 32, 256)
+    buf = torch.zeros(wq.size + 2, dtype=torch.uint8, device=DEV)
+    buf[2:] = to_dev(wq.reshape(-1))
+    y, _ = qmm.quantize_prefill(O.IQ4XS, to_dev(acts(rng, 40, 256)))
+    with pytest.raises(qmm.QmmError, match="4-byte aligned"):
+        qmm.mmq(O.IQ4XS, buf[2:], y, 256, 32, 40)
