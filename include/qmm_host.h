@@ -43,6 +43,16 @@ int qmm_qmatmul_forward(const qmm_qtensor *w, const void *xs, uint32_t in_dtype,
 int qmm_qmatmul_gather_forward(const qmm_qtensor *w, const float *xs, int64_t batch, int64_t xdim1,
                                const uint32_t *ids, int64_t topk, float *ys, void *stream);
 
+/* fast_mmq::down_from_glu (gguf/fast_mmq.rs:717-833): ys[rows, N] = (act(gate) * up)[rows, K] . W^T, gate / up f32
+ * [rows, K], ys f32 [rows, N]; the GLU is applied inside the activation quantization (prefill matmul at any rows).
+ * activation 0 SiLU, 1 GELU (tanh form), 2 ReLU, 3 GELU (erf form), 4 sigmoid. */
+int qmm_qmatmul_down_from_glu(const qmm_qtensor *w, const float *gate, const float *up, int64_t rows, int activation,
+                              float *ys, void *stream);
+/* fast_mmq::fused_ffn (gguf/fast_mmq.rs:883-899): ys[rows, hidden] = down(act(gate(xs)) * up(xs)), xs f32
+ * [rows, hidden]; gate / up [inter, hidden] of one type (Q8_0, Q4_K or Q6_K), down [hidden, inter]. */
+int qmm_fused_ffn(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, const float *xs,
+                  int64_t rows, int activation, float *ys, void *stream);
+
 /* MoE experts block: gate/up [E, inter, hidden], down [E, hidden, inter]; activation 0 SiLU, 1 GELU, 2 ReLU, 3 GELU (erf), 4 sigmoid.
  * forward: out[t] = sum_s w[t,s] * down_e(act(gate_e(x_t)) * up_e(x_t)), e = ids[t,s]; f32 / int32 device
  * pointers.  force_grouped = 1 takes the grouped prefill path at any token count. */

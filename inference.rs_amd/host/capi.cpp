@@ -115,6 +115,18 @@ int qmm_qmatmul_gather_forward(const qmm_qtensor *w, const float *xs, int64_t ba
   return guarded([&] { QMatMul(w->t).gather_forward(xs, batch, xdim1, ids, topk, ys, (hipStream_t)stream); });
 }
 
+int qmm_qmatmul_down_from_glu(const qmm_qtensor *w, const float *gate, const float *up, int64_t rows, int activation,
+                              float *ys, void *stream) {
+  return guarded([&] { QMatMul(w->t).down_from_glu(gate, up, rows, activation, ys, (hipStream_t)stream); });
+}
+
+int qmm_fused_ffn(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, const float *xs,
+                  int64_t rows, int activation, float *ys, void *stream) {
+  return guarded([&] {
+    fused_ffn(QMatMul(gate->t), QMatMul(up->t), QMatMul(down->t), xs, rows, activation, ys, (hipStream_t)stream);
+  });
+}
+
 int qmm_moe_new(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, int activation,
                 qmm_moe **out) {
   return guarded([&] { *out = new qmm_moe{MoeExperts(gate->t, up->t, down->t, activation)}; });

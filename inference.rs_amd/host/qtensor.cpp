@@ -66,6 +66,11 @@ Workspace &workspace() {
   thread_local Workspace ws;
   return ws;
 }
+// fused_ffn's intermediates (the gate and up outputs), kept apart from the scratch of the QMatMul calls it makes
+Workspace &ffn_workspace() {
+  thread_local Workspace ws;
+  return ws;
+}
 
 // Carves consecutive 256-byte aligned slices out of one workspace allocation.
 struct Carver {
@@ -137,6 +142,16 @@ mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
     default: throw Error("QMatMul: unsupported weight type");
   }
 #undef QMM_PICK
+}
+
+typedef void (*mmvq_glu_fn)(const void *, const void *, const void *, void *, int, int, int, int, int, int, void *);
+mmvq_glu_fn decode_fused_glu(GgmlDType w) {
+  switch (w) {
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_f32_fused_glu;
+    case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_f32_fused_glu;
+    case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_f32_fused_glu;
+    default: throw Error("fused_ffn: unsupported weight type");
+  }
 }
 
 mmq_fn prefill_matmul(GgmlDType w) {
@@ -418,6 +433,89 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
                       160 * 1024, 64, (int)in_dtype, stream);
     abi_check("QMatMul::forward (matmul)");
   }
+}
+
+void QMatMul::down_from_glu(const float *gate, const float *up, int64_t rows, int activation, float *ys,
+                            hipStream_t stream) const {
+  const QTensor &w = *w_;
+  check_weight(w, "QMatMul::down_from_glu", true);
+  if (w.shape().size() != 2) throw Error("QMatMul::down_from_glu: the weight must be 2-D");
+  if (!has_prefill(w.dtype())) throw Error("QMatMul::down_from_glu: weight type has no prefill matmul");
+  if (activation < 0 || activation > 4) throw Error("QMatMul::down_from_glu: activation must be 0..4");
+  if (rows < 0) throw Error("QMatMul::down_from_glu: negative row count");
+  if (rows == 0) return;
+  const int64_t k = w.cols(), n = w.rows();
+  const GgmlDType t = w.dtype();
+  if (k % (int64_t)block_size(t) != 0) throw Error("QMatMul::down_from_glu: K is not a multiple of the block size");
+  hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
+  const int64_t kp = pad_to(k, 256);
+  const int nsm = device_cus(w.device().ordinal);
+  Carver c;
+  const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+  const size_t o_fix = c.add(fixup_bytes(nsm));
+  uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
+  (act_q8_0(t) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8k_f32)(gate, up, nullptr, ws + o_y, k, k,
+                                                                                      kp, rows, activation, stream);
+  abi_check("QMatMul::down_from_glu (GLU + quantize)");
+  prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
+                    160 * 1024, 64, 0, stream);
+  abi_check("QMatMul::down_from_glu (matmul)");
+}
+
+void fused_ffn(const QMatMul &gate, const QMatMul &up, const QMatMul &down, const float *xs, int64_t rows,
+               int activation, float *ys, hipStream_t stream) {
+  const QTensor &g = gate.weight(), &u = up.weight(), &d = down.weight();
+  check_weight(g, "fused_ffn (gate)");
+  check_weight(u, "fused_ffn (up)");
+  check_weight(d, "fused_ffn (down)", true);
+  if (g.shape().size() != 2 || g.shape() != u.shape() || g.dtype() != u.dtype())
+    throw Error("fused_ffn: gate and up must be 2-D weights of one type and shape");
+  if (d.shape().size() != 2 || d.cols() != g.rows() || d.rows() != g.cols())
+    throw Error("fused_ffn: down must be [hidden, inter] for gate / up [inter, hidden]");
+  if (g.device().ordinal != d.device().ordinal || u.device().ordinal != d.device().ordinal)
+    throw Error("fused_ffn: the weights are on different devices");
+  if (activation < 0 || activation > 4) throw Error("fused_ffn: activation must be 0..4");
+  if (rows < 0) throw Error("fused_ffn: negative row count");
+  if (rows == 0) return;
+  const int64_t hidden = g.cols(), inter = g.rows();
+  const GgmlDType t = g.dtype();
+  const int ordinal = g.device().ordinal;
+  hip_check(hipSetDevice(ordinal), "hipSetDevice");
+  if (rows <= QMatMul::kMaxDecodeRows) {
+    // decode: one activation quantization, the fused-GLU matvec, then down on act(gate) * up
+    const int64_t kp = pad_to(hidden, act_block(t));
+    Carver c;
+    const size_t o_y = c.add((size_t)(rows * (kp / act_block(t)) * act_block_bytes(t)));
+    const size_t o_mid = c.add((size_t)(rows * inter * 4));
+    uint8_t *ws = (uint8_t *)ffn_workspace().get(ordinal, c.total, stream);
+    decode_quantizer(t, GgmlDType::F32)(xs, ws + o_y, (int)hidden, (int)kp, (int)rows, stream);
+    abi_check("fused_ffn (quantize)");
+    decode_fused_glu(t)(g.device_ptr(), u.device_ptr(), ws + o_y, ws + o_mid, (int)hidden, (int)inter,
+                        (int)(kp / act_block(t)), (int)inter, (int)rows, activation, stream);
+    abi_check("fused_ffn (gate/up)");
+    down.forward(ws + o_mid, GgmlDType::F32, rows, ys, stream);
+    return;
+  }
+  // prefill: one tile-layout quantization read by both matmuls, then down_from_glu on their f32 outputs
+  const int64_t kp = pad_to(hidden, 256);
+  const int nsm = device_cus(ordinal);
+  Carver c;
+  const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+  const size_t o_fix = c.add(fixup_bytes(nsm));
+  const size_t o_g = c.add((size_t)(rows * inter * 4));
+  const size_t o_u = c.add((size_t)(rows * inter * 4));
+  uint8_t *ws = (uint8_t *)ffn_workspace().get(ordinal, c.total, stream);
+  (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(xs, nullptr, ws + o_y, 0, hidden, hidden,
+                                                                     hidden * rows, hidden * rows, kp, rows, 1, 1,
+                                                                     stream);
+  abi_check("fused_ffn (quantize)");
+  for (int which = 0; which < 2; which++) {
+    const QTensor &w = which == 0 ? g : u;
+    prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ws + (which == 0 ? o_g : o_u), hidden, inter, rows,
+                      hidden / (int64_t)block_size(t), inter, 0, nsm, 160 * 1024, 64, 0, stream);
+    abi_check("fused_ffn (gate/up)");
+  }
+  down.down_from_glu((const float *)(ws + o_g), (const float *)(ws + o_u), rows, activation, ys, stream);
 }
 
 void QMatMul::gather_forward(const float *xs, int64_t batch, int64_t xdim1, const uint32_t *ids, int64_t topk,

@@ -138,9 +138,25 @@ class QMatMul {
   void gather_forward(const float *xs, int64_t batch, int64_t xdim1, const uint32_t *ids, int64_t topk, float *ys,
                       hipStream_t stream) const;
 
+  // fast_mmq::down_from_glu (gguf/fast_mmq.rs:717-833): ys[rows, N] = (act(gate) * up)[rows, K] . W^T for this
+  // [N, K] weight; gate, up f32 [rows, K] and ys f32 [rows, N] device pointers; activation 0 SiLU, 1 GELU (tanh
+  // form), 2 ReLU, 3 GELU (erf form), 4 sigmoid.  The GLU is applied while the activations are quantized
+  // (launch_mmq_quantize_glu_*, one launch), so act(gate) * up is never stored; every row count takes the prefill
+  // matmul, as the reference's MMQ function does.
+  void down_from_glu(const float *gate, const float *up, int64_t rows, int activation, float *ys,
+                     hipStream_t stream) const;
+
  private:
   std::shared_ptr<QTensor> w_;
 };
+
+// fast_mmq::fused_ffn (gguf/fast_mmq.rs:883-899): ys[rows, hidden] = down(act(gate(xs)) * up(xs)) for f32 xs
+// [rows, hidden], gate and up [inter, hidden] of one type, down [hidden, inter].  Gate and up read one activation
+// quantization (shared_lhs, fast_mmq.rs:537-602).  Up to QMatMul::kMaxDecodeRows rows they run as the fused-GLU
+// matvec (launch_mmvq_gguf_<t>_f32_fused_glu, which stores act(gate) * up) and down as QMatMul::forward; above, as
+// two prefill matmuls whose f32 outputs go through down.down_from_glu.
+void fused_ffn(const QMatMul &gate, const QMatMul &up, const QMatMul &down, const float *xs, int64_t rows,
+               int activation, float *ys, hipStream_t stream);
 
 // The MoE experts block of the reference's grouped prefill / indexed decode
 // (crates/inference-nn/src/moe/experts/backends.rs:1382-1489, 1966-2402): gate/up/down expert stacks,
