@@ -22,6 +22,7 @@
 #include "common.h"
 #include "inferencequant.h"
 #include "planes.h"
+#include "routesum.h"
 #include "skinny.h"
 #include "units.h"
 
@@ -154,7 +155,8 @@ template <class WT, class Out, int TM>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
-                                            const int32_t *__restrict__ dst_rows, float *__restrict__ part) {
+                                            const int32_t *__restrict__ dst_rows, float *__restrict__ part,
+                                            const RouteSum &rsum = RouteSum{}) {
   constexpr int BMt = 32 * TM;
   // Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a register
   // ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
@@ -298,19 +300,24 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     step(sb + 2, 2);
   }
 
-  if (n >= nrows_w) return;
+  if (n < nrows_w) {
 #pragma unroll
-  for (int t = 0; t < TM; t++)
+    for (int t = 0; t < TM; t++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int64_t m = m0 + 32 * t + out_row(r, g);
-      if (m < mrows) {
-        if (part)  // split K: this split's partial sum, row m of the activation order (summed by k_split_sum)
-          part[m * nrows_w + n] = fa[t][r];
-        else
-          Out::store(dst, (dst_rows ? dst_rows[m] : m) * ldd + n, fa[t][r]);
+      for (int r = 0; r < 16; r++) {
+        const int64_t m = m0 + 32 * t + out_row(r, g);
+        if (m < mrows) {
+          if (part)  // split K: this split's partial sum, row m of the activation order (summed by k_split_sum)
+            part[m * nrows_w + n] = fa[t][r];
+          else
+            Out::store(dst, (dst_rows ? dst_rows[m] : m) * ldd + n, fa[t][r]);
+        }
       }
-    }
+  }
+  // grouped down projection with the weighted sum folded in (no split K there): every thread takes part
+  if (rsum.out)
+    route_sum_finish<256, BMt>(rsum, (const float *)(const void *)dst, ldd, dst_rows, m0, mrows, n0,
+                               (int)(nrows_w - n0 < BN ? nrows_w - n0 : BN), (int)(n0 / BN));
 }
 
 // Split K: split s of a tile writes its partial sums to plane s of the caller's fixup buffer (planes of rows x cols
@@ -804,7 +811,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
                                                     const int32_t *__restrict__ bounds,
                                                     const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
                                                     float *__restrict__ dst, int64_t ldd, float *__restrict__ part,
-                                                    int64_t ncols_dst) {
+                                                    int64_t ncols_dst, RouteSum rsum) {
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
   if (m0 >= m1) return;  // uniform over the workgroup
@@ -813,7 +820,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   if (sb0 >= sb1) return;
   mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
-                                part ? part + split * ncols_dst * nrows_w : nullptr);
+                                part ? part + split * ncols_dst * nrows_w : nullptr, rsum);
 }
 
 template <class WB>
@@ -1025,7 +1032,8 @@ void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int
 
 void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
              void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
-             int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who) {
+             int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who,
+             RouteSum rsum = RouteSum{}) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst)) return;
   if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
     qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
@@ -1042,8 +1050,14 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   // a few rows per expert: the few-row kernel streams each expert's weights once, without 64-row tiles of padding
   const bool b32 = qmm_block_size(type) == 32;  // Q8_0, Q4_0, Q5_0: the Q8_0-layout kernel
   if (!b32 && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
-                                              ncols_dst, stride_col_dst, num_experts, s))
+                                              ncols_dst, stride_col_dst, num_experts, s, rsum))
     return;
+  // the 32-value types store their route rows, then the weighted sum runs as its own launch (the same arithmetic)
+  auto separate_sum = [&] {
+    if (rsum.out)
+      launch_moe_weighted_reduce_flat(dst, rsum.weights, rsum.out, (int)(ncols_dst / rsum.topk), (int)nrows_x,
+                                      rsum.topk, stream);
+  };
   const uint8_t *w = (const uint8_t *)x;
   float *d = (float *)dst;
   if (b32 && b32_runs(w, ncols_x, w_row_bytes)) {
@@ -1056,6 +1070,7 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
     else
       launch_b32_moe<wr_q8_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
                               ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
+    separate_sum();
     return;
   }
   // 32-row tiles for a few rows per expert, and always for Q5_K (its third plane does not fit two waves per SIMD at
@@ -1065,37 +1080,39 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
   // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
   const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
-  const int64_t splits = b32 ? 1 : k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
+  // (no split K with the weighted sum folded in: each route row of a column tile is stored once, by one workgroup)
+  const int64_t splits = b32 || rsum.out ? 1 : k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
+  rsum.col_tiles = (int32_t)ntiles;
   float *part = splits > 1 ? (float *)tmp_fixup : nullptr;
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
   switch (type) {
     case QMM_TYPE_Q4K:
       if (small)
         k_mmq_kq_moe<wq4k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
       else
         k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q5K:  // always 32-row tiles (small)
       k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                  splits, d, stride_col_dst, part, ncols_dst);
+                                                  splits, d, stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q6K:
       if (small)
         k_mmq_kq_moe<wq6k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
       else
         k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst);
+                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_IQ4_XS:
       if (small)
         k_mmq_kq_moe<wiq4xs, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                      splits, d, stride_col_dst, part, ncols_dst);
+                                                      splits, d, stride_col_dst, part, ncols_dst, rsum);
       else
         k_mmq_kq_moe<wiq4xs, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                      splits, d, stride_col_dst, part, ncols_dst);
+                                                      splits, d, stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q4_0:
       k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
@@ -1110,6 +1127,29 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
                                                    ids_dst, nsb, d, stride_col_dst);
   }
   if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, stride_col_dst, ids_dst, s);
+  if (b32) separate_sum();  // (the Q8_0-layout kernel of rows that are not whole dword-aligned superblocks)
+}
+
+void moe_wsum(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
+              float *routes, const float *weights, int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,
+              int64_t ncols_dst, int64_t stride_row_x, int64_t num_experts, int64_t ncols_max, int topk, int nsm,
+              void *stream, const char *who) {
+  if (topk <= 0 || ncols_dst % topk != 0 || !routes || !weights || !counters || !out) {
+    qmm_set_error("%s: topk=%d ncols_dst=%lld (a multiple of topk), routes, topk_weights, counters and out required",
+                  who, topk, (long long)ncols_dst);
+    return;
+  }
+  RouteSum rs;
+  rs.out = out;
+  rs.weights = weights;
+  rs.counters = counters;
+  rs.ldo = nrows_x;
+  rs.topk = topk;
+  rs.col_tiles = 0;  // set by the kernel's launcher
+  // no split K (each route row of a column tile is stored once, by one workgroup), whatever tmp_fixup holds
+  (void)tmp_fixup;
+  mmq_moe(type, nullptr, x, y, ids_dst, bounds, routes, ncols_x, nrows_x, ncols_dst, stride_row_x, nrows_x,
+          num_experts, ncols_max, nsm, stream, who, rs);
 }
 
 }  // namespace
@@ -1130,6 +1170,14 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
     (void)cc, (void)smpbo, (void)warp_size;                                                                        \
     mmq_moe(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,         \
             stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe");                                \
+  }                                                                                                                \
+  void launch_mmq_gguf_##t##_moe_wsum(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,      \
+                                      const int32_t *expert_bounds, float *routes, const float *topk_weights,     \
+                                      int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,            \
+                                      int64_t ncols_dst, int64_t stride_row_x, int64_t num_experts,               \
+                                      int64_t ncols_max, int topk, int nsm, void *stream) {                       \
+    moe_wsum(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, routes, topk_weights, counters, out, ncols_x, nrows_x, \
+             ncols_dst, stride_row_x, num_experts, ncols_max, topk, nsm, stream, "mmq_" #t "_moe_wsum");           \
   }
 
 extern "C" {

@@ -139,6 +139,7 @@ struct moe_route {
   const int32_t *bounds;
   const int32_t *ids_dst;
   int64_t expert_bytes;
+  RouteSum sum;  // sum.out set: fold the weighted sum over each token's routes into sum.out (routesum.h)
 };
 
 // The NW waves' partial 32x32 tiles, summed through LDS.  Plain: lane (g, li) of wave w stores output registers
@@ -263,6 +264,11 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
       }
     }
     reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, m0, m_end, ids, dst, ldd, activation);
+    if constexpr (MOE) {
+      if (route.sum.out)  // (uniform: a kernel argument)
+        route_sum_finish<64 * NW, 32>(route.sum, (const float *)(const void *)dst, ldd, ids, m0, m_end, n0,
+                                      (int)rows_here, (int)blockIdx.x);
+    }
     if (!MOE) break;
     __syncthreads();  // the next chunk rewrites the reduction buffer
   }
@@ -445,13 +451,14 @@ void launch_tc(const void *vx, const void *vy, void *dst, int ncols_x, int nrows
 template <class WT>
 void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                 int64_t nrows_x, int64_t w_row_bytes, int64_t nsb, int64_t ncols_dst, int64_t ldd, int64_t num_experts,
-                int64_t chunks, hipStream_t s) {
+                int64_t chunks, hipStream_t s, RouteSum sum) {
   act_tiles ap;
   ap.base = (const uint8_t *)y;
   ap.rows = (uint32_t)ncols_dst;
   ap.nsb = (uint32_t)nsb;
   ap.bytes = nsb * ncols_dst * 292;
-  const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes};
+  sum.col_tiles = (int32_t)qmm_ceil_div(nrows_x, 32);
+  const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes, sum};
   const dim3 grid((unsigned)qmm_ceil_div(nrows_x, 32), (unsigned)chunks, (unsigned)num_experts);
   const uint8_t *w = (const uint8_t *)x;
   if (nsb >= 32)  // long rows: 8 waves split K
@@ -521,7 +528,7 @@ bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void 
 
 bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                     int64_t ncols_x, int64_t nrows_x, int64_t w_row_bytes, int64_t ncols_dst, int64_t ldd,
-                    int64_t num_experts, hipStream_t s) {
+                    int64_t num_experts, hipStream_t s, RouteSum sum) {
   if (ncols_x % 256 != 0 || ncols_dst <= 0 || num_experts <= 0 || num_experts > 65535) return false;
   if (ncols_dst > QMM_SKINNY_MOE_ROWS * num_experts) return false;
   const int64_t nsb = ncols_x / 256;
@@ -529,9 +536,11 @@ bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_d
   // enough 32-row chunks for an expert of average size; larger experts loop over theirs
   const int64_t chunks = qmm_ceil_div(qmm_ceil_div(ncols_dst, num_experts), 32);
   if (type == QMM_TYPE_Q4K)
-    launch_moe<wq4k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
+    launch_moe<wq4k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s,
+                     sum);
   else if (type == QMM_TYPE_Q6K)
-    launch_moe<wq6k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
+    launch_moe<wq6k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s,
+                     sum);
   else
     return false;
   return true;
