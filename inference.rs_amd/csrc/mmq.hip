@@ -805,7 +805,9 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W,
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
-template <class WT, int TMv>
+// FUSED: the weighted sum over each token's routes folded in (rsum); a separate instantiation, so that the grouped
+// matmul without it keeps its register allocation
+template <class WT, int TMv, bool FUSED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
@@ -820,7 +822,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   if (sb0 >= sb1) return;
   mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
-                                part ? part + split * ncols_dst * nrows_w : nullptr, rsum);
+                                part ? part + split * ncols_dst * nrows_w : nullptr, FUSED ? rsum : RouteSum{});
 }
 
 template <class WB>
@@ -1030,6 +1032,18 @@ void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int
   }
 }
 
+template <class WT, int TMv>
+void kq_moe(dim3 grid, hipStream_t s, const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes,
+            const ActTile &a, const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, int64_t splits, float *d,
+            int64_t ldd, float *part, int64_t ncols_dst, const RouteSum &rsum) {
+  if (rsum.out)
+    k_mmq_kq_moe<WT, TMv, true><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                     splits, d, ldd, part, ncols_dst, rsum);
+  else
+    k_mmq_kq_moe<WT, TMv, false><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                      splits, d, ldd, part, ncols_dst, rsum);
+}
+
 void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
              void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
              int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who,
@@ -1088,31 +1102,31 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   switch (type) {
     case QMM_TYPE_Q4K:
       if (small)
-        k_mmq_kq_moe<wq4k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wq4k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       else
-        k_mmq_kq_moe<wq4k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wq4k, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q5K:  // always 32-row tiles (small)
-      k_mmq_kq_moe<wq5k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                  splits, d, stride_col_dst, part, ncols_dst, rsum);
+      kq_moe<wq5k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q6K:
       if (small)
-        k_mmq_kq_moe<wq6k, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wq6k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       else
-        k_mmq_kq_moe<wq6k, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                    splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wq6k, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_IQ4_XS:
       if (small)
-        k_mmq_kq_moe<wiq4xs, 1><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                      splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wiq4xs, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       else
-        k_mmq_kq_moe<wiq4xs, 2><<<gridk, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                      splits, d, stride_col_dst, part, ncols_dst, rsum);
+        kq_moe<wiq4xs, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                        stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q4_0:
       k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,

@@ -179,7 +179,9 @@ __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane,
 // 16..31 load nothing and their columns come out zero)
 // GLU: W2 holds the up weights; waves [0, NW/2) take the gate rows and [NW/2, NW) the up rows.
 // MOE: the activation rows and weights of expert blockIdx.z (moe_route); otherwise rows [0, mrows).
-template <class WT, class AP, class Out, int NW, int TR, bool GLU, bool MOE = false>
+// FUSED (MOE only): fold the weighted sum over each token's routes into route.sum.out (a separate instantiation, so
+// that the grouped matmul without it keeps its register allocation)
+template <class WT, class AP, class Out, int NW, int TR, bool GLU, bool MOE = false, bool FUSED = false>
 __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                                     int64_t nrows_w, int64_t w_row_bytes, AP ap, int mrows,
                                                     int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
@@ -264,11 +266,9 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
       }
     }
     reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, m0, m_end, ids, dst, ldd, activation);
-    if constexpr (MOE) {
-      if (route.sum.out)  // (uniform: a kernel argument)
-        route_sum_finish<64 * NW, 32>(route.sum, (const float *)(const void *)dst, ldd, ids, m0, m_end, n0,
-                                      (int)rows_here, (int)blockIdx.x);
-    }
+    if constexpr (MOE && FUSED)
+      route_sum_finish<64 * NW, 32>(route.sum, (const float *)(const void *)dst, ldd, ids, m0, m_end, n0,
+                                    (int)rows_here, (int)blockIdx.x);
     if (!MOE) break;
     __syncthreads();  // the next chunk rewrites the reduction buffer
   }
@@ -461,9 +461,15 @@ void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int3
   const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes, sum};
   const dim3 grid((unsigned)qmm_ceil_div(nrows_x, 32), (unsigned)chunks, (unsigned)num_experts);
   const uint8_t *w = (const uint8_t *)x;
-  if (nsb >= 32)  // long rows: 8 waves split K
+  if (nsb >= 32 && sum.out)  // long rows: 8 waves split K
+    k_skinny<WT, act_tiles, out_f32, 8, 32, false, true, true><<<grid, 512, 0, s>>>(w, nullptr, nrows_x, w_row_bytes,
+                                                                                    ap, 0, nsb, dst, ldd, 0, rt);
+  else if (nsb >= 32)
     k_skinny<WT, act_tiles, out_f32, 8, 32, false, true><<<grid, 512, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
                                                                               nsb, dst, ldd, 0, rt);
+  else if (sum.out)
+    k_skinny<WT, act_tiles, out_f32, 4, 32, false, true, true><<<grid, 256, 0, s>>>(w, nullptr, nrows_x, w_row_bytes,
+                                                                                    ap, 0, nsb, dst, ldd, 0, rt);
   else
     k_skinny<WT, act_tiles, out_f32, 4, 32, false, true><<<grid, 256, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
                                                                               nsb, dst, ldd, 0, rt);
