@@ -271,7 +271,9 @@ QMM_DECLARE_MMQ(iq4_xs)
  * workgroup that stores a token's last route row of a column tile adds the token's rows up (agent-scope release
  * before its count, acquire after); counters: int32[tokens * ceil(nrows_x / 32)], all zero before the first call and
  * left zero by every call.  Calls that overlap on one counters buffer race.  The K-quant types fold the sum into
- * the matmul's workgroups; the 32-value types (Q8_0, Q4_0, Q5_0) run the reduce as a second launch. */
+ * the matmul's workgroups; the 32-value types (Q8_0, Q4_0, Q5_0) run the reduce as a second launch.  Measured on
+ * MI355X it is slower than the two launches (the agent-scope release and acquire of every workgroup write back and
+ * invalidate its XCD's L2): the C++ host's MoE block keeps the two. */
 /* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
  * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
  * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by

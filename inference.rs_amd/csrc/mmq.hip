@@ -45,10 +45,12 @@ struct ActTile {
 
 // One superblock of the activation tile (BMt rows x 256 values: int8 qs, f16 bsums, f32 d) in registers on its
 // way from global memory to an LDS slot.  The prefill layout keeps a superblock's rows contiguous, so thread t
-// moves 16-byte chunks t, t + 256, ... of each section; every address is a per-thread constant plus a scalar.
-template <int BMt, bool MIN>
+// moves 16-byte chunks t, t + NT, ... of each section (NT threads); every address is a per-thread constant plus a
+// scalar.
+template <int BMt, bool MIN, int NT>
 struct ActStage {
-  static constexpr int NQ = BMt * 16 / 256;  // qs chunks per thread
+  static_assert(BMt * 16 % NT == 0, "whole qs chunks per thread");
+  static constexpr int NQ = BMt * 16 / NT;  // qs chunks per thread
   static constexpr int QS = BMt * 256;       // LDS bytes: qs, row r's chunk c at chunk slot c ^ (r % 16)
   static constexpr int BSB = MIN ? BMt * 32 : 0;
   static constexpr int STAGE = QS + BSB + BMt * 4;
@@ -62,7 +64,7 @@ struct ActStage {
                                        uint32_t s_d) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < NQ; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[0] + s_qs + 4096 * i, 0, 0);
+    for (int i = 0; i < NQ; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[0] + s_qs + 16 * NT * i, 0, 0);
     if (MIN && tid < 2 * BMt) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
     if (tid < BMt / 4) d = __builtin_amdgcn_raw_buffer_load_b128(r, voff[2] + s_d, 0, 0);
   }
@@ -70,7 +72,7 @@ struct ActStage {
     const int tid = threadIdx.x;
     const int swz = (tid & 15) ^ ((tid >> 4) & 15);
 #pragma unroll
-    for (int i = 0; i < NQ; i++) *(u32x4 *)(slot + 4096 * i + 256 * (tid >> 4) + 16 * swz) = q[i];
+    for (int i = 0; i < NQ; i++) *(u32x4 *)(slot + 16 * NT * i + 256 * (tid >> 4) + 16 * swz) = q[i];
     if (MIN && tid < 2 * BMt) *(u32x4 *)(slot + QS + 16 * tid) = bs;
     if (tid < BMt / 4) *(u32x4 *)(slot + QS + BSB + 16 * tid) = d;
   }
@@ -79,16 +81,18 @@ struct ActStage {
 // The same superblock loaded by DMA straight into an LDS slot (buffer loads with the LDS flag): no registers hold
 // it on the way, so the ring can be deep without spilling.  Wave w's lane l writes LDS byte 16 l (4 l for the
 // 4-byte sections) of each 1 KB (256 B) piece it loads; it fetches the global bytes that belong at that place of
-// the swizzled layout.  Every wave issues kLoads loads per superblock.  The compiler does not order LDS reads
-// after these writes: the tile loop waits for them with an explicit vmcnt before its barrier.
-template <int BMt, bool MIN>
+// the swizzled layout.  Every one of the NW waves issues kLoads loads per superblock (the same count: the tile loop's
+// wait counts on it).  The compiler does not order LDS reads after these writes: the tile loop waits for them with an
+// explicit vmcnt before its barrier.
+template <int BMt, bool MIN, int NW>
 struct ActDma {
+  static_assert(BMt % (4 * NW) == 0 && (!MIN || BMt % (8 * NW) == 0), "the same load count in every wave");
   static constexpr int QS = BMt * 256;
   static constexpr int BSB = MIN ? BMt * 32 : 0;
   static constexpr int STAGE = QS + BSB + BMt * 4;
-  static constexpr int NQ = BMt / 16;            // 1 KB qs pieces per wave
-  static constexpr int NB = MIN ? BMt / 32 : 0;  // 256 B bsum pieces per wave
-  static constexpr int ND = BMt / 4;             // lanes of each wave that load one f32 scale
+  static constexpr int NQ = BMt / (4 * NW);            // 1 KB qs pieces per wave
+  static constexpr int NB = MIN ? BMt / (8 * NW) : 0;  // 256 B bsum pieces per wave
+  static constexpr int ND = BMt / NW;                  // lanes of each wave that load one f32 scale
   static constexpr int kLoads = NQ + NB + 1;
   uint32_t oq[NQ], ob[NB > 0 ? NB : 1], od;
 
@@ -97,12 +101,12 @@ struct ActDma {
   __device__ __forceinline__ void init(int wave, int lane, int64_t m0, int64_t rows, int64_t nsb) {
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
-      const int L = 64 * (4 * i + wave) + lane, r = L >> 4, c = (L & 15) ^ (r & 15);
+      const int L = 64 * (NW * i + wave) + lane, r = L >> 4, c = (L & 15) ^ (r & 15);
       oq[i] = (uint32_t)((m0 + r) * 256 + 16 * c);
     }
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-      const int D = 64 * (4 * i + wave) + lane, r = D >> 3, k = D & 7;
+      const int D = 64 * (NW * i + wave) + lane, r = D >> 3, k = D & 7;
       ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * 32 + 4 * k);
     }
     od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 4);
@@ -112,12 +116,12 @@ struct ActDma {
 #if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
     for (int i = 0; i < NQ; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (4 * i + wave)),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (NW * i + wave)),
                                                16, oq[i] + 256 * sb_rows, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < NB; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (4 * i + wave)), 4, ob[i] + 32 * sb_rows, 0,
+          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (NW * i + wave)), 4, ob[i] + 32 * sb_rows, 0,
           0, 0);
     if (lane < ND)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -146,29 +150,43 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows; wave w's lanes hold
-// weight row n0 + 32w + (lane % 32) as the MFMA B column and TM 32x32 output tiles.  Three LDS slots and three
+// One workgroup: NW (4 or 8) waves x 32 weight rows (32 NW of them) against BMt = 32 TM activation rows; wave w's lanes
+// hold weight row n0 + 32w + (lane % 32) as the MFMA B column and TM 32x32 output tiles.  The activation tile in LDS
+// serves all NW waves, so 8 waves halve the activation bytes read per weight row.  Three LDS slots and three
 // register sets rotate: during superblock s the workgroup computes from slot s, writes the activations of s + 1
 // (loaded one step earlier) into slot s + 1, and has the activations and weights of s + 2 in flight, so global
 // latency is covered by two steps of MFMA work.  One LDS barrier per superblock.
-template <class WT, class Out, int TM>
+template <class WT, class Out, int TM, int NW>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
                                             const int32_t *__restrict__ dst_rows, float *__restrict__ part,
                                             const RouteSum &rsum = RouteSum{}) {
   constexpr int BMt = 32 * TM;
+  constexpr int BNt = 32 * NW;
   // Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a register
   // ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
   constexpr bool kDma = WT::kDma;
-  typedef ActStage<BMt, WT::kMin> AS;
-  typedef ActDma<BMt, WT::kMin> AD;
+  typedef ActStage<BMt, WT::kMin, 64 * NW> AS;
+  typedef ActDma<BMt, WT::kMin, NW> AD;
   static_assert(AS::STAGE == AD::STAGE, "one LDS layout");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AS::STAGE];
+  // kLw: the weight superblocks go by DMA into LDS too, as the tile's rows' contiguous 16-byte pieces, and each wave
+  // reads its B-operand bytes from there.  Loaded straight into registers, one 16-byte load per lane covers 32 weight
+  // rows, 32 bytes of each, and the texture addresser's per-cache-line work for those loads bounds the kernel; as
+  // contiguous pieces the same bytes take a quarter of the cache-line accesses.  Two stages of activations and
+  // weights (the LDS does not hold three), so the next superblock's loads are in flight during one step.
+  constexpr bool kLw = WT::kLdsWeights && kDma && TM == 2;
+  constexpr int kChunks = WT::kBytes / 16;                           // 16-byte pieces per weight superblock
+  constexpr int kWI = kLw ? (BNt * kChunks + 64 * NW - 1) / (64 * NW) : 0;  // weight DMA loads per wave
+  // weight bytes per stage: every lane of every load writes its 16 bytes, the padding lanes past the slab included
+  constexpr int WST = kWI * 64 * NW * 16;
+  constexpr int STG = AS::STAGE + WST;
+  static_assert(!kLw || (AS::STAGE % 16 == 0 && WT::kBytes % 16 == 0), "16-byte aligned stages");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[(kLw ? 2 : 3) * STG];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
-  const int64_t nlast = (nrows_w - n0 < BN ? nrows_w - n0 : BN) - 1;
+  const int64_t nlast = (nrows_w - n0 < BNt ? nrows_w - n0 : BNt) - 1;
   const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;  // row within the tile, clamped
 
   // activations: one resource over the channel; the scalar part of each address moves with the superblock
@@ -194,7 +212,27 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   AS st[kDma ? 1 : 3];
   AD dma;
   if (kDma) dma.init(wave, lane, m0, rows, nsb);
-  typename WT::Raw raw[3];
+  typename WT::Raw raw[kLw ? 1 : 3];
+  // kLw: lane's weight piece C = 64 (NW i + wave) + lane of the stage's slab (row C / kChunks, piece C % kChunks), at
+  // LDS byte 16 C of the stage's weight part; pieces past the slab read past the resource (no memory traffic)
+  uint32_t woff[kWI > 0 ? kWI : 1];
+#pragma unroll
+  for (int i = 0; i < kWI; i++) {
+    const int C = 64 * (NW * i + wave) + lane, r = C / kChunks, pc = C - r * kChunks;
+    woff[i] = C < BNt * kChunks ? (uint32_t)(r * w_row_bytes + 16 * pc) : 0x80000000u;
+  }
+  auto issue_lw = [&](int64_t sb, int u) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_barrier(0);
+    dma.issue(ra, lds + u * STG, wave, lane, (uint32_t)(sb * rows));
+#pragma unroll
+    for (int i = 0; i < kWI; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (__attribute__((address_space(3))) void *)(lds + u * STG + AS::STAGE + 1024 * (NW * i + wave)), 16,
+          woff[i] + (uint32_t)sb * WT::kBytes, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  };
   // DMA first, then the weights (WT::kLoads 16-byte loads, which cannot merge): the explicit wait in step()
   // counts on that order
   auto issue = [&](int64_t sb, int u, AS &as, typename WT::Raw &rr) {
@@ -290,6 +328,25 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     __builtin_amdgcn_sched_barrier(0);  // steps do not interleave: each one's registers die at its end
   };
 
+  if constexpr (kLw) {
+    // two stages: after the barrier of step s every wave is done with stage (s + 1) % 2, so the loads of s + 1 go
+    // there while s is computed from stage s % 2
+    issue_lw(sb0, 0);
+    for (int64_t sb = sb0; sb < sb1; sb += 2) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int64_t s = sb + u;
+        if (s < sb1) {  // (uniform over the workgroup)
+          __builtin_amdgcn_sched_barrier(0);
+          dma_barrier<0>();
+          if (s + 1 < sb1) issue_lw(s + 1, u ^ 1);
+          WT::load_lds(lds + u * STG + AS::STAGE + (uint32_t)(nl * WT::kBytes), g, raw[0]);
+          compute(lds + u * STG, raw[0]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  } else {
   issue(sb0, 0, st[0], raw[0]);
   issue(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1, st[kDma ? 0 : 1], raw[1]);
   if constexpr (!kDma) st[0].store(lds);
@@ -298,6 +355,7 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     step(sb, 0);
     step(sb + 1, 1);
     step(sb + 2, 2);
+  }
   }
 
   if (n < nrows_w) {
@@ -316,8 +374,8 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   }
   // grouped down projection with the weighted sum folded in (no split K there): every thread takes part
   if (rsum.out)
-    route_sum_finish<256, BMt>(rsum, (const float *)(const void *)dst, ldd, dst_rows, m0, mrows, n0,
-                               (int)(nrows_w - n0 < BN ? nrows_w - n0 : BN), (int)(n0 / BN));
+    route_sum_finish<64 * NW, BMt>(rsum, (const float *)(const void *)dst, ldd, dst_rows, m0, mrows, n0,
+                                   (int)(nrows_w - n0 < BNt ? nrows_w - n0 : BNt), (int)(n0 / BNt));
 }
 
 // Split K: split s of a tile writes its partial sums to plane s of the caller's fixup buffer (planes of rows x cols
@@ -780,18 +838,18 @@ constexpr int kq_waves() { return WT::kMin && TMv <= (WT::kPlanes == 3 ? 1 : 2) 
 
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst, or with more
 // than one split into plane s of `part` (mrows x nrows_w f32 per plane)
-template <class WT, class Out, int TMv>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq(
+template <class WT, class Out, int TMv, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
     int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd, float *__restrict__ part) {
-  constexpr int BMt = 32 * TMv;
+  constexpr int BMt = 32 * TMv, BNt = 32 * NW;
   int64_t mt, nt, split;
-  tile_of((mrows + BMt - 1) / BMt, (nrows_w + BN - 1) / BN, splits, mt, nt, split);
+  tile_of((mrows + BMt - 1) / BMt, (nrows_w + BNt - 1) / BNt, splits, mt, nt, split);
   const int64_t per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
-                            part ? part + split * mrows * nrows_w : nullptr);
+  mmq_kq_tile<WT, Out, TMv, NW>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BNt, sb0, sb1, dst, ldd, nullptr,
+                                part ? part + split * mrows * nrows_w : nullptr);
 }
 
 template <class WB, class Out>
@@ -820,7 +878,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
+  mmq_kq_tile<WT, out_f32, TMv, 4>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
                                 part ? part + split * ncols_dst * nrows_w : nullptr, FUSED ? rsum : RouteSum{});
 }
@@ -908,22 +966,34 @@ int64_t k_splits(int64_t tiles, int64_t nsb, int64_t rows, int64_t cols, const v
   return s;
 }
 
+// Waves (weight rows / 32) per workgroup of the plain K-quant prefill from 64 activation rows per wave on (32-row
+// tiles keep 4: their per-wave DMA share would not be uniform over 8).  Measured on MI355X for Q4_K at M = 512 with
+// the weights staged in LDS: 8 waves 95.6 us, 4 waves 90.9 us -- a workgroup's waves run in lockstep between its
+// barriers, and two 4-wave workgroups per CU let one's VALU epilogue overlap the other's MFMAs.
+#ifndef QMM_KQ_WAVES
+#define QMM_KQ_WAVES 4
+#endif
+
 template <class WT, class Out>
 void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y, int64_t nsb,
                typename Out::T *d, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
-  const int64_t ntiles = (nrows_x + BN - 1) / BN;
   // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
   const int tm = ncols_y <= 32 || kq_tm_max<WT>() < 2 ? 1 : ncols_y <= 64 || kq_tm_max<WT>() < 4 ? 2 : 4;
+  // (8 waves per workgroup fit where one wave needs at most 256 registers: Q4_K at 64 rows; Q6_K / IQ4_XS take 128
+  // rows at one wave per SIMD and keep 4)
+  constexpr int NW = WT::kMin && kq_tm_max<WT>() == 2 ? QMM_KQ_WAVES : 4;
+  const int nw = tm == 1 ? 4 : NW;
+  const int64_t ntiles = (nrows_x + 32 * nw - 1) / (32 * nw);
   const int64_t tiles = ((ncols_y + 32 * tm - 1) / (32 * tm)) * ntiles;
   const int64_t splits = k_splits(tiles, nsb, ncols_y, nrows_x, fixup, nsm);
   float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1) {
-    k_mmq_kq<WT, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 1, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   } else if (tm == 2) {
-    k_mmq_kq<WT, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 2, NW><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   } else if constexpr (kq_tm_max<WT>() >= 4) {  // (not instantiated where it cannot be chosen)
-    k_mmq_kq<WT, Out, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 4, NW><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   }
   if (part) split_sum<Out>(part, splits, ncols_y, nrows_x, d, ldd, nullptr, s);
 }

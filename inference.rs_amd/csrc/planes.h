@@ -58,6 +58,13 @@ struct wq4k {
 #pragma unroll
     for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * c + 16 * g, 0, 0);
   }
+  // the same bytes of one superblock already in LDS (16-byte aligned)
+  static constexpr bool kLdsWeights = true;
+  static __device__ __forceinline__ void load_lds(const uint8_t *sb, int g, Raw &r) {
+    r.hdr = *(const u32x4 *)sb;
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = *(const u32x4 *)(sb + 16 + 32 * c + 16 * g);
+  }
   struct Prep {
     float d, dmin;
     v8h bmin;
@@ -108,6 +115,8 @@ struct wq5k {
   static constexpr bool kMin = true;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 6;  // header, this lane's 16 qh bytes, four 16-byte nibble chunks
+  static constexpr bool kLdsWeights = false;
+  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
   // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
   static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   struct Raw {
@@ -152,6 +161,8 @@ struct wq6k {
   static constexpr bool kMin = false;
   static constexpr bool kDma = false;
   static constexpr int kLoads = 6;  // at least six loads (16-byte ones; the 4-byte ones may merge)
+  static constexpr bool kLdsWeights = false;
+  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
   // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
   static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   // 16 bytes at a 2-byte aligned offset, kept as the five dwords that cover them: realigned only when used, so a
@@ -247,6 +258,8 @@ struct wiq4xs {
   static constexpr bool kMin = false;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 5;  // one 8-byte header load and four 16-byte loads (none adjacent to another)
+  static constexpr bool kLdsWeights = false;
+  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
   static __device__ __forceinline__ int chunk(int j, int g) { return 8 * g + j; }
   struct Raw {
     u32x2 h;  // d | scales_h << 16, scales_l
