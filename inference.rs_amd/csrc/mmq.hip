@@ -181,6 +181,8 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   // weight bytes per stage: every lane of every load writes its 16 bytes, the padding lanes past the slab included
   constexpr int WST = kWI * 64 * NW * 16;
   constexpr int STG = AS::STAGE + WST;
+  // (only where two workgroups share each SIMD: at one wave per SIMD it measured no gain)
+  constexpr bool kPrio = kLw;
   static_assert(!kLw || (AS::STAGE % 16 == 0 && WT::kBytes % 16 == 0), "16-byte aligned stages");
   __shared__ __attribute__((aligned(16))) uint8_t lds[(kLw ? 2 : 3) * STG];
 
@@ -260,6 +262,10 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
     v4i av[2][TM];
 #pragma unroll
     for (int t = 0; t < TM; t++) av[0][t] = *(const v4i *)(slot + 8192 * t + qoff[0]);
+    // The two waves on a SIMD come from two workgroups and drift apart: a wave in its MFMA chain gets the issue slots
+    // first, so the other's VALU epilogue fills the matrix core's cycles instead of the two taking turns (MI355X,
+    // Q4_K at M = 512: 90 -> 83 us)
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       if (kAhead && j < 7) {
@@ -279,6 +285,7 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
         if constexpr (WT::kPlanes == 3) acc3[t] = mfma_i8(a, b3, acc3[t]);
       }
     }
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       v16f fmin = (v16f){};
