@@ -164,27 +164,41 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
                                             const RouteSum &rsum = RouteSum{}) {
   constexpr int BMt = 32 * TM;
   constexpr int BNt = 32 * NW;
-  // Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a register
-  // ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
-  constexpr bool kDma = WT::kDma;
-  typedef ActStage<BMt, WT::kMin, 64 * NW> AS;
-  typedef ActDma<BMt, WT::kMin, NW> AD;
-  static_assert(AS::STAGE == AD::STAGE, "one LDS layout");
   // kLw: the weight superblocks go by DMA into LDS too, as the tile's rows' contiguous 16-byte pieces, and each wave
   // reads its B-operand bytes from there.  Loaded straight into registers, one 16-byte load per lane covers 32 weight
   // rows, 32 bytes of each, and the texture addresser's per-cache-line work for those loads bounds the kernel; as
-  // contiguous pieces the same bytes take a quarter of the cache-line accesses.  Two stages of activations and
-  // weights (the LDS does not hold three), so the next superblock's loads are in flight during one step.
-  constexpr bool kLw = WT::kLdsWeights && kDma && TM == 2;
-  constexpr int kChunks = WT::kBytes / 16;                           // 16-byte pieces per weight superblock
-  constexpr int kWI = kLw ? (BNt * kChunks + 64 * NW - 1) / (64 * NW) : 0;  // weight DMA loads per wave
+  // contiguous pieces the same bytes take a quarter of the cache-line accesses.  Two stages of activations, so the
+  // next superblock's loads are in flight during one step (the LDS does not hold three).
+  constexpr bool kLw = WT::kLdsWeights && TM == WT::kLwTM;
+  // Without kLw, Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a
+  // register ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
+  constexpr bool kDma = WT::kDma || kLw;
+  typedef ActStage<BMt, WT::kMin, 64 * NW> AS;
+  typedef ActDma<BMt, WT::kMin, NW> AD;
+  static_assert(AS::STAGE == AD::STAGE, "one LDS layout");
+  // Superblocks of a multiple of 16 bytes (Q4_K: 16-byte aligned) are copied as their own pieces and kept row after
+  // row.  Others (Q6_K: 210 bytes, 2-byte aligned) are copied as the 16-byte pieces of a window that starts at the
+  // dword holding their first byte, and kept piece-major: piece k of tile row r at 16 (BNt k + r).  Then each DMA
+  // round of the workgroup (64 NW lanes = 2 BNt) takes pieces 2i and 2i + 1 of every row, so a lane's global offset
+  // is one row's window plus a constant, and the reads of a piece by consecutive rows are consecutive 16 bytes.
+  constexpr bool kRowMajor = WT::kBytes % 16 == 0;
+  constexpr int kPieces = kRowMajor ? WT::kBytes / 16 : (WT::kBytes + 3 + 15) / 16;  // pieces per superblock
+  constexpr int kWI = kLw ? (BNt * kPieces + 64 * NW - 1) / (64 * NW) : 0;  // weight DMA loads per wave
   // weight bytes per stage: every lane of every load writes its 16 bytes, the padding lanes past the slab included
   constexpr int WST = kWI * 64 * NW * 16;
   constexpr int STG = AS::STAGE + WST;
+  // weight stages: two where two workgroups still fit the 160 KB of a CU, else one, reloaded once every wave has
+  // read it (a second barrier per superblock)
+  constexpr int kWS = 2 * STG <= (TM == 2 ? 80 : 160) * 1024 ? 2 : 1;
+  constexpr int kPS = kRowMajor ? 16 : 16 * BNt;  // LDS bytes from one piece of a row to its next
   // (only where two workgroups share each SIMD: at one wave per SIMD it measured no gain)
-  constexpr bool kPrio = kLw;
-  static_assert(!kLw || (AS::STAGE % 16 == 0 && WT::kBytes % 16 == 0), "16-byte aligned stages");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[(kLw ? 2 : 3) * STG];
+  constexpr bool kPrio = kLw && TM == 2;
+  static_assert(!kLw || AS::STAGE % 16 == 0, "16-byte aligned stages");
+  static_assert(!kLw || kRowMajor || 64 * NW == 2 * BNt, "two pieces of every row per DMA round");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLw ? 2 * AS::STAGE + kWS * WST : 3 * AS::STAGE];
+  // kLw stage u: activations and weights (two weight stages: as STG-byte stages, activations first)
+  auto act_slot = [&](int u) { return lds + u * (kWS == 2 ? STG : AS::STAGE); };
+  auto w_slot = [&](int u) { return kWS == 2 ? lds + u * STG + AS::STAGE : lds + 2 * AS::STAGE; };
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
@@ -197,9 +211,14 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   const uint32_t voff[3] = {(uint32_t)(m0 * 256 + 16 * tid),
                             (uint32_t)(nsb * rows * 260 + m0 * 32 + 16 * tid),
                             (uint32_t)(nsb * rows * 256 + m0 * 4 + 16 * tid)};
-  // weights: one resource over the tile's rows
-  const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, (nlast + 1) * w_row_bytes);
-  const uint32_t wrow = (uint32_t)(nl * w_row_bytes);
+  // weights: one resource over the tile's rows, from the dword that holds the tile's first byte (wdelta bytes
+  // before it), so offsets that are multiples of 4 from the resource are dword aligned in memory, to the end of the
+  // dword that holds its last byte: the range check passes or zeroes whole dwords, and a superblock that ends inside
+  // a dword (Q6_K) has its last bytes there
+  const uintptr_t wt = (uintptr_t)(W + n0 * w_row_bytes);
+  const uint32_t wdelta = (uint32_t)(wt & 3);
+  const rsrc_t rw = make_rsrc((const uint8_t *)(wt - wdelta), ((nlast + 1) * w_row_bytes + wdelta + 3) & ~(int64_t)3);
+  const uint32_t wrow = (uint32_t)(nl * w_row_bytes) + wdelta;
 
   // LDS read offsets of this lane's A fragments: row 32t + li, chunk WT::chunk(j, g) (2j + g but for IQ4_XS),
   // swizzled
@@ -215,23 +234,36 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   AD dma;
   if (kDma) dma.init(wave, lane, m0, rows, nsb);
   typename WT::Raw raw[kLw ? 1 : 3];
-  // kLw: lane's weight piece C = 64 (NW i + wave) + lane of the stage's slab (row C / kChunks, piece C % kChunks), at
-  // LDS byte 16 C of the stage's weight part; pieces past the slab read past the resource (no memory traffic)
-  uint32_t woff[kWI > 0 ? kWI : 1];
+  // kLw: lane's weight piece C = 64 (NW i + wave) + lane of the stage's slab goes to LDS byte 16 C of the stage's
+  // weight part.  Row-major: row C / kPieces, piece C % kPieces, and pieces past the slab read past the resource (no
+  // memory traffic).  Piece-major: row C % BNt = 64 wave + lane - BNt (wave >= NW / 2), piece C / BNt = 2i + (wave >=
+  // NW / 2); a piece index past the window is not loaded.
+  constexpr int kWO = kRowMajor ? (kWI > 0 ? kWI : 1) : 1;
+  uint32_t woff[kWO];
+  const int whalf = wave >= NW / 2 ? 1 : 0;
+  if constexpr (kRowMajor) {
 #pragma unroll
-  for (int i = 0; i < kWI; i++) {
-    const int C = 64 * (NW * i + wave) + lane, r = C / kChunks, pc = C - r * kChunks;
-    woff[i] = C < BNt * kChunks ? (uint32_t)(r * w_row_bytes + 16 * pc) : 0x80000000u;
+    for (int i = 0; i < kWI; i++) {
+      const int C = 64 * (NW * i + wave) + lane, r = C / kPieces, pc = C - r * kPieces;
+      woff[i] = C < BNt * kPieces ? (uint32_t)(r * w_row_bytes + 16 * pc) : 0x80000000u;
+    }
+  } else {
+    woff[0] = (uint32_t)((64 * wave + lane - BNt * whalf) * w_row_bytes) + wdelta + 16 * whalf;
   }
   auto issue_lw = [&](int64_t sb, int u) {
 #if defined(__HIP_DEVICE_COMPILE__)
     __builtin_amdgcn_sched_barrier(0);
-    dma.issue(ra, lds + u * STG, wave, lane, (uint32_t)(sb * rows));
+    dma.issue(ra, act_slot(u), wave, lane, (uint32_t)(sb * rows));
+    // (piece-major: the window starts at the dword of the superblock's first byte; whalf's 16 bytes are a multiple
+    // of 4, so they survive the rounding)
+    const uint32_t wv = kRowMajor ? 0u : (woff[0] + (uint32_t)sb * WT::kBytes) & ~3u;
 #pragma unroll
-    for (int i = 0; i < kWI; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rw, (__attribute__((address_space(3))) void *)(lds + u * STG + AS::STAGE + 1024 * (NW * i + wave)), 16,
-          woff[i] + (uint32_t)sb * WT::kBytes, 0, 0, 0);
+    for (int i = 0; i < kWI; i++) {
+      if (kRowMajor || 2 * i + 1 < kPieces || whalf == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rw, (__attribute__((address_space(3))) void *)(w_slot(u) + 1024 * (NW * i + wave)), 16,
+            kRowMajor ? woff[i] + (uint32_t)sb * WT::kBytes : wv + 32 * i, 0, 0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #endif
   };
@@ -337,7 +369,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 
   if constexpr (kLw) {
     // two stages: after the barrier of step s every wave is done with stage (s + 1) % 2, so the loads of s + 1 go
-    // there while s is computed from stage s % 2
+    // there while s is computed from stage s % 2.  With one weight stage, the weights of s go to registers first
+    // and a second barrier waits until every wave has read them before the loads of s + 1 overwrite them.
+    const uint32_t wl = kRowMajor ? (uint32_t)(nl * WT::kBytes) : (uint32_t)(16 * nl);  // the lane's row in a stage
     issue_lw(sb0, 0);
     for (int64_t sb = sb0; sb < sb1; sb += 2) {
 #pragma unroll
@@ -346,9 +380,14 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
         if (s < sb1) {  // (uniform over the workgroup)
           __builtin_amdgcn_sched_barrier(0);
           dma_barrier<0>();
-          if (s + 1 < sb1) issue_lw(s + 1, u ^ 1);
-          WT::load_lds(lds + u * STG + AS::STAGE + (uint32_t)(nl * WT::kBytes), g, raw[0]);
-          compute(lds + u * STG, raw[0]);
+          const uint32_t off = kRowMajor ? 0u : (wrow + (uint32_t)s * WT::kBytes) & 3u;
+          if constexpr (kWS == 1) WT::template load_lds<kPS>(w_slot(u) + wl, off, g, raw[0]);
+          if (s + 1 < sb1) {
+            if constexpr (kWS == 1) dma_barrier<0>();
+            issue_lw(s + 1, u ^ 1);
+          }
+          if constexpr (kWS == 2) WT::template load_lds<kPS>(w_slot(u) + wl, off, g, raw[0]);
+          compute(act_slot(u), raw[0]);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -839,9 +878,11 @@ ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
 // Q4_K (measured on MI355X): 64 activation rows per wave at 2 waves per SIMD beats 128 rows at 1 wave; Q6_K, whose
 // plane building needs more registers, runs 1 wave per SIMD and takes 128 rows.
 template <class WT>
-constexpr int kq_tm_max() { return WT::kPlanes == 3 ? 1 : WT::kMin ? 2 : 4; }
+constexpr int kq_tm_max() { return WT::kPlanes == 3 ? 1 : WT::kMin ? 2 : WT::kLdsWeights && WT::kLwTM ? WT::kLwTM : 4; }
 template <class WT, int TMv>
-constexpr int kq_waves() { return WT::kMin && TMv <= (WT::kPlanes == 3 ? 1 : 2) ? 2 : 1; }
+constexpr int kq_waves() {
+  return (WT::kMin || (WT::kLdsWeights && WT::kLwTM == 2)) && TMv <= (WT::kPlanes == 3 ? 1 : 2) ? 2 : 1;
+}
 
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst, or with more
 // than one split into plane s of `part` (mrows x nrows_w f32 per plane)

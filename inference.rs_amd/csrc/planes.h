@@ -1,7 +1,8 @@
 // Int8 MFMA operand builders shared by the prefill matmul and the skinny (few-row) matmul: the two int8 weight
 // planes that fold the K-quant sub-block scales into the MFMA operand, the MFMA wrappers and the 32x32 output
 // layout.  Exactness: Q4_K sc (6 bit) = 8 sh + sl, so sc * q4 = 8 (sh * q4) + (sl * q4) with both planes <= 105;
-// Q6_K sc * (q6 - 32) in [-4096, 4064] = 64 wh + wl.  Each superblock's integer dot is exact in int32.
+// Q6_K w = sc * (q6 - 32) in [-4064, 4096] (and IQ4_XS's (ls - 32) * kv in [-4064, 4032]) = 256 wh + wl with wh in
+// [-16, 16] and wl in [-128, 127] (split256).  Each superblock's integer dot is exact in int32.
 #pragma once
 
 #include "common.h"
@@ -32,6 +33,25 @@ __device__ __forceinline__ void swap_lane_halves(uint32_t &lo, uint32_t &hi) {
 #endif
 }
 
+// The two int8 planes of four weights w in [-4224, 4095]: lo and hi hold w + 128 of weights (0, 2) and (1, 3) in
+// their 16-bit lanes.  w + 128 = 256 wh + (wl + 128): wh is the high byte of the lane, wl its low byte less 128
+// (the low byte with its top bit flipped, as int8), so each plane is one byte permute.
+// (v_perm_b32 (S0, S1, sel): byte k of the result is byte sel_k of the eight bytes S1 (0..3), S0 (4..7); sel 12 = 0)
+__device__ __forceinline__ void split256(s2 lo, s2 hi, v4i &b1, v4i &b2, int i) {
+  const uint32_t l = __builtin_bit_cast(uint32_t, lo), h = __builtin_bit_cast(uint32_t, hi);
+  b2[i] = (int)(__builtin_amdgcn_perm(h, l, 0x06020400u) ^ 0x80808080u);  // low bytes of l.x, h.x, l.y, h.y
+  b1[i] = (int)__builtin_amdgcn_perm(h, l, 0x07030501u);                  // their high bytes
+}
+
+// Q6_K values q6 = ql | qh << 4 of four bytes (ql's low nibbles, the 2-bit fields of qh at bit hsh (even) of each
+// byte) as 16-bit lanes: *lo = bytes 0 and 2, *hi = bytes 1 and 3
+__device__ __forceinline__ void q6_lanes(uint32_t ql, uint32_t qh, int hsh, s2 &lo, s2 &hi) {
+  const uint32_t b = (hsh <= 4 ? qh << (4 - hsh) : qh >> (hsh - 4)) & 0x30303030u;
+  const uint32_t v6 = (ql & 0x0f0f0f0fu) | b;
+  lo = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, v6, 0x0c020c00u));
+  hi = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, v6, 0x0c030c01u));
+}
+
 // Row of 32x32 output register r of lane group g (v_mfma 32x32 D layout): 8 (r / 4) + 4 g + r % 4
 __device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
@@ -58,12 +78,15 @@ struct wq4k {
 #pragma unroll
     for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 + 32 * c + 16 * g, 0, 0);
   }
-  // the same bytes of one superblock already in LDS (16-byte aligned)
+  // the same bytes of one superblock already in LDS, as 16-byte pieces PS bytes apart: piece k holds bytes
+  // 16 k .. +16 (off, the superblock's start within its first dword, is 0: Q4_K superblocks are 16-byte aligned)
   static constexpr bool kLdsWeights = true;
-  static __device__ __forceinline__ void load_lds(const uint8_t *sb, int g, Raw &r) {
-    r.hdr = *(const u32x4 *)sb;
+  static constexpr int kLwTM = 2;  // the activation tile (32 kLwTM rows per wave) that takes weights from LDS
+  template <int PS>
+  static __device__ __forceinline__ void load_lds(const uint8_t *p, uint32_t, int g, Raw &r) {
+    r.hdr = *(const u32x4 *)p;
 #pragma unroll
-    for (int c = 0; c < 4; c++) r.q[c] = *(const u32x4 *)(sb + 16 + 32 * c + 16 * g);
+    for (int c = 0; c < 4; c++) r.q[c] = *(const u32x4 *)(p + PS * (1 + 2 * c + g));
   }
   struct Prep {
     float d, dmin;
@@ -116,7 +139,8 @@ struct wq5k {
   static constexpr bool kDma = true;
   static constexpr int kLoads = 6;  // header, this lane's 16 qh bytes, four 16-byte nibble chunks
   static constexpr bool kLdsWeights = false;
-  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
+  static constexpr int kLwTM = 0;
+  template <int PS, class R> static __device__ void load_lds(const uint8_t *, uint32_t, int, R &) {}
   // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
   static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   struct Raw {
@@ -157,12 +181,15 @@ struct wq5k {
 struct wq6k {
   static constexpr int kBytes = 210;
   static constexpr int kPlanes = 2;
-  static constexpr int kShift = 6;  // I = 64 * wh + wl
+  static constexpr int kShift = 8;  // I = 256 * wh + wl (split256)
   static constexpr bool kMin = false;
   static constexpr bool kDma = false;
   static constexpr int kLoads = 6;  // at least six loads (16-byte ones; the 4-byte ones may merge)
-  static constexpr bool kLdsWeights = false;
-  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
+  static constexpr bool kLdsWeights = true;
+#ifndef QMM_Q6K_LW_TM
+#define QMM_Q6K_LW_TM 4
+#endif
+  static constexpr int kLwTM = QMM_Q6K_LW_TM;
   // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
   static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   // 16 bytes at a 2-byte aligned offset, kept as the five dwords that cover them: realigned only when used, so a
@@ -199,6 +226,25 @@ struct wq6k {
     r.off = off;
     r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
   }
+  // The same bytes from LDS, where the 224 bytes from the dword holding the superblock's first byte lie as 16-byte
+  // pieces PS bytes apart (piece k: bytes 16 k .. +16 of that window); off = the superblock's start in the window
+  template <int PS>
+  static __device__ __forceinline__ void lds16(const uint8_t *p, int k, Chunk &c) {
+    c.v = *(const u32x4 *)(p + PS * k);
+    c.e = *(const uint32_t *)(p + PS * (k + 1));
+  }
+  template <int PS>
+  static __device__ __forceinline__ void load_lds(const uint8_t *p, uint32_t off, int g, Raw &r) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+      for (int q = 0; q < 2; q++) lds16<PS>(p, 4 * h + 2 * q + g, r.ql[h][q]);
+      lds16<PS>(p, 8 + 2 * h + g, r.qh[h]);
+    }
+    lds16<PS>(p, 12, r.sc);
+    r.off = off;
+    r.d = *(const uint16_t *)(p + PS * 13 + off);
+  }
   struct Prep {
     int sc[8];
     float d;
@@ -230,16 +276,12 @@ struct wq6k {
     const uint32_t *ql = p.ql[h][q & 1];
     const int nsh = (q >> 1) * 4;
     const s2 sc2 = {(short)p.sc[j], (short)p.sc[j]};
+    const s2 c2 = (s2){128, 128} - (s2){32, 32} * sc2;  // (q6 - 32) sc + 128 = q6 sc + c2
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((p.qh[h][i] >> (2 * q)) & 0x03030303u) << 4);
-      // bytes 0,2 and 1,3 in 16-bit lanes, minus 32, times the scale: w in [-4096, 4064]
-      const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
-      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
-      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
-      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+      s2 lo, hi;
+      q6_lanes(ql[i] >> nsh, p.qh[h][i], 2 * q, lo, hi);
+      split256(lo * sc2 + c2, hi * sc2 + c2, b1, b2, i);  // w + 128
     }
   }
 };
@@ -254,12 +296,13 @@ struct wq6k {
 struct wiq4xs {
   static constexpr int kBytes = 136;
   static constexpr int kPlanes = 2;
-  static constexpr int kShift = 6;
+  static constexpr int kShift = 8;  // split256
   static constexpr bool kMin = false;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 5;  // one 8-byte header load and four 16-byte loads (none adjacent to another)
   static constexpr bool kLdsWeights = false;
-  template <class R> static __device__ void load_lds(const uint8_t *, int, R &) {}
+  static constexpr int kLwTM = 0;
+  template <int PS, class R> static __device__ void load_lds(const uint8_t *, uint32_t, int, R &) {}
   static __device__ __forceinline__ int chunk(int j, int g) { return 8 * g + j; }
   struct Raw {
     u32x2 h;  // d | scales_h << 16, scales_l
@@ -294,13 +337,10 @@ struct wiq4xs {
     for (int i = 0; i < 4; i++) {
       const uint32_t nib = (j & 1) ? ((w[i] >> 4) & 0x0f0f0f0fu) : (w[i] & 0x0f0f0f0fu);
       const uint32_t v = unit_iq4xs::lookup(nib);  // four int8 table values
-      // bytes 0,2 and 1,3 sign-extended into 16-bit lanes, times the scale
-      const s2 lo = (__builtin_bit_cast(s2, v << 8) >> (s2){8, 8}) * sc2;
-      const s2 hi = (__builtin_bit_cast(s2, v) >> (s2){8, 8}) * sc2;
-      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
-      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
-      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
-      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+      // bytes 0,2 and 1,3 sign-extended into 16-bit lanes, times the scale, plus 128
+      const s2 lo = (__builtin_bit_cast(s2, v << 8) >> (s2){8, 8}) * sc2 + (s2){128, 128};
+      const s2 hi = (__builtin_bit_cast(s2, v) >> (s2){8, 8}) * sc2 + (s2){128, 128};
+      split256(lo, hi, b1, b2, i);
     }
   }
 };
@@ -390,7 +430,7 @@ struct wq4k16 {
 // the 2-bit fields 2q, q = 2(t%2) + kg/2, of qh[32(t/2) + 16(kg%2) ..], scale sc[4t + kg].
 struct wq6k16 {
   static constexpr int kBytes = 210;
-  static constexpr int kShift = 6;
+  static constexpr int kShift = 8;  // split256
   static constexpr bool kMin = false;
   // chunks kept unaligned until prepare(), as in wq6k
   typedef wq6k::Chunk Chunk;
@@ -437,15 +477,12 @@ struct wq6k16 {
     const uint32_t *ql = p.ql[t >> 1], *qh = p.qh[t >> 1];
     const int nsh = 4 * (t & 1), hsh = 4 * (t & 1) + 2 * (kg >> 1);
     const s2 sc2 = {(short)p.sc[t], (short)p.sc[t]};
+    const s2 c2 = (s2){128, 128} - (s2){32, 32} * sc2;  // (q6 - 32) sc + 128 = q6 sc + c2
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t v6 = ((ql[i] >> nsh) & 0x0f0f0f0fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
-      const s2 lo = (__builtin_bit_cast(s2, v6 & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const s2 hi = (__builtin_bit_cast(s2, (v6 >> 8) & 0x00ff00ffu) - (s2){32, 32}) * sc2;
-      const uint32_t lo_u = __builtin_bit_cast(uint32_t, lo), hi_u = __builtin_bit_cast(uint32_t, hi);
-      b2[i] = (int)((lo_u & 0x003f003fu) | ((hi_u & 0x003f003fu) << 8));
-      const uint32_t lh = __builtin_bit_cast(uint32_t, lo >> (s2){6, 6}), hh = __builtin_bit_cast(uint32_t, hi >> (s2){6, 6});
-      b1[i] = (int)((lh & 0x00ff00ffu) | ((hh & 0x00ff00ffu) << 8));
+      s2 lo, hi;
+      q6_lanes(ql[i] >> nsh, qh[i], hsh, lo, hi);
+      split256(lo * sc2 + c2, hi * sc2 + c2, b1, b2, i);  // w + 128
     }
   }
 };

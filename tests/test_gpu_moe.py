@@ -125,6 +125,24 @@ def test_grouped_prefill_matches_the_oracle(gtype, case):
     assert_parity(out.cpu().numpy(), want)
 
 
+# Q6_K experts of an odd row count with an odd superblock count per row: every other expert starts 2 bytes past a
+# dword (the 64-row tile stages superblocks in LDS from the dword holding their first byte); 200 tokens take the
+# 64-row tiles, 24 the 32-row ones.
+@pytest.mark.parametrize("tokens", [24, 200])
+def test_grouped_q6_k_experts_2_bytes_past_a_dword(tokens):
+    rng = np.random.default_rng(17 + tokens)
+    E, n, k, topk = 4, 129, 768, 2
+    wq = experts(rng, O.Q6K, E, n, k)
+    ids = routing(rng, tokens, E, topk)[0]
+    x = acts(rng, tokens, k)
+    want = O.indexed_moe(O.Q6K, wq, E, n, k, x[:, None], ids.astype(np.uint32)).reshape(tokens * topk, n)
+    bounds, tok, src, counts, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
+    y, kp = qmm.quantize_prefill(O.Q6K, to_dev(x), ids=src)
+    out = torch.full((tokens * topk, n), float("nan"), device=DEV)
+    qmm.mmq_moe(O.Q6K, to_dev(wq), y, tok, bounds, E, k, n, tokens * topk, int(counts.max().item()), out)
+    assert_parity(out.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("case", ["uniform64", "skewed64", "uniform400", "top4"])
 @pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q5K, O.IQ4XS, O.Q8_0, O.Q4_0])
 def test_grouped_down_with_folded_weighted_sum(gtype, case):

@@ -259,3 +259,18 @@ def test_mmq_iq4_xs_rejects_misaligned_weights():
     y, _ = qmm.quantize_prefill(O.IQ4XS, to_dev(acts(rng, 40, 256)))
     with pytest.raises(qmm.QmmError, match="4-byte aligned"):
         qmm.mmq(O.IQ4XS, buf[2:], y, 256, 32, 40)
+
+
+# Q6_K superblocks are 210 bytes, 2-byte aligned: the 64-row tile stages each row's superblock in LDS from the dword
+# that holds its first byte.  Weights 2 bytes past a dword boundary, with an odd superblock count per row (rows
+# alternately 0 and 2 bytes past a dword), against the oracle.
+@pytest.mark.parametrize("m,n,k", [(130, 200, 768), (64, 129, 256), (512, 300, 1280), (100, 33, 2816)])
+def test_mmq_q6_k_weights_2_bytes_past_a_dword(m, n, k):
+    rng = np.random.default_rng(43 + m + n + k)
+    wq = O.quantize(O.Q6K, weights(rng, n, k))
+    x = acts(rng, m, k)
+    buf = torch.zeros(wq.size + 2, dtype=torch.uint8, device=DEV)
+    buf[2:] = to_dev(wq.reshape(-1))
+    y, _ = qmm.quantize_prefill(O.Q6K, to_dev(x))
+    got = qmm.mmq(O.Q6K, buf[2:], y, k, n, m).cpu().numpy()
+    assert_parity(got, O.matmul(O.Q6K, x, wq, n), terms(O.Q6K, x, wq, n), what=f"q6_k +2 m{m} n{n} k{k}")
