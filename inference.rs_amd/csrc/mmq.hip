@@ -26,6 +26,12 @@
 #include "skinny.h"
 #include "units.h"
 
+// 1: the K-quant kernel's 32-row activation tiles (small batches, the expert-grouped matmul) take Q4_K weights
+// from LDS too
+#ifndef QMM_KQ_LW_TM1
+#define QMM_KQ_LW_TM1 1
+#endif
+
 namespace {
 
 constexpr int BM = 128;
@@ -168,8 +174,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   // reads its B-operand bytes from there.  Loaded straight into registers, one 16-byte load per lane covers 32 weight
   // rows, 32 bytes of each, and the texture addresser's per-cache-line work for those loads bounds the kernel; as
   // contiguous pieces the same bytes take a quarter of the cache-line accesses.  Two stages of activations, so the
-  // next superblock's loads are in flight during one step (the LDS does not hold three).
-  constexpr bool kLw = WT::kLdsWeights && TM == WT::kLwTM;
+  // next superblock's loads are in flight during one step (the LDS does not hold three).  Q4_K takes this path at
+  // 64-row activation tiles and (QMM_KQ_LW_TM1) at 32-row ones (MI355X, 14336x4096 at M = 32: 21.2 -> 16.8 us).
+  constexpr bool kLw = WT::kLdsWeights && (TM == WT::kLwTM || (QMM_KQ_LW_TM1 && TM == 1 && WT::kMin));
   // Without kLw, Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a
   // register ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
   constexpr bool kDma = WT::kDma || kLw;
@@ -188,7 +195,8 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   constexpr int WST = kWI * 64 * NW * 16;
   constexpr int STG = AS::STAGE + WST;
   // weight stages: two where two workgroups still fit the 160 KB of a CU, else one, reloaded once every wave has
-  // read it (a second barrier per superblock)
+  // read it (a second barrier per superblock).  (Three to five stages for 32-row activation tiles, at one workgroup
+  // per CU, measured slower than two at two workgroups.)
   constexpr int kWS = 2 * STG <= (TM == 2 ? 80 : 160) * 1024 ? 2 : 1;
   constexpr int kPS = kRowMajor ? 16 : 16 * BNt;  // LDS bytes from one piece of a row to its next
   // (only where two workgroups share each SIMD: at one wave per SIMD it measured no gain)
