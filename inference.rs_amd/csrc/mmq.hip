@@ -26,6 +26,12 @@
 #include "skinny.h"
 #include "units.h"
 
+// 1: the expert-grouped matmul takes 32-row tiles when the average expert has at most 32 rows (0: the largest).
+// MI355X, 8 x Q4_K 14336x4096 / 4096x14336 experts, 64 tokens top-2 (16 rows per expert on average, more than 32
+// in the largest): MoE step 303 -> 227 us.
+#ifndef QMM_MOE_SMALL_AVG
+#define QMM_MOE_SMALL_AVG 1
+#endif
 // 1: the K-quant kernel's 32-row activation tiles (small batches, the expert-grouped matmul) take Q4_K weights
 // from LDS too
 #ifndef QMM_KQ_LW_TM1
@@ -1081,7 +1087,8 @@ void launch_b32_moe(const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int
                     const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, float *d, int64_t ldd,
                     int64_t ncols_dst, int64_t ncols_max, int64_t num_experts, void *fixup, int nsm, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
-  const int tm = ncols_max <= 32 ? 1 : 2;
+  // 32-row tiles where the experts' rows are few on average (an expert with more takes several)
+  const int tm = (QMM_MOE_SMALL_AVG ? (ncols_dst + num_experts - 1) / num_experts : ncols_max) <= 32 ? 1 : 2;
   const int64_t bm = 32 * tm;
   // expected work: about ncols_dst / bm row tiles per n tile over all experts
   const int64_t splits = k_splits(ntiles * ((ncols_dst + bm - 1) / bm), nsb, ncols_dst, nrows_x, fixup, nsm);
@@ -1215,7 +1222,9 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   }
   // 32-row tiles for a few rows per expert, and always for Q5_K (its third plane does not fit two waves per SIMD at
   // 64 rows, the form the plain prefill measured slower)
-  const bool small = ncols_max <= 32 || type == QMM_TYPE_Q5K;
+  // 32-row tiles where the experts' rows are few on average (an expert with more takes several)
+  const bool small = (QMM_MOE_SMALL_AVG ? (ncols_dst + num_experts - 1) / num_experts : ncols_max) <= 32 ||
+                     type == QMM_TYPE_Q5K;
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
   // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
