@@ -138,14 +138,24 @@ struct wq5k {
   static constexpr bool kMin = true;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 6;  // header, this lane's 16 qh bytes, four 16-byte nibble chunks
-  static constexpr bool kLdsWeights = false;
-  static constexpr int kLwTM = 0;
-  template <int PS, class R> static __device__ void load_lds(const uint8_t *, uint32_t, int, R &) {}
+#ifndef QMM_Q5K_LW
+#define QMM_Q5K_LW 1
+#endif
+  static constexpr bool kLdsWeights = QMM_Q5K_LW;
+  static constexpr int kLwTM = 1;  // (three planes: 32-row activation tiles only)
   // activation chunk (16 values) of MFMA step j for lane half g: values 32 j + 16 g .. +16
   static __device__ __forceinline__ int chunk(int j, int g) { return 2 * j + g; }
   struct Raw {
     u32x4 hdr, qh, q[4];
   };
+  // the same bytes of one superblock already in LDS, as 16-byte pieces PS bytes apart (superblocks 16-byte aligned)
+  template <int PS>
+  static __device__ __forceinline__ void load_lds(const uint8_t *p, uint32_t, int g, Raw &r) {
+    r.hdr = *(const u32x4 *)p;
+    r.qh = *(const u32x4 *)(p + PS * (1 + g));
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = *(const u32x4 *)(p + PS * (3 + 2 * c + g));
+  }
   typedef wq4k::Prep Prep;
   static __device__ __forceinline__ void load(rsrc_t rs, uint32_t row, uint32_t sb, int g, Raw &r) {
     const uint32_t o = row + sb * kBytes;
