@@ -310,9 +310,11 @@ struct wiq4xs {
   static constexpr bool kMin = false;
   static constexpr bool kDma = true;
   static constexpr int kLoads = 5;  // one 8-byte header load and four 16-byte loads (none adjacent to another)
-  static constexpr bool kLdsWeights = false;
-  static constexpr int kLwTM = 0;
-  template <int PS, class R> static __device__ void load_lds(const uint8_t *, uint32_t, int, R &) {}
+#ifndef QMM_IQ4XS_LW_TM
+#define QMM_IQ4XS_LW_TM 4
+#endif
+  static constexpr bool kLdsWeights = QMM_IQ4XS_LW_TM != 0;
+  static constexpr int kLwTM = QMM_IQ4XS_LW_TM;
   static __device__ __forceinline__ int chunk(int j, int g) { return 8 * g + j; }
   struct Raw {
     u32x2 h;  // d | scales_h << 16, scales_l
@@ -323,6 +325,18 @@ struct wiq4xs {
     r.h = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0);
 #pragma unroll
     for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 8 + 64 * g + 16 * c, 0, 0);
+  }
+  // The same bytes from LDS, where the superblock (4-byte aligned: it starts its window) lies as 16-byte pieces PS
+  // bytes apart; a 16-byte chunk at byte 8 + 16 k is the back half of piece k and the front half of piece k + 1
+  template <int PS>
+  static __device__ __forceinline__ void load_lds(const uint8_t *p, uint32_t, int g, Raw &r) {
+    r.h = *(const u32x2 *)p;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int k = 4 * g + c;
+      const u32x2 lo = *(const u32x2 *)(p + PS * k + 8), hi = *(const u32x2 *)(p + PS * (k + 1));
+      r.q[c] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+    }
   }
   struct Prep {
     int sc[4];  // ls - 32 of sub-blocks 4g .. 4g + 3
