@@ -272,7 +272,7 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     return res
 
 
-def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
+def moe_workload(torch, qmm, steps, warmup, seed, tokens=64, force_grouped=False):
     """8 experts, gate/up Q4_K 14336x4096 and down Q4_K 4096x14336; `tokens` tokens, top-2 from softmax(N(0,1)
     logits) (Mixtral renormalisation): the grouped prefill path of the MoE experts block at 64 tokens, the indexed
     decode path (gate/up GLU matvec, then down with the weighted sum folded in) at 8 or fewer."""
@@ -304,7 +304,7 @@ def moe_workload(torch, qmm, steps, warmup, seed, tokens=64):
 
     def step(i):
         rc = H.qmm_moe_forward(moe, x.data_ptr(), tokens, ids_d.data_ptr(), w_d.data_ptr(), topk, out.data_ptr(),
-                               torch.cuda.current_stream().cuda_stream, 1)
+                               torch.cuda.current_stream().cuda_stream, 1 if force_grouped else 0)
         if rc != 0:
             raise RuntimeError(H.qmm_host_last_error().decode())
 
