@@ -94,10 +94,11 @@ def test_mmq_matches_the_cpu_qmatmul(gtype, m, n, k):
 
 # (gtype, m, n, k): f16 / bf16 outputs of every prefill kernel -- the K-quant kernel (Q4_K, Q6_K, Q5_K), the pipelined
 # 32-value kernel (Q8_0, Q4_0, Q5_0 with K a multiple of 256) and the simple Q8_0-layout kernel (K = 1056); the 17-row
-# cases take split K, whose plane sum rounds to the output type once
+# cases take split K, whose plane sum rounds to the output type once; Q6_K at 130 rows takes the 128-row tile with its
+# weights staged in LDS
 HALF_CASES = [(O.Q4K, 64, 128, 1024), (O.Q6K, 64, 128, 1024), (O.Q5K, 64, 128, 1024), (O.Q8_0, 64, 128, 1024),
               (O.Q4_0, 64, 128, 1024), (O.Q5_0, 64, 128, 1024), (O.Q8_0, 40, 96, 1056), (O.Q4_0, 40, 96, 1056),
-              (O.Q5_0, 40, 96, 1056), (O.Q4K, 17, 300, 4096), (O.Q8_0, 17, 300, 4096)]
+              (O.Q5_0, 40, 96, 1056), (O.Q4K, 17, 300, 4096), (O.Q8_0, 17, 300, 4096), (O.Q6K, 130, 200, 1024)]
 
 
 @pytest.mark.parametrize("out", ["f16", "bf16"])
@@ -227,9 +228,10 @@ def test_mmq_iq4_xs_matches_the_cpu_qmatmul(m, n, k):
 
 
 @pytest.mark.parametrize("out", ["f16", "bf16"])
-def test_mmq_iq4_xs_half_outputs(out):
-    rng = np.random.default_rng(29)
-    n, k, m = 128, 1024, 64
+@pytest.mark.parametrize("m", [64, 130])  # (130: the 128-row tile, weights staged in LDS)
+def test_mmq_iq4_xs_half_outputs(out, m):
+    rng = np.random.default_rng(29 + m)
+    n, k = 128, 1024
     wq = iq4xs_weight(rng, n, k)
     x = acts(rng, m, k)
     want = O.matmul(O.IQ4XS, x, wq, n).astype(np.float64)
