@@ -28,7 +28,8 @@
 
 // 1: the expert-grouped matmul takes 32-row tiles when the average expert has at most 32 rows (0: the largest).
 // MI355X, 8 x Q4_K 14336x4096 / 4096x14336 experts, 64 tokens top-2 (16 rows per expert on average, more than 32
-// in the largest): MoE step 303 -> 227 us.
+// in the largest): MoE step 303 -> 227 us; a grouped 14336x4096 projection with 64 rows in one expert and 16 on
+// average: Q8_0 222 -> 185 us, Q4_0 166 -> 120 us.
 #ifndef QMM_MOE_SMALL_AVG
 #define QMM_MOE_SMALL_AVG 1
 #endif
