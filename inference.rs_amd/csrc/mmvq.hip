@@ -211,6 +211,86 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
   }
 }
 
+// Wide rows at one column (more than two units per lane): the two waves of a pair split each row's units, wave 2p
+// taking units [0, 128) and wave 2p + 1 units [128, 256), so each wave holds two units per lane (its activation units
+// in registers for the whole launch, and the next row's weights requested before this row's math) and more waves fit
+// on a CU.  A workgroup's two pairs take rows 2b and 2b + 1, then 2b + 2G and 2b + 2G + 1 (G workgroups), every wave
+// running the same number of iterations, so every wave reaches every barrier.  The second half's sum reaches the
+// first through one of two LDS slots (alternating, so a slot is rewritten only after the barrier that follows its
+// read) and is added to the first half's sum: a fixed order.
+template <class U, class Out, bool FULL>
+__global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
+                                                 typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
+                                                 int nunits) {
+  constexpr int S = 2;
+  __shared__ float part[2][2];  // [slot][pair]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pair = wave >> 1, half = wave & 1;
+  const int ubase = half * 64 * S;
+  auto has = [&](int s) { return FULL || ubase + lane + 64 * s < nunits; };
+  typename U::A areg[S];
+#pragma unroll
+  for (int s = 0; s < S; s++)
+    if (has(s)) U::load_a(act, ubase + lane + 64 * s, areg[s]);
+  const int step = gridDim.x * 2;
+  const int iters = (nrows + step - 1) / step;  // the same for every wave of the grid
+  int row = blockIdx.x * 2 + pair;
+  typename U::W w[S];
+  if (row < nrows) {
+#pragma unroll
+    for (int s = 0; s < S; s++)
+      if (has(s)) U::load_w(vx + (int64_t)row * row_bytes, ubase + lane + 64 * s, w[s]);
+  }
+  for (int it = 0; it < iters; it++, row += step) {
+    typename U::W wn[S];
+    if (row + step < nrows) {
+#pragma unroll
+      for (int s = 0; s < S; s++)
+        if (has(s)) U::load_w(vx + (int64_t)(row + step) * row_bytes, ubase + lane + 64 * s, wn[s]);
+    }
+    float acc = 0.0f;
+    if (row < nrows) {
+#pragma unroll
+      for (int s = 0; s < S; s++)
+        if (has(s)) acc += U::dot(w[s], areg[s], ubase + lane + 64 * s);
+    }
+    const float v =
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc)), 63));
+    if (half == 1 && lane == 0) part[it & 1][pair] = v;
+    __syncthreads();
+    if (half == 0 && row < nrows && lane == 0) Out::store(dst, row, v + part[it & 1][pair]);
+#pragma unroll
+    for (int s = 0; s < S; s++) w[s] = wn[s];
+  }
+}
+
+// Which types take k_mmvq_p2 for wide rows at one column.  On MI355X at 4096 x 14336, b = 1: Q4_K 10.7 -> 10.0 us,
+// IQ4_XS 10.65 -> 10.17, Q5_0 11.75 -> 11.22, Q4_0 9.8 -> 9.57, Q8_0 13.76 -> 13.54; slower for Q6_K (14.3 -> 14.9,
+// whose 84-byte units held twice over leave three waves per SIMD) and Q5_K (12.1 -> 12.5), which keep k_mmvq_p.
+template <class U>
+constexpr bool split_wide_rows() {
+  return U::kType != QMM_TYPE_Q6K && U::kType != QMM_TYPE_Q5K;
+}
+
+// Grid of k_mmvq_p2: row pairs spread evenly over as many rounds of the workgroups a CU holds as they need.
+template <class U, class Out>
+void launch_p2(const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows, hipStream_t s) {
+  const int64_t rb = U::row_bytes(k);
+  const int nu = U::units(k);
+  const int64_t pairs = qmm_ceil_div(nrows, 2);
+  auto grid = [&](int per_cu) {
+    const int64_t cap = (int64_t)(per_cu < 8 ? per_cu : 8) * qmm_device_cus();
+    const int64_t rounds = qmm_ceil_div(pairs, cap);
+    return dim3((unsigned)qmm_ceil_div(pairs, rounds));
+  };
+  if (nu == 256)
+    k_mmvq_p2<U, Out, true><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, true>>(256, 0)), 256, 0, s>>>(
+        vx, act, dst, nrows, rb, nu);
+  else
+    k_mmvq_p2<U, Out, false><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, false>>(256, 0)), 256, 0, s>>>(
+        vx, act, dst, nrows, rb, nu);
+}
+
 // ------------------------------------------------------------------------------------------------ fused quantization
 
 // The persistent matvec against NC f32 activation rows that it quantizes itself.  Every workgroup quantizes the rows
@@ -404,8 +484,9 @@ void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, typename Out
   };
   const int64_t rb = U::row_bytes(k);
   const int nu = U::units(k);
-  const bool full = nu % 64 == 0;
-#define QMM_P_F(NC, SS, FF)                                                                                      \
+  // three units per lane run the four-unit kernel, so only 64, 128 or 256 units leave no lane idle (192 does not)
+  const bool full = nu == 64 * (S <= 2 ? S : 4);
+#define QMM_P_F(NC, SS, FF)                                                                                    \
   k_mmvq_p<U, Out, NC, SS, FF><<<grid(qmm_resident_per_cu<k_mmvq_p<U, Out, NC, SS, FF>>(256, 0)), 256, 0, s>>>( \
       vx, act, dst, nrows, rb, nu, act_row_bytes, stride_col_dst)
 #define QMM_P(NC, SS)         \
@@ -447,8 +528,11 @@ void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int
   if (S <= QMM_PERSISTENT_MAX_S) {
     for (int j0 = 0; j0 < b; j0 += 8) {
       const int nc = b - j0 < 8 ? b - j0 : 8;
-      launch_p<U, Out>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
-                       act_row_bytes, stride_col_dst, s);
+      if (nc == 1 && S > 2 && split_wide_rows<U>())
+        launch_p2<U, Out>(vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows, s);
+      else
+        launch_p<U, Out>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
+                         act_row_bytes, stride_col_dst, s);
     }
     return;
   }

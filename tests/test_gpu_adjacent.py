@@ -180,3 +180,39 @@ def test_adjacent_indexed_moe(gtype, xdim1):
     got = qmm.indexed_moe(gtype, to_dev(w), to_dev(x), to_dev(ids), n).cpu().numpy()
     want = O.indexed_moe(gtype, w, E, n, k, x, ids)
     assert_parity(got, want, what=f"indexed type {gtype} xdim1={xdim1}")
+
+
+# Rows of more than two 64-value units per lane at one column: the types whose wide rows are split over two waves
+# (Q4_K, Q8_0, Q4_0, Q5_0, IQ4_XS) and the two that keep one wave per row (Q6_K, Q5_K); odd and single-row counts
+# (a pair with no row), 224 units (a partly idle second half), 256 (every lane full), 192 (three units per lane), and
+# the ninth column of b = 9 (a one-column pass after a full one); 192 units at b = 2 run the four-unit persistent kernel
+# with its last unit idle on every lane.
+WIDE_SHAPES = [(37, 14336, 1), (1, 14336, 1), (64, 16384, 1), (33, 12288, 1), (3, 14336, 9), (29, 12288, 2)]
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q8_0, O.Q4_0, O.Q5_0, O.IQ4XS, O.Q6K, O.Q5K])
+@pytest.mark.parametrize("shape", range(len(WIDE_SHAPES)))
+def test_wide_rows_at_one_column(gtype, shape):
+    n, k, b = WIDE_SHAPES[shape]
+    rng = np.random.default_rng(500 + 10 * gtype + shape)
+    wq = weight_bytes(gtype, n, k, rng)
+    x = acts(rng, b, k)
+    x[:, ::64] *= 30.0
+    got, want, aq = run_matvec(gtype, wq, x, n)
+    assert_parity(got, want, terms(gtype, aq, wq, b, n, k), what=f"type {gtype} n={n} k={k} b={b}")
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q4_0])
+@pytest.mark.parametrize("out", ["f16", "bf16"])
+def test_wide_rows_half_outputs(gtype, out):
+    rng = np.random.default_rng(900 + gtype)
+    n, k = 37, 14336
+    wq = weight_bytes(gtype, n, k, rng, random_bytes=True)
+    x = acts(rng, 1, k)
+    odt = {"f16": torch.float16, "bf16": torch.bfloat16}[out]
+    got, want, _ = run_matvec(gtype, wq, x, n, out_dtype=odt)
+    # the f32 result rounded once to the output type: the north-star bound plus half an ulp of each value
+    ulp = 2.0 ** -8 if out == "bf16" else 2.0 ** -11
+    want = np.asarray(want, np.float64)
+    err = np.abs(np.asarray(got, np.float64) - want)
+    assert np.all(err <= 1e-3 * np.abs(want).max() + ulp * np.abs(want)), f"type {gtype} {out}"
