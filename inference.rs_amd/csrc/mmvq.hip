@@ -218,20 +218,22 @@ __global__ __launch_bounds__(256) void k_mmvq_p(const uint8_t *__restrict__ vx, 
 // running the same number of iterations, so every wave reaches every barrier.  The second half's sum reaches the
 // first through one of two LDS slots (alternating, so a slot is rewritten only after the barrier that follows its
 // read) and is added to the first half's sum: a fixed order.
-template <class U, class Out, bool FULL>
+template <class U, class Out, int NC, bool FULL>
 __global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
                                                  typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
-                                                 int nunits) {
+                                                 int nunits, int64_t act_row_bytes, int stride_col_dst) {
   constexpr int S = 2;
-  __shared__ float part[2][2];  // [slot][pair]
+  __shared__ float part[2][2][NC];  // [slot][pair][column]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pair = wave >> 1, half = wave & 1;
   const int ubase = half * 64 * S;
   auto has = [&](int s) { return FULL || ubase + lane + 64 * s < nunits; };
-  typename U::A areg[S];
+  typename U::A areg[S * NC];
 #pragma unroll
   for (int s = 0; s < S; s++)
-    if (has(s)) U::load_a(act, ubase + lane + 64 * s, areg[s]);
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+      if (has(s)) U::load_a(act + j * act_row_bytes, ubase + lane + 64 * s, areg[s * NC + j]);
   const int step = gridDim.x * 2;
   const int iters = (nrows + step - 1) / step;  // the same for every wave of the grid
   int row = blockIdx.x * 2 + pair;
@@ -248,17 +250,30 @@ __global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx,
       for (int s = 0; s < S; s++)
         if (has(s)) U::load_w(vx + (int64_t)(row + step) * row_bytes, ubase + lane + 64 * s, wn[s]);
     }
-    float acc = 0.0f;
+    float acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) acc[j] = 0.0f;
     if (row < nrows) {
 #pragma unroll
       for (int s = 0; s < S; s++)
-        if (has(s)) acc += U::dot(w[s], areg[s], ubase + lane + 64 * s);
+#pragma unroll
+        for (int j = 0; j < NC; j++)
+          if (has(s)) acc[j] += U::dot(w[s], areg[s * NC + j], ubase + lane + 64 * s);
     }
-    const float v =
-        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc)), 63));
-    if (half == 1 && lane == 0) part[it & 1][pair] = v;
+    float v[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+      v[j] = __builtin_bit_cast(float,
+                                __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc[j])), 63));
+    if (half == 1 && lane == 0) {
+#pragma unroll
+      for (int j = 0; j < NC; j++) part[it & 1][pair][j] = v[j];
+    }
     __syncthreads();
-    if (half == 0 && row < nrows && lane == 0) Out::store(dst, row, v + part[it & 1][pair]);
+    if (half == 0 && row < nrows && lane == 0) {
+#pragma unroll
+      for (int j = 0; j < NC; j++) Out::store(dst, (int64_t)j * stride_col_dst + row, v[j] + part[it & 1][pair][j]);
+    }
 #pragma unroll
     for (int s = 0; s < S; s++) w[s] = wn[s];
   }
@@ -267,14 +282,18 @@ __global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx,
 // Which types take k_mmvq_p2 for wide rows at one column.  On MI355X at 4096 x 14336, b = 1: Q4_K 10.7 -> 10.0 us,
 // IQ4_XS 10.65 -> 10.17, Q5_0 11.75 -> 11.22, Q4_0 9.8 -> 9.57, Q8_0 13.76 -> 13.54; slower for Q6_K (14.3 -> 14.9,
 // whose 84-byte units held twice over leave three waves per SIMD) and Q5_K (12.1 -> 12.5), which keep k_mmvq_p.
+// At two columns (b = 2): Q4_K 14.9 -> 13.5 us, Q4_0 14.1 -> 12.5, Q8_0 18.3 -> 16.0; IQ4_XS (14.1 -> 16.1) and Q5_0
+// (15.5 -> 16.0) keep k_mmvq_p there.
 template <class U>
-constexpr bool split_wide_rows() {
-  return U::kType != QMM_TYPE_Q6K && U::kType != QMM_TYPE_Q5K;
+constexpr bool split_wide_rows(int nc) {
+  if (nc == 1) return U::kType != QMM_TYPE_Q6K && U::kType != QMM_TYPE_Q5K;
+  return nc == 2 && (U::kType == QMM_TYPE_Q4K || U::kType == QMM_TYPE_Q4_0 || U::kType == QMM_TYPE_Q8_0);
 }
 
 // Grid of k_mmvq_p2: row pairs spread evenly over as many rounds of the workgroups a CU holds as they need.
 template <class U, class Out>
-void launch_p2(const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows, hipStream_t s) {
+void launch_p2(int nc, const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows,
+               int64_t act_row_bytes, int stride_col_dst, hipStream_t s) {
   const int64_t rb = U::row_bytes(k);
   const int nu = U::units(k);
   const int64_t pairs = qmm_ceil_div(nrows, 2);
@@ -283,12 +302,21 @@ void launch_p2(const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int 
     const int64_t rounds = qmm_ceil_div(pairs, cap);
     return dim3((unsigned)qmm_ceil_div(pairs, rounds));
   };
-  if (nu == 256)
-    k_mmvq_p2<U, Out, true><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, true>>(256, 0)), 256, 0, s>>>(
-        vx, act, dst, nrows, rb, nu);
-  else
-    k_mmvq_p2<U, Out, false><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, false>>(256, 0)), 256, 0, s>>>(
-        vx, act, dst, nrows, rb, nu);
+#define QMM_P2_F(NC, FF)                                                                                  \
+  k_mmvq_p2<U, Out, NC, FF><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, NC, FF>>(256, 0)), 256, 0, s>>>( \
+      vx, act, dst, nrows, rb, nu, act_row_bytes, stride_col_dst)
+  if (nc == 1) {
+    if (nu == 256)
+      QMM_P2_F(1, true);
+    else
+      QMM_P2_F(1, false);
+  } else {
+    if (nu == 256)
+      QMM_P2_F(2, true);
+    else
+      QMM_P2_F(2, false);
+  }
+#undef QMM_P2_F
 }
 
 // ------------------------------------------------------------------------------------------------ fused quantization
@@ -528,8 +556,9 @@ void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int
   if (S <= QMM_PERSISTENT_MAX_S) {
     for (int j0 = 0; j0 < b; j0 += 8) {
       const int nc = b - j0 < 8 ? b - j0 : 8;
-      if (nc == 1 && S > 2 && split_wide_rows<U>())
-        launch_p2<U, Out>(vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows, s);
+      if (S > 2 && split_wide_rows<U>(nc))
+        launch_p2<U, Out>(nc, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
+                          act_row_bytes, stride_col_dst, s);
       else
         launch_p<U, Out>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
                          act_row_bytes, stride_col_dst, s);

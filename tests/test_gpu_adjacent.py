@@ -182,12 +182,13 @@ def test_adjacent_indexed_moe(gtype, xdim1):
     assert_parity(got, want, what=f"indexed type {gtype} xdim1={xdim1}")
 
 
-# Rows of more than two 64-value units per lane at one column: the types whose wide rows are split over two waves
+# Rows of more than two 64-value units per lane at one or two columns: the types whose wide rows are split over two waves
 # (Q4_K, Q8_0, Q4_0, Q5_0, IQ4_XS) and the two that keep one wave per row (Q6_K, Q5_K); odd and single-row counts
 # (a pair with no row), 224 units (a partly idle second half), 256 (every lane full), 192 (three units per lane), and
-# the ninth column of b = 9 (a one-column pass after a full one); 192 units at b = 2 run the four-unit persistent kernel
-# with its last unit idle on every lane.
-WIDE_SHAPES = [(37, 14336, 1), (1, 14336, 1), (64, 16384, 1), (33, 12288, 1), (3, 14336, 9), (29, 12288, 2)]
+# the ninth column of b = 9 (a one-column pass after a full one); the same at two columns (b = 2, and the last two
+# of b = 10).
+WIDE_SHAPES = [(37, 14336, 1), (1, 14336, 1), (64, 16384, 1), (33, 12288, 1), (3, 14336, 9), (29, 12288, 2),
+               (37, 14336, 2), (64, 16384, 2), (5, 14336, 10)]
 
 
 @pytest.mark.parametrize("gtype", [O.Q4K, O.Q8_0, O.Q4_0, O.Q5_0, O.IQ4XS, O.Q6K, O.Q5K])
