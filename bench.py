@@ -3,9 +3,9 @@
 HBM peak); prefill int8 TOPS at M=512").
 
 One step = one pass of the hot path over one batch of synthetic input, with every input resident in HBM:
-  headline: activation f32 [1, 4096] -> Q8_K -> Q4_K 14336x4096 matvec -> f32 [1, 14336]
+  headline: activation f32 [1, 4096] -> Q8_K values -> Q4_K 14336x4096 matvec -> f32 [1, 14336]
   in one launch, launch_mmvq_gguf_q4_k_f32_quantize_plain, whose output is bit-identical to the reference's two
-  launches (launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain, fast_mmvq::plain); the two-launch
+  launches (launch_mmvq_gguf_quantize_q8_1_f32 + launch_mmvq_gguf_q4_k_f32_plain, fast_mmvq::plain); the two-launch
   step and its matvec alone are reported in "extra".  Weights rotate over 16 copies (528 MB > the 256 MB
   Infinity Cache), so every step streams its weight from HBM.  K steps are captured in one HIP graph and
   replayed once between a synchronize on both sides; `value` = algorithmic bytes per step / time per step.
@@ -308,7 +308,7 @@ def moe_workload(torch, qmm, steps, warmup, seed, tokens=64, force_grouped=False
         if rc != 0:
             raise RuntimeError(H.qmm_host_last_error().decode())
 
-    st = max(4, steps // 10)
+    st = max(20, steps // 10)
     t = graph_time(torch, step, st, 2)
     per = t / st
     # weight bytes the step must read: every expert at 64 tokens; at decode sizes only the experts routed to
@@ -328,7 +328,7 @@ def read_floor_workload(torch, qmm, steps, warmup, seed):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     out = torch.empty(16 * cus * 256, dtype=torch.int32, device="cuda")
     res = {"bytes": nbytes, "copies": 16}
-    L = qmm.lib()
+    L = qmm.bench_lib()
 
     def run(pattern, per_cu, depth):
         def fn(i):
@@ -357,6 +357,80 @@ def read_floor_workload(torch, qmm, steps, warmup, seed):
     res["floor_gb_s"] = nbytes / best[0] / 1e9
     res["floor_form"] = best[1]
     res["matvec_rows_gb_s"] = nbytes / rows / 1e9
+    return res
+
+
+def peaks_workload(torch, qmm, steps, warmup, seed):
+    """What this box measures against the published peaks (8.0 TB/s HBM, 5.0 POP/s dense int8), with the probes of
+    libqmmbench.so:
+      copy        one grid-stride 16-byte copy of 1 GB (bytes read + written per second), best of a small sweep of
+                  workgroups per CU and loads in flight;
+      read_sizes  one launch streaming 33, 66, 132, 264 and 528 MB (the grid-stride read at its best shape), each
+                  rotated over copies totalling more than 256 MB (the Infinity Cache); a least-squares line
+                  t = t0 + bytes / B gives the fixed cost of a launch (t0) and the asymptotic read rate (B);
+      int8_mfma   every wave of 2 workgroups per CU issuing four independent v_mfma_i32_32x32x32_i8 chains."""
+    B = qmm.bench_lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(16 * cus * 256, dtype=torch.int32, device="cuda")
+    res = {}
+
+    def timed(fn, st, wu):
+        return graph_time(torch, fn, st, wu) / st
+
+    # copy: 1 GB, two buffer pairs alternated
+    nb = 1 << 30
+    bufs = [torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(4)]
+    best = None
+    for per_cu in (2, 4, 8):
+        for depth in (1, 2, 4):
+            def fn(i, per_cu=per_cu, depth=depth):
+                src, dst = (bufs[0], bufs[1]) if i % 2 == 0 else (bufs[2], bufs[3])
+                if B.qmm_bench_copy(qmm._ptr(src), qmm._ptr(dst), nb, per_cu, depth, qmm._stream()) != 0:
+                    raise RuntimeError(qmm.last_error())
+            t = timed(fn, 20, 4)
+            if best is None or t < best[0]:
+                best = (t, per_cu, depth)
+    res["copy"] = {"bytes_read_plus_written": 2 * nb, "us": best[0] * 1e6, "gb_s": 2 * nb / best[0] / 1e9,
+                   "form": f"wg{best[1]} d{best[2]}"}
+    del bufs
+
+    # one-launch reads at five sizes (grid-stride read, best of 2 / 4 / 8 workgroups per CU at 4 loads in flight)
+    pts = []
+    for mb in (33, 66, 132, 264, 528):
+        nbytes = mb * 1000 * 1000 // 16 * 16
+        ncop = max(2, -(-300 * 1000 * 1000 // nbytes))
+        cps = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(ncop)]
+        tb = None
+        for per_cu in (2, 4, 8):
+            def fn(i, per_cu=per_cu):
+                if B.qmm_hbm_read_probe(qmm._ptr(cps[i % ncop]), nbytes, 0, per_cu, 4, qmm._ptr(out),
+                                        qmm._stream()) != 0:
+                    raise RuntimeError(qmm.last_error())
+            st = max(8, min(steps // 4, int(2e10 // nbytes)))
+            t = timed(fn, st, max(2, st // 10))
+            tb = t if tb is None else min(tb, t)
+        pts.append((nbytes, tb))
+        res[f"read_{mb}mb"] = {"bytes": nbytes, "copies": ncop, "us": tb * 1e6, "gb_s": nbytes / tb / 1e9}
+        del cps
+    xs = np.array([p[0] for p in pts], dtype=np.float64)
+    ts = np.array([p[1] for p in pts], dtype=np.float64)
+    slope, t0 = np.polyfit(xs, ts, 1)
+    res["read_fit"] = {"launch_us": t0 * 1e6, "asymptotic_gb_s": 1.0 / slope / 1e9,
+                       "note": "least-squares t = launch_us + bytes / asymptotic rate over the five one-launch reads"}
+
+    # dense int8 MFMA
+    iters = 4096
+    ops = [0.0]
+
+    def mf(i):
+        ops[0] = B.qmm_bench_mfma_i8(2, iters, qmm._ptr(out), qmm._stream())
+        if ops[0] <= 0:
+            raise RuntimeError(qmm.last_error())
+    t = timed(mf, 10, 2)
+    res["int8_mfma"] = {"ops_per_launch": ops[0], "us": t * 1e6, "tops": ops[0] / t / 1e12,
+                        "form": "2 workgroups x 4 waves per CU, 4 independent v_mfma_i32_32x32x32_i8 chains per wave"}
+    res["summary"] = {"hbm_copy_gb_s": res["copy"]["gb_s"], "hbm_read_asymptotic_gb_s": res["read_fit"]["asymptotic_gb_s"],
+                      "read_launch_us": res["read_fit"]["launch_us"], "int8_mfma_tops": res["int8_mfma"]["tops"]}
     return res
 
 
@@ -433,7 +507,7 @@ def cpu_baseline(wq, n, k, seconds=10.0):
 EXTRA_NAMES = {"q4_k_decode_b4", "q4_k_decode_b16", "q8_0_decode_4096", "q4_k_prefill_m512", "q6_k_prefill_m512",
                "llama3_8b_linear_stack", "moe_8x_q4_k_64tok_top2", "q4_0_decode", "q5_0_decode", "q5_k_decode",
                "iq4_xs_decode", "q6_k_decode", "moe_8x_q4_k_4tok_top2", "q4_0_prefill_m512", "q8_0_prefill_m512",
-               "q5_0_prefill_m512", "q5_k_prefill_m512", "iq4_xs_prefill_m512", "read_floor"}
+               "q5_0_prefill_m512", "q5_k_prefill_m512", "iq4_xs_prefill_m512", "read_floor", "peaks"}
 
 
 def decode_summary(r):
@@ -519,6 +593,7 @@ def main():
         "iq4_xs_decode": lambda: decode_summary(decode_workload(torch, qmm, IQ4XS, n, k, 1, 16, args.steps // 2,
                                                                 args.warmup // 2, SEED + 44)),
         "read_floor": lambda: read_floor_workload(torch, qmm, args.steps // 4, args.warmup // 4, SEED),
+        "peaks": lambda: peaks_workload(torch, qmm, args.steps, args.warmup, SEED),
     }
     assert set(extra_runs) == EXTRA_NAMES
     if args.only:
@@ -534,7 +609,7 @@ def main():
 
     extra = {"q4_k_decode_b1_two_launch": {
         "ms_per_step": head["ms_per_step"], "gb_s": head["gb_s"],
-        "step": "launch_mmvq_gguf_quantize_q8k_f32 + launch_mmvq_gguf_q4_k_f32_plain",
+        "step": "launch_mmvq_gguf_quantize_q8_1_f32 + launch_mmvq_gguf_q4_k_f32_plain",
         "matvec": {"kernel": "k_mmvq_p<unit_q4k, out_f32, 1, 1, true>", "kernel_us": head["kernel_us"],
                    "gb_s": head["kernel_gb_s"], "algorithmic_bytes": head["kernel_bytes"],
                    "frac_hbm_peak": head["kernel_gb_s"] / HBM_PEAK_GBS}}}
@@ -571,7 +646,8 @@ def main():
         "data": "synthetic: weights N(0,0.02) quantized by the library's QTensor quantizer, activations N(0,1), "
                 f"seed {SEED}; 16 weight copies rotated (528 MB)",
         "config": {"workload": "q4_k_decode_14336x4096_b1", "weight": "Q4_K 14336x4096", "batch": 1,
-                   "activation": "f32 [1,4096] -> Q8_K", "frac_hbm_peak": round(one["gb_s"] / HBM_PEAK_GBS, 4),
+                   "activation": "f32 [1,4096] -> Q8_K values (in the reference's Q8_1 scratch layout)",
+                   "frac_hbm_peak": round(one["gb_s"] / HBM_PEAK_GBS, 4),
                    "step": "launch_mmvq_gguf_q4_k_f32_quantize_plain (quantize + matvec in one launch, the same "
                            "bits as the reference's two launches), HIP graph of K steps"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -583,6 +659,10 @@ def main():
     }
     if "q4_k_prefill_m512" in extra:
         line["prefill_int8_tops_m512"] = round(extra["q4_k_prefill_m512"]["kernel_tops"], 1)
+    if "peaks" in extra:
+        pk = extra["peaks"]["summary"]
+        line["measured_peaks"] = pk
+        line["roofline"]["frac_of_measured_read"] = round(achieved / pk["hbm_read_asymptotic_gb_s"], 4)
     print(json.dumps(line), flush=True)
 
 

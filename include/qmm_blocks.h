@@ -66,6 +66,17 @@ typedef struct {
   int16_t bsums[16];
 } qmm_block_q8k;
 
+/* The activation block of the reference-named decode entries, in the reference's Q8_1 scratch of 36 bytes per 32
+ * values (crates/inference-quant/src/gguf/fast_mmvq.rs:17-18): BlockQ8K's d and qs as BlockQ8K::from_float writes
+ * them, the int16 sums of each 32 qs, and 12 zero bytes; 288 bytes per 256 values.  No counterpart in the reference
+ * (whose GPU quantizer writes Q8_1 blocks of 32). */
+typedef struct {
+  float d;
+  int8_t qs[256];
+  int16_t s32[8];
+  uint8_t pad[12];
+} qmm_block_q8ks;
+
 /* BlockQ4_0: f16 d, 16 bytes of nibbles; value j = low nibble of qs[j] - 8, value j + 16 = its high nibble - 8;
  * 18 bytes (k_quants.rs:116-120, 313-330) */
 typedef struct {
@@ -110,6 +121,7 @@ static_assert(sizeof(qmm_block_q8_0) == 34, "BlockQ8_0 is 34 bytes");
 static_assert(sizeof(qmm_block_q4k) == 144, "BlockQ4K is 144 bytes");
 static_assert(sizeof(qmm_block_q6k) == 210, "BlockQ6K is 210 bytes");
 static_assert(sizeof(qmm_block_q8k) == 292, "BlockQ8K is 292 bytes");
+static_assert(sizeof(qmm_block_q8ks) == 288, "the Q8_1-slot block is 288 bytes");
 #else
 _Static_assert(sizeof(qmm_block_q4_0) == 18, "BlockQ4_0 is 18 bytes");
 _Static_assert(sizeof(qmm_block_q5_0) == 22, "BlockQ5_0 is 22 bytes");
@@ -119,6 +131,7 @@ _Static_assert(sizeof(qmm_block_q8_0) == 34, "BlockQ8_0 is 34 bytes");
 _Static_assert(sizeof(qmm_block_q4k) == 144, "BlockQ4K is 144 bytes");
 _Static_assert(sizeof(qmm_block_q6k) == 210, "BlockQ6K is 210 bytes");
 _Static_assert(sizeof(qmm_block_q8k) == 292, "BlockQ8K is 292 bytes");
+_Static_assert(sizeof(qmm_block_q8ks) == 288, "the Q8_1-slot block is 288 bytes");
 #endif
 
 /* bytes per block and values per block (GgmlDType::type_size / block_size, quantized/mod.rs:669-703) */
@@ -157,5 +170,13 @@ static inline size_t qmm_block_size(int t) {
 /* the activation block type a weight type is dotted with (GgmlType::VecDotType): Q8_0 for the 32-value types,
  * Q8_K for the super-block types (IQ4_XS: cpu_dot.rs:67-68) */
 static inline int qmm_vec_dot_type(int t) { return qmm_block_size(t) == 32 ? QMM_TYPE_Q8_0 : QMM_TYPE_Q8K; }
+
+/* The decode / prefill boundary of QMatMul::forward, shared by the host layer and qmm_qmatmul_forward_noalloc: up to
+ * this many activation rows take the decode launchers (fast_mmvq.rs TENSOR_CORE_MAX_ROWS = 16, re-derived for gfx950:
+ * Q4_K, and Q6_K rows of at most 8192 values, stay on the decode launcher up to 32 rows, where its few-row MFMA
+ * kernel still beats the prefill matmul), more the prefill matmul. */
+static inline int64_t qmm_max_decode_rows(int type, int64_t k) {
+  return type == QMM_TYPE_Q4K || (type == QMM_TYPE_Q6K && k <= 8192) ? 32 : 16;
+}
 
 #endif

@@ -1,14 +1,17 @@
+// Measurement probes for bench.py, built into lib/libqmmbench.so (not into the product library): no counterpart in
+// the reference; they compute nothing but what keeps the compiler from dropping their loads or matrix operations.
+//
 // HBM read probes: the time one launch needs to stream a buffer of the decode weight's size, the floor the decode
-// matvec is measured against.  No counterpart in the reference; they compute nothing but a per-lane XOR of what they
-// read (written out so the loads cannot be dropped).
+// matvec is measured against (a per-lane XOR of what is read is written out).
 //   pattern 0  grid stride: wave slot s of the persistent grid reads 16-byte chunks s * 64 + lane, s + S, ... with
 //              `depth` loads in flight per lane
 //   pattern 1  the decode matvec's walk over Q4_K rows (k_mmvq_p): row r of wave slot s = r mod S, each lane loading
 //              the 16-byte header and two 16-byte nibble chunks of its quarter superblock, `depth` rows in flight
 //   pattern 2  the same rows read as contiguous 16-byte chunks per lane (1 KB per wave instruction)
 //   pattern 3  pattern 2 plus each lane's 16-byte superblock header
+// Copy probe: a grid-stride 16-byte copy, the measured HBM copy rate (bytes read + bytes written per second).
+// MFMA probe: the measured dense int8 matrix rate, every wave issuing independent v_mfma_i32_32x32x32_i8 chains.
 #include "common.h"
-#include "inferencequant.h"
 #include "units.h"
 
 namespace {
@@ -72,6 +75,39 @@ __global__ __launch_bounds__(256) void k_read_rows(const uint8_t *__restrict__ w
   out[(int64_t)blockIdx.x * 256 + threadIdx.x] = x;
 }
 
+// grid-stride copy of `chunks` 16-byte chunks, D chunks in flight per lane
+template <int D>
+__global__ __launch_bounds__(256) void k_copy(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, int64_t chunks) {
+  const int64_t S = (int64_t)gridDim.x * 256;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += S * D) {
+    u32x4 v[D];
+#pragma unroll
+    for (int i = 0; i < D; i++)
+      if (c + i * S < chunks) v[i] = src[c + i * S];
+#pragma unroll
+    for (int i = 0; i < D; i++)
+      if (c + i * S < chunks) dst[c + i * S] = v[i];
+  }
+}
+
+// Four independent accumulator chains per wave hide the MFMA's dependency latency; operands differ per lane and
+// iteration count comes from the host, so nothing folds.  2 * 32 * 32 * 32 int8 ops per instruction.
+__global__ __launch_bounds__(256) void k_mfma_i8(int iters, int seed, int *__restrict__ out) {
+  const int t = threadIdx.x + seed;
+  const v4i a = {t, t * 3, t * 5, t * 7}, b = {t ^ 0x5a5a5a5a, t + 11, t * 13, ~t};
+  v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int i = 0; i < iters; i++) {
+    c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, b, c3, 0, 0, 0);
+  }
+  int x = 0;
+#pragma unroll
+  for (int r = 0; r < 16; r++) x ^= c0[r] + c1[r] + c2[r] + c3[r];
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = x;
+}
+
 }  // namespace
 
 extern "C" int qmm_hbm_read_probe(const void *src, int64_t bytes, int pattern, int per_cu, int depth, uint32_t *out,
@@ -106,4 +142,35 @@ extern "C" int qmm_hbm_read_probe(const void *src, int64_t bytes, int pattern, i
 #undef QMM_RR
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// One grid-stride copy of `bytes` (a multiple of 16; both pointers 16-byte aligned) from src to dst with per_cu
+// workgroups of 256 threads per CU and `depth` (1, 2 or 4) chunks in flight per lane.  Returns 0, or -1 with
+// qmm_last_error() set.
+extern "C" int qmm_bench_copy(const void *src, void *dst, int64_t bytes, int per_cu, int depth, void *stream) {
+  if (!src || !dst || bytes <= 0 || bytes % 16 != 0 || per_cu < 1 || per_cu > 16 || (uintptr_t)src % 16 != 0 ||
+      (uintptr_t)dst % 16 != 0) {
+    qmm_set_error("bench_copy: src %p dst %p bytes %lld per_cu %d", src, dst, (long long)bytes, per_cu);
+    return -1;
+  }
+  const unsigned grid = (unsigned)(per_cu * qmm_device_cus());
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t chunks = bytes / 16;
+  if (depth <= 1) k_copy<1><<<grid, 256, 0, s>>>((const u32x4 *)src, (u32x4 *)dst, chunks);
+  else if (depth == 2) k_copy<2><<<grid, 256, 0, s>>>((const u32x4 *)src, (u32x4 *)dst, chunks);
+  else k_copy<4><<<grid, 256, 0, s>>>((const u32x4 *)src, (u32x4 *)dst, chunks);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// per_cu workgroups of 4 waves per CU, each wave issuing 4 * iters v_mfma_i32_32x32x32_i8 (65,536 int8 ops each);
+// out holds per_cu * CUs * 256 ints.  Returns the int8 ops launched (> 0), or -1 with qmm_last_error() set.
+extern "C" double qmm_bench_mfma_i8(int per_cu, int iters, int *out, void *stream) {
+  if (!out || per_cu < 1 || per_cu > 8 || iters < 1) {
+    qmm_set_error("bench_mfma_i8: per_cu %d iters %d", per_cu, iters);
+    return -1.0;
+  }
+  const unsigned grid = (unsigned)(per_cu * qmm_device_cus());
+  k_mfma_i8<<<grid, 256, 0, (hipStream_t)stream>>>(iters, per_cu, out);
+  if (hipGetLastError() != hipSuccess) return -1.0;
+  return (double)grid * 4 * 4 * (double)iters * 65536.0;
 }

@@ -338,6 +338,31 @@ void q8_0_exact(const void *vx, const void *vy, void *dst, int ncols_x, int nrow
   }
 }
 
+
+// ------------------------------------------------------------------------------------------------ raw row gather
+
+// launch_gather_rows_u8: dst row r = src row ids[r] (rows of row_bytes bytes), zeros for an id past the last row.
+// Workgroup (x, y) copies chunk x of rows y, y + gridDim.y, ...: 16-byte pieces when every row is, else bytes.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gather_rows_u8(const uint8_t *__restrict__ src, const uint32_t *__restrict__ ids,
+                                                        uint8_t *__restrict__ dst, int64_t row_bytes, int64_t rows,
+                                                        int64_t n) {
+  constexpr int W = VEC ? 16 : 1;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * W;
+  if (i >= row_bytes) return;
+  for (int64_t r = blockIdx.y; r < n; r += gridDim.y) {
+    const int64_t id = ids[r];
+    uint8_t *o = dst + r * row_bytes + i;
+    if (VEC) {
+      u32x4 v = {0, 0, 0, 0};
+      if (id < rows) v = *(const u32x4 *)(src + id * row_bytes + i);
+      *(u32x4 *)o = v;
+    } else {
+      *o = id < rows ? src[id * row_bytes + i] : 0;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -389,3 +414,22 @@ void launch_mmvq_gguf_q8_0_bf16_exact(const void *vx, const void *vy, void *dst,
 }
 
 }  // extern "C"
+
+extern "C" void launch_gather_rows_u8(const void *src, const void *ids, void *dst, int64_t row_bytes, int64_t rows,
+                                      int64_t n, void *stream) {
+  if (!src || !ids || !dst || row_bytes <= 0 || rows < 0 || n < 0) {
+    qmm_set_error("gather_rows_u8: row_bytes=%lld rows=%lld n=%lld", (long long)row_bytes, (long long)rows,
+                  (long long)n);
+    return;
+  }
+  if (n == 0) return;
+  const bool vec = row_bytes % 16 == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0;
+  const int64_t per = vec ? 16 : 1;
+  const dim3 grid((unsigned)qmm_ceil_div(row_bytes, 256 * per), (unsigned)(n < 65535 ? n : 65535));
+  if (vec)
+    k_gather_rows_u8<true><<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t *)src, (const uint32_t *)ids,
+                                                                  (uint8_t *)dst, row_bytes, rows, n);
+  else
+    k_gather_rows_u8<false><<<grid, 256, 0, (hipStream_t)stream>>>((const uint8_t *)src, (const uint32_t *)ids,
+                                                                   (uint8_t *)dst, row_bytes, rows, n);
+}

@@ -7,7 +7,8 @@
 // dots exactly; the per-32 / per-16 integer scales of the K-quants are folded into the weight operand, which
 // then needs more than 8 bits, so it is split into two int8 planes:
 //   Q4_K  sc (6 bit) = 8 sh + sl:   sc*q4 = 8 (sh*q4) + (sl*q4), both planes <= 105
-//         min term  sum_j m_j * bsum32_j  through one f16 MFMA (bsums per 16 and 6-bit mins are exact in f16)
+//         min term  sum_j m_j * S_j  through one f16 MFMA (S_j, the activation sum of sub-block j, split as
+//         64 h + l so both parts are exact in f16; planes.h min_frag)
 //   Q6_K  w = sc * (q6 - 32) in [-4096, 4064] = 64 wh + wl, wl in [0, 63], wh in [-64, 63]
 //   Q8_0  one plane; the f32 scales apply per 32-value block (so this one is VALU-bound by design)
 // Each superblock's integer result is exact in int32; the f32 epilogue per superblock mirrors the
@@ -15,7 +16,7 @@
 //
 // Tiling: a 256-thread workgroup owns BN = 128 weight rows x 32 TM activation rows (TM = 1, 2 or 4); wave w takes
 // weight rows [32w, 32w+32) against all of them (TM MFMA tiles of 32x32).  Per 256-value K step the workgroup
-// moves the activation superblock (int8 qs, f32 d, f16 bsums) global -> registers -> one of three LDS slots, and
+// moves the activation superblock (int8 qs, f32 d, int16 sums of 32) global -> registers -> one of three LDS slots, and
 // each wave loads its weight rows straight from HBM into registers two superblocks ahead and builds the B
 // operands there.  A and B fragments use the same lane/byte -> k assignment, so the hardware's k order inside an
 // MFMA does not matter.  The Q8_0 kernel keeps a simpler single-buffered loop.
@@ -47,16 +48,17 @@ constexpr int TM = BM / 32;
 constexpr int QS_STRIDE = 272;  // LDS row stride of the activation tile: 256 + 16 (bank spread)
 
 struct ActTile {
-  // global views of one channel of the prefill activation layout (include/inferencequant.h)
+  // global views of one channel of a prefill activation layout (include/inferencequant.h)
   const uint8_t *qs;     // [nsb][rows][256]
-  const uint16_t *d8;    // [nsb][rows][8] f16      (Q8_0; Q8_K's d f32 [nsb][rows] and bsums f16 [nsb][rows][16]
-                         //                          follow qs and are addressed from qs)
+  const uint16_t *d8;    // Q8_0 blocks: [nsb][rows][8] f16
+  const float *d32;      // Q8_K tiles: [nsb][rows] f32 (the int16 sums of 32, [nsb][rows][8], follow and are
+                         //             addressed from qs)
   int64_t rows, nsb;
 };
 
 // ------------------------------------------------------------------------------------------ K-quant kernel
 
-// One superblock of the activation tile (BMt rows x 256 values: int8 qs, f16 bsums, f32 d) in registers on its
+// One superblock of the activation tile (BMt rows x 256 values: int8 qs, int16 sums of 32, f32 d) in registers on its
 // way from global memory to an LDS slot.  The prefill layout keeps a superblock's rows contiguous, so thread t
 // moves 16-byte chunks t, t + NT, ... of each section (NT threads); every address is a per-thread constant plus a
 // scalar.
@@ -65,10 +67,11 @@ struct ActStage {
   static_assert(BMt * 16 % NT == 0, "whole qs chunks per thread");
   static constexpr int NQ = BMt * 16 / NT;  // qs chunks per thread
   static constexpr int QS = BMt * 256;       // LDS bytes: qs, row r's chunk c at chunk slot c ^ (r % 16)
+  // the sums of row r at QS + 16 r (the second half of the area is the DMA form's overrun: ActDma)
   static constexpr int BSB = MIN ? BMt * 32 : 0;
   static constexpr int STAGE = QS + BSB + BMt * 4;
   u32x4 q[NQ];
-  u32x4 bs;  // MIN, threads < 2 BMt: 8 bsums
+  u32x4 bs;  // MIN, threads < BMt: one row's 8 sums
   u32x4 d;   // threads < BMt / 4: 4 scales
 
   // voff: per-thread byte offsets (qs, bsums, d) of row m0; s_*: offsets of superblock sb.  The whole offset
@@ -78,7 +81,7 @@ struct ActStage {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NQ; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[0] + s_qs + 16 * NT * i, 0, 0);
-    if (MIN && tid < 2 * BMt) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
+    if (MIN && tid < BMt) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
     if (tid < BMt / 4) d = __builtin_amdgcn_raw_buffer_load_b128(r, voff[2] + s_d, 0, 0);
   }
   __device__ __forceinline__ void store(uint8_t *slot) const {
@@ -86,7 +89,7 @@ struct ActStage {
     const int swz = (tid & 15) ^ ((tid >> 4) & 15);
 #pragma unroll
     for (int i = 0; i < NQ; i++) *(u32x4 *)(slot + 16 * NT * i + 256 * (tid >> 4) + 16 * swz) = q[i];
-    if (MIN && tid < 2 * BMt) *(u32x4 *)(slot + QS + 16 * tid) = bs;
+    if (MIN && tid < BMt) *(u32x4 *)(slot + QS + 16 * tid) = bs;
     if (tid < BMt / 4) *(u32x4 *)(slot + QS + BSB + 16 * tid) = d;
   }
 };
@@ -104,7 +107,9 @@ struct ActDma {
   static constexpr int BSB = MIN ? BMt * 32 : 0;
   static constexpr int STAGE = QS + BSB + BMt * 4;
   static constexpr int NQ = BMt / (4 * NW);            // 1 KB qs pieces per wave
-  static constexpr int NB = MIN ? BMt / (8 * NW) : 0;  // 256 B bsum pieces per wave
+  // 256 B pieces of sums per wave: twice the 16 BMt bytes of the tile's rows, so that every wave issues the same
+  // number of loads; the second half reads the rows after the tile into the second half of the area, unused
+  static constexpr int NB = MIN ? BMt / (8 * NW) : 0;
   static constexpr int ND = BMt / NW;                  // lanes of each wave that load one f32 scale
   static constexpr int kLoads = NQ + NB + 1;
   uint32_t oq[NQ], ob[NB > 0 ? NB : 1], od;
@@ -119,8 +124,8 @@ struct ActDma {
     }
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-      const int D = 64 * (NW * i + wave) + lane, r = D >> 3, k = D & 7;
-      ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * 32 + 4 * k);
+      const int D = 64 * (NW * i + wave) + lane, r = D >> 2, k = D & 3;
+      ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * 16 + 4 * k);
     }
     od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 4);
   }
@@ -134,7 +139,7 @@ struct ActDma {
 #pragma unroll
     for (int i = 0; i < NB; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (NW * i + wave)), 4, ob[i] + 32 * sb_rows, 0,
+          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (NW * i + wave)), 4, ob[i] + 16 * sb_rows, 0,
           0, 0);
     if (lane < ND)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -222,9 +227,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 
   // activations: one resource over the channel; the scalar part of each address moves with the superblock
   const int64_t rows = a.rows, nsb = a.nsb;
-  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 292);
+  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 276);
   const uint32_t voff[3] = {(uint32_t)(m0 * 256 + 16 * tid),
-                            (uint32_t)(nsb * rows * 260 + m0 * 32 + 16 * tid),
+                            (uint32_t)(nsb * rows * 260 + m0 * 16 + 16 * tid),
                             (uint32_t)(nsb * rows * 256 + m0 * 4 + 16 * tid)};
   // weights: one resource over the tile's rows, from the dword that holds the tile's first byte (wdelta bytes
   // before it), so offsets that are multiples of 4 from the resource are dword aligned in memory, to the end of the
@@ -291,7 +296,7 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
       WT::load(rw, wrow, (uint32_t)sb, g, rr);
       __builtin_amdgcn_sched_barrier(0);
     } else {
-      as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 32), (uint32_t)(sb * rows * 4));
+      as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 16), (uint32_t)(sb * rows * 4));
       WT::load(rw, wrow, (uint32_t)sb, g, rr);
     }
   };
@@ -336,9 +341,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       v16f fmin = (v16f){};
-      if (WT::kMin) {
-        const v8h abs_ = *(const v8h *)(slot + AS::QS + (32 * t + li) * 32 + 16 * g);
-        fmin = mfma_f16(abs_, p.bmin, fmin);
+      if (WT::kMin) {  // the sums of sub-blocks 4g .. 4g + 3 of row 32t + li
+        const u32x2 sm = *(const u32x2 *)(slot + AS::QS + (32 * t + li) * 16 + 8 * g);
+        fmin = mfma_f16(min_frag(sm.x, sm.y), p.bmin, fmin);
       }
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -529,7 +534,7 @@ struct wb_q5_0 {
   }
 };
 
-template <class WB, class Out>
+template <class WB, class Out, bool F32D>
 __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                               int64_t nblk_w, const ActTile &a, int64_t m0, int64_t mrows, int64_t n0,
                                               int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
@@ -574,7 +579,7 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
       const int i = it * 256 + tid;
       const int row = i >> 3, j = i & 7;
       const int64_t m = m0 + row;
-      s_da[row * 9 + j] = m < mrows ? f16_bits_to_f32(a.d8[(sb * a.rows + m) * 8 + j]) : 0.0f;
+      s_da[row * 9 + j] = m >= mrows ? 0.0f : F32D ? a.d32[sb * a.rows + m] : f16_bits_to_f32(a.d8[(sb * a.rows + m) * 8 + j]);
     }
     __syncthreads();
 #pragma unroll
@@ -679,14 +684,16 @@ struct RunLoad {
   }
 };
 
-// Activation superblock of the Q8_0 prefill layout (int8 qs, f16 d per 32 values) by DMA into an LDS slot: qs as
-// in ActDma (swizzled 256-byte rows), then the rows' 16-byte scale groups in row order.
-template <int BMt>
+// Activation superblock of a prefill layout by DMA into an LDS slot: qs as in ActDma (swizzled 256-byte rows), then
+// the scales.  Q8_0 blocks (F32D false): the rows' 16-byte groups of eight f16 (one per 32 values) in row order.
+// Q8_K tiles (F32D): one f32 per row and superblock; every wave loads 64 rows' (row 64 w + l at byte 4 (64 w + l) of
+// a 1 KB area), so every wave issues the same loads, and the rows past the tile land in the area's unused part.
+template <int BMt, bool F32D = false>
 struct ActDma8 {
   static constexpr int QS = BMt * 256;
-  static constexpr int STAGE = QS + BMt * 16;
+  static constexpr int STAGE = QS + (F32D ? 1024 : BMt * 16);
   static constexpr int NQ = BMt / 16;  // 1 KB qs pieces per wave
-  static constexpr int ND = BMt / 4;   // lanes of each wave that load one row's 16 bytes of scales
+  static constexpr int ND = BMt / 4;   // (Q8_0 blocks) lanes of each wave that load one row's 16 bytes of scales
   static constexpr int kLoads = NQ + 1;
   uint32_t oq[NQ], od;
 
@@ -696,7 +703,8 @@ struct ActDma8 {
       const int L = 64 * (4 * i + wave) + lane, r = L >> 4, c = (L & 15) ^ (r & 15);
       oq[i] = (uint32_t)((m0 + r) * 256 + 16 * c);
     }
-    od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 16);
+    od = F32D ? (uint32_t)(nsb * rows * 256 + (m0 + 64 * wave + lane) * 4)
+              : (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 16);
   }
   // (device pass only: the host pass rejects the gfx950 16-byte LDS load inside this template)
   __device__ __forceinline__ void issue(rsrc_t r, uint8_t *slot, int wave, int lane, uint32_t sb_rows) const {
@@ -705,7 +713,10 @@ struct ActDma8 {
     for (int i = 0; i < NQ; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + 1024 * (4 * i + wave)),
                                                16, oq[i] + 256 * sb_rows, 0, 0, 0);
-    if (lane < ND)
+    if (F32D)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * wave), 4,
+                                               od + 4 * sb_rows, 0, 0, 0);
+    else if (lane < ND)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           r, (__attribute__((address_space(3))) void *)(slot + QS + 16 * ND * wave), 16, od + 16 * sb_rows, 0, 0, 0);
 #endif
@@ -739,13 +750,13 @@ __device__ __forceinline__ void b32_group(v4i av, const v4i (&b)[8], const float
 // One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows, superblocks [sb0, sb1).
 // Three LDS slots and three weight register sets rotate as in mmq_kq_tile: the activations and weights of s + 2 are
 // in flight while s is computed.
-template <class WR, class Out, int TM>
+template <class WR, class Out, int TM, bool F32D>
 __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                              const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                              int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
                                              const int32_t *__restrict__ dst_rows, float *__restrict__ part) {
   constexpr int BMt = 32 * TM;
-  typedef ActDma8<BMt> AD;
+  typedef ActDma8<BMt, F32D> AD;
   typedef RunLoad<WR> RL;
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AD::STAGE];
 
@@ -755,7 +766,7 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
   const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;
 
   const int64_t rows = a.rows, nsb = a.nsb;
-  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 272);
+  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * (F32D ? 276 : 272));
   const rsrc_t rw = make_rsrc(W + n0 * w_row_bytes, (nlast + 1) * w_row_bytes);
   const uint32_t wrun = (uint32_t)(nl * w_row_bytes + 4 * WR::kBytes * g);
 
@@ -802,13 +813,18 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
   // ahead (the compiler would otherwise issue every group's MFMAs first and spill their results), and by then the
   // fragment has arrived.
   auto compute = [&](const uint8_t *slot) {
-    // this lane's activation rows 32t + li: scales of blocks 4g .. 4g + 3
+    // this lane's activation rows 32t + li: scales of blocks 4g .. 4g + 3 (Q8_K tiles: the row's one scale)
     float da[TM][4];
 #pragma unroll
     for (int t = 0; t < TM; t++) {
-      const uint2 d4 = *(const uint2 *)(slot + AD::QS + 16 * (32 * t + li) + 8 * g);
-      da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
-      da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
+      if constexpr (F32D) {
+        const float d = *(const float *)(slot + AD::QS + 4 * (32 * t + li));
+        da[t][0] = da[t][1] = da[t][2] = da[t][3] = d;
+      } else {
+        const uint2 d4 = *(const uint2 *)(slot + AD::QS + 16 * (32 * t + li) + 8 * g);
+        da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
+        da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
+      }
     }
     auto frag = [&](int k) { return *(const v4i *)(slot + 8192 * (k >> 3) + qoff[k & 7]); };
     v16i acc[2];
@@ -887,6 +903,7 @@ ActTile act_tile(const void *y, int64_t rows, int64_t nsb) {
   a.rows = rows;
   a.nsb = nsb;
   a.d8 = (const uint16_t *)((const uint8_t *)y + nsb * rows * 256);
+  a.d32 = (const float *)((const uint8_t *)y + nsb * rows * 256);
   return a;
 }
 
@@ -915,13 +932,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kq_wave
                                 part ? part + split * mrows * nrows_w : nullptr);
 }
 
-template <class WB, class Out>
+template <class WB, class Out, bool F32D>
 __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                                   int64_t nblk_w, ActTile a, int64_t mrows, int64_t nsb,
                                                   typename Out::T *__restrict__ dst, int64_t ldd) {
   int64_t mt, nt, split;
   tile_of((mrows + BM - 1) / BM, (nrows_w + BN - 1) / BN, 1, mt, nt, split);
-  mmq_q8_0_tile<WB, Out>(W, nrows_w, w_row_bytes, nblk_w, a, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
+  mmq_q8_0_tile<WB, Out, F32D>(W, nrows_w, w_row_bytes, nblk_w, a, mt * BM, mrows, nt * BN, nsb, dst, ldd, nullptr);
 }
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
@@ -946,7 +963,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
                                 part ? part + split * ncols_dst * nrows_w : nullptr, FUSED ? rsum : RouteSum{});
 }
 
-template <class WB>
+template <class WB, bool F32D>
 __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                       int64_t nrows_w, int64_t w_row_bytes, int64_t nblk_w, ActTile a,
                                                       const int32_t *__restrict__ bounds,
@@ -955,7 +972,7 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict_
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * BM, m1 = bounds[e + 1];
   if (m0 >= m1) return;
-  mmq_q8_0_tile<WB, out_f32>(W + e * expert_bytes, nrows_w, w_row_bytes, nblk_w, a, m0, m1, (int64_t)blockIdx.x * BN,
+  mmq_q8_0_tile<WB, out_f32, F32D>(W + e * expert_bytes, nrows_w, w_row_bytes, nblk_w, a, m0, m1, (int64_t)blockIdx.x * BN,
                              nsb, dst, ldd, ids_dst);
 }
 
@@ -963,7 +980,7 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0_moe(const uint8_t *__restrict_
 template <int TMv>
 constexpr int b32_waves() { return 2; }
 
-template <class WR, class Out, int TMv>
+template <class WR, class Out, int TMv, bool F32D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
     int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd, float *__restrict__ part) {
@@ -973,11 +990,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<T
   const int64_t per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_b32_tile<WR, Out, TMv>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
+  mmq_b32_tile<WR, Out, TMv, F32D>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BN, sb0, sb1, dst, ldd, nullptr,
                              part ? part + split * mrows * nrows_w : nullptr);
 }
 
-template <class WR, int TMv>
+template <class WR, int TMv, bool F32D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<TMv>()))) void k_mmq_b32_moe(
     const uint8_t *__restrict__ W, int64_t expert_bytes, int64_t nrows_w, int64_t w_row_bytes, ActTile a,
     const int32_t *__restrict__ bounds, const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
@@ -988,7 +1005,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(b32_waves<T
   const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_b32_tile<WR, out_f32, TMv>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
+  mmq_b32_tile<WR, out_f32, TMv, F32D>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                  (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
                                  part ? part + split * ncols_dst * nrows_w : nullptr);
 }
@@ -1067,7 +1084,7 @@ bool b32_runs(const void *x, int64_t ncols_x, int64_t w_row_bytes) {
   return ncols_x % 256 == 0 && w_row_bytes % 4 == 0 && (uintptr_t)x % 4 == 0;
 }
 
-template <class WR, class Out>
+template <class WR, class Out, bool F32D>
 void launch_b32(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y,
                 int64_t nsb, typename Out::T *d, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   const int64_t ntiles = (nrows_x + BN - 1) / BN;
@@ -1077,13 +1094,13 @@ void launch_b32(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Ac
   float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1)
-    k_mmq_b32<WR, Out, 1><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_b32<WR, Out, 1, F32D><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   else
-    k_mmq_b32<WR, Out, 2><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_b32<WR, Out, 2, F32D><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   if (part) split_sum<Out>(part, splits, ncols_y, nrows_x, d, ldd, nullptr, s);
 }
 
-template <class WR>
+template <class WR, bool F32D>
 void launch_b32_moe(const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a,
                     const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, float *d, int64_t ldd,
                     int64_t ncols_dst, int64_t ncols_max, int64_t num_experts, void *fixup, int nsm, hipStream_t s) {
@@ -1096,15 +1113,17 @@ void launch_b32_moe(const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int
   float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(ntiles * splits), (unsigned)((ncols_max + bm - 1) / bm), (unsigned)num_experts);
   if (tm == 1)
-    k_mmq_b32_moe<WR, 1><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+    k_mmq_b32_moe<WR, 1, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                splits, d, ldd, part, ncols_dst);
   else
-    k_mmq_b32_moe<WR, 2><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+    k_mmq_b32_moe<WR, 2, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
                                                splits, d, ldd, part, ncols_dst);
   if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, ldd, ids_dst, s);
 }
 
-template <class Out>
+// F32D: the Q8_K tile layout (every type; the reference-named entries); else Q8_0 blocks (the 32-value types' _q8_0
+// entries)
+template <class Out, bool F32D>
 void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_y,
                int64_t stride_row_x, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   const int64_t nsb = (ncols_x + 255) / 256;
@@ -1112,7 +1131,7 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
   const ActTile a = act_tile(y, ncols_y, nsb);
   typename Out::T *d = (typename Out::T *)dst;
   const uint8_t *w = (const uint8_t *)x;
-  switch (type) {
+  switch (F32D ? type : QMM_TYPE_Q8_0) {
     case QMM_TYPE_Q4K: launch_kq<wq4k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     case QMM_TYPE_Q6K: launch_kq<wq6k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
     case QMM_TYPE_Q5K: launch_kq<wq5k, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s); break;
@@ -1120,27 +1139,27 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
     default: {
       if (b32_runs(w, ncols_x, w_row_bytes)) {
         if (type == QMM_TYPE_Q4_0)
-          launch_b32<wr_q4_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
+          launch_b32<wr_q4_0, Out, F32D>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         else if (type == QMM_TYPE_Q5_0)
-          launch_b32<wr_q5_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
+          launch_b32<wr_q5_0, Out, F32D>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         else
-          launch_b32<wr_q8_0, Out>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
+          launch_b32<wr_q8_0, Out, F32D>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, d, ldd, fixup, nsm, s);
         break;
       }
       const dim3 grid((unsigned)(((ncols_y + BM - 1) / BM) * ((nrows_x + BN - 1) / BN)));
       if (type == QMM_TYPE_Q4_0)
-        k_mmq_q8_0<wb_q4_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+        k_mmq_q8_0<wb_q4_0, Out, F32D><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
       else if (type == QMM_TYPE_Q5_0)
-        k_mmq_q8_0<wb_q5_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+        k_mmq_q8_0<wb_q5_0, Out, F32D><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
       else
-        k_mmq_q8_0<wb_q8_0, Out><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
+        k_mmq_q8_0<wb_q8_0, Out, F32D><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, ncols_x / 32, a, ncols_y, nsb, d, ldd);
     }
   }
 }
 
 // The kernels address one activation channel with 32-bit offsets.
 bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows) {
-  if ((ncols_x + 255) / 256 * rows * 292 > 0x7ffffff0) {
+  if ((ncols_x + 255) / 256 * rows * 276 > 0x7ffffff0) {
     qmm_set_error("%s: activation channel of %lld x %lld values exceeds 2 GiB", who, (long long)rows,
                   (long long)ncols_x);
     return false;
@@ -1148,9 +1167,10 @@ bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows) {
   return true;
 }
 
-void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x,
-         int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int nsm, int type_dst, void *stream,
-         const char *who) {
+// q8_0: the activations are Q8_0 blocks (the 32-value types' _q8_0 entries), else Q8_K tiles
+void mmq(int type, bool q8_0, void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,
+         int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int nsm, int type_dst,
+         void *stream, const char *who) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_y)) return;
   if (ncols_y < 0 || stride_col_dst < nrows_x) {
     qmm_set_error("%s: ncols_y=%lld stride_col_dst=%lld", who, (long long)ncols_y, (long long)stride_col_dst);
@@ -1158,12 +1178,18 @@ void mmq(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int
   }
   if (ncols_y == 0) return;
   hipStream_t s = (hipStream_t)stream;
+#define QMM_MMQ_P(Out)                                                                                            \
+  (q8_0 ? mmq_plain<Out, false>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup,  \
+                                nsm, s)                                                                             \
+        : mmq_plain<Out, true>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup,   \
+                               nsm, s))
   switch (type_dst) {
-    case QMM_TYPE_F32: mmq_plain<out_f32>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
-    case QMM_TYPE_F16: mmq_plain<out_f16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
-    case QMM_TYPE_BF16: mmq_plain<out_bf16>(type, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, tmp_fixup, nsm, s); break;
+    case QMM_TYPE_F32: QMM_MMQ_P(out_f32); break;
+    case QMM_TYPE_F16: QMM_MMQ_P(out_f16); break;
+    case QMM_TYPE_BF16: QMM_MMQ_P(out_bf16); break;
     default: qmm_set_error("%s: type_dst=%d (0 f32, 1 f16, 30 bf16)", who, type_dst);
   }
+#undef QMM_MMQ_P
 }
 
 template <class WT, int TMv>
@@ -1178,10 +1204,11 @@ void kq_moe(dim3 grid, hipStream_t s, const uint8_t *w, int64_t expert_bytes, in
                                                       splits, d, ldd, part, ncols_dst, rsum);
 }
 
-void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
-             void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
-             int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who,
-             RouteSum rsum = RouteSum{}) {
+template <bool F32D>
+void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
+               void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
+               int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who,
+               RouteSum rsum) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst)) return;
   if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
     qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
@@ -1197,7 +1224,7 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   hipStream_t s = (hipStream_t)stream;
   // a few rows per expert: the few-row kernel streams each expert's weights once, without 64-row tiles of padding
   const bool b32 = qmm_block_size(type) == 32;  // Q8_0, Q4_0, Q5_0: the Q8_0-layout kernel
-  if (!b32 && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
+  if (!b32 && F32D && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
                                               ncols_dst, stride_col_dst, num_experts, s, rsum))
     return;
   // the 32-value types store their route rows, then the weighted sum runs as its own launch (the same arithmetic)
@@ -1210,13 +1237,13 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   float *d = (float *)dst;
   if (b32 && b32_runs(w, ncols_x, w_row_bytes)) {
     if (type == QMM_TYPE_Q4_0)
-      launch_b32_moe<wr_q4_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+      launch_b32_moe<wr_q4_0, F32D>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
                               ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     else if (type == QMM_TYPE_Q5_0)
-      launch_b32_moe<wr_q5_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+      launch_b32_moe<wr_q5_0, F32D>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
                               ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     else
-      launch_b32_moe<wr_q8_0>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
+      launch_b32_moe<wr_q8_0, F32D>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
                               ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
     separate_sum();
     return;
@@ -1235,7 +1262,7 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
   rsum.col_tiles = (int32_t)ntiles;
   float *part = splits > 1 ? (float *)tmp_fixup : nullptr;
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
-  switch (type) {
+  switch (F32D ? type : QMM_TYPE_Q8_0) {
     case QMM_TYPE_Q4K:
       if (small)
         kq_moe<wq4k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
@@ -1265,19 +1292,32 @@ void mmq_moe(int type, void *tmp_fixup, const void *x, const void *y, const int3
                         stride_col_dst, part, ncols_dst, rsum);
       break;
     case QMM_TYPE_Q4_0:
-      k_mmq_q8_0_moe<wb_q4_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+      k_mmq_q8_0_moe<wb_q4_0, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
                                                    ids_dst, nsb, d, stride_col_dst);
       break;
     case QMM_TYPE_Q5_0:
-      k_mmq_q8_0_moe<wb_q5_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+      k_mmq_q8_0_moe<wb_q5_0, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
                                                    ids_dst, nsb, d, stride_col_dst);
       break;
     default:
-      k_mmq_q8_0_moe<wb_q8_0><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
+      k_mmq_q8_0_moe<wb_q8_0, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
                                                    ids_dst, nsb, d, stride_col_dst);
   }
   if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, stride_col_dst, ids_dst, s);
   if (b32) separate_sum();  // (the Q8_0-layout kernel of rows that are not whole dword-aligned superblocks)
+}
+
+// q8_0: the activations are Q8_0 blocks (the 32-value types' _q8_0 entries), else Q8_K tiles
+void mmq_moe(int type, bool q8_0, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,
+             const int32_t *bounds, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst,
+             int64_t stride_row_x, int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm,
+             void *stream, const char *who, RouteSum rsum = RouteSum{}) {
+  if (q8_0)
+    mmq_moe_t<false>(type, tmp_fixup, x, y, ids_dst, bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,
+                     stride_col_dst, num_experts, ncols_max, nsm, stream, who, rsum);
+  else
+    mmq_moe_t<true>(type, tmp_fixup, x, y, ids_dst, bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,
+                    stride_col_dst, num_experts, ncols_max, nsm, stream, who, rsum);
 }
 
 void moe_wsum(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
@@ -1298,29 +1338,32 @@ void moe_wsum(int type, void *tmp_fixup, const void *x, const void *y, const int
   rs.col_tiles = 0;  // set by the kernel's launcher
   // no split K (each route row of a column tile is stored once, by one workgroup), whatever tmp_fixup holds
   (void)tmp_fixup;
-  mmq_moe(type, nullptr, x, y, ids_dst, bounds, routes, ncols_x, nrows_x, ncols_dst, stride_row_x, nrows_x,
+  mmq_moe(type, false, nullptr, x, y, ids_dst, bounds, routes, ncols_x, nrows_x, ncols_dst, stride_row_x, nrows_x,
           num_experts, ncols_max, nsm, stream, who, rs);
 }
 
 }  // namespace
 
+// launch_mmq_gguf_<t><sfx> and launch_mmq_gguf_<t>_moe<sfx> (sfx _q8_0: Q8_0-block activations)
+#define QMM_DEFINE_MMQ_ENTRIES(t, TYPE, Q8_0, sfx)                                                                 \
+  void launch_mmq_gguf_##t##sfx(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,        \
+                                int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst,   \
+                                int cc, int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream) {      \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq(TYPE, Q8_0, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, nsm, type_dst,  \
+        stream, "mmq_" #t #sfx);                                                                                   \
+  }                                                                                                                \
+  void launch_mmq_gguf_##t##_moe##sfx(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,      \
+                                      const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,   \
+                                      int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,             \
+                                      int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,      \
+                                      int warp_size, void *stream) {                                               \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq_moe(TYPE, Q8_0, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,   \
+            stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe" #sfx);                           \
+  }
 #define QMM_DEFINE_MMQ(t, TYPE)                                                                                    \
-  void launch_mmq_gguf_##t(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,             \
-                           int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc, \
-                           int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream) {                    \
-    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
-    mmq(TYPE, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, nsm, type_dst,        \
-        stream, "mmq_" #t);                                                                                        \
-  }                                                                                                                \
-  void launch_mmq_gguf_##t##_moe(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,           \
-                                 const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,        \
-                                 int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,                  \
-                                 int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,           \
-                                 int warp_size, void *stream) {                                                    \
-    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
-    mmq_moe(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,         \
-            stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe");                                \
-  }                                                                                                                \
+  QMM_DEFINE_MMQ_ENTRIES(t, TYPE, false, )                                                                         \
   void launch_mmq_gguf_##t##_moe_wsum(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,      \
                                       const int32_t *expert_bounds, float *routes, const float *topk_weights,     \
                                       int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,            \
@@ -1338,4 +1381,7 @@ QMM_DEFINE_MMQ(q5_k, QMM_TYPE_Q5K)
 QMM_DEFINE_MMQ(q4_0, QMM_TYPE_Q4_0)
 QMM_DEFINE_MMQ(q5_0, QMM_TYPE_Q5_0)
 QMM_DEFINE_MMQ(iq4_xs, QMM_TYPE_IQ4_XS)
+QMM_DEFINE_MMQ_ENTRIES(q8_0, QMM_TYPE_Q8_0, true, _q8_0)
+QMM_DEFINE_MMQ_ENTRIES(q4_0, QMM_TYPE_Q4_0, true, _q8_0)
+QMM_DEFINE_MMQ_ENTRIES(q5_0, QMM_TYPE_Q5_0, true, _q8_0)
 }

@@ -1,6 +1,7 @@
-// Decode matvec for GGUF Q8_0 / Q4_K / Q6_K weights (and Q4_0 / Q5_0 / Q5_K / IQ4_XS) against Q8_0 / Q8_K
-// activations (b = 1..16 rows),
-// plus the expert-indexed MoE matvec (optionally fused gate/up with the GLU activation).
+// Decode matvec kernels shared by the per-type translation units mmvq_<t>.hip: GGUF Q8_0 / Q4_K / Q6_K (and Q4_0 /
+// Q5_0 / Q5_K / IQ4_XS) weights against quantized activations (b = 1..16 rows; 32 for Q4_K / Q6_K), plus the
+// expert-indexed MoE matvec (optionally fused gate/up with the GLU activation).  Each translation unit instantiates
+// the kernels of its weight types only, so the library builds in parallel.
 //
 // Replaces mmvq_gguf.cuh:650-759 (mmvq_core_impl) and its launchers (1542-1553, 1647-1702, 1762-1834),
 // mmvq_gguf.cuh:961-1038 / 1600-1643 (MoE) and indexed_moe.cu:664-1000, all in
@@ -8,6 +9,12 @@
 // stride over the rows' units (units.h), issue every 16-byte weight load of the R rows before using any,
 // dot them with v_dot4 against activation units read once per column, and reduce each row with a wave
 // butterfly.  Activations are tiny and hit L2.
+//
+// Two activation layouts (units.h): the Q8_1 slots of the reference-named entries (every weight type, 288 bytes per
+// 256 values, stride_col_y in 36-byte Q8_1 blocks as the reference passes it) and, for the 32-value weight types, the
+// Q8_0 blocks of their CPU dot product (the _q8_0 entries, 34 bytes per 32 values, stride_col_y in blocks).
+#pragma once
+
 #include "common.h"
 #include "inferencequant.h"
 #include "q8.h"
@@ -21,6 +28,8 @@ constexpr int kWaves = 4;  // waves per workgroup
 #ifndef QMM_PERSISTENT_MAX_S
 #define QMM_PERSISTENT_MAX_S 4
 #endif
+// the persistent kernels hold at most 4 units per lane (k_mmvq_p's widest instantiation; k_mmvq_p2's two waves of two)
+static_assert(QMM_PERSISTENT_MAX_S >= 1 && QMM_PERSISTENT_MAX_S <= 4, "persistent rows hold at most 4 units per lane");
 
 
 template <class U, class Out, int NC, int R>
@@ -290,6 +299,24 @@ constexpr bool split_wide_rows(int nc) {
   return nc == 2 && (U::kType == QMM_TYPE_Q4K || U::kType == QMM_TYPE_Q4_0 || U::kType == QMM_TYPE_Q8_0);
 }
 
+// The form of the decode kernel a row of `units` units takes at nc columns: k_mmvq_p (kFormP) holds s = 1, 2 or 4 units
+// per lane, k_mmvq_p2 (kFormP2) two waves of two per row (256 units), k_mmvq (kFormPasses) any row, its units in
+// passes.  `full` (no per-unit guard) only where the row fills every lane's units exactly: three units per lane run
+// the four-unit kernel, so 192 units are not full.  Exported as qmm_decode_form for the tests.
+enum { kFormP = 0, kFormP2 = 1, kFormPasses = 2 };
+struct DecodeForm {
+  int kernel, s;
+  bool full;
+};
+template <class U>
+constexpr DecodeForm decode_form(int units, int nc) {
+  const int S = (units + 63) / 64;
+  if (S > QMM_PERSISTENT_MAX_S) return {kFormPasses, S, false};
+  if (S > 2 && split_wide_rows<U>(nc)) return {kFormP2, 4, units == 256};
+  const int s = S <= 2 ? S : 4;
+  return {kFormP, s, units == 64 * s};
+}
+
 // Grid of k_mmvq_p2: row pairs spread evenly over as many rounds of the workgroups a CU holds as they need.
 template <class U, class Out>
 void launch_p2(int nc, const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows,
@@ -305,13 +332,14 @@ void launch_p2(int nc, const uint8_t *vx, const uint8_t *act, typename Out::T *d
 #define QMM_P2_F(NC, FF)                                                                                  \
   k_mmvq_p2<U, Out, NC, FF><<<grid(qmm_resident_per_cu<k_mmvq_p2<U, Out, NC, FF>>(256, 0)), 256, 0, s>>>( \
       vx, act, dst, nrows, rb, nu, act_row_bytes, stride_col_dst)
+  const bool full = decode_form<U>(nu, nc).full;
   if (nc == 1) {
-    if (nu == 256)
+    if (full)
       QMM_P2_F(1, true);
     else
       QMM_P2_F(1, false);
   } else {
-    if (nu == 256)
+    if (full)
       QMM_P2_F(2, true);
     else
       QMM_P2_F(2, false);
@@ -446,7 +474,8 @@ __global__ __launch_bounds__(256) void k_mmvq_moe(const uint8_t *__restrict__ vx
 // dot is the same per-lane sum and wave reduction as k_mmvq_moe's, and the sum over routes is the same expression,
 // in the same order, as the standalone weighted reduce, so the result equals the two-kernel sequence's.  A route of
 // weight zero is skipped, as the reduce skips reading it.
-template <class U, int R>
+// ACC: added to what dst holds (the reference's fused down projection accumulates into a zeroed buffer)
+template <class U, int R, bool ACC = false>
 __global__ __launch_bounds__(256) void k_mmvq_moe_wsum(const uint8_t *__restrict__ vx, int64_t expert_stride,
                                                        const uint8_t *__restrict__ vy, const uint32_t *__restrict__ ids,
                                                        const float *__restrict__ weights, float *__restrict__ dst,
@@ -482,7 +511,10 @@ __global__ __launch_bounds__(256) void k_mmvq_moe_wsum(const uint8_t *__restrict
   }
 #pragma unroll
   for (int r = 0; r < R; r++)
-    if (lane == 63 && row0 + r < nrows) dst[(int64_t)t * nrows + row0 + r] = out[r];
+    if (lane == 63 && row0 + r < nrows) {
+      float *o = dst + (int64_t)t * nrows + row0 + r;
+      *o = ACC ? *o + out[r] : out[r];
+    }
 }
 
 template <class U, class Out, int NC>
@@ -512,8 +544,7 @@ void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, typename Out
   };
   const int64_t rb = U::row_bytes(k);
   const int nu = U::units(k);
-  // three units per lane run the four-unit kernel, so only 64, 128 or 256 units leave no lane idle (192 does not)
-  const bool full = nu == 64 * (S <= 2 ? S : 4);
+  const bool full = decode_form<U>(nu, nc).full;
 #define QMM_P_F(NC, SS, FF)                                                                                    \
   k_mmvq_p<U, Out, NC, SS, FF><<<grid(qmm_resident_per_cu<k_mmvq_p<U, Out, NC, SS, FF>>(256, 0)), 256, 0, s>>>( \
       vx, act, dst, nrows, rb, nu, act_row_bytes, stride_col_dst)
@@ -545,22 +576,22 @@ void launch_p(int nc, int S, const uint8_t *vx, const uint8_t *act, typename Out
 #undef QMM_P_F
 }
 
-int out_type_of(const out_f32 *) { return QMM_TYPE_F32; }
-int out_type_of(const out_f16 *) { return QMM_TYPE_F16; }
-int out_type_of(const out_bf16 *) { return QMM_TYPE_BF16; }
+inline int out_type_of(const out_f32 *) { return QMM_TYPE_F32; }
+inline int out_type_of(const out_f16 *) { return QMM_TYPE_F16; }
+inline int out_type_of(const out_bf16 *) { return QMM_TYPE_BF16; }
 
 template <class U, class Out>
 void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
                  int stride_col_dst, int b, hipStream_t s) {
-  const int S = (int)qmm_ceil_div(U::units(k), 64);
-  if (S <= QMM_PERSISTENT_MAX_S) {
+  if (decode_form<U>(U::units(k), 1).kernel != kFormPasses) {
     for (int j0 = 0; j0 < b; j0 += 8) {
       const int nc = b - j0 < 8 ? b - j0 : 8;
-      if (S > 2 && split_wide_rows<U>(nc))
+      const DecodeForm f = decode_form<U>(U::units(k), nc);
+      if (f.kernel == kFormP2)
         launch_p2<U, Out>(nc, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
                           act_row_bytes, stride_col_dst, s);
       else
-        launch_p<U, Out>(nc, S, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
+        launch_p<U, Out>(nc, f.s, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
                          act_row_bytes, stride_col_dst, s);
     }
     return;
@@ -580,91 +611,6 @@ void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int
       case 7: launch_nc<U, Out, 7>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
       default: launch_nc<U, Out, 8>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
     }
-  }
-}
-
-// Shape checks shared by the plain and MoE launchers. Returns false (and records why) when the
-// arguments cannot be served.
-// Byte alignment the decode units need of a weight pointer: 16-byte loads for Q4_K / Q5_K, dword loads for IQ4_XS,
-// 16-bit loads (or realigned dwords) for the rest.
-uintptr_t weight_align(int type) {
-  switch (type) {
-    case QMM_TYPE_Q4K: case QMM_TYPE_Q5K: return 16;
-    case QMM_TYPE_IQ4_XS: return 4;
-    default: return 2;
-  }
-}
-
-bool check_mmvq(const char *who, int type, const void *vx, int ncols_x, int nrows_x, int stride_col_y, int b) {
-  const int bs = (int)qmm_block_size(type);
-  const int abs_ = (int)qmm_block_size(qmm_vec_dot_type(type));
-  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0) {
-    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x, bs);
-    return false;
-  }
-  if ((int64_t)stride_col_y * abs_ < ncols_x) {
-    qmm_set_error("%s: stride_col_y=%d blocks holds fewer than ncols_x=%d values", who, stride_col_y, ncols_x);
-    return false;
-  }
-  // Q4_K / Q6_K take up to 32 rows (the few-row MFMA kernel holds 32 activation rows in one tile); the rest 16
-  const int bmax = type == QMM_TYPE_Q4K || type == QMM_TYPE_Q6K ? 32 : 16;
-  if (b < 0 || b > bmax) {
-    qmm_set_error("%s: b_size=%d outside 1..%d", who, b, bmax);
-    return false;
-  }
-  const uintptr_t align = weight_align(type);
-  if ((uintptr_t)vx % align != 0) {
-    qmm_set_error("%s: weight pointer not %zu-byte aligned", who, (size_t)align);
-    return false;
-  }
-  return true;
-}
-
-template <class Out>
-void plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_y,
-           int stride_col_dst, int b, void *stream, const char *who) {
-  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, stride_col_y, b)) return;
-  if (b == 0) return;
-  hipStream_t s = (hipStream_t)stream;
-  const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
-  typename Out::T *d = (typename Out::T *)dst;
-  if (b >= qmm_skinny_min_rows(type) &&
-      qmm_skinny_decode(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_y,
-                        stride_col_dst, b, s))
-    return;
-  switch (type) {
-    case QMM_TYPE_Q4K:
-      launch_cols<unit_q4k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
-      break;
-    case QMM_TYPE_Q6K:
-      launch_cols<unit_q6k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
-      break;
-    case QMM_TYPE_Q5K:
-      launch_cols<unit_q5k, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
-      break;
-    case QMM_TYPE_IQ4_XS:
-      launch_cols<unit_iq4xs, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 292, stride_col_dst, b, s);
-      break;
-    case QMM_TYPE_Q4_0:
-    case QMM_TYPE_Q5_0: {
-      // block pairs as dwords when every pair starts dword aligned, else one block per unit
-      const bool pairs = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0;
-      const int64_t ay = (int64_t)stride_col_y * 34;
-      if (type == QMM_TYPE_Q4_0) {
-        if (pairs) launch_cols<unit_b32<QMM_TYPE_Q4_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
-        else launch_cols<unit_b32_odd<QMM_TYPE_Q4_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
-      } else {
-        if (pairs) launch_cols<unit_b32<QMM_TYPE_Q5_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
-        else launch_cols<unit_b32_odd<QMM_TYPE_Q5_0>, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
-      }
-      break;
-    }
-    default:  // Q8_0
-      if (ncols_x % 64 == 0 && stride_col_y % 2 == 0 && (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0)
-        launch_cols<unit_q8_0, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 34, stride_col_dst, b, s);
-      else
-        launch_cols<unit_q8_0_odd, Out>(x, y, d, ncols_x, nrows_x, (int64_t)stride_col_y * 34, stride_col_dst, b, s);
-      break;
   }
 }
 
@@ -718,45 +664,6 @@ void launch_pq(const uint8_t *vx, const float *x, int64_t stride_x, typename Out
     launch_pq_nw<U, Out, NC, 16>(vx, x, stride_x, dst, k, nrows, stride_col_dst, s);
 }
 
-template <class Out>
-void quantize_plain(int type, const void *vx, const float *x, void *dst, int ncols_x, int nrows_x, int stride_col_x,
-                    int stride_col_dst, int b, void *stream, const char *who) {
-  const int bs = (int)qmm_block_size(type);
-  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0 || (type == QMM_TYPE_Q8_0 && ncols_x % 64 != 0)) {
-    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x,
-                  type == QMM_TYPE_Q8_0 ? 64 : bs);
-    return;
-  }
-  if (b < 0 || b > 2 || (b > 1 && stride_col_x < ncols_x)) {
-    qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
-    return;
-  }
-  // one unit per lane; every activation block of the b rows within kPqSteps wave steps of one workgroup
-  if (ncols_x > 64 * 64) {
-    qmm_set_error("%s: ncols_x=%d (at most 4096)", who, ncols_x);
-    return;
-  }
-  const uintptr_t align = type == QMM_TYPE_Q6K ? 2 : (type == QMM_TYPE_Q8_0 ? 4 : 16);
-  if ((uintptr_t)vx % align != 0 || (uintptr_t)x % 4 != 0) {
-    qmm_set_error("%s: weights must be %zu-byte and x 4-byte aligned", who, (size_t)align);
-    return;
-  }
-  if (b == 0) return;
-  hipStream_t s = (hipStream_t)stream;
-  const uint8_t *w = (const uint8_t *)vx;
-  typename Out::T *d = (typename Out::T *)dst;
-#define QMM_PQ_T(U)                                                                                      \
-  if (b == 1)                                                                                            \
-    launch_pq<U, Out, 1>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);                    \
-  else                                                                                                   \
-    launch_pq<U, Out, 2>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);
-  switch (type) {
-    case QMM_TYPE_Q4K: QMM_PQ_T(unit_q4k) break;
-    case QMM_TYPE_Q6K: QMM_PQ_T(unit_q6k) break;
-    default: QMM_PQ_T(unit_q8_0) break;
-  }
-#undef QMM_PQ_T
-}
 
 template <class U>
 void moe_launch(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
@@ -776,10 +683,157 @@ void moe_launch(const void *vx_gate, const void *vx_up, int64_t expert_stride, c
                                                  activation);
 }
 
-void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
-         float *dst, int ncols_x, int nrows_x, int stride_col_y, int y_div, int n_pairs, int activation,
-         void *stream, const char *who) {
-  if (!check_mmvq(who, type, vx_gate, ncols_x, nrows_x, stride_col_y, 1)) return;
+
+template <class U, bool ACC = false>
+void moe_wsum_launch(const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
+                     float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int n_tokens, int topk,
+                     hipStream_t s) {
+  constexpr int R = 2;  // as moe_launch, so each route's dot is the same sum
+  const dim3 grid((unsigned)n_tokens, (unsigned)qmm_ceil_div(nrows_x, kWaves * R));
+  k_mmvq_moe_wsum<U, R, ACC><<<grid, 256, 0, s>>>((const uint8_t *)vx, expert_stride, (const uint8_t *)vy,
+                                             (const uint32_t *)ids, weights, dst, nrows_x, U::row_bytes(ncols_x),
+                                             U::units(ncols_x), act_row_bytes, topk);
+}
+
+
+// ------------------------------------------------------------------------------------------------ per-type dispatch
+
+// Shape checks shared by the decode launchers. Returns false (and records why) when the arguments cannot be served.
+// Slots: stride_col_y counts 36-byte Q8_1 blocks of 32 values, a whole number of 288-byte slots (a multiple of 8);
+// Q8_0 blocks: stride_col_y counts 34-byte blocks.
+template <int T, int F>
+bool check_mmvq(const char *who, const void *vx, int ncols_x, int nrows_x, int stride_col_y, int b) {
+  const int bs = (int)qmm_block_size(T);
+  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0) {
+    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x, bs);
+    return false;
+  }
+  if ((int64_t)stride_col_y * 32 < ncols_x || (F == kActSlots && stride_col_y % 8 != 0)) {
+    qmm_set_error("%s: stride_col_y=%d blocks of 32 values hold fewer than ncols_x=%d values%s", who, stride_col_y,
+                  ncols_x, F == kActSlots ? " or are not whole 256-value slots" : "");
+    return false;
+  }
+  // Q4_K / Q6_K take up to 32 rows (the few-row MFMA kernel holds 32 activation rows in one tile); the rest 16
+  const int bmax = T == QMM_TYPE_Q4K || T == QMM_TYPE_Q6K ? 32 : 16;
+  if (b < 0 || b > bmax) {
+    qmm_set_error("%s: b_size=%d outside 1..%d", who, b, bmax);
+    return false;
+  }
+  if ((uintptr_t)vx % weight_align(T) != 0) {
+    qmm_set_error("%s: weight pointer not %zu-byte aligned", who, (size_t)weight_align(T));
+    return false;
+  }
+  return true;
+}
+
+// Rows the non-persistent kernel serves: the 32-value types' odd-block rows (a rare shape) take only k_mmvq, so their
+// units add few kernels to the build.
+template <class U, class Out>
+void launch_nc_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int k, int nrows, int64_t act_row_bytes,
+                    int stride_col_dst, int b, hipStream_t s) {
+  for (int j0 = 0; j0 < b; j0 += 8) {
+    const int nc = b - j0 < 8 ? b - j0 : 8;
+    const uint8_t *y = vy + (int64_t)j0 * act_row_bytes;
+    typename Out::T *d = dst + (int64_t)j0 * stride_col_dst;
+    switch (nc) {
+      case 1: launch_nc<U, Out, 1>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 2: launch_nc<U, Out, 2>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 3: launch_nc<U, Out, 3>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 4: launch_nc<U, Out, 4>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 5: launch_nc<U, Out, 5>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 6: launch_nc<U, Out, 6>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      case 7: launch_nc<U, Out, 7>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+      default: launch_nc<U, Out, 8>(vx, y, d, k, nrows, act_row_bytes, stride_col_dst, s); break;
+    }
+  }
+}
+
+// launch_mmvq_gguf_<t>_<dt>_plain (slots) and its _plain_q8_0 twin
+template <int T, int F, class Out>
+void plain_t(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_y, int stride_col_dst,
+             int b, void *stream, const char *who) {
+  if (!check_mmvq<T, F>(who, vx, ncols_x, nrows_x, stride_col_y, b)) return;
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
+  typename Out::T *d = (typename Out::T *)dst;
+  if constexpr (T == QMM_TYPE_Q4K || T == QMM_TYPE_Q6K) {
+    if (b >= qmm_skinny_min_rows(T) &&
+        qmm_skinny_decode(T, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_y,
+                          stride_col_dst, b, s))
+      return;
+  }
+  typedef decode_units<T, F> DU;
+  const int64_t ay = act_row_bytes<F>(stride_col_y);
+  if (reads_pairs<T, F>(ncols_x, stride_col_y, vy, {vx}))
+    launch_cols<typename DU::pairs, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+  else
+    launch_nc_cols<typename DU::odd, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+}
+
+// launch_mmvq_gguf_<t>_<dt>_quantize_plain: the one-launch decode of Q8_0 / Q4_K / Q6_K (b 1 or 2, K <= 4096)
+template <int T, class Out>
+void quantize_plain_t(const void *vx, const float *x, void *dst, int ncols_x, int nrows_x, int stride_col_x,
+                      int stride_col_dst, int b, void *stream, const char *who) {
+  const int bs = (int)qmm_block_size(T);
+  if (ncols_x <= 0 || nrows_x <= 0 || ncols_x % bs != 0 || (T == QMM_TYPE_Q8_0 && ncols_x % 64 != 0)) {
+    qmm_set_error("%s: ncols_x=%d nrows_x=%d (ncols_x must be a positive multiple of %d)", who, ncols_x, nrows_x,
+                  T == QMM_TYPE_Q8_0 ? 64 : bs);
+    return;
+  }
+  if (b < 0 || b > 2 || (b > 1 && stride_col_x < ncols_x)) {
+    qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
+    return;
+  }
+  // one unit per lane; every activation block of the b rows within kPqSteps wave steps of one workgroup
+  if (ncols_x > 64 * 64) {
+    qmm_set_error("%s: ncols_x=%d (at most 4096)", who, ncols_x);
+    return;
+  }
+  const uintptr_t align = T == QMM_TYPE_Q6K ? 2 : (T == QMM_TYPE_Q8_0 ? 4 : 16);
+  if ((uintptr_t)vx % align != 0 || (uintptr_t)x % 4 != 0) {
+    qmm_set_error("%s: weights must be %zu-byte and x 4-byte aligned", who, (size_t)align);
+    return;
+  }
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *w = (const uint8_t *)vx;
+  typename Out::T *d = (typename Out::T *)dst;
+  typedef typename std::conditional<T == QMM_TYPE_Q4K, unit_q4k,
+                                    typename std::conditional<T == QMM_TYPE_Q6K, unit_q6k, unit_q8_0>::type>::type U;
+  if (b == 1)
+    launch_pq<U, Out, 1>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);
+  else
+    launch_pq<U, Out, 2>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);
+}
+
+// The reference's tensor-core matvec entries (launch_mmvq_tc_gguf_<t>_<dt>_plain, crates/inference-quant/src/gguf/
+// ffi.rs:966-998; routed by fast_mmvq.rs:505-513 for 1..16 rows) over the tensor-core entries' activation layout
+// (launch_mmvq_tc_quantize_*: rows of ncols_x / 256 blocks {f32 d; int8 qs[256]}, units.h): the persistent matvec
+// below the few-row threshold, the few-row MFMA kernel from it, with the same integer dots as the plain entries.
+// cfg names one of the reference's CUDA tile shapes (fast_mmvq.rs:1845-1881); it is accepted and has no meaning here.
+// b_size 1..32 (the reference passes at most 16).
+template <int T, class Out>
+void tc_plain_t(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_dst, int b,
+                int cfg, void *stream, const char *who) {
+  (void)cfg;
+  if (!check_mmvq<T, kActSlots>(who, vx, ncols_x, nrows_x, ncols_x / 32, b)) return;
+  if (b == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  if (b >= qmm_skinny_min_rows(T) &&
+      qmm_skinny_tc(T, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s))
+    return;
+  typedef typename std::conditional<T == QMM_TYPE_Q4K, unit_q4k_tc, unit_q6k_tc>::type U;
+  launch_cols<U, Out>((const uint8_t *)vx, (const uint8_t *)vy, (typename Out::T *)dst, ncols_x, nrows_x,
+                      (int64_t)(ncols_x / 256) * 260, stride_col_dst, b, s);
+}
+
+// launch_mmvq_gguf_<t>_moe (slots) and its _moe_q8_0 twin
+template <int T, int F>
+void moe_t(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids, float *dst,
+           int ncols_x, int nrows_x, int stride_col_y, int y_div, int n_pairs, int activation, void *stream,
+           const char *who) {
+  if (!check_mmvq<T, F>(who, vx_gate, ncols_x, nrows_x, stride_col_y, 1)) return;
   if (n_pairs < 0 || y_div <= 0 || activation < 0 || activation >= kGluActivations || expert_stride < 0) {
     qmm_set_error("%s: n_pairs=%d y_div=%d activation=%d expert_stride=%lld", who, n_pairs, y_div, activation,
                   (long long)expert_stride);
@@ -790,306 +844,183 @@ void moe(int type, const void *vx_gate, const void *vx_up, int64_t expert_stride
     qmm_set_error("%s: n_pairs=%d too large", who, n_pairs);
     return;
   }
-  hipStream_t s = (hipStream_t)stream;
-  switch (type) {
-    case QMM_TYPE_Q4K:
-      if (expert_stride % 16 != 0 || (vx_up && (uintptr_t)vx_up % 16 != 0)) {
-        qmm_set_error("%s: Q4_K expert_stride / vx_up not 16-byte aligned", who);
-        return;
-      }
-      moe_launch<unit_q4k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
-      break;
-    case QMM_TYPE_Q6K:
-      moe_launch<unit_q6k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
-      break;
-    case QMM_TYPE_Q5K:
-      if (expert_stride % 16 != 0 || (vx_up && (uintptr_t)vx_up % 16 != 0)) {
-        qmm_set_error("%s: Q5_K expert_stride / vx_up not 16-byte aligned", who);
-        return;
-      }
-      moe_launch<unit_q5k>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                           (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
-      break;
-    case QMM_TYPE_IQ4_XS:
-      if (expert_stride % 4 != 0 || (vx_up && (uintptr_t)vx_up % 4 != 0)) {
-        qmm_set_error("%s: IQ4_XS expert_stride / vx_up not 4-byte aligned", who);
-        return;
-      }
-      moe_launch<unit_iq4xs>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                             (int64_t)stride_col_y * 292, y_div, n_pairs, activation, s);
-      break;
-    case QMM_TYPE_Q4_0:
-    case QMM_TYPE_Q5_0: {
-      const bool pairs = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
-                         (uintptr_t)vx_gate % 4 == 0 && (!vx_up || (uintptr_t)vx_up % 4 == 0) && (uintptr_t)vy % 4 == 0;
-      const int64_t ay = (int64_t)stride_col_y * 34;
-      if (type == QMM_TYPE_Q4_0) {
-        if (pairs)
-          moe_launch<unit_b32<QMM_TYPE_Q4_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div,
-                                              n_pairs, activation, s);
-        else
-          moe_launch<unit_b32_odd<QMM_TYPE_Q4_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay,
-                                                  y_div, n_pairs, activation, s);
-      } else {
-        if (pairs)
-          moe_launch<unit_b32<QMM_TYPE_Q5_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div,
-                                              n_pairs, activation, s);
-        else
-          moe_launch<unit_b32_odd<QMM_TYPE_Q5_0>>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay,
-                                                  y_div, n_pairs, activation, s);
-      }
-      break;
-    }
-    default: {
-      const bool fast = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
-                        (uintptr_t)vx_gate % 4 == 0 && (!vx_up || (uintptr_t)vx_up % 4 == 0) && (uintptr_t)vy % 4 == 0;
-      if (fast)
-        moe_launch<unit_q8_0>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                              (int64_t)stride_col_y * 34, y_div, n_pairs, activation, s);
-      else
-        moe_launch<unit_q8_0_odd>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x,
-                                  (int64_t)stride_col_y * 34, y_div, n_pairs, activation, s);
-    }
+  if (expert_stride % (int64_t)weight_align(T) != 0 || (vx_up && (uintptr_t)vx_up % weight_align(T) != 0)) {
+    qmm_set_error("%s: expert_stride / vx_up not %zu-byte aligned", who, (size_t)weight_align(T));
+    return;
   }
+  hipStream_t s = (hipStream_t)stream;
+  typedef decode_units<T, F> DU;
+  const int64_t ay = act_row_bytes<F>(stride_col_y);
+  if (reads_pairs<T, F>(ncols_x, stride_col_y, vy, {vx_gate, vx_up}, expert_stride))
+    moe_launch<typename DU::pairs>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div, n_pairs,
+                                   activation, s);
+  else
+    moe_launch<typename DU::odd>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, ay, y_div, n_pairs,
+                                 activation, s);
 }
 
-template <class U>
-void moe_wsum_launch(const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
-                     float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int n_tokens, int topk,
-                     hipStream_t s) {
-  constexpr int R = 2;  // as moe_launch, so each route's dot is the same sum
-  const dim3 grid((unsigned)n_tokens, (unsigned)qmm_ceil_div(nrows_x, kWaves * R));
-  k_mmvq_moe_wsum<U, R><<<grid, 256, 0, s>>>((const uint8_t *)vx, expert_stride, (const uint8_t *)vy,
-                                             (const uint32_t *)ids, weights, dst, nrows_x, U::row_bytes(ncols_x),
-                                             U::units(ncols_x), act_row_bytes, topk);
-}
-
-void moe_wsum(int type, const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
-              float *dst, int ncols_x, int nrows_x, int stride_col_y, int n_tokens, int topk, void *stream,
-              const char *who) {
-  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, stride_col_y, 1)) return;
+// launch_mmvq_gguf_<t>_moe_wsum (slots) and its _moe_wsum_q8_0 twin (ACC: added to dst)
+template <int T, int F, bool ACC = false>
+void moe_wsum_t(const void *vx, int64_t expert_stride, const void *vy, const void *ids, const float *weights,
+                float *dst, int ncols_x, int nrows_x, int stride_col_y, int n_tokens, int topk, void *stream,
+                const char *who) {
+  if (!check_mmvq<T, F>(who, vx, ncols_x, nrows_x, stride_col_y, 1)) return;
   if (n_tokens < 0 || n_tokens > 65535 * 1024 || topk <= 0 || expert_stride < 0 || !weights) {
     qmm_set_error("%s: n_tokens=%d topk=%d expert_stride=%lld weights=%p", who, n_tokens, topk,
                   (long long)expert_stride, (const void *)weights);
     return;
   }
   if (n_tokens == 0) return;
-  hipStream_t s = (hipStream_t)stream;
-  switch (type) {
-    case QMM_TYPE_Q4K:
-      if (expert_stride % 16 != 0) {
-        qmm_set_error("%s: Q4_K expert_stride not 16-byte aligned", who);
-        return;
-      }
-      moe_wsum_launch<unit_q4k>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
-                                (int64_t)stride_col_y * 292, n_tokens, topk, s);
-      break;
-    case QMM_TYPE_Q6K:
-      moe_wsum_launch<unit_q6k>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
-                                (int64_t)stride_col_y * 292, n_tokens, topk, s);
-      break;
-    default: {  // Q8_0
-      const bool fast = ncols_x % 64 == 0 && stride_col_y % 2 == 0 && expert_stride % 4 == 0 &&
-                        (uintptr_t)vx % 4 == 0 && (uintptr_t)vy % 4 == 0;
-      if (fast)
-        moe_wsum_launch<unit_q8_0>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
-                                   (int64_t)stride_col_y * 34, n_tokens, topk, s);
-      else
-        moe_wsum_launch<unit_q8_0_odd>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x,
-                                       (int64_t)stride_col_y * 34, n_tokens, topk, s);
-    }
+  if (expert_stride % (int64_t)weight_align(T) != 0) {
+    qmm_set_error("%s: expert_stride not %zu-byte aligned", who, (size_t)weight_align(T));
+    return;
   }
+  hipStream_t s = (hipStream_t)stream;
+  typedef decode_units<T, F> DU;
+  const int64_t ay = act_row_bytes<F>(stride_col_y);
+  if (reads_pairs<T, F>(ncols_x, stride_col_y, vy, {vx}, expert_stride))
+    moe_wsum_launch<typename DU::pairs, ACC>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x, ay,
+                                             n_tokens, topk, s);
+  else
+    moe_wsum_launch<typename DU::odd, ACC>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x, ay, n_tokens,
+                                           topk, s);
 }
 
-void indexed(int type, const void *w, const void *x, const uint32_t *ids, float *out, int n, int k, int batch,
-             int topk, int k_padded, int input_dim1, void *stream, const char *who) {
-  if (batch < 0 || topk <= 0 || (input_dim1 != 1 && input_dim1 != topk) || k_padded < k) {
+// launch_indexed_moe_forward_<t>_q8_1 (slots; k_padded / 32 Q8_1 blocks per input row) and the _q8_0 forms of the
+// 32-value types (k_padded / 32 Q8_0 blocks per input row): all_outputs[(b * topk + s) * n + row] =
+// W[indices[b * topk + s]][row] . x[b * input_dim1 + (input_dim1 == 1 ? 0 : s)]
+template <int T, int F>
+void indexed_t(const void *w, const void *x, const uint32_t *ids, float *out, int n, int k, int batch, int topk,
+               int k_padded, int input_dim1, void *stream, const char *who) {
+  if (batch < 0 || topk <= 0 || (input_dim1 != 1 && input_dim1 != topk) || k_padded < k || k <= 0 ||
+      k % (int)qmm_block_size(T) != 0) {
     qmm_set_error("%s: batch=%d topk=%d input_dim1=%d k=%d k_padded=%d", who, batch, topk, input_dim1, k, k_padded);
     return;
   }
-  const int abs_ = (int)qmm_block_size(qmm_vec_dot_type(type));
-  if (k_padded % abs_ != 0) {
-    qmm_set_error("%s: k_padded=%d not a multiple of %d", who, k_padded, abs_);
+  if (k_padded % (F == kActSlots ? 256 : 32) != 0) {
+    qmm_set_error("%s: k_padded=%d not a multiple of %d", who, k_padded, F == kActSlots ? 256 : 32);
     return;
   }
-  const int64_t expert_stride = (int64_t)n * (k / (int)qmm_block_size(type)) * (int64_t)qmm_type_size(type);
-  moe(type, w, nullptr, expert_stride, x, ids, out, k, n, k_padded / abs_, input_dim1 == 1 ? topk : 1, batch * topk,
-      0, stream, who);
+  const int64_t expert_stride = (int64_t)n * (k / (int)qmm_block_size(T)) * (int64_t)qmm_type_size(T);
+  moe_t<T, F>(w, nullptr, expert_stride, x, ids, out, k, n, k_padded / 32, input_dim1 == 1 ? topk : 1, batch * topk,
+              0, stream, who);
 }
 
-// The reference's tensor-core matvec entries (launch_mmvq_tc_gguf_<t>_<dt>_plain, crates/inference-quant/src/gguf/
-// ffi.rs:966-998; routed by fast_mmvq.rs:505-513 for 1..16 rows) over the tensor-core entries' activation layout
-// (launch_mmvq_tc_quantize_*: rows of ncols_x / 256 blocks {f32 d; int8 qs[256]}, units.h): the persistent matvec
-// below the few-row threshold, the few-row MFMA kernel from it, with the same integer dots as the plain entries.
-// cfg names one of the reference's CUDA tile shapes (fast_mmvq.rs:1845-1881); it is accepted and has no meaning here.
-template <class Out>
-void tc_plain(int type, const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_dst,
-              int b, int cfg, void *stream, const char *who) {
-  (void)cfg;
-  if (!check_mmvq(who, type, vx, ncols_x, nrows_x, ncols_x / 256, b)) return;
-  if (b == 0) return;
-  hipStream_t s = (hipStream_t)stream;
-  if (b >= qmm_skinny_min_rows(type) &&
-      qmm_skinny_tc(type, out_type_of((const Out *)nullptr), vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b, s))
+// The reference's fused MoE decode launchers (gguf/ffi.rs:280-440; kernels indexed_moe.cu:1189-1330; host
+// gguf/cuda.rs:1355-1520), over slot-layout inputs of k_padded values per row, f32 outputs:
+//   launch_moe_gemv_fused_gate_up_<t>_q8_1: all_outputs[p * n + row] = act(W_gate[e] . x_b) * (W_up[e] . x_b) for
+//       route p = b * topk + s, e = indices[p], x_b = input row b; act_type 0 is GELU (tanh form), any other SiLU,
+//       as the reference's kernel reads it (indexed_moe.cu:1254-1256);
+//   launch_moe_gemv_down_aggregate_<t>_q8_1: all_outputs[b * n + row] += sum over s < topk of topk_weights[p] *
+//       (W[e] . x_p), x_p = input row p.  The reference adds each route with an atomic add into a buffer its caller
+//       zeroes (gguf/cuda.rs:1475-1477); here one lane adds the routes' products in slot order and then adds that
+//       to the buffer, so the result does not depend on scheduling.  A route of weight zero is not read.
+// The experts' weight tensors hold n rows of k values each.
+template <int T>
+void moe_gemv_gate_up_t(const void *wg, const void *wu, const void *x, const uint32_t *ids, float *out, int n, int k,
+                        int batch, int topk, int k_padded, int act_type, void *stream, const char *who) {
+  if (!wg || !wu || n <= 0 || k <= 0 || k % (int)qmm_block_size(T) != 0 || k_padded < k || k_padded % 256 != 0 ||
+      batch < 0 || topk <= 0) {
+    qmm_set_error("%s: n=%d k=%d k_padded=%d batch=%d topk=%d", who, n, k, k_padded, batch, topk);
     return;
-  const uint8_t *x = (const uint8_t *)vx, *y = (const uint8_t *)vy;
-  typename Out::T *d = (typename Out::T *)dst;
-  const int64_t ay = (int64_t)(ncols_x / 256) * 260;
-  if (type == QMM_TYPE_Q4K)
-    launch_cols<unit_q4k_tc, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
-  else
-    launch_cols<unit_q6k_tc, Out>(x, y, d, ncols_x, nrows_x, ay, stride_col_dst, b, s);
+  }
+  const int64_t expert_stride = (int64_t)n * (k / (int)qmm_block_size(T)) * (int64_t)qmm_type_size(T);
+  moe_t<T, kActSlots>(wg, wu, expert_stride, x, ids, out, k, n, k_padded / 32, topk, batch * topk,
+                      act_type == 0 ? 1 : 0, stream, who);
+}
+
+template <int T>
+void moe_gemv_down_aggregate_t(const void *w, const void *x, const uint32_t *ids, const float *weights, float *out,
+                               int n, int k, int batch, int topk, int k_padded, void *stream, const char *who) {
+  if (n <= 0 || k <= 0 || k % (int)qmm_block_size(T) != 0 || k_padded < k || k_padded % 256 != 0 || batch < 0 ||
+      topk <= 0) {
+    qmm_set_error("%s: n=%d k=%d k_padded=%d batch=%d topk=%d", who, n, k, k_padded, batch, topk);
+    return;
+  }
+  const int64_t expert_stride = (int64_t)n * (k / (int)qmm_block_size(T)) * (int64_t)qmm_type_size(T);
+  moe_wsum_t<T, kActSlots, true>(w, expert_stride, x, ids, weights, out, k, n, k_padded / 32, batch, topk, stream,
+                                 who);
 }
 
 }  // namespace
 
-#define QMM_DEFINE_TC(t, TYPE)                                                                                    \
-  void launch_mmvq_tc_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
-                                           int stride_col_dst, int b_size, int cfg, void *stream) {             \
-    tc_plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream, "mmvq_tc_" #t "_f32"); \
-  }                                                                                                               \
-  void launch_mmvq_tc_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
-                                           int stride_col_dst, int b_size, int cfg, void *stream) {             \
-    tc_plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream, "mmvq_tc_" #t "_f16"); \
-  }                                                                                                               \
-  void launch_mmvq_tc_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,\
-                                            int stride_col_dst, int b_size, int cfg, void *stream) {            \
-    tc_plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream,                  \
-                       "mmvq_tc_" #t "_bf16");                                                                    \
-  }
+// ------------------------------------------------------------------------------------------------ entry points
 
-#define QMM_DEFINE_PLAIN_ONLY(t, TYPE)                                                                            \
-  void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
-                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
-    plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
-                   "mmvq_" #t "_f32");                                                                            \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
-                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
-    plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
-                   "mmvq_" #t "_f16");                                                                            \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,   \
-                                         int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
-    plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
-                    "mmvq_" #t "_bf16");                                                                          \
+#define QMM_MMVQ_PLAIN_DT(t, T, F, sfx, dt, Out)                                                                 \
+  void launch_mmvq_gguf_##t##_##dt##_plain##sfx(const void *vx, const void *vy, void *dst, int ncols_x,          \
+                                                int nrows_x, int stride_col_y, int stride_col_dst, int b_size,   \
+                                                void *stream) {                                                  \
+    plain_t<T, F, Out>(vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,              \
+                       "mmvq_" #t "_" #dt "_plain" #sfx);                                                        \
   }
+// launch_mmvq_gguf_<t>_{f32,f16,bf16}_plain<sfx>
+#define QMM_MMVQ_PLAIN(t, T, F, sfx)                   \
+  QMM_MMVQ_PLAIN_DT(t, T, F, sfx, f32, out_f32)        \
+  QMM_MMVQ_PLAIN_DT(t, T, F, sfx, f16, out_f16)        \
+  QMM_MMVQ_PLAIN_DT(t, T, F, sfx, bf16, out_bf16)
 
-#define QMM_DEFINE_MOE(t, TYPE)                                                                                   \
-  void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy,  \
-                                  const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \
-                                  int y_div, int n_pairs, int activation, int grouped, void *stream) {            \
+#define QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, dt, Out)                                                                \
+  void launch_mmvq_gguf_##t##_##dt##_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,      \
+                                                    int nrows_x, int stride_col_x, int stride_col_dst,          \
+                                                    int b_size, void *stream) {                                 \
+    quantize_plain_t<T, Out>(vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,         \
+                             "mmvq_" #t "_" #dt "_quantize");                                                    \
+  }
+#define QMM_MMVQ_QUANTIZE_PLAIN(t, T)               \
+  QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, f32, out_f32)    \
+  QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, f16, out_f16)    \
+  QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, bf16, out_bf16)
+
+// launch_mmvq_gguf_<t>_moe<sfx> and launch_mmvq_gguf_<t>_moe_wsum<sfx>
+#define QMM_MMVQ_MOE(t, T, F, sfx)                                                                                 \
+  void launch_mmvq_gguf_##t##_moe##sfx(const void *vx_gate, const void *vx_up, int64_t expert_stride,             \
+                                       const void *vy, const void *ids, float *dst, int ncols_x, int nrows_x,     \
+                                       int stride_col_y, int y_div, int n_pairs, int activation, int grouped,     \
+                                       void *stream) {                                                            \
     (void)grouped;                                                                                                \
-    moe(TYPE, vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, stride_col_y, y_div, n_pairs,        \
-        activation, stream, "mmvq_" #t "_moe");                                                                   \
+    moe_t<T, F>(vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, stride_col_y, y_div, n_pairs,      \
+                activation, stream, "mmvq_" #t "_moe" #sfx);                                                      \
+  }                                                                                                               \
+  void launch_mmvq_gguf_##t##_moe_wsum##sfx(const void *vx, int64_t expert_stride, const void *vy,                \
+                                            const void *ids, const float *weights, float *dst, int ncols_x,       \
+                                            int nrows_x, int stride_col_y, int n_tokens, int topk, void *stream) { \
+    moe_wsum_t<T, F>(vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x, stride_col_y, n_tokens, topk,    \
+                     stream, "mmvq_" #t "_moe_wsum" #sfx);                                                        \
   }
 
-#define QMM_DEFINE_PLAIN(t, TYPE)                                                                                 \
-  void launch_mmvq_gguf_##t##_f32_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
-                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
-    plain<out_f32>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
-                   "mmvq_" #t "_f32");                                                                            \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_f16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,    \
-                                        int stride_col_y, int stride_col_dst, int b_size, void *stream) {        \
-    plain<out_f16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,           \
-                   "mmvq_" #t "_f16");                                                                            \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_bf16_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x,   \
-                                         int stride_col_y, int stride_col_dst, int b_size, void *stream) {       \
-    plain<out_bf16>(TYPE, vx, vy, dst, ncols_x, nrows_x, stride_col_y, stride_col_dst, b_size, stream,          \
-                    "mmvq_" #t "_bf16");                                                                          \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_f32_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
-                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
-                                                 void *stream) {                                                 \
-    quantize_plain<out_f32>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,     \
-                            "mmvq_" #t "_f32_quantize");                                                          \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_f16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
-                                                 int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \
-                                                 void *stream) {                                                 \
-    quantize_plain<out_f16>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,     \
-                            "mmvq_" #t "_f16_quantize");                                                          \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_bf16_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,         \
-                                                  int nrows_x, int stride_col_x, int stride_col_dst, int b_size, \
-                                                  void *stream) {                                                \
-    quantize_plain<out_bf16>(TYPE, vx, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size, stream,    \
-                             "mmvq_" #t "_bf16_quantize");                                                        \
-  }                                                                                                               \
-  void launch_mmvq_gguf_##t##_moe(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy,  \
-                                  const void *ids, float *dst, int ncols_x, int nrows_x, int stride_col_y,       \
-                                  int y_div, int n_pairs, int activation, int grouped, void *stream) {            \
-    (void)grouped;                                                                                                \
-    moe(TYPE, vx_gate, vx_up, expert_stride, vy, ids, dst, ncols_x, nrows_x, stride_col_y, y_div, n_pairs,        \
-        activation, stream, "mmvq_" #t "_moe");                                                                   \
+// launch_indexed_moe_forward_<rt>_<act> (rt: the reference's type name, q4k / q8_0 / ...)
+#define QMM_MMVQ_INDEXED(rt, T, F, act)                                                                            \
+  void launch_indexed_moe_forward_##rt##_##act(const void *all_weights, const void *all_inputs,                   \
+                                               const uint32_t *indices, float *all_outputs, int n, int k,         \
+                                               int batch, int topk, int k_padded, int input_dim1, void *stream) { \
+    indexed_t<T, F>(all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,       \
+                    stream, "indexed_moe_" #rt "_" #act);                                                         \
   }
 
-extern "C" {
-QMM_DEFINE_TC(q4_k, QMM_TYPE_Q4K)
-QMM_DEFINE_TC(q6_k, QMM_TYPE_Q6K)
-QMM_DEFINE_PLAIN(q8_0, QMM_TYPE_Q8_0)
-QMM_DEFINE_PLAIN(q4_k, QMM_TYPE_Q4K)
-QMM_DEFINE_PLAIN(q6_k, QMM_TYPE_Q6K)
-QMM_DEFINE_PLAIN_ONLY(q4_0, QMM_TYPE_Q4_0)
-QMM_DEFINE_PLAIN_ONLY(q5_0, QMM_TYPE_Q5_0)
-QMM_DEFINE_PLAIN_ONLY(q5_k, QMM_TYPE_Q5K)
-QMM_DEFINE_PLAIN_ONLY(iq4_xs, QMM_TYPE_IQ4_XS)
-QMM_DEFINE_MOE(q4_0, QMM_TYPE_Q4_0)
-QMM_DEFINE_MOE(q5_0, QMM_TYPE_Q5_0)
-QMM_DEFINE_MOE(q5_k, QMM_TYPE_Q5K)
-QMM_DEFINE_MOE(iq4_xs, QMM_TYPE_IQ4_XS)
-
-#define QMM_DEFINE_MOE_WSUM(t, TYPE)                                                                              \
-  void launch_mmvq_gguf_##t##_moe_wsum(const void *vx, int64_t expert_stride, const void *vy, const void *ids,    \
-                                       const float *weights, float *dst, int ncols_x, int nrows_x,                \
-                                       int stride_col_y, int n_tokens, int topk, void *stream) {                  \
-    moe_wsum(TYPE, vx, expert_stride, vy, ids, weights, dst, ncols_x, nrows_x, stride_col_y, n_tokens, topk,      \
-             stream, "mmvq_" #t "_moe_wsum");                                                                     \
+// launch_moe_gemv_fused_gate_up_<rt>_q8_1 and launch_moe_gemv_down_aggregate_<rt>_q8_1
+#define QMM_MOE_GEMV(rt, T)                                                                                        \
+  void launch_moe_gemv_fused_gate_up_##rt##_q8_1(const void *gate_weights, const void *up_weights,                \
+                                                 const void *all_inputs, const uint32_t *indices,                 \
+                                                 float *all_outputs, int n, int k, int batch, int topk,           \
+                                                 int k_padded, int act_type, void *stream) {                      \
+    moe_gemv_gate_up_t<T>(gate_weights, up_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, \
+                          act_type, stream, "moe_gemv_fused_gate_up_" #rt);                                       \
+  }                                                                                                               \
+  void launch_moe_gemv_down_aggregate_##rt##_q8_1(const void *all_weights, const void *all_inputs,                \
+                                                  const uint32_t *indices, const float *topk_weights,             \
+                                                  float *all_outputs, int n, int k, int batch, int topk,          \
+                                                  int k_padded, void *stream) {                                   \
+    moe_gemv_down_aggregate_t<T>(all_weights, all_inputs, indices, topk_weights, all_outputs, n, k, batch, topk,  \
+                                 k_padded, stream, "moe_gemv_down_aggregate_" #rt);                               \
   }
-QMM_DEFINE_MOE_WSUM(q8_0, QMM_TYPE_Q8_0)
-QMM_DEFINE_MOE_WSUM(q4_k, QMM_TYPE_Q4K)
-QMM_DEFINE_MOE_WSUM(q6_k, QMM_TYPE_Q6K)
-#undef QMM_DEFINE_MOE_WSUM
 
-void launch_indexed_moe_forward_q8_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                          int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q8_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q8_0");
-}
-void launch_indexed_moe_forward_q4k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                        int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q4K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q4k");
-}
-void launch_indexed_moe_forward_q6k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                        int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q6K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q6k");
-}
-void launch_indexed_moe_forward_q4_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                          int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q4_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q4_0");
-}
-void launch_indexed_moe_forward_q5_0_q8_0(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                          float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                          int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q5_0, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q5_0");
-}
-void launch_indexed_moe_forward_q5k_q8k(const void *all_weights, const void *all_inputs, const uint32_t *indices,
-                                        float *all_outputs, int n, int k, int batch, int topk, int k_padded,
-                                        int input_dim1, void *stream) {
-  indexed(QMM_TYPE_Q5K, all_weights, all_inputs, indices, all_outputs, n, k, batch, topk, k_padded, input_dim1,
-          stream, "indexed_moe_q5k");
-}
-}
-
+// launch_mmvq_tc_gguf_<t>_{f32,f16,bf16}_plain
+#define QMM_MMVQ_TC_DT(t, T, dt, Out)                                                                              \
+  void launch_mmvq_tc_gguf_##t##_##dt##_plain(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, \
+                                              int stride_col_dst, int b_size, int cfg, void *stream) {            \
+    tc_plain_t<T, Out>(vx, vy, dst, ncols_x, nrows_x, stride_col_dst, b_size, cfg, stream, "mmvq_tc_" #t "_" #dt); \
+  }
+#define QMM_MMVQ_TC(t, T)               \
+  QMM_MMVQ_TC_DT(t, T, f32, out_f32)    \
+  QMM_MMVQ_TC_DT(t, T, f16, out_f16)    \
+  QMM_MMVQ_TC_DT(t, T, bf16, out_bf16)

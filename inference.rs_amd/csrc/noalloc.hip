@@ -19,11 +19,6 @@ constexpr size_t kActBytes = (size_t)16 << 20;
 constexpr size_t kFixupBytes = (size_t)16 << 20;
 constexpr size_t kScratchBytes = kActBytes + kFixupBytes;
 constexpr int kMaxDevices = 64;
-// the host QMatMul's decode / prefill boundary (QMatMul::max_decode_rows): 32 rows for Q4_K and for Q6_K rows of
-// at most 8192 values (the few-row MFMA kernel), 16 otherwise
-int64_t decode_rows(int type, int64_t k) {
-  return type == QMM_TYPE_Q4K || (type == QMM_TYPE_Q6K && k <= 8192) ? 32 : 16;
-}
 }  // namespace
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
@@ -61,35 +56,36 @@ typedef void (*mmvq_q_fn)(const void *, const float *, void *, int, int, int, in
 typedef void (*mmq_fn)(void *, const void *, const void *, void *, int64_t, int64_t, int64_t, int64_t, int64_t, int,
                        int, int64_t, int, int, void *);
 
+// activation geometry as the host layer's: Q8_0 blocks (34 bytes per 32 values) for the 32-value types, Q8_1 slots
+// (288 bytes per 256) for the rest; stride_col_y in 32-value blocks either way; prefill tiles 272 or 276 bytes per 256
 bool act_q8_0(int w) { return qmm_vec_dot_type(w) == QMM_TYPE_Q8_0; }
 int64_t act_block(int w) { return act_q8_0(w) ? 32 : 256; }
-int64_t act_block_bytes(int w) { return act_q8_0(w) ? 34 : 292; }
-int64_t tile_bytes_per_256(int w) { return act_q8_0(w) ? 272 : 292; }
+int64_t act_row_bytes(int w, int64_t kp) { return act_q8_0(w) ? kp / 32 * 34 : kp / 256 * 288; }
+int64_t tile_bytes_per_256(int w) { return act_q8_0(w) ? 272 : 276; }
 int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 bool has_all_routes(int t) { return t == QMM_TYPE_Q8_0 || t == QMM_TYPE_Q4K || t == QMM_TYPE_Q6K; }
 
 quant_fn decode_quantizer(int w, int in) {
   const bool k = !act_q8_0(w);
   switch (in) {
-    case QMM_TYPE_F32: return k ? launch_mmvq_gguf_quantize_q8k_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
-    case QMM_TYPE_F16: return k ? launch_mmvq_gguf_quantize_q8k_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
-    default: return k ? launch_mmvq_gguf_quantize_q8k_bf16 : launch_mmvq_gguf_quantize_q8_0_bf16;
+    case QMM_TYPE_F32: return k ? launch_mmvq_gguf_quantize_q8_1_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
+    case QMM_TYPE_F16: return k ? launch_mmvq_gguf_quantize_q8_1_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
+    default: return k ? launch_mmvq_gguf_quantize_q8_1_bf16 : launch_mmvq_gguf_quantize_q8_0_bf16;
   }
 }
 
 mmvq_fn decode_matvec(int w, int out) {
-#define QMM_PICK(t)                                               \
-  return out == QMM_TYPE_F32   ? launch_mmvq_gguf_##t##_f32_plain \
-         : out == QMM_TYPE_F16 ? launch_mmvq_gguf_##t##_f16_plain \
-                               : launch_mmvq_gguf_##t##_bf16_plain;
+#define QMM_PICK(t, sfx)                                                \
+  return out == QMM_TYPE_F32   ? launch_mmvq_gguf_##t##_f32_plain##sfx \
+         : out == QMM_TYPE_F16 ? launch_mmvq_gguf_##t##_f16_plain##sfx \
+                               : launch_mmvq_gguf_##t##_bf16_plain##sfx;
   switch (w) {
-    case QMM_TYPE_Q8_0: QMM_PICK(q8_0)
-    case QMM_TYPE_Q4K: QMM_PICK(q4_k)
-    case QMM_TYPE_Q6K: QMM_PICK(q6_k)
-    case QMM_TYPE_Q4_0: QMM_PICK(q4_0)
-    case QMM_TYPE_Q5_0: QMM_PICK(q5_0)
-    case QMM_TYPE_Q5K: QMM_PICK(q5_k)
-    default: QMM_PICK(iq4_xs)
+    case QMM_TYPE_Q8_0: QMM_PICK(q8_0, _q8_0)
+    case QMM_TYPE_Q4K: QMM_PICK(q4_k, )
+    case QMM_TYPE_Q6K: QMM_PICK(q6_k, )
+    case QMM_TYPE_Q4_0: QMM_PICK(q4_0, _q8_0)
+    case QMM_TYPE_Q5_0: QMM_PICK(q5_0, _q8_0)
+    default: QMM_PICK(q5_k, )
   }
 #undef QMM_PICK
 }
@@ -104,18 +100,19 @@ mmvq_q_fn decode_matvec_quantize(int w) {
 
 mmq_fn prefill_matmul(int w) {
   switch (w) {
-    case QMM_TYPE_Q8_0: return launch_mmq_gguf_q8_0;
+    case QMM_TYPE_Q8_0: return launch_mmq_gguf_q8_0_q8_0;
     case QMM_TYPE_Q4K: return launch_mmq_gguf_q4_k;
     case QMM_TYPE_Q6K: return launch_mmq_gguf_q6_k;
-    case QMM_TYPE_Q4_0: return launch_mmq_gguf_q4_0;
-    case QMM_TYPE_Q5_0: return launch_mmq_gguf_q5_0;
-    case QMM_TYPE_Q5K: return launch_mmq_gguf_q5_k;
-    default: return nullptr;  // IQ4_XS: matvec route only
+    case QMM_TYPE_Q4_0: return launch_mmq_gguf_q4_0_q8_0;
+    case QMM_TYPE_Q5_0: return launch_mmq_gguf_q5_0_q8_0;
+    default: return launch_mmq_gguf_q5_k;
   }
 }
 
+// the weight types the host QMatMul serves (IQ4_XS, which the reference's QTensor does not hold, is refused there
+// and here)
 bool supported(int t) {
-  return has_all_routes(t) || t == QMM_TYPE_Q4_0 || t == QMM_TYPE_Q5_0 || t == QMM_TYPE_Q5K || t == QMM_TYPE_IQ4_XS;
+  return has_all_routes(t) || t == QMM_TYPE_Q4_0 || t == QMM_TYPE_Q5_0 || t == QMM_TYPE_Q5K;
 }
 
 // returns 0, or -1 with the error recorded
@@ -145,10 +142,10 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
   }
   uint8_t *ptr = scratch_ptr();
   if (!ptr) return -1;
-  const int64_t per = decode_rows(wtype, k);
-  if (rows <= per || !mm) {
+  const int64_t per = qmm_max_decode_rows(wtype, k);
+  if (rows <= per) {
     const int64_t kp = pad_to(k, act_block(wtype));
-    const int64_t row_bytes = kp / act_block(wtype) * act_block_bytes(wtype);
+    const int64_t row_bytes = act_row_bytes(wtype, kp);
     if (rows * row_bytes > (int64_t)kActBytes) {
       qmm_set_error("qmatmul_forward_noalloc: %lld x %lld activations need %lld bytes of scratch, above the %zu held",
                     (long long)rows, (long long)k, (long long)(rows * row_bytes), kActBytes);
@@ -159,7 +156,7 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
     for (int64_t r0 = 0; r0 < rows; r0 += per) {
       const int64_t b = rows - r0 < per ? rows - r0 : per;
       decode_matvec(wtype, in_dtype)(w, ptr + r0 * row_bytes, (uint8_t *)ys + r0 * n * out_elem, (int)k, (int)n,
-                                     (int)(kp / act_block(wtype)), (int)n, (int)b, stream);
+                                     (int)(kp / 32), (int)n, (int)b, stream);
     }
     return 0;
   }
@@ -170,9 +167,12 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
                   (long long)rows, (long long)k, (long long)act, kActBytes);
     return -1;
   }
-  (act_q8_0(wtype) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(xs, nullptr, ptr, in_dtype, k, k, k * rows,
-                                                                           k * rows, kp, rows, 1, 1, stream);
-  // the fixup region holds nsm * 128 * 128 f32 for nsm up to 256; a device with more compute units splits K less
+  (act_q8_0(wtype) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(xs, nullptr, ptr, in_dtype, k, k,
+                                                                               k * rows, k * rows, kp, rows, 1, 1,
+                                                                               stream);
+  // the fixup region holds nsm * 128 * 128 f32 for nsm up to 256 (MI355X has 256 compute units); a device with more
+  // would split K less than the host layer does, and its output would then differ from QMatMul::forward's in the f32
+  // summation order
   const int nsm = qmm_device_cus() < (int)(kFixupBytes / 65536) ? qmm_device_cus() : (int)(kFixupBytes / 65536);
   mm(ptr + kActBytes, w, ptr, ys, k, n, rows, k / (int64_t)qmm_block_size(wtype), n, 0, nsm, 160 * 1024, 64, in_dtype,
      stream);

@@ -52,6 +52,27 @@ __device__ __forceinline__ void q6_lanes(uint32_t ql, uint32_t qh, int hsh, s2 &
   hi = __builtin_bit_cast(s2, __builtin_amdgcn_perm(0u, v6, 0x0c030c01u));
 }
 
+// The Q4_K / Q5_K min term sum_j m_j * S_j goes through an f16 MFMA, exact in f32.  The activation sums of 32 values
+// S_j (int16, |S| <= 4064) are not exact in f16, so each is split as S = 64 h + l, l in [0, 63], h in [-64, 63],
+// both exact, and the weight side carries (64 m_j, m_j).  The halves come from the f16 bit patterns of 1024 + v
+// (0x6400 + v for 0 <= v < 1024) less 1024 in packed f16 arithmetic.  For one dword of two sums (S_a low, S_b high):
+// hpair = (f16 h_a, f16 h_b), lpair = (f16 l_a, f16 l_b).  The A fragment of sub-blocks (a, b, c, d) is
+// (h_a, h_b, l_a, l_b, h_c, h_d, l_c, l_d) and the B fragment (64 m_a, 64 m_b, m_a, m_b, 64 m_c, 64 m_d, m_c, m_d).
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void s32_split(uint32_t sums, uint32_t &hpair, uint32_t &lpair) {
+  const s2 h = (__builtin_bit_cast(s2, sums) >> (s2){6, 6}) + (s2){0x6440, 0x6440};  // 0x6400 + (h + 64)
+  const uint32_t l = (sums & 0x003f003fu) | 0x64006400u;                              // 0x6400 + l
+  hpair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, h) - (h2){(_Float16)1088.0f, (_Float16)1088.0f});
+  lpair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, l) - (h2){(_Float16)1024.0f, (_Float16)1024.0f});
+}
+// the A fragment of four sub-blocks from their two dwords of sums
+__device__ __forceinline__ v8h min_frag(uint32_t s01, uint32_t s23) {
+  uint32_t f[4];
+  s32_split(s01, f[0], f[1]);
+  s32_split(s23, f[2], f[3]);
+  return __builtin_bit_cast(v8h, (u32x4){f[0], f[1], f[2], f[3]});
+}
+
 // Row of 32x32 output register r of lane group g (v_mfma 32x32 D layout): 8 (r / 4) + 4 g + r % 4
 __device__ __forceinline__ int out_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
@@ -104,14 +125,15 @@ struct wq4k {
     auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
     p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
     p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
-    // B operand of the min-term MFMA: k = 8g + b <-> bsum16 index 8g + b <-> sub-block 4g + b / 2, whose 6-bit
-    // min is byte(4 + i) & 63 (g = 0) or (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4) (g = 1), i = b / 2
+    // B operand of the min-term MFMA for sub-blocks 4g + i (i = 0..3), whose 6-bit min is byte(4 + i) & 63 (g = 0)
+    // or (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4) (g = 1): k = 8g + 4 (i / 2) + i % 2 holds 64 m, two further
+    // on m (min_frag's order)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t lo = byte(4 + i) & 63, hi = (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4);
-      const _Float16 m = (_Float16)(float)(g ? hi : lo);
-      p.bmin[2 * i] = m;
-      p.bmin[2 * i + 1] = m;
+      const uint32_t m = g ? hi : lo;
+      p.bmin[4 * (i >> 1) + (i & 1)] = (_Float16)(float)(64 * m);
+      p.bmin[4 * (i >> 1) + (i & 1) + 2] = (_Float16)(float)m;
     }
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
@@ -427,7 +449,7 @@ struct wq4k16 {
     }
     p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
     p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
-    // min-term B: bsum16 index 4kg + i <-> sub-block 2kg + i / 2
+    // min-term B of sub-blocks 2kg, 2kg + 1: (64 m0, 64 m1, m0, m1), min_frag's order
     uint32_t m0 = m[0], m1 = m[1];
 #pragma unroll
     for (int q = 1; q < 4; q++)
@@ -435,8 +457,7 @@ struct wq4k16 {
         m0 = m[2 * q];
         m1 = m[2 * q + 1];
       }
-    const _Float16 h0 = (_Float16)(float)m0, h1 = (_Float16)(float)m1;
-    p.bmin = (v4h){h0, h0, h1, h1};
+    p.bmin = (v4h){(_Float16)(float)(64 * m0), (_Float16)(float)(64 * m1), (_Float16)(float)m0, (_Float16)(float)m1};
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int t, v4i &b1, v4i &b2, int) {
     const u32x4 q = r.q[t >> 1];

@@ -10,37 +10,41 @@
 
 namespace qmm_q8 {
 
-// Output addressing of one 256-value Q8_K block: decode layout (array of qmm_block_q8k, bsums int16), the
-// tensor-core entries' layout (no bsums) or the prefill tile layout (qs[nsb][rows][256], d[nsb][rows] f32, bsums[nsb][rows][16] as f16, which holds every
-// bsum exactly: |bsum| <= 16 * 128 = 2048).
+// Output addressing of one 256-value Q8_K block:
+//   decode   the 292-byte qmm_block_q8k (int16 bsums of 16), the one-launch matvec's LDS copy
+//   tc       the tensor-core entries' {f32 d; int8 qs[256]} of 260 bytes (no sums)
+//   slot     the 288-byte qmm_block_q8ks of the reference-named decode entries: int16 sums of each 32, 12 zero bytes
+//   tile     the prefill layout of one channel: qs[nsb][rows][256], d[nsb][rows] f32, s32[nsb][rows][8] int16 sums of
+//            each 32 (276 bytes per 256 values)
 struct q8k_dst {
   uint8_t *qs;
   float *d;
-  uint16_t *bsums;
-  bool bsums_f16;
+  uint16_t *bsums;  // int16 sums of 16 values
+  int16_t *s32;     // int16 sums of 32 values
+  uint32_t *pad;    // three dwords set to zero
 };
 
 __device__ __forceinline__ q8k_dst q8k_decode_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8k);
-  return {b + 4, (float *)b, (uint16_t *)(b + 260), false};
+  return {b + 4, (float *)b, (uint16_t *)(b + 260), nullptr, nullptr};
 }
 
-// tensor-core entry layout: {f32 d; int8 qs[256]} blocks of 260 bytes, no bsums
 __device__ __forceinline__ q8k_dst q8k_tc_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * 260;
-  return {b + 4, (float *)b, nullptr, false};
+  return {b + 4, (float *)b, nullptr, nullptr, nullptr};
+}
+
+__device__ __forceinline__ q8k_dst q8k_slot_dst(uint8_t *vy, int64_t block) {
+  uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8ks);
+  return {b + 4, (float *)b, nullptr, (int16_t *)(b + 260), (uint32_t *)(b + 276)};
 }
 
 __device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
   const int64_t i = sb * rows + r;
   uint8_t *qs = chan + i * 256;
   float *d = (float *)(chan + nsb * rows * 256) + i;
-  uint16_t *bs = (uint16_t *)(chan + nsb * rows * 260) + i * 16;
-  return {qs, d, bs, true};
-}
-
-__device__ __forceinline__ uint16_t bsum_bits(int s, bool f16) {
-  return f16 ? f32_to_f16_bits((float)s) : (uint16_t)(int16_t)s;
+  int16_t *s32 = (int16_t *)(chan + nsb * rows * 260) + i * 8;
+  return {qs, d, nullptr, s32, nullptr};
 }
 
 // One wave quantizes G blocks: v[t][0..3] of lanes 0..63 are values 4*lane .. 4*lane+3 of block t, written to
@@ -82,12 +86,16 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
     int q[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) q[i] = nz ? sat_i8(roundf(iscale * x[i])) : 0;
-    const int s = quad_sum(q[0] + q[1] + q[2] + q[3]);
+    const int s = quad_sum(q[0] + q[1] + q[2] + q[3]);  // values 16 (lane / 4) .. +16
+    // row_shr:4: lane 8i + 4 adds the sum of the quad before it, values 32 i .. +32
+    const int s32 = s + __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xf, false);
     if (!store[t]) continue;
     const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *(uint32_t *)(dst[t].qs + 4 * lane) = packed;
-    if ((lane & 3) == 0 && dst[t].bsums) dst[t].bsums[lane >> 2] = bsum_bits(s, dst[t].bsums_f16);  // +0 for a zero block
+    if ((lane & 3) == 0 && dst[t].bsums) dst[t].bsums[lane >> 2] = (uint16_t)(int16_t)s;  // +0 for a zero block
+    if ((lane & 7) == 4 && dst[t].s32) dst[t].s32[lane >> 3] = (int16_t)s32;
+    if (lane < 3 && dst[t].pad) dst[t].pad[lane] = 0u;
     if (lane == 0) *dst[t].d = nz ? 1.0f / iscale : 0.0f;
   }
 }

@@ -15,9 +15,11 @@ using namespace qmm_q8;
 
 // ------------------------------------------------------------------ decode layout kernels
 
+// the reference-named decode layout: rows of kx_padded / 256 qmm_block_q8ks (288 bytes: d, qs, int16 sums of 32)
 template <class In>
-__global__ __launch_bounds__(256) void k_quantize_q8k_rows(const typename In::T *__restrict__ x, uint8_t *__restrict__ vy,
-                                                           int kx, int kx_padded, int num_rows) {
+__global__ __launch_bounds__(256) void k_quantize_q8ks_rows(const typename In::T *__restrict__ x,
+                                                            uint8_t *__restrict__ vy, int kx, int kx_padded,
+                                                            int num_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t nsb = kx_padded / 256;
   const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -25,7 +27,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8k_rows(const typename In::T 
   const int64_t row = blk / nsb, sb = blk % nsb;
   float v[4];
   load4<In>(x + row * (int64_t)kx, sb * 256 + lane * 4, kx, v);
-  q8k_wave(v, lane, q8k_decode_dst(vy, blk));
+  q8k_wave(v, lane, q8k_slot_dst(vy, blk));
 }
 
 // the tensor-core entries' layout: rows of kx / 256 blocks {f32 d; int8 qs[256]}
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8k_tiles(const typename In::T
   const int64_t src_row = ids ? ids[r] : r;
   float v[4];
   load4<In>(x + i3 * s03 + i2 * s02 + src_row * s01, sb * 256 + lane * 4, ne00, v);
-  q8k_wave(v, lane, q8k_tile_dst(vy + ch * per_chan * 292, ne1, nsb, sb, r));
+  q8k_wave(v, lane, q8k_tile_dst(vy + ch * per_chan * 276, ne1, nsb, sb, r));
 }
 
 template <class In>
@@ -104,8 +106,29 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_tiles(const typename In::
 }
 
 // act(gate) * up of row ids[r] (or r), quantized into the prefill tile layout: the fused GLU requantization
-// between the gate/up and down matmuls (mmq_gguf/mmq_quantize.cu:238-330).
-__global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const float *__restrict__ gate, const float *__restrict__ up,
+// between the gate/up and down matmuls (mmq_gguf/mmq_quantize.cu:230-330).  f32 inputs: act(gate) * up in f32;
+// f16 / bf16 inputs: act(gate) rounded to the input type, times up, rounded again, as the reference's
+// mmq_glu_product<input_t> (mmq_quantize.cu:230-235).
+template <class In>
+__device__ __forceinline__ float glu_product(float g, float u, int activation);
+template <>
+__device__ __forceinline__ float glu_product<in_f32>(float g, float u, int activation) {
+  return glu_act(activation, g) * u;
+}
+template <>
+__device__ __forceinline__ float glu_product<in_f16>(float g, float u, int activation) {
+  const float a = f16_bits_to_f32(f32_to_f16_bits(glu_act(activation, g)));
+  return f16_bits_to_f32(f32_to_f16_bits(a * u));  // the product of two f16 is exact in f32: one rounding
+}
+template <>
+__device__ __forceinline__ float glu_product<in_bf16>(float g, float u, int activation) {
+  const float a = bf16_bits_to_f32(f32_to_bf16_bits(glu_act(activation, g)));
+  return bf16_bits_to_f32(f32_to_bf16_bits(a * u));
+}
+
+template <class In>
+__global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const typename In::T *__restrict__ gate,
+                                                                const typename In::T *__restrict__ up,
                                                                 const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
                                                                 int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1,
                                                                 int activation, int64_t nblk) {
@@ -119,7 +142,7 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const float *__r
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int64_t k = sb * 256 + lane * 4 + i;
-    v[i] = k < ne00 ? glu_act(activation, gate[src + k]) * up[src + k] : 0.0f;
+    v[i] = k < ne00 ? glu_product<In>(In::load(gate, src + k), In::load(up, src + k), activation) : 0.0f;
   }
   q8k_wave(v, lane, q8k_tile_dst(vy, ne1, nsb, sb, r));
 }
@@ -149,15 +172,15 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8_0_tiles(const float *__
 }
 
 template <class In>
-void decode_q8k(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+void decode_q8ks(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
   if (kx < 0 || num_rows < 0 || kx_padded % 256 != 0 || kx_padded < kx) {
-    qmm_set_error("quantize_q8k: kx=%d kx_padded=%d num_rows=%d (kx_padded must be a multiple of 256, >= kx)", kx,
+    qmm_set_error("quantize_q8_1: kx=%d kx_padded=%d num_rows=%d (kx_padded must be a multiple of 256, >= kx)", kx,
                   kx_padded, num_rows);
     return;
   }
   const int64_t blocks = (int64_t)kx_padded / 256 * num_rows;
   if (blocks == 0) return;
-  k_quantize_q8k_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
+  k_quantize_q8ks_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
       (const typename In::T *)x, (uint8_t *)vy, kx, kx_padded, num_rows);
 }
 
@@ -195,18 +218,24 @@ bool tile_args_ok(const char *who, int64_t ne00, int64_t ne0, int64_t ne1, int64
   return true;
 }
 
+// The prefill tiles hold ceil(ne00 / 256) super-blocks per row, whatever ne0 (the caller's k_padded, a multiple of 256
+// at least ne00): the matmuls are handed K, not k_padded, and read that many.  A reference caller pads K to 512
+// (fast_mmq.rs) and sizes its scratch for that; the super-blocks past ceil(K / 256), all zeros there, are neither
+// written nor read here.
+int64_t tile_width(int64_t ne00) { return (ne00 + 255) / 256 * 256; }
+
 }  // namespace
 
 extern "C" {
 
-void launch_mmvq_gguf_quantize_q8k_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
-  decode_q8k<in_f32>(x, vy, kx, kx_padded, num_rows, stream);
+void launch_mmvq_gguf_quantize_q8_1_f32(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8ks<in_f32>(x, vy, kx, kx_padded, num_rows, stream);
 }
-void launch_mmvq_gguf_quantize_q8k_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
-  decode_q8k<in_f16>(x, vy, kx, kx_padded, num_rows, stream);
+void launch_mmvq_gguf_quantize_q8_1_f16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8ks<in_f16>(x, vy, kx, kx_padded, num_rows, stream);
 }
-void launch_mmvq_gguf_quantize_q8k_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
-  decode_q8k<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
+void launch_mmvq_gguf_quantize_q8_1_bf16(const void *x, void *vy, int kx, int kx_padded, int num_rows, void *stream) {
+  decode_q8ks<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
 }
 void launch_mmvq_tc_quantize_f32(const void *x, void *vy, int kx, int num_rows, void *stream) {
   tc_q8k<in_f32>(x, vy, kx, num_rows, stream);
@@ -228,81 +257,129 @@ void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx
   decode_q8_0<in_bf16>(x, vy, kx, kx_padded, num_rows, stream);
 }
 
-void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
-                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
-                             void *stream) {
-  if (!tile_args_ok("mmq_quantize_q8k", ne00, ne0, ne1, ne2, ne3)) return;
-  const int64_t nblk = ne0 / 256 * ne1 * ne2 * ne3;
+}  // extern "C"
+
+namespace {
+void mmq_quantize_q8ks(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01, int64_t s02,
+                       int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, void *stream) {
+  if (!tile_args_ok("mmq_quantize_q8_1", ne00, ne0, ne1, ne2, ne3)) return;
+  const int64_t kt = tile_width(ne00);
+  const int64_t nblk = kt / 256 * ne1 * ne2 * ne3;
   if (nblk == 0) return;
   const dim3 grid((unsigned)qmm_ceil_div(nblk, 4));
   hipStream_t s = (hipStream_t)stream;
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
-      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2, nblk);
+      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, ne2, nblk);
       break;
     case QMM_TYPE_F16:
-      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2,
+      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1, ne2,
                                                         nblk);
       break;
     case QMM_TYPE_BF16:
-      k_quantize_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+      k_quantize_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
                                                          ne2, nblk);
       break;
-    default: qmm_set_error("mmq_quantize_q8k: unsupported input type %d", type_x);
+    default: qmm_set_error("mmq_quantize_q8_1: unsupported input type %d", type_x);
   }
 }
+
+void mmq_quantize_glu_q8ks(const void *gate, const void *up, const int32_t *ids, void *vy, int type_x, int64_t ne00,
+                           int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
+  if (!tile_args_ok("mmq_quantize_glu_q8_1", ne00, ne0, ne1, 1, 1)) return;
+  const int64_t kt = tile_width(ne00);
+  if (activation < 0 || activation >= kGluActivations) {
+    qmm_set_error("mmq_quantize_glu_q8_1: activation %d", activation);
+    return;
+  }
+  const int64_t nblk = kt / 256 * ne1;
+  if (nblk == 0) return;
+  const dim3 grid((unsigned)qmm_ceil_div(nblk, 4));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t *y = (uint8_t *)vy;
+  switch (type_x) {
+    case QMM_TYPE_F32:
+      k_quantize_glu_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)gate, (const float *)up, ids, y, ne00, s01,
+                                                            kt, ne1, activation, nblk);
+      break;
+    case QMM_TYPE_F16:
+      k_quantize_glu_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y, ne00,
+                                                            s01, kt, ne1, activation, nblk);
+      break;
+    case QMM_TYPE_BF16:
+      k_quantize_glu_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y,
+                                                             ne00, s01, kt, ne1, activation, nblk);
+      break;
+    default: qmm_set_error("mmq_quantize_glu_q8_1: unsupported input type %d", type_x);
+  }
+}
+}  // namespace
+
+extern "C" {
+
+// The three scale layouts the reference's MMQ kernels distinguish (fast_mmq.rs:160-200) write one layout here:
+// every prefill kernel of this library reads the same tile layout.
+#define QMM_DEFINE_MMQ_Q8_1(L)                                                                                      \
+  void launch_mmq_quantize_q8_1_##L(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00,         \
+                                    int64_t s01, int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2,  \
+                                    int64_t ne3, void *stream) {                                                   \
+    mmq_quantize_q8ks(x, ids, vy, type_x, ne00, s01, s02, s03, ne0, ne1, ne2, ne3, stream);                        \
+  }                                                                                                                \
+  void launch_mmq_quantize_glu_q8_1_##L##_f32(const float *gate, const float *up, const int32_t *ids, void *vy,    \
+                                              int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1, int activation, \
+                                              void *stream) {                                                      \
+    mmq_quantize_glu_q8ks(gate, up, ids, vy, QMM_TYPE_F32, ne00, s01, ne0, ne1, activation, stream);               \
+  }                                                                                                                \
+  void launch_mmq_quantize_glu_q8_1_##L(const void *gate, const void *up, const int32_t *ids, void *vy, int type_x, \
+                                        int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1, int activation,       \
+                                        void *stream) {                                                            \
+    mmq_quantize_glu_q8ks(gate, up, ids, vy, type_x, ne00, s01, ne0, ne1, activation, stream);                     \
+  }
+QMM_DEFINE_MMQ_Q8_1(D4)
+QMM_DEFINE_MMQ_Q8_1(DS4)
+QMM_DEFINE_MMQ_Q8_1(D2S6)
+#undef QMM_DEFINE_MMQ_Q8_1
 
 void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
                               int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
                               void *stream) {
   if (!tile_args_ok("mmq_quantize_q8_0", ne00, ne0, ne1, ne2, ne3)) return;
-  const int64_t nblk = ne0 / 32 * ne1 * ne2 * ne3;
+  const int64_t kt = tile_width(ne00);
+  const int64_t nblk = kt / 32 * ne1 * ne2 * ne3;
   if (nblk == 0) return;
   const dim3 grid((unsigned)qmm_ceil_div(nblk, 32));
   hipStream_t s = (hipStream_t)stream;
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
-      k_quantize_q8_0_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, ne0, ne1, ne2,
+      k_quantize_q8_0_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, ne2,
                                                          nblk);
       break;
     case QMM_TYPE_F16:
-      k_quantize_q8_0_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+      k_quantize_q8_0_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
                                                          ne2, nblk);
       break;
     case QMM_TYPE_BF16:
-      k_quantize_q8_0_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, ne0, ne1,
+      k_quantize_q8_0_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
                                                           ne2, nblk);
       break;
     default: qmm_set_error("mmq_quantize_q8_0: unsupported input type %d", type_x);
   }
 }
 
-void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
-                                     int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
-  if (!tile_args_ok("mmq_quantize_glu_q8k", ne00, ne0, ne1, 1, 1)) return;
-  if (activation < 0 || activation >= kGluActivations) {
-    qmm_set_error("mmq_quantize_glu_q8k: activation %d", activation);
-    return;
-  }
-  const int64_t nblk = ne0 / 256 * ne1;
-  if (nblk == 0) return;
-  k_quantize_glu_q8k_tiles<<<dim3((unsigned)qmm_ceil_div(nblk, 4)), 256, 0, (hipStream_t)stream>>>(
-      gate, up, ids, (uint8_t *)vy, ne00, s01, ne0, ne1, activation, nblk);
-}
-
 void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
                                       int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
   if (!tile_args_ok("mmq_quantize_glu_q8_0", ne00, ne0, ne1, 1, 1)) return;
+  const int64_t kt = tile_width(ne00);
   if (activation < 0 || activation >= kGluActivations) {
     qmm_set_error("mmq_quantize_glu_q8_0: activation %d", activation);
     return;
   }
-  const int64_t nblk = ne0 / 32 * ne1;
+  const int64_t nblk = kt / 32 * ne1;
   if (nblk == 0) return;
   k_quantize_glu_q8_0_tiles<<<dim3((unsigned)qmm_ceil_div(nblk, 32)), 256, 0, (hipStream_t)stream>>>(
-      gate, up, ids, (uint8_t *)vy, ne00, s01, ne0, ne1, activation, nblk);
+      gate, up, ids, (uint8_t *)vy, ne00, s01, kt, ne1, activation, nblk);
 }
 
 }  // extern "C"

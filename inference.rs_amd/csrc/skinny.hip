@@ -33,16 +33,17 @@ namespace {
 #define QMM_SKINNY_WIDE_TILES 384
 #endif
 
-// A-side fragments of one superblock for activation row li: 8 x 16 int8 (k = 32j + 16g + 0..15), the 8 bsums of
-// 16 values 8g .. 8g + 7 as f16, and the row's scale d.
+// A-side fragments of one superblock for activation row li: 8 x 16 int8 (k = 32j + 16g + 0..15), the min-term
+// operand of sub-blocks 4g .. 4g + 3 (planes.h min_frag: their 32-value sums split as 64 h + l, in f16), and the
+// row's scale d.
 struct ActFrag {
   v4i q[8];
   v8h bs;
   float d;
 };
 
-// Decode layout: row m = blocks [m * stride, ...) of 292-byte qmm_block_q8k (f32 d, int8 qs[256], int16 bsums[16]).
-struct act_decode {
+// Q8_1-slot layout (units.h): row m = 288-byte slots {f32 d; int8 qs[256]; int16 s32[8]; pad}, row_bytes apart.
+struct act_slot {
   const uint8_t *base;
   int64_t bytes;
   uint32_t row_bytes;
@@ -52,26 +53,21 @@ struct act_decode {
     return valid ? (uint32_t)m * row_bytes : 0x80000000u;
   }
   __device__ __forceinline__ void load(rsrc_t r, uint32_t row_off, int64_t sb, int g, bool min, ActFrag &f) const {
-    const uint32_t o = row_off + (uint32_t)sb * 292;
+    const uint32_t o = row_off + (uint32_t)sb * kSlotBytes;
 #pragma unroll
     for (int j = 0; j < 8; j++)
       f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, o + 4 + 32 * j + 16 * g, 0, 0));
     if (min) {
-      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, o + 260 + 16 * g, 0, 0);
-      const uint32_t w[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {  // int16 -> f16, exact (|bsum| <= 2048)
-        f.bs[2 * i] = (_Float16)(float)(int16_t)(w[i] & 0xffff);
-        f.bs[2 * i + 1] = (_Float16)(float)(int16_t)(w[i] >> 16);
-      }
+      const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(r, o + 260 + 8 * g, 0, 0);  // sums of 4g .. 4g + 3
+      f.bs = min_frag(b.x, b.y);
     }
     f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
   }
 };
 
-// Tensor-core entry layout (units.h): row m = K / 256 blocks of 260 bytes {f32 d; int8 qs[256]}, no bsums.  Lane
-// (li, g) sums its own fragments -- q[j] is values 32 j + 16 g .. +16, bsum index 2 j + g -- and trades half of
-// them with its partner lane so that it ends with bsums 8 g .. 8 g + 7, the order act_decode loads them in.
+// Tensor-core entry layout (units.h): row m = K / 256 blocks of 260 bytes {f32 d; int8 qs[256]}, no sums.  Lane
+// (li, g) sums its own fragments -- q[j] is values 32 j + 16 g .. +16 -- and adds its partner lane's sum of the
+// other half of the same 32 values, so both lanes hold S_j; lane half g keeps sub-blocks 4g .. 4g + 3.
 struct act_tc {
   const uint8_t *base;
   int64_t bytes;
@@ -86,30 +82,32 @@ struct act_tc {
     for (int j = 0; j < 8; j++)
       f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, o + 4 + 32 * j + 16 * g, 0, 0));
     if (min) {
-      uint32_t s[8];
+      int s[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
         int acc = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) acc = sdot4(f.q[j][i], 0x01010101, acc);
-        s[j] = (uint32_t)acc;
+        s[j] = acc;
       }
-      // lo = own bsum 2i + g, hi = own bsum 2 (i + 4) + g; after the swap lane half g holds 8 g + 2i in lo and
-      // 8 g + 2i + 1 in hi
+      // s[j]: this lane's 16 values of sub-block j.  After the swap lane half 0 holds both lanes' sums of sub-block i
+      // and lane half 1 both lanes' sums of sub-block i + 4, so w[i] is the whole sum of sub-block 4g + i.
+      uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        swap_lane_halves(s[i], s[i + 4]);
-        f.bs[2 * i] = (_Float16)(float)(int)s[i];  // exact: |bsum| <= 2048
-        f.bs[2 * i + 1] = (_Float16)(float)(int)s[i + 4];
+        uint32_t pa = (uint32_t)s[i], pb = (uint32_t)s[i + 4];
+        swap_lane_halves(pa, pb);
+        w[i] = (uint32_t)((int)pa + (int)pb);
       }
+      f.bs = min_frag((w[0] & 0xffffu) | (w[1] << 16), (w[2] & 0xffffu) | (w[3] << 16));
     }
     f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
   }
 };
 
 // Prefill layout of one channel (include/inferencequant.h): qs[nsb][rows][256] int8, then d[nsb][rows] f32, then
-// bsums[nsb][rows][16] f16.  The handle is the lane's offset 256 m of row m inside one superblock's qs slab, with
-// bit 31 set for a row that reads as zero; the superblock's part of every offset is uniform and goes in the
+// s32[nsb][rows][8] int16 sums of 32.  The handle is the lane's offset 256 m of row m inside one superblock's qs slab,
+// with bit 31 set for a row that reads as zero; the superblock's part of every offset is uniform and goes in the
 // scalar offset, outside the range check, which the vector part alone fails for such a row.
 struct act_tiles {
   const uint8_t *base;
@@ -124,9 +122,10 @@ struct act_tiles {
 #pragma unroll
     for (int j = 0; j < 8; j++)
       f.q[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, h + 32 * j + 16 * g, 256 * srow, 0));
-    if (min)
-      f.bs = __builtin_bit_cast(v8h, __builtin_amdgcn_raw_buffer_load_b128(r, ((h >> 3) + 16 * g) | zero,
-                                                                           nsb * rows * 260 + 32 * srow, 0));
+    if (min) {
+      const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(r, ((h >> 4) + 8 * g) | zero, nsb * rows * 260 + 16 * srow, 0);
+      f.bs = min_frag(b.x, b.y);
+    }
     f.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (h >> 6) | zero,
                                                                           nsb * rows * 256 + 4 * srow, 0));
   }
@@ -288,8 +287,8 @@ struct Wt16<wq6k> {
 };
 
 // A-side fragments of one superblock for the 16x16x64 form: lane (kg, r) holds activation row r's values
-// act_offset(t, kg) .. +16 for the four steps, the bsums 4kg .. 4kg + 3 of row r as f16, and the scales of output
-// rows 4kg + i.
+// act_offset(t, kg) .. +16 for the four steps, the min-term operand of sub-blocks 2kg, 2kg + 1 of row r, and the
+// scales of output rows 4kg + i.
 struct ActFrag16 {
   v4i q[4];
   v4h bs;
@@ -300,7 +299,7 @@ struct ActFrag16 {
 // D[activation row 4kg + i][weight row r] (v_mfma 16x16 D layout).
 template <class WT, class Out, int NW>
 __global__ __launch_bounds__(64 * NW) void k_skinny16(const uint8_t *__restrict__ W, int64_t nrows_w,
-                                                      int64_t w_row_bytes, act_decode ap, int mrows, int64_t nsb,
+                                                      int64_t w_row_bytes, act_slot ap, int mrows, int64_t nsb,
                                                       typename Out::T *__restrict__ dst, int64_t ldd) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kg = lane >> 4, r = lane & 15;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
@@ -322,19 +321,19 @@ __global__ __launch_bounds__(64 * NW) void k_skinny16(const uint8_t *__restrict_
   ActFrag16 af[2];
   auto issue = [&](int64_t sb, int u) {
     WT::load(rw, wrow, (uint32_t)sb, kg, raw[u]);
-    const uint32_t o = arow + (uint32_t)sb * 292;
+    const uint32_t o = arow + (uint32_t)sb * kSlotBytes;
 #pragma unroll
     for (int t = 0; t < 4; t++)
       af[u].q[t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, o + 4 + WT::act_offset(t, kg), 0, 0));
-    if (WT::kMin) {
-      const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(ra, o + 260 + 8 * kg, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; i++)  // int16 -> f16, exact
-        af[u].bs[i] = (_Float16)(float)(int16_t)(((i < 2 ? b.x : b.y) >> (16 * (i & 1))) & 0xffff);
+    if (WT::kMin) {  // sums of sub-blocks 2kg, 2kg + 1, split as planes.h min_frag does
+      uint32_t hp, lp;
+      s32_split(__builtin_amdgcn_raw_buffer_load_b32(ra, o + 260 + 4 * kg, 0, 0), hp, lp);
+      af[u].bs = __builtin_bit_cast(v4h, (u32x2){hp, lp});
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      af[u].dy[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, dyrow[i] + (uint32_t)sb * 292, 0, 0));
+      af[u].dy[i] =
+          __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, dyrow[i] + (uint32_t)sb * kSlotBytes, 0, 0));
   };
   auto compute = [&](int u) {
     typename WT::Prep p;
@@ -385,8 +384,8 @@ template <class WT, class Out>
 void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, int ncols_x, int nrows_x,
                    int stride_col_y, int stride_col_dst, int b, int activation, hipStream_t s) {
   const int64_t nsb = ncols_x / 256;
-  act_decode ap;
-  ap.row_bytes = (uint32_t)stride_col_y * 292;
+  act_slot ap;
+  ap.row_bytes = (uint32_t)stride_col_y * 36;
   ap.base = (const uint8_t *)vy;
   ap.bytes = (int64_t)b * ap.row_bytes;
   const uint8_t *w = (const uint8_t *)vx, *w2 = (const uint8_t *)vx2;
@@ -394,10 +393,10 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
   const int64_t wrb = nsb * WT::kBytes;
   if (w2) {  // gate and up in one workgroup: 4 waves each
     if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
-      k_skinny<WT, act_decode, Out, 8, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 512, 0, s>>>(
+      k_skinny<WT, act_slot, Out, 8, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 512, 0, s>>>(
           w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation, moe_route{});
     else
-      k_skinny<WT, act_decode, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+      k_skinny<WT, act_slot, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
           w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation, moe_route{});
     return;
   }
@@ -415,13 +414,13 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
     return;
   }
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
-    k_skinny<WT, act_decode, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
+    k_skinny<WT, act_slot, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
   else if (nsb >= 32)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
-    k_skinny<WT, act_decode, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
+    k_skinny<WT, act_slot, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
   else
-    k_skinny<WT, act_decode, Out, 4, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
+    k_skinny<WT, act_slot, Out, 4, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 256, 0, s>>>(
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
 }
 
@@ -456,7 +455,7 @@ void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int3
   ap.base = (const uint8_t *)y;
   ap.rows = (uint32_t)ncols_dst;
   ap.nsb = (uint32_t)nsb;
-  ap.bytes = nsb * ncols_dst * 292;
+  ap.bytes = nsb * ncols_dst * 276;
   sum.col_tiles = (int32_t)qmm_ceil_div(nrows_x, 32);
   const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes, sum};
   const dim3 grid((unsigned)qmm_ceil_div(nrows_x, 32), (unsigned)chunks, (unsigned)num_experts);
@@ -477,7 +476,8 @@ void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int3
 
 bool dispatch(int type, int out_type, const void *vx, const void *vx2, const void *vy, void *dst, int ncols_x,
               int nrows_x, int stride_col_y, int stride_col_dst, int b, int activation, hipStream_t s) {
-  if (b < 1 || b > 32 || ncols_x % 256 != 0 || (int64_t)b * stride_col_y * 292 > 0x7ffffff0) return false;
+  if (b < 1 || b > 32 || ncols_x % 256 != 0 || stride_col_y % 8 != 0 || (int64_t)b * stride_col_y * 36 > 0x7ffffff0)
+    return false;
   if (type != QMM_TYPE_Q4K && type != QMM_TYPE_Q6K) return false;
 #define QMM_SK(WT)                                                                                              \
   switch (out_type) {                                                                                           \
@@ -538,7 +538,7 @@ bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_d
   if (ncols_x % 256 != 0 || ncols_dst <= 0 || num_experts <= 0 || num_experts > 65535) return false;
   if (ncols_dst > QMM_SKINNY_MOE_ROWS * num_experts) return false;
   const int64_t nsb = ncols_x / 256;
-  if (nsb * ncols_dst * 292 > 0x7ffffff0 || 32 * w_row_bytes > 0x7ffffff0) return false;
+  if (nsb * ncols_dst * 276 > 0x7ffffff0 || 32 * w_row_bytes > 0x7ffffff0) return false;
   // enough 32-row chunks for an expert of average size; larger experts loop over theirs
   const int64_t chunks = qmm_ceil_div(qmm_ceil_div(ncols_dst, num_experts), 32);
   if (type == QMM_TYPE_Q4K)

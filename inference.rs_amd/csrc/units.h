@@ -17,6 +17,8 @@
 //                                                   (inference-quant/src/gguf/cpu_dot.rs:416-440)
 #pragma once
 
+#include <initializer_list>
+
 #include "common.h"
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -691,3 +693,175 @@ struct unit_q6k_tc : unit_q6k {
     a.d = __builtin_bit_cast(float, ld32(p0));
   }
 };
+
+// ------------------------------------------------------------------------------------------------ Q8_1-slot layout
+// Activations of the reference-named decode entries (launch_mmvq_gguf_quantize_q8_1_* and every matvec that reads
+// them): the reference's Q8_1 scratch holds 36 bytes per 32 values (crates/inference-quant/src/gguf/fast_mmvq.rs:
+// 17-18, 534-542), 288 per 256, and the quantizer cannot know which weight type will read it.  Each 256 values are
+// one qmm_block_q8ks {f32 d; int8 qs[256]; int16 s32[8]; pad}: BlockQ8K::from_float's d and qs (bit-exact with the
+// CPU quantizer of the K-quant types) and the sums of each 32 of the qs.  The super-block types read it as their CPU
+// dot product does; the 32-value types (Q8_0, Q4_0, Q5_0), whose CPU dot products take Q8_0 blocks, read each 32
+// values of it as a block with the scale d of its 256 (the per-block f32 scaling is unchanged).
+constexpr int kSlotBytes = 288;
+
+struct unit_q4k_s : unit_q4k {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * kSlotBytes;
+    const int c = u & 3;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const u32x4 v = ld_a4(p + 4 + 64 * c + 16 * i);
+      a.q[4 * i + 0] = v.x;
+      a.q[4 * i + 1] = v.y;
+      a.q[4 * i + 2] = v.z;
+      a.q[4 * i + 3] = v.w;
+    }
+    const uint32_t s = ld32(p + 260 + 4 * c);  // sums of sub-blocks 2c, 2c + 1
+    a.b0 = (int)(int16_t)(s & 0xffff);
+    a.b1 = (int)(int16_t)(s >> 16);
+    a.d = __builtin_bit_cast(float, ld32(p));
+  }
+};
+struct unit_q5k_s : unit_q5k {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k_s::load_a(row, u, a); }
+};
+struct unit_iq4xs_s : unit_iq4xs {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) { unit_q4k_s::load_a(row, u, a); }
+};
+// Q6_K's 16-value sums are not in the slot: the unit sums its int8 values itself (as the tensor-core unit does)
+struct unit_q6k_s : unit_q6k {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p0 = row + (int64_t)(u >> 2) * kSlotBytes;
+    const int h = (u >> 1) & 1, p = u & 1;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const u32x4 v = ld_a4(p0 + 4 + 128 * h + 32 * q + 16 * p);
+      a.q[4 * q + 0] = v.x;
+      a.q[4 * q + 1] = v.y;
+      a.q[4 * q + 2] = v.z;
+      a.q[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) a.bs[q] = byte_sum(a.q + 4 * q, 4, 0);  // bsums[8h + 2q + p]
+    a.d = __builtin_bit_cast(float, ld32(p0));
+  }
+};
+
+// 32-value types: unit u (a block pair) is values 64 (u % 4) .. +64 of slot u / 4
+struct unit_q8_0_s : unit_q8_0 {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static constexpr int kActBlockValues = 256;
+  static __device__ __forceinline__ void load_qs(const uint8_t *p, uint32_t (&q)[8]) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const u32x4 v = ld_a4(p + 16 * i);
+      q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
+    }
+  }
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * kSlotBytes;
+    const int c = u & 3;
+    load_qs(p + 4 + 64 * c, a.qa);
+    load_qs(p + 36 + 64 * c, a.qb);
+    a.da = a.db = __builtin_bit_cast(float, ld32(p));
+  }
+};
+// one block per unit: values 32 (u % 8) .. +32 of slot u / 8
+struct unit_q8_0_odd_s : unit_q8_0_odd {
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static constexpr int kActBlockValues = 256;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 3) * kSlotBytes;
+    unit_q8_0_s::load_qs(p + 4 + 32 * (u & 7), a.q);
+    a.d = __builtin_bit_cast(float, ld32(p));
+  }
+};
+template <int T>
+struct unit_b32_s : unit_b32<T> {
+  using A = typename unit_b32<T>::A;
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static constexpr int kActBlockValues = 256;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 2) * kSlotBytes;
+    const int c = u & 3;
+    unit_q8_0_s::load_qs(p + 4 + 64 * c, a.qa);
+    unit_q8_0_s::load_qs(p + 36 + 64 * c, a.qb);
+    a.da = a.db = __builtin_bit_cast(float, ld32(p));
+    const uint32_t s = ld32(p + 260 + 4 * c);  // sums of the two blocks
+    a.sa = (int)(int16_t)(s & 0xffff);
+    a.sb = (int)(int16_t)(s >> 16);
+  }
+};
+template <int T>
+struct unit_b32_odd_s : unit_b32_odd<T> {
+  using A = typename unit_b32_odd<T>::A;
+  static constexpr int kActBlockBytes = kSlotBytes;
+  static constexpr int kActBlockValues = 256;
+  static __device__ __forceinline__ void load_a(const uint8_t *row, int u, A &a) {
+    const uint8_t *p = row + (int64_t)(u >> 3) * kSlotBytes;
+    unit_q8_0_s::load_qs(p + 4 + 32 * (u & 7), a.q);
+    a.d = __builtin_bit_cast(float, ld32(p));
+    a.s = (int)(int16_t)ld16(p + 260 + 2 * (u & 7));
+  }
+};
+
+// ------------------------------------------------------------------------------------------------ unit choice
+
+// activation layout of a decode launch
+enum ActFmt { kActSlots = 0, kActQ8_0 = 1 };
+
+constexpr bool is_b32(int t) { return t == QMM_TYPE_Q8_0 || t == QMM_TYPE_Q4_0 || t == QMM_TYPE_Q5_0; }
+
+// The units of weight type T against layout F: `pairs` for rows the unit reads as block pairs (every row of the
+// super-block types; 32-value rows of an even number of blocks, dword aligned), `odd` otherwise.
+template <int T, int F>
+struct decode_units;
+template <> struct decode_units<QMM_TYPE_Q4K, kActSlots> { typedef unit_q4k_s pairs; typedef unit_q4k_s odd; };
+template <> struct decode_units<QMM_TYPE_Q6K, kActSlots> { typedef unit_q6k_s pairs; typedef unit_q6k_s odd; };
+template <> struct decode_units<QMM_TYPE_Q5K, kActSlots> { typedef unit_q5k_s pairs; typedef unit_q5k_s odd; };
+template <> struct decode_units<QMM_TYPE_IQ4_XS, kActSlots> { typedef unit_iq4xs_s pairs; typedef unit_iq4xs_s odd; };
+template <> struct decode_units<QMM_TYPE_Q8_0, kActSlots> { typedef unit_q8_0_s pairs; typedef unit_q8_0_odd_s odd; };
+template <> struct decode_units<QMM_TYPE_Q8_0, kActQ8_0> { typedef unit_q8_0 pairs; typedef unit_q8_0_odd odd; };
+template <> struct decode_units<QMM_TYPE_Q4_0, kActSlots> {
+  typedef unit_b32_s<QMM_TYPE_Q4_0> pairs;
+  typedef unit_b32_odd_s<QMM_TYPE_Q4_0> odd;
+};
+template <> struct decode_units<QMM_TYPE_Q4_0, kActQ8_0> {
+  typedef unit_b32<QMM_TYPE_Q4_0> pairs;
+  typedef unit_b32_odd<QMM_TYPE_Q4_0> odd;
+};
+template <> struct decode_units<QMM_TYPE_Q5_0, kActSlots> {
+  typedef unit_b32_s<QMM_TYPE_Q5_0> pairs;
+  typedef unit_b32_odd_s<QMM_TYPE_Q5_0> odd;
+};
+template <> struct decode_units<QMM_TYPE_Q5_0, kActQ8_0> {
+  typedef unit_b32<QMM_TYPE_Q5_0> pairs;
+  typedef unit_b32_odd<QMM_TYPE_Q5_0> odd;
+};
+
+// bytes of one activation row of stride_col_y blocks: 36-byte Q8_1 blocks (slots, 8 per 256 values) or 34-byte Q8_0
+template <int F>
+constexpr int64_t act_row_bytes(int stride_col_y) { return (int64_t)stride_col_y * (F == kActSlots ? 36 : 34); }
+
+// Byte alignment the decode units need of a weight pointer: 16-byte loads for Q4_K / Q5_K, dword loads for IQ4_XS,
+// 16-bit loads (or realigned dwords) for the rest.
+constexpr uintptr_t weight_align(int type) {
+  return type == QMM_TYPE_Q4K || type == QMM_TYPE_Q5K ? 16 : type == QMM_TYPE_IQ4_XS ? 4 : 2;
+}
+
+// Whether a 32-value row reads as block pairs: an even number of blocks per row, every weight pointer and row
+// dword aligned, and (Q8_0 blocks) every activation pair too
+template <int T, int F>
+inline bool reads_pairs(int ncols_x, int stride_col_y, const void *vy, std::initializer_list<const void *> ws,
+                 int64_t expert_stride = 0) {
+  if (!is_b32(T)) return true;
+  bool ok = ncols_x % 64 == 0 && expert_stride % 4 == 0;
+  if (F == kActQ8_0) ok = ok && stride_col_y % 2 == 0 && (uintptr_t)vy % 4 == 0;
+  for (const void *w : ws) ok = ok && (w == nullptr || (uintptr_t)w % 4 == 0);
+  return ok;
+}
+

@@ -96,9 +96,9 @@ typedef void (*indexed_fn)(const void *, const void *, const uint32_t *, float *
 quant_fn decode_quantizer(GgmlDType w, GgmlDType in) {
   const bool k = qmm_vec_dot_type((int)w) == QMM_TYPE_Q8K;
   switch (in) {
-    case GgmlDType::F32: return k ? launch_mmvq_gguf_quantize_q8k_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
-    case GgmlDType::F16: return k ? launch_mmvq_gguf_quantize_q8k_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
-    case GgmlDType::BF16: return k ? launch_mmvq_gguf_quantize_q8k_bf16 : launch_mmvq_gguf_quantize_q8_0_bf16;
+    case GgmlDType::F32: return k ? launch_mmvq_gguf_quantize_q8_1_f32 : launch_mmvq_gguf_quantize_q8_0_f32;
+    case GgmlDType::F16: return k ? launch_mmvq_gguf_quantize_q8_1_f16 : launch_mmvq_gguf_quantize_q8_0_f16;
+    case GgmlDType::BF16: return k ? launch_mmvq_gguf_quantize_q8_1_bf16 : launch_mmvq_gguf_quantize_q8_0_bf16;
     default: throw Error("QMatMul: activations must be F32, F16 or BF16");
   }
 }
@@ -124,21 +124,23 @@ bool has_matvec(GgmlDType t) {
   return has_all_routes(t) || t == GgmlDType::Q4_0 || t == GgmlDType::Q5_0 || t == GgmlDType::Q5K;
 }
 
+// The matvec over the quantizer's layout: Q8_1 slots for the super-block types (the reference-named entries), Q8_0
+// blocks for the 32-value types (their _q8_0 entries), as each type's CPU dot product quantizes
 mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
-#define QMM_PICK(t)                                                              \
+#define QMM_PICK(t, sfx)                                                         \
   switch (out) {                                                                 \
-    case GgmlDType::F32: return launch_mmvq_gguf_##t##_f32_plain;                \
-    case GgmlDType::F16: return launch_mmvq_gguf_##t##_f16_plain;                \
-    case GgmlDType::BF16: return launch_mmvq_gguf_##t##_bf16_plain;              \
+    case GgmlDType::F32: return launch_mmvq_gguf_##t##_f32_plain##sfx;           \
+    case GgmlDType::F16: return launch_mmvq_gguf_##t##_f16_plain##sfx;           \
+    case GgmlDType::BF16: return launch_mmvq_gguf_##t##_bf16_plain##sfx;         \
     default: throw Error("QMatMul: output must be F32, F16 or BF16");            \
   }
   switch (w) {
-    case GgmlDType::Q8_0: QMM_PICK(q8_0)
-    case GgmlDType::Q4K: QMM_PICK(q4_k)
-    case GgmlDType::Q6K: QMM_PICK(q6_k)
-    case GgmlDType::Q4_0: QMM_PICK(q4_0)
-    case GgmlDType::Q5_0: QMM_PICK(q5_0)
-    case GgmlDType::Q5K: QMM_PICK(q5_k)
+    case GgmlDType::Q8_0: QMM_PICK(q8_0, _q8_0)
+    case GgmlDType::Q4K: QMM_PICK(q4_k, )
+    case GgmlDType::Q6K: QMM_PICK(q6_k, )
+    case GgmlDType::Q4_0: QMM_PICK(q4_0, _q8_0)
+    case GgmlDType::Q5_0: QMM_PICK(q5_0, _q8_0)
+    case GgmlDType::Q5K: QMM_PICK(q5_k, )
     default: throw Error("QMatMul: unsupported weight type");
   }
 #undef QMM_PICK
@@ -147,7 +149,7 @@ mmvq_fn decode_matvec(GgmlDType w, GgmlDType out) {
 typedef void (*mmvq_glu_fn)(const void *, const void *, const void *, void *, int, int, int, int, int, int, void *);
 mmvq_glu_fn decode_fused_glu(GgmlDType w) {
   switch (w) {
-    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_f32_fused_glu;
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_f32_fused_glu_q8_0;
     case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_f32_fused_glu;
     case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_f32_fused_glu;
     default: throw Error("fused_ffn: unsupported weight type");
@@ -156,9 +158,9 @@ mmvq_glu_fn decode_fused_glu(GgmlDType w) {
 
 mmq_fn prefill_matmul(GgmlDType w) {
   switch (w) {
-    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0;
-    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0;
-    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0;
+    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_q8_0;
+    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_q8_0;
+    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_q8_0;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k;
     case GgmlDType::Q5K: return launch_mmq_gguf_q5_k;
@@ -168,9 +170,9 @@ mmq_fn prefill_matmul(GgmlDType w) {
 
 mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
   switch (w) {
-    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_moe;
-    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_moe;
-    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_moe;
+    case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_moe_q8_0;
+    case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_moe_q8_0;
+    case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_moe_q8_0;
     case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k_moe;
     case GgmlDType::Q5K: return launch_mmq_gguf_q5_k_moe;
@@ -180,7 +182,7 @@ mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
 
 mmvq_moe_fn decode_matvec_moe(GgmlDType w) {
   switch (w) {
-    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe;
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe_q8_0;
     case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_moe;
     case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_moe;
     default: throw Error("MoE: unsupported weight type");
@@ -191,7 +193,7 @@ typedef void (*mmvq_moe_wsum_fn)(const void *, int64_t, const void *, const void
                                  int, int, int, void *);
 mmvq_moe_wsum_fn decode_matvec_moe_wsum(GgmlDType w) {
   switch (w) {
-    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe_wsum;
+    case GgmlDType::Q8_0: return launch_mmvq_gguf_q8_0_moe_wsum_q8_0;
     case GgmlDType::Q4K: return launch_mmvq_gguf_q4_k_moe_wsum;
     case GgmlDType::Q6K: return launch_mmvq_gguf_q6_k_moe_wsum;
     default: throw Error("MoE: unsupported weight type");
@@ -201,20 +203,22 @@ mmvq_moe_wsum_fn decode_matvec_moe_wsum(GgmlDType w) {
 indexed_fn indexed_moe(GgmlDType w) {
   switch (w) {
     case GgmlDType::Q8_0: return launch_indexed_moe_forward_q8_0_q8_0;
-    case GgmlDType::Q4K: return launch_indexed_moe_forward_q4k_q8k;
-    case GgmlDType::Q6K: return launch_indexed_moe_forward_q6k_q8k;
+    case GgmlDType::Q4K: return launch_indexed_moe_forward_q4k_q8_1;
+    case GgmlDType::Q6K: return launch_indexed_moe_forward_q6k_q8_1;
     case GgmlDType::Q4_0: return launch_indexed_moe_forward_q4_0_q8_0;
     case GgmlDType::Q5_0: return launch_indexed_moe_forward_q5_0_q8_0;
-    case GgmlDType::Q5K: return launch_indexed_moe_forward_q5k_q8k;
+    case GgmlDType::Q5K: return launch_indexed_moe_forward_q5k_q8_1;
     default: throw Error("gather_forward: unsupported weight type");
   }
 }
 
-// activation block geometry of a weight type (GgmlType::VecDotType)
+// activation geometry of a weight type (GgmlType::VecDotType): Q8_0 blocks of 34 bytes per 32 values, or Q8_1 slots of
+// 288 bytes per 256 (qmm_block_q8ks); stride_col_y counts 32-value blocks either way; prefill tiles 272 or 276 bytes
+// per 256 values
 bool act_q8_0(GgmlDType w) { return qmm_vec_dot_type((int)w) == QMM_TYPE_Q8_0; }
 int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
-int64_t act_block_bytes(GgmlDType w) { return act_q8_0(w) ? 34 : 292; }
-int64_t tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : 292; }
+int64_t act_row_bytes(GgmlDType w, int64_t kp) { return act_q8_0(w) ? kp / 32 * 34 : kp / 256 * 288; }
+int64_t tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : 276; }
 
 // matvec_only: the route needs the decode matvec kernels alone (QMatMul::forward, gather_forward); else every route
 void check_weight(const QTensor &w, const char *who, bool matvec_only = false) {
@@ -381,10 +385,7 @@ QMatMul::QMatMul(std::shared_ptr<QTensor> w) : w_(std::move(w)) {
   if (!w_) throw Error("QMatMul: null weight");
 }
 
-int64_t QMatMul::max_decode_rows(GgmlDType dtype, int64_t k) {
-  if (dtype == GgmlDType::Q4K || (dtype == GgmlDType::Q6K && k <= kMaxFewRowK)) return kMaxFewRows;
-  return kMaxDecodeRows;
-}
+int64_t QMatMul::max_decode_rows(GgmlDType dtype, int64_t k) { return qmm_max_decode_rows((int)dtype, k); }
 
 bool QMatMul::prefers_mmvq(GgmlDType dtype, int64_t rows, int64_t k) { return rows <= max_decode_rows(dtype, k); }
 
@@ -408,7 +409,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     // the decode matvec; a type without a prefill kernel takes every batch this way, max_decode_rows rows a launch
     const int64_t per = max_decode_rows(t, k);
     const int64_t kp = pad_to(k, act_block(t));
-    const int64_t row_bytes = (kp / act_block(t)) * act_block_bytes(t);
+    const int64_t row_bytes = act_row_bytes(t, kp);
     void *vy = workspace().get(w.device().ordinal, (size_t)(rows * row_bytes), stream);
     decode_quantizer(t, in_dtype)(xs, vy, (int)k, (int)kp, (int)rows, stream);
     abi_check("QMatMul::forward (quantize)");
@@ -416,7 +417,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     for (int64_t r0 = 0; r0 < rows; r0 += per) {
       const int64_t b = rows - r0 < per ? rows - r0 : per;
       decode_matvec(t, in_dtype)(w.device_ptr(), (const uint8_t *)vy + r0 * row_bytes, (uint8_t *)ys + r0 * n * out_elem,
-                                 (int)k, (int)n, (int)(kp / act_block(t)), (int)n, (int)b, stream);
+                                 (int)k, (int)n, (int)(kp / 32), (int)n, (int)b, stream);
       abi_check("QMatMul::forward (matvec)");
     }
   } else {
@@ -426,7 +427,7 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
     const size_t o_fix = c.add(fixup_bytes(nsm));
     uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
-    (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
+    (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(
         xs, nullptr, ws + o_y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
     abi_check("QMatMul::forward (quantize)");
     prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
@@ -454,8 +455,8 @@ void QMatMul::down_from_glu(const float *gate, const float *up, int64_t rows, in
   const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
   const size_t o_fix = c.add(fixup_bytes(nsm));
   uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
-  (act_q8_0(t) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8k_f32)(gate, up, nullptr, ws + o_y, k, k,
-                                                                                      kp, rows, activation, stream);
+  (act_q8_0(t) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8_1_DS4_f32)(
+      gate, up, nullptr, ws + o_y, k, k, kp, rows, activation, stream);
   abi_check("QMatMul::down_from_glu (GLU + quantize)");
   prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
                     160 * 1024, 64, 0, stream);
@@ -485,13 +486,13 @@ void fused_ffn(const QMatMul &gate, const QMatMul &up, const QMatMul &down, cons
     // decode: one activation quantization, the fused-GLU matvec, then down on act(gate) * up
     const int64_t kp = pad_to(hidden, act_block(t));
     Carver c;
-    const size_t o_y = c.add((size_t)(rows * (kp / act_block(t)) * act_block_bytes(t)));
+    const size_t o_y = c.add((size_t)(rows * act_row_bytes(t, kp)));
     const size_t o_mid = c.add((size_t)(rows * inter * 4));
     uint8_t *ws = (uint8_t *)ffn_workspace().get(ordinal, c.total, stream);
     decode_quantizer(t, GgmlDType::F32)(xs, ws + o_y, (int)hidden, (int)kp, (int)rows, stream);
     abi_check("fused_ffn (quantize)");
     decode_fused_glu(t)(g.device_ptr(), u.device_ptr(), ws + o_y, ws + o_mid, (int)hidden, (int)inter,
-                        (int)(kp / act_block(t)), (int)inter, (int)rows, activation, stream);
+                        (int)(kp / 32), (int)inter, (int)rows, activation, stream);
     abi_check("fused_ffn (gate/up)");
     down.forward(ws + o_mid, GgmlDType::F32, rows, ys, stream);
     return;
@@ -505,9 +506,9 @@ void fused_ffn(const QMatMul &gate, const QMatMul &up, const QMatMul &down, cons
   const size_t o_g = c.add((size_t)(rows * inter * 4));
   const size_t o_u = c.add((size_t)(rows * inter * 4));
   uint8_t *ws = (uint8_t *)ffn_workspace().get(ordinal, c.total, stream);
-  (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(xs, nullptr, ws + o_y, 0, hidden, hidden,
-                                                                     hidden * rows, hidden * rows, kp, rows, 1, 1,
-                                                                     stream);
+  (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(xs, nullptr, ws + o_y, 0, hidden, hidden,
+                                                                         hidden * rows, hidden * rows, kp, rows, 1, 1,
+                                                                         stream);
   abi_check("fused_ffn (quantize)");
   for (int which = 0; which < 2; which++) {
     const QTensor &w = which == 0 ? g : u;
@@ -529,8 +530,7 @@ void QMatMul::gather_forward(const float *xs, int64_t batch, int64_t xdim1, cons
   const GgmlDType t = w.dtype();
   const int64_t kp = pad_to(k, act_block(t));
   hip_check(hipSetDevice(w.device().ordinal), "hipSetDevice");
-  void *vy = workspace().get(w.device().ordinal, (size_t)(batch * xdim1 * (kp / act_block(t)) * act_block_bytes(t)),
-                             stream);
+  void *vy = workspace().get(w.device().ordinal, (size_t)(batch * xdim1 * act_row_bytes(t, kp)), stream);
   decode_quantizer(t, GgmlDType::F32)(xs, vy, (int)k, (int)kp, (int)(batch * xdim1), stream);
   abi_check("gather_forward (quantize)");
   indexed_moe(t)(w.device_ptr(), vy, ids, ys, (int)n, (int)k, (int)batch, (int)topk, (int)kp, (int)xdim1, stream);
@@ -568,21 +568,21 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
     // decode: fused gate/up matvec per routed pair, then down with the weighted sum over slots folded in
     const int64_t kp1 = pad_to(hidden, act_block(tg)), kp2 = pad_to(inter, act_block(td));
     Carver c;
-    const size_t o_x = c.add((size_t)(tokens * (kp1 / act_block(tg)) * act_block_bytes(tg)));
+    const size_t o_x = c.add((size_t)(tokens * act_row_bytes(tg, kp1)));
     const size_t o_mid = c.add((size_t)(pairs * inter * 4));
-    const size_t o_midq = c.add((size_t)(pairs * (kp2 / act_block(td)) * act_block_bytes(td)));
+    const size_t o_midq = c.add((size_t)(pairs * act_row_bytes(td, kp2)));
     uint8_t *ws = (uint8_t *)workspace().get(ordinal, c.total, stream);
     decode_quantizer(tg, GgmlDType::F32)(xs, ws + o_x, (int)hidden, (int)kp1, (int)tokens, stream);
     abi_check("MoE decode (quantize x)");
     decode_matvec_moe(tg)(gate_->device_ptr(), up_->device_ptr(), (int64_t)(inter * gate_->row_bytes()), ws + o_x,
-                          ids, (float *)(ws + o_mid), (int)hidden, (int)inter, (int)(kp1 / act_block(tg)), (int)topk,
+                          ids, (float *)(ws + o_mid), (int)hidden, (int)inter, (int)(kp1 / 32), (int)topk,
                           (int)pairs, activation_, 1, stream);
     abi_check("MoE decode (gate/up)");
     decode_quantizer(td, GgmlDType::F32)(ws + o_mid, ws + o_midq, (int)inter, (int)kp2, (int)pairs, stream);
     abi_check("MoE decode (quantize mid)");
     // down projection and the weighted sum over each token's routes in one launch
     decode_matvec_moe_wsum(td)(down_->device_ptr(), (int64_t)(hidden * down_->row_bytes()), ws + o_midq, ids, weights,
-                               out, (int)inter, (int)hidden, (int)(kp2 / act_block(td)), (int)tokens, (int)topk,
+                               out, (int)inter, (int)hidden, (int)(kp2 / 32), (int)tokens, (int)topk,
                                stream);
     abi_check("MoE decode (down + weighted sum)");
     return;
@@ -608,7 +608,7 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   launch_moe_dispatch(ids, bounds, tok, src, (int)pairs, (int)E, (int)topk, (int32_t *)(ws + o_cnt),
                       (int32_t *)(ws + o_cur), stream);
   abi_check("MoE grouped (dispatch)");
-  (tg == GgmlDType::Q8_0 ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8k)(
+  (act_q8_0(tg) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(
       xs, src, ws + o_x, 0, hidden, hidden, hidden * tokens, hidden * tokens, kp1, pairs, 1, 1, stream);
   abi_check("MoE grouped (quantize x)");
   for (int which = 0; which < 2; which++) {
@@ -618,7 +618,7 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
                            stream);
     abi_check("MoE grouped (gate/up)");
   }
-  (td == GgmlDType::Q8_0 ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8k_f32)(
+  (act_q8_0(td) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8_1_DS4_f32)(
       (const float *)(ws + o_g), (const float *)(ws + o_u), tok, ws + o_mq, inter, inter, kp2, pairs, activation_,
       stream);
   abi_check("MoE grouped (GLU + quantize)");

@@ -19,6 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "lib", "libinferencequant.so")
 HOST_LIB_PATH = os.path.join(HERE, "lib", "libinferencequant_host.so")
+BENCH_LIB_PATH = os.path.join(HERE, "lib", "libqmmbench.so")
 HEADERS = [os.path.join(REPO, "include", "inferencequant.h"), os.path.join(REPO, "include", "qmm_host.h")]
 
 # GGUF type ids (crates/inference-tensor/src/quantized/mod.rs:582-603) and block geometry
@@ -30,7 +31,27 @@ TYPE_SIZE = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292, Q4_0: 18, Q5_0: 22, Q5K: 17
 ACT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K, Q4_0: Q8_0, Q5_0: Q8_0, Q5K: Q8K, IQ4XS: Q8K}
 TYPE_NAME = {Q8_0: "q8_0", Q4K: "q4_k", Q6K: "q6_k"}
 ADJ_TYPE_NAME = {Q4_0: "q4_0", Q5_0: "q5_0", Q5K: "q5_k", IQ4XS: "iq4_xs"}
-MOE_NAME = {Q8_0: "q8_0_q8_0", Q4K: "q4k_q8k", Q6K: "q6k_q8k", Q4_0: "q4_0_q8_0", Q5_0: "q5_0_q8_0", Q5K: "q5k_q8k"}
+# the reference's type names in the indexed / fused MoE symbols (gguf/ffi.rs:60-224, 280-440)
+MOE_TYPE = {Q8_0: "q8_0", Q4K: "q4k", Q6K: "q6k", Q4_0: "q4_0", Q5_0: "q5_0", Q5K: "q5k"}
+B32 = (Q8_0, Q4_0, Q5_0)  # the 32-value types: their CPU dot products take Q8_0 activation blocks
+
+# Activation layouts (include/inferencequant.h).  q8_1=True: the reference-named quantizers and entries (Q8_K in the
+# reference's Q8_1-sized buffers: 36 bytes per 32 values for decode, 276 per 256 for prefill), every weight type.
+# q8_1=False: the 32-value types' _q8_0 entries over Q8_0 blocks.  The default (None) is what the C++ host layer uses:
+# Q8_1 slots for the super-block types, Q8_0 blocks for the 32-value types -- each the CPU QMatMul's own quantization.
+
+
+def _q8_1(wtype: int, q8_1) -> bool:
+    return (wtype not in B32) if q8_1 is None else bool(q8_1)
+
+
+def _sfx(wtype: int, q8_1) -> str:
+    """Entry-name suffix: the _q8_0 twin for a 32-value type over Q8_0 blocks."""
+    return "" if _q8_1(wtype, q8_1) else "_q8_0"
+
+
+def tname(wtype: int) -> str:
+    return TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]
 
 _lib = None
 
@@ -73,67 +94,43 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_CTYPE_RET = {"void": None, "int": ctypes.c_int, "double": ctypes.c_double}
+
+
+def _ctype_of(decl: str):
+    """ctypes type of one C parameter declaration (type plus name) of the ABI headers."""
+    if "*" in decl:
+        return ctypes.c_void_p
+    words = decl.replace("const", " ").split()
+    base = " ".join(words[:-1]) if len(words) > 1 else words[0]
+    return {"int64_t": ctypes.c_int64, "uint32_t": ctypes.c_uint32, "int32_t": ctypes.c_int32, "int": ctypes.c_int,
+            "bool": ctypes.c_bool, "_Bool": ctypes.c_bool, "float": ctypes.c_float,
+            "double": ctypes.c_double}[base]
+
+
+def prototypes(header: str | None = None) -> dict:
+    """name -> (restype, argtypes) of every function the C header declares (after macro expansion, gcc -E)."""
+    h = header or HEADERS[0]
+    out = subprocess.run(["gcc", "-E", "-P", "-x", "c", "-I", os.path.join(REPO, "include"), h], check=True,
+                         capture_output=True, text=True).stdout
+    protos = {}
+    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b((?:launch|qmm|moe_router)_\w+)\s*\(([^()]*)\)\s*;", out):
+        ret, name, args = m.group(1).strip(), m.group(2), m.group(3).strip()
+        ret_words = ret.replace("const", " ").split()
+        if "*" in ret:
+            restype = ctypes.c_char_p if "char" in ret_words else ctypes.c_void_p
+        else:
+            restype = _CTYPE_RET[ret_words[-1]]
+        argtypes = [] if args in ("", "void") else [_ctype_of(a) for a in args.split(",")]
+        protos[name] = (restype, argtypes)
+    return protos
+
+
 def _declare(L: ctypes.CDLL) -> None:
-    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-    L.qmm_last_error.restype = ctypes.c_char_p
-    L.qmm_last_error.argtypes = []
-    L.qmm_clear_error.argtypes = []
-    for src in ("f32", "f16", "bf16"):
-        for blk in ("q8k", "q8_0"):
-            getattr(L, f"launch_mmvq_gguf_quantize_{blk}_{src}").argtypes = [vp, vp, i32, i32, i32, vp]
-    for t in TYPE_NAME.values():
-        for o in ("f32", "f16", "bf16"):
-            getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
-            getattr(L, f"launch_mmvq_gguf_{t}_{o}_quantize_plain").argtypes = [vp, vp, vp] + [i32] * 5 + [vp]
-            getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_glu").argtypes = [vp, vp, vp, vp] + [i32] * 6 + [vp]
-            getattr(L, f"launch_mmvq_gguf_{t}_{o}_fused_qkv").argtypes = [vp] * 7 + [i32] * 6 + [vp]
-        getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
-                                                            i32, vp]
-    L.qmm_hbm_read_probe.argtypes = [vp, i64, i32, i32, i32, vp, vp]
-    L.qmm_hbm_read_probe.restype = i32
-    for src in ("f32", "f16", "bf16"):
-        getattr(L, f"launch_mmvq_tc_quantize_{src}").argtypes = [vp, vp, i32, i32, vp]
-    for t in ("q4_k", "q6_k"):
-        for o in ("f32", "f16", "bf16"):
-            getattr(L, f"launch_mmvq_tc_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
-    for t in TYPE_NAME.values():
-        getattr(L, f"launch_mmvq_gguf_{t}_moe_wsum").argtypes = [vp, i64, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
-    for name in MOE_NAME.values():
-        getattr(L, f"launch_indexed_moe_forward_{name}").argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
-    L.launch_moe_dispatch.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]
-    for suffix in ("", "_bf16", "_f16_input", "_bf16_input"):
-        f = getattr(L, f"launch_moe_weighted_reduce_flat{suffix}")
-        f.argtypes = [vp, vp, vp, i32, i32, i32, vp]
-        f.restype = ctypes.c_int
-    for blk in ("q8k", "q8_0"):
-        f = getattr(L, f"launch_mmq_quantize_{blk}", None)
-        if f is not None:
-            f.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
-    for blk in ("q8k", "q8_0"):
-        getattr(L, f"launch_mmq_quantize_glu_{blk}_f32").argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
-    for t in ADJ_TYPE_NAME.values():
-        for o in ("f32", "f16", "bf16"):
-            getattr(L, f"launch_mmvq_gguf_{t}_{o}_plain").argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
-        getattr(L, f"launch_mmvq_gguf_{t}_moe").argtypes = [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32,
-                                                            i32, vp]
-    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k"]:
-        for o in ("f32", "f16", "bf16"):
-            getattr(L, f"launch_dequantize_{t}_{o}").argtypes = [vp, vp, i64, vp]
-        getattr(L, f"launch_get_rows_{t}").argtypes = [vp, vp, vp, i64, i64, i64, vp]
-    for o in ("f32", "f16", "bf16"):
-        getattr(L, f"launch_dequantize_iq4_xs_{o}").argtypes = [vp, vp, i64, i64, vp]
-    for o in ("f32", "bf16"):
-        getattr(L, f"launch_mmvq_gguf_q8_0_{o}_exact").argtypes = [vp, vp, vp, i32, i32, i32, vp]
-    for t in list(TYPE_NAME.values()) + ["q4_0", "q5_0", "q5_k", "iq4_xs"]:
-        f = getattr(L, f"launch_mmq_gguf_{t}", None)
-        if f is not None:
-            f.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i64, i32, i32, vp]
-        f = getattr(L, f"launch_mmq_gguf_{t}_moe", None)
-        if f is not None:
-            f.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i32, i32, i64, i32, vp]
-        f = getattr(L, f"launch_mmq_gguf_{t}_moe_wsum", None)
-        if f is not None:
-            f.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp]
+    for name, (restype, argtypes) in prototypes().items():
+        f = getattr(L, name)
+        f.restype = restype
+        f.argtypes = argtypes
 
 
 def last_error() -> str:
@@ -146,6 +143,28 @@ def check() -> None:
     if msg:
         lib().qmm_clear_error()
         raise QmmError(msg)
+
+
+_bench = None
+
+
+def bench_lib() -> ctypes.CDLL:
+    """Load libqmmbench.so, bench.py's measurement probes (HBM read floor, copy rate, int8 MFMA rate)."""
+    global _bench
+    if _bench is None:
+        lib()
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise QmmError(f"{BENCH_LIB_PATH} is missing: run `make -C {HERE}`")
+        B = ctypes.CDLL(BENCH_LIB_PATH)
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        B.qmm_hbm_read_probe.argtypes = [vp, i64, i32, i32, i32, vp, vp]
+        B.qmm_hbm_read_probe.restype = i32
+        B.qmm_bench_copy.argtypes = [vp, vp, i64, i32, i32, vp]
+        B.qmm_bench_copy.restype = i32
+        B.qmm_bench_mfma_i8.argtypes = [i32, i32, vp, vp]
+        B.qmm_bench_mfma_i8.restype = ctypes.c_double
+        _bench = B
+    return _bench
 
 
 def build_id() -> str:
@@ -172,9 +191,9 @@ def pad_to(k: int, m: int) -> int:
     return (k + m - 1) // m * m
 
 
-def act_bytes(wtype: int, rows: int, kp: int) -> int:
-    at = ACT_TYPE[wtype]
-    return rows * kp // BLOCK_SIZE[at] * TYPE_SIZE[at]
+def act_bytes(wtype: int, rows: int, kp: int, q8_1=None) -> int:
+    """Bytes of `rows` decode activation rows of kp values: Q8_1-slot rows (36 per 32 values) or Q8_0 blocks."""
+    return rows * kp // 32 * (36 if _q8_1(wtype, q8_1) else 34)
 
 
 _DT = {}
@@ -185,30 +204,37 @@ def _src_name(x) -> str:
     return {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[x.dtype]
 
 
-def quantize_decode(wtype: int, x, kp: int | None = None, out=None):
-    """Quantize activation rows x [rows, k] (f32/f16/bf16, on the GPU) to the decode layout of wtype's
-    activation blocks.  Returns (uint8 tensor, k_padded)."""
+def quantize_decode(wtype: int, x, kp: int | None = None, out=None, q8_1=None):
+    """Quantize activation rows x [rows, k] (f32/f16/bf16, on the GPU) for wtype's decode entries:
+    launch_mmvq_gguf_quantize_q8_1_<src> (Q8_1 slots; kp defaults to pad(k, 512) as the reference's fast_mmvq
+    pads) or launch_mmvq_gguf_quantize_q8_0_<src> (Q8_0 blocks, kp = pad(k, 32)).  Returns (uint8 tensor, kp)."""
     torch = _torch()
     rows, k = x.shape
-    at = ACT_TYPE[wtype]
-    kp = kp or pad_to(k, BLOCK_SIZE[at])
+    slots = _q8_1(wtype, q8_1)
+    kp = kp or pad_to(k, 512 if slots else 32)
     if out is None:
-        out = torch.empty(act_bytes(wtype, rows, kp), dtype=torch.uint8, device=x.device)
-    blk = "q8k" if at == Q8K else "q8_0"
+        out = torch.empty(act_bytes(wtype, rows, kp, q8_1), dtype=torch.uint8, device=x.device)
+    blk = "q8_1" if slots else "q8_0"
     getattr(lib(), f"launch_mmvq_gguf_quantize_{blk}_{_src_name(x)}")(_ptr(x), _ptr(out), k, kp, rows, _stream())
     check()
     return out, kp
 
 
-def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out=None, stride_col_dst=None):
-    """Decode matvec: dst [b, n] = Q(y) . W^T through launch_mmvq_gguf_<t>_<dtype>_plain."""
+def _oname(t) -> str:
+    torch = _torch()
+    return {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[t.dtype]
+
+
+def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out=None, stride_col_dst=None,
+         q8_1=None):
+    """Decode matvec: dst [b, n] = Q(y) . W^T through launch_mmvq_gguf_<t>_<dtype>_plain (or _plain_q8_0);
+    stride_col_y = kp / 32 as the reference passes it."""
     torch = _torch()
     out_dtype = out_dtype or torch.float32
     if out is None:
         out = torch.empty((b, stride_col_dst or n), dtype=out_dtype, device=w.device)
-    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_{oname}_plain")(
-        _ptr(w), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], stride_col_dst or n, b, _stream())
+    getattr(lib(), f"launch_mmvq_gguf_{tname(wtype)}_{_oname(out)}_plain{_sfx(wtype, q8_1)}")(
+        _ptr(w), _ptr(vy), _ptr(out), k, n, kp // 32, stride_col_dst or n, b, _stream())
     check()
     return out
 
@@ -228,30 +254,27 @@ def mmvq_quantize(wtype: int, w, x, n: int, out_dtype=None, out=None):
 
 
 def mmvq_fused_glu(wtype: int, w_gate, w_up, vy, k: int, n: int, b: int, kp: int, activation: int = 0,
-                   out_dtype=None, out=None):
+                   out_dtype=None, out=None, q8_1=None):
     """dst [b, n] = act(Q(y) . W_gate^T) * (Q(y) . W_up^T) through launch_mmvq_gguf_<t>_<dtype>_fused_glu."""
     torch = _torch()
     if out is None:
         out = torch.empty((b, n), dtype=out_dtype or torch.float32, device=w_gate.device)
-    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[out.dtype]
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_fused_glu")(
-        _ptr(w_gate), _ptr(w_up), _ptr(vy), _ptr(out), k, n, kp // BLOCK_SIZE[ACT_TYPE[wtype]], out.shape[1], b,
-        activation, _stream())
+    getattr(lib(), f"launch_mmvq_gguf_{tname(wtype)}_{_oname(out)}_fused_glu{_sfx(wtype, q8_1)}")(
+        _ptr(w_gate), _ptr(w_up), _ptr(vy), _ptr(out), k, n, kp // 32, out.shape[1], b, activation, _stream())
     check()
     return out
 
 
 def mmvq_fused_qkv(wtype: int, wq, wk, wv, vy, k: int, nq: int, nk: int, nv: int, b: int, kp: int, out_dtype=None,
-                   outs=None):
+                   outs=None, q8_1=None):
     """(q [b, nq], k [b, nk], v [b, nv]) through one launch_mmvq_gguf_<t>_<dtype>_fused_qkv."""
     torch = _torch()
     if outs is None:
         dt = out_dtype or torch.float32
         outs = tuple(torch.empty((b, n), dtype=dt, device=wq.device) for n in (nq, nk, nv))
-    oname = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[outs[0].dtype]
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{oname}_fused_qkv")(
+    getattr(lib(), f"launch_mmvq_gguf_{tname(wtype)}_{_oname(outs[0])}_fused_qkv{_sfx(wtype, q8_1)}")(
         _ptr(wq), _ptr(wk), _ptr(wv), _ptr(vy), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), k, nq, nk, nv,
-        kp // BLOCK_SIZE[ACT_TYPE[wtype]], b, _stream())
+        kp // 32, b, _stream())
     check()
     return outs
 
@@ -286,48 +309,82 @@ def mmvq_tc(wtype: int, w, vy, k: int, n: int, b: int, cfg: int = 0, out_dtype=N
     return out
 
 
-def qmatmul_decode(wtype: int, w, x, n: int, out_dtype=None):
+def qmatmul_decode(wtype: int, w, x, n: int, out_dtype=None, q8_1=None):
     """x [b, k] -> [b, n]: quantize then matvec (the two launches fast_mmvq::plain makes)."""
-    vy, kp = quantize_decode(wtype, x)
-    return mmvq(wtype, w, vy, x.shape[1], n, x.shape[0], kp, out_dtype=out_dtype)
+    vy, kp = quantize_decode(wtype, x, q8_1=q8_1)
+    return mmvq(wtype, w, vy, x.shape[1], n, x.shape[0], kp, out_dtype=out_dtype, q8_1=q8_1)
 
 
 def mmvq_moe(wtype: int, w_gate, w_up, expert_stride: int, vy, ids, k: int, n: int, kp: int, y_div: int,
-             n_pairs: int, activation: int = 0, out=None):
+             n_pairs: int, activation: int = 0, out=None, q8_1=None):
     torch = _torch()
     if out is None:
         out = torch.empty((n_pairs, n), dtype=torch.float32, device=w_gate.device)
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
-        _ptr(w_gate), _ptr(w_up), expert_stride, _ptr(vy), _ptr(ids), _ptr(out), k, n,
-        kp // BLOCK_SIZE[ACT_TYPE[wtype]], y_div, n_pairs, activation, 1, _stream())
+    getattr(lib(), f"launch_mmvq_gguf_{tname(wtype)}_moe{_sfx(wtype, q8_1)}")(
+        _ptr(w_gate), _ptr(w_up), expert_stride, _ptr(vy), _ptr(ids), _ptr(out), k, n, kp // 32, y_div, n_pairs,
+        activation, 1, _stream())
     check()
     return out
 
 
 def mmvq_moe_wsum(wtype: int, w, expert_stride: int, vy, ids, weights, k: int, n: int, kp: int, n_tokens: int,
-                  topk: int, out=None):
+                  topk: int, out=None, q8_1=None):
     """MoE down projection with the weighted sum over each token's routes: launch_mmvq_gguf_<t>_moe_wsum.
     vy: n_tokens * topk activation rows; ids u32 and weights f32 [n_tokens, topk] -> out [n_tokens, n] f32."""
     torch = _torch()
     if out is None:
         out = torch.empty((n_tokens, n), dtype=torch.float32, device=w.device)
-    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_moe_wsum")(
-        _ptr(w), expert_stride, _ptr(vy), _ptr(ids), _ptr(weights), _ptr(out), k, n,
-        kp // BLOCK_SIZE[ACT_TYPE[wtype]], n_tokens, topk, _stream())
+    getattr(lib(), f"launch_mmvq_gguf_{tname(wtype)}_moe_wsum{_sfx(wtype, q8_1)}")(
+        _ptr(w), expert_stride, _ptr(vy), _ptr(ids), _ptr(weights), _ptr(out), k, n, kp // 32, n_tokens, topk,
+        _stream())
     check()
     return out
 
 
-def indexed_moe(wtype: int, w, x, ids, n: int, out=None):
-    """The op-level gather_forward: x [batch, xdim1, k] f32, ids [batch, topk] u32 -> [batch, topk, n]."""
+def indexed_moe(wtype: int, w, x, ids, n: int, out=None, q8_1=None):
+    """The op-level gather_forward: x [batch, xdim1, k] f32, ids [batch, topk] u32 -> [batch, topk, n], through
+    launch_indexed_moe_forward_<t>_q8_1 (or _q8_0)."""
     torch = _torch()
     batch, xdim1, k = x.shape
     topk = ids.shape[1]
-    vy, kp = quantize_decode(wtype, x.reshape(batch * xdim1, k))
+    vy, kp = quantize_decode(wtype, x.reshape(batch * xdim1, k), q8_1=q8_1)
     if out is None:
         out = torch.zeros((batch, topk, n), dtype=torch.float32, device=x.device)
-    getattr(lib(), f"launch_indexed_moe_forward_{MOE_NAME[wtype]}")(
+    act = "q8_1" if _q8_1(wtype, q8_1) else "q8_0"
+    getattr(lib(), f"launch_indexed_moe_forward_{MOE_TYPE[wtype]}_{act}")(
         _ptr(w), _ptr(vy), _ptr(ids), _ptr(out), n, k, batch, topk, kp, xdim1, _stream())
+    check()
+    return out
+
+
+def moe_gemv_gate_up(wtype: int, w_gate, w_up, vy, ids, n: int, k: int, batch: int, topk: int, kp: int,
+                     act_type: int = 1, out=None):
+    """launch_moe_gemv_fused_gate_up_<t>_q8_1: vy = batch Q8_1-slot rows of kp values; out [batch * topk, n] f32 =
+    act(W_gate[e] . x_b) * (W_up[e] . x_b), act_type 0 GELU (tanh), else SiLU."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((batch * topk, n), dtype=torch.float32, device=w_gate.device)
+    getattr(lib(), f"launch_moe_gemv_fused_gate_up_{MOE_TYPE[wtype]}_q8_1")(
+        _ptr(w_gate), _ptr(w_up), _ptr(vy), _ptr(ids), _ptr(out), n, k, batch, topk, kp, act_type, _stream())
+    check()
+    return out
+
+
+def moe_gemv_down_aggregate(wtype: int, w, vy, ids, weights, n: int, k: int, batch: int, topk: int, kp: int, out):
+    """launch_moe_gemv_down_aggregate_<t>_q8_1: vy = batch * topk Q8_1-slot rows of kp values; out [batch, n] f32
+    += sum over slots of weights * (W[e] . x_p)."""
+    getattr(lib(), f"launch_moe_gemv_down_aggregate_{MOE_TYPE[wtype]}_q8_1")(
+        _ptr(w), _ptr(vy), _ptr(ids), _ptr(weights), _ptr(out), n, k, batch, topk, kp, _stream())
+    check()
+    return out
+
+
+def gather_rows_u8(src, ids, row_bytes: int, rows: int, out=None):
+    """launch_gather_rows_u8: out [len(ids), row_bytes] uint8 = rows ids of src (zeros for an id >= rows)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty((ids.numel(), row_bytes), dtype=torch.uint8, device=src.device)
+    lib().launch_gather_rows_u8(_ptr(src), _ptr(ids), _ptr(out), row_bytes, rows, ids.numel(), _stream())
     check()
     return out
 
@@ -368,23 +425,24 @@ def moe_weighted_reduce(inp, weights, out_dtype=None):
 
 # ------------------------------------------------------------------------------------------------ prefill
 
-def mmq_act_bytes(wtype: int, rows: int, kp: int) -> int:
-    return rows * kp // 256 * (292 if ACT_TYPE[wtype] == Q8K else 272)
+def mmq_act_bytes(wtype: int, rows: int, kp: int, q8_1=None) -> int:
+    return rows * kp // 256 * (276 if _q8_1(wtype, q8_1) else 272)
 
 
-def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None):
-    """Quantize x [rows, k] (or the rows ids selects) into the prefill tile layout.  Returns (uint8 tensor, kp)."""
+def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None, q8_1=None):
+    """Quantize x [rows, k] (or the rows ids selects) into wtype's prefill tile layout: launch_mmq_quantize_q8_1_DS4
+    (Q8_K tiles) or launch_mmq_quantize_q8_0.  Returns (uint8 tensor, kp)."""
     torch = _torch()
     k = x.shape[-1]
     kp = pad_to(k, 256)
     ne1 = rows if rows is not None else (ids.numel() if ids is not None else x.shape[0])
     if out is None:
-        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp), 1), dtype=torch.uint8, device=x.device)
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1), 1), dtype=torch.uint8, device=x.device)
     type_x = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[x.dtype]
-    blk = "q8k" if ACT_TYPE[wtype] == Q8K else "q8_0"
-    getattr(lib(), f"launch_mmq_quantize_{blk}")(_ptr(x), _ptr(ids), _ptr(out), type_x, k, x.stride(0),
-                                                 x.stride(0) * x.shape[0], x.stride(0) * x.shape[0], kp, ne1, 1, 1,
-                                                 _stream())
+    name = "q8_1_DS4" if _q8_1(wtype, q8_1) else "q8_0"
+    getattr(lib(), f"launch_mmq_quantize_{name}")(_ptr(x), _ptr(ids), _ptr(out), type_x, k, x.stride(0),
+                                                  x.stride(0) * x.shape[0], x.stride(0) * x.shape[0], kp, ne1, 1, 1,
+                                                  _stream())
     check()
     return out, kp
 
@@ -403,63 +461,71 @@ def fixup(device):
     return _fixups[idx]
 
 
-def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, out=None):
-    """act(gate[r]) * up[r] for r = ids[i] (or i), f32 [rows, k] inputs, quantized into the prefill tile layout
-    through launch_mmq_quantize_glu_{q8k,q8_0}_f32.  Returns (uint8 tensor, kp)."""
+def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, out=None, q8_1=None):
+    """act(gate[r]) * up[r] for r = ids[i] (or i), [rows, k] inputs, quantized into the prefill tile layout through
+    launch_mmq_quantize_glu_q8_1_DS4_f32 (f32 inputs) / launch_mmq_quantize_glu_q8_1_DS4 (f16 / bf16 inputs) or
+    launch_mmq_quantize_glu_q8_0_f32.  Returns (uint8 tensor, kp)."""
     torch = _torch()
     k = gate.shape[-1]
     kp = pad_to(k, 256)
     ne1 = ids.numel() if ids is not None else gate.shape[0]
     if out is None:
-        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp), 1), dtype=torch.uint8, device=gate.device)
-    blk = "q8k" if ACT_TYPE[wtype] == Q8K else "q8_0"
-    getattr(lib(), f"launch_mmq_quantize_glu_{blk}_f32")(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0),
-                                                         kp, ne1, activation, _stream())
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1), 1), dtype=torch.uint8, device=gate.device)
+    if not _q8_1(wtype, q8_1):
+        lib().launch_mmq_quantize_glu_q8_0_f32(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0), kp, ne1,
+                                               activation, _stream())
+    elif gate.dtype == torch.float32:
+        lib().launch_mmq_quantize_glu_q8_1_DS4_f32(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0), kp,
+                                                   ne1, activation, _stream())
+    else:
+        type_x = {torch.float16: F16, torch.bfloat16: BF16}[gate.dtype]
+        lib().launch_mmq_quantize_glu_q8_1_DS4(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), type_x, k, gate.stride(0),
+                                               kp, ne1, activation, _stream())
     check()
     return out, kp
 
 
-def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None, tmp_fixup=True):
-    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t>.  tmp_fixup=False passes no fixup buffer (no split-K)."""
+def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None, tmp_fixup=True, q8_1=None):
+    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t> (or _q8_0).  tmp_fixup=False passes no fixup buffer
+    (no split-K)."""
     torch = _torch()
     out_dtype = out_dtype or torch.float32
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=w.device)
     type_dst = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[out.dtype]
     fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
-    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}")(
+    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}{_sfx(wtype, q8_1)}")(
         _ptr(fx), _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, nsm, 160 * 1024, 64, type_dst,
         _stream())
     check()
     return out
 
 
-def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None):
-    y, _ = quantize_prefill(wtype, x)
-    return mmq(wtype, w, y, x.shape[1], n, x.shape[0], out_dtype=out_dtype)
+def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None, q8_1=None):
+    y, _ = quantize_prefill(wtype, x, q8_1=q8_1)
+    return mmq(wtype, w, y, x.shape[1], n, x.shape[0], out_dtype=out_dtype, q8_1=q8_1)
 
 
 def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
-            ncols_max: int, out, tmp_fixup=True):
+            ncols_max: int, out, tmp_fixup=True, q8_1=None):
     fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
-    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe")(
+    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}_moe{_sfx(wtype, q8_1)}")(
         _ptr(fx), _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
         k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, nsm, 160 * 1024, 64, _stream())
     check()
     return out
 
 
-
 def mmq_moe_wsum(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
                  ncols_max: int, weights, topk: int, counters, out, routes=None):
-    """Grouped matmul with the weighted sum over each token's routes folded in (launch_mmq_gguf_<t>_moe_wsum):
-    out [ncols_dst / topk, n]; routes [ncols_dst, n] f32 receives the per-route rows; counters int32
+    """Grouped matmul with the weighted sum over each token's routes folded in (launch_mmq_gguf_<t>_moe_wsum, over
+    Q8_K tiles: quantize_prefill(..., q8_1=True)): out [ncols_dst / topk, n]; routes [ncols_dst, n] f32 receives the per-route rows; counters int32
     [tokens * ceil(n / 32)], zero before the call and left zero.  Returns (out, routes)."""
     torch = _torch()
     if routes is None:
         routes = torch.empty((ncols_dst, n), dtype=torch.float32, device=w.device)
     fx, nsm = fixup(w.device)
-    getattr(lib(), f"launch_mmq_gguf_{TYPE_NAME.get(wtype) or ADJ_TYPE_NAME[wtype]}_moe_wsum")(
+    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}_moe_wsum")(
         _ptr(fx), _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(routes), _ptr(weights), _ptr(counters),
         _ptr(out), k, n, ncols_dst, k // BLOCK_SIZE[wtype], n_experts, ncols_max, topk, nsm, _stream())
     check()

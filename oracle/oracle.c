@@ -938,6 +938,66 @@ int oracle_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, c
     return rc;
 }
 
+/* The values (weight q - offset) and f16 scale of 32-value block b of a Q8_0 / Q4_0 / Q5_0 row */
+static uint16_t b32_values(int type, const void *row, int64_t b, int32_t v[32]) {
+    if (type == OR_Q8_0) {
+        const or_block_q8_0 *x = (const or_block_q8_0 *)row + b;
+        for (int j = 0; j < 32; j++) v[j] = x->qs[j];
+        return x->d;
+    }
+    if (type == OR_Q4_0) {
+        const or_block_q4_0 *x = (const or_block_q4_0 *)row + b;
+        for (int j = 0; j < 16; j++) {
+            v[j] = (int32_t)(x->qs[j] & 0x0F) - 8;
+            v[j + 16] = (int32_t)(x->qs[j] >> 4) - 8;
+        }
+        return x->d;
+    }
+    const or_block_q5_0 *x = (const or_block_q5_0 *)row + b;
+    uint32_t qh;
+    memcpy(&qh, x->qh, 4);
+    for (int j = 0; j < 16; j++) {
+        v[j] = ((int32_t)(x->qs[j] & 0x0F) | (int32_t)(((qh >> j) & 1u) << 4)) - 16;
+        v[j + 16] = ((int32_t)(x->qs[j] >> 4) | (int32_t)(((qh >> (j + 16)) & 1u) << 4)) - 16;
+    }
+    return x->d;
+}
+
+int oracle_matmul_q8k_act(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const void *rhs, float *dst,
+                          int threads) {
+    if (type != OR_Q8_0 && type != OR_Q4_0 && type != OR_Q5_0) return oracle_matmul(type, m, k, n, lhs, rhs, dst, threads);
+    if (k % 32 != 0) return -1;
+    const int64_t kp = (k + 255) / 256 * 256, nb = k / 32;
+    const size_t row_bytes = (size_t)nb * oracle_type_size(type);
+    float *xp = (float *)calloc((size_t)kp, sizeof(float));
+    or_block_q8k *a = (or_block_q8k *)malloc((size_t)(kp / 256) * sizeof(or_block_q8k));
+    if (!xp || !a) {
+        free(xp);
+        free(a);
+        return -1;
+    }
+    for (int64_t r = 0; r < m; r++) {
+        memcpy(xp, lhs + r * k, (size_t)k * sizeof(float));
+        oracle_quantize_q8k(xp, kp, a);
+        for (int64_t c = 0; c < n; c++) {
+            const void *wrow = (const char *)rhs + (size_t)c * row_bytes;
+            float sumf = 0.0f;
+            for (int64_t b = 0; b < nb; b++) {
+                int32_t v[32];
+                const uint16_t dw = b32_values(type, wrow, b, v);
+                const or_block_q8k *y = a + b / 8;
+                int32_t sumi = 0;
+                for (int j = 0; j < 32; j++) sumi += v[j] * y->qs[32 * (b % 8) + j];
+                sumf += (float)sumi * oracle_f16_to_f32(dw) * y->d;
+            }
+            dst[r * n + c] = sumf;
+        }
+    }
+    free(xp);
+    free(a);
+    return 0;
+}
+
 /* ---------------------------------------------------------------- MoE */
 
 int oracle_indexed_moe(int type, int64_t n_experts, int64_t n, int64_t k, const void *w, const float *x,

@@ -93,6 +93,18 @@ int oracle_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, c
 int oracle_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const void *lhs_q, const void *rhs, float *dst,
                        int threads);
 
+/* The arithmetic of this library's reference-named entries for the 32-value weight types (Q8_0, Q4_0, Q5_0): no
+ * counterpart in the reference, whose GPU path gives them Q8_1 activations and whose CPU path Q8_0 ones
+ * (k_quants.rs:2824-2830).  The reference sizes its activation buffers for Q8_1 (36 bytes per 32 values), which holds
+ * a Q8_K quantization but not a Q8_K and a Q8_0 one, so those entries read Q8_K activations: each lhs row is quantized
+ * with BlockQ8K::from_float over 256-value blocks (k padded to 256 with zeros), and
+ *   dst[m][n] = sum over 32-value blocks b, in order, of (float)(sum_j w_j a_j) * d_w(b) * d_a(b / 8)
+ * with the per-block integer dot of the weight's values (q - 8 for Q4_0, q - 16 for Q5_0) and the activation's int8
+ * values, as vec_dot_q8_0_q8_0 / q4_0 / q5_0 scale a block (k_quants.rs:982-999, 432-449, 615-637) but with the f32
+ * scale of the activation's 256-value block.  For the other types it is oracle_matmul.  Returns 0, or -1. */
+int oracle_matmul_q8k_act(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const void *rhs, float *dst,
+                          int threads);
+
 /* Expert-indexed matmul, the contract of QuantMethod::gather_forward
  * (crates/inference-quant/src/gguf/mod.rs:573-608, cpu.rs:23-104, quantized/mod.rs:1457-1461):
  * y[b][s][:] = W[ids[b][s]] . Q8(x[b][s % xdim1][:]),  W [E, n, k], x [batch, xdim1, k], ids [batch, topk],

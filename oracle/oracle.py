@@ -64,6 +64,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_dequantize.argtypes = [ctypes.c_int, vp, i64, vp]
         L.oracle_matmul.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, ctypes.c_int]
         L.oracle_matmul_preq.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, ctypes.c_int]
+        L.oracle_matmul_q8k_act.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, ctypes.c_int]
         L.oracle_indexed_moe.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, i64, i64, i64, vp, vp, ctypes.c_int]
         L.oracle_moe_dispatch.argtypes = [vp, i32, i32, i32, vp, vp, vp]
         L.oracle_moe_weighted_reduce.argtypes = [vp, vp, vp, i32, i32, i32]
@@ -152,6 +153,19 @@ def matmul(gtype: int, x: np.ndarray, w: np.ndarray, n: int, threads: int = 0) -
     assert w.size == n * k // BLOCK_SIZE[gtype] * TYPE_SIZE[gtype]
     dst = np.zeros((m, n), dtype=np.float32)
     rc = lib().oracle_matmul(gtype, m, k, n, _p(x), _p(w), _p(dst), threads)
+    assert rc == 0
+    return dst
+
+
+def matmul_q8k_act(gtype: int, x: np.ndarray, w: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    """The arithmetic of the library's reference-named entries (oracle.h oracle_matmul_q8k_act): Q8_K activations for
+    every weight type; for the super-block types the same as matmul()."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    assert w.size == n * k // BLOCK_SIZE[gtype] * TYPE_SIZE[gtype]
+    dst = np.zeros((m, n), dtype=np.float32)
+    rc = lib().oracle_matmul_q8k_act(gtype, m, k, n, _p(x), _p(w), _p(dst), threads)
     assert rc == 0
     return dst
 

@@ -7,7 +7,7 @@ import pytest
 
 import oracle as O
 import qmm
-from helpers import acts, assert_parity, weights
+from helpers import acts, assert_parity, decode_act_blocks, weights
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -38,9 +38,9 @@ def run_matvec(gtype, wq, x, n, out_dtype=torch.float32):
     vy, kp = qmm.quantize_decode(gtype, to_dev(x))
     got = qmm.mmvq(gtype, w, vy, k, n, m, kp, out_dtype=out_dtype)
     torch.cuda.synchronize()
-    aq = vy.cpu().numpy()
-    assert kp == k  # K is whole weight blocks, and a weight block is as long as its activation block
-    # the oracle on the activation blocks the GPU made (bit-exact with the oracle's own quantizer, checked below)
+    # the activation blocks the GPU made, as the oracle's blocks of the first k values (bit-exact with the oracle's own
+    # quantizer, checked below); the oracle's matmul on them
+    aq = decode_act_blocks(gtype, vy.cpu().numpy(), m, kp, k)
     want = O.matmul_preq(gtype, aq, m, k, wq, n)
     return got.float().cpu().numpy(), want, aq
 
@@ -62,10 +62,7 @@ def test_adjacent_matvec_matches_the_oracle(gtype, kidx, b):
     x = acts(rng, b, k)
     x[:, ::64] *= 30.0
     got, want, aq = run_matvec(gtype, wq, x, n)
-    kp = qmm.pad_to(k, O.BLOCK_SIZE[O.ACT_TYPE[gtype]])
-    xp = np.zeros((b, kp), np.float32)
-    xp[:, :k] = x
-    assert np.array_equal(aq, O.quantize(O.ACT_TYPE[gtype], xp).reshape(-1))
+    assert np.array_equal(aq, O.quantize(O.ACT_TYPE[gtype], x).reshape(-1))
     assert_parity(got, want, terms(gtype, aq, wq, b, n, k), what=f"type {gtype} k={k} b={b}")
 
 
@@ -217,3 +214,17 @@ def test_wide_rows_half_outputs(gtype, out):
     want = np.asarray(want, np.float64)
     err = np.abs(np.asarray(got, np.float64) - want)
     assert np.all(err <= 1e-3 * np.abs(want).max() + ulp * np.abs(want)), f"type {gtype} {out}"
+
+
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4_0, O.Q5_0])
+@pytest.mark.parametrize("shape", [0, 3, 4, 5, 7, 8])
+def test_wide_rows_reference_entries(gtype, shape):
+    """The same wide rows through the reference-named entries over Q8_1 slots (unit_*_s: per-256 f32 scales of the
+    activation), against the oracle's matmul over Q8_K activations."""
+    n, k, b = WIDE_SHAPES[shape]
+    rng = np.random.default_rng(700 + 10 * gtype + shape)
+    wq = weight_bytes(gtype, n, k, rng)
+    x = acts(rng, b, k)
+    x[:, ::64] *= 30.0
+    got = qmm.qmatmul_decode(gtype, to_dev(wq.reshape(-1)), to_dev(x), n, q8_1=True).cpu().numpy()
+    assert_parity(got, O.matmul_q8k_act(gtype, x, wq, n), what=f"type {gtype} n={n} k={k} b={b}")

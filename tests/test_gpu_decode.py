@@ -1,11 +1,14 @@
 """GPU parity of the decode path through the C ABI: activation quantizers (bit-exact with the oracle) and the
-Q8_0 / Q4_K / Q6_K matvec (max rel. error <= 1e-3 against the oracle's CPU QMatMul on the same bytes)."""
+Q8_0 / Q4_K / Q6_K matvec (max rel. error <= 1e-3 against the oracle's CPU QMatMul on the same bytes).  The
+super-block types read Q8_1 slots (launch_mmvq_gguf_quantize_q8_1_*, 36 bytes per 32 values as the reference sizes
+them, holding BlockQ8K::from_float's d and qs); Q8_0 reads Q8_0 blocks through its _q8_0 entries, or Q8_1 slots through
+the reference-named ones (then checked against the oracle's matmul over Q8_K activations)."""
 import numpy as np
 import pytest
 
 import oracle as O
 import qmm
-from helpers import acts, assert_parity, patterned, terms, weights
+from helpers import acts, assert_parity, decode_act_blocks, patterned, terms, weights
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -27,18 +30,26 @@ def special_rows(rng, m, k):
 
 @pytest.mark.parametrize("k", [256, 300, 4096, 14336])
 @pytest.mark.parametrize("src", ["f32", "f16", "bf16"])
-def test_q8k_decode_quantizer_is_bit_exact(k, src):
+def test_q8_1_decode_quantizer_is_bit_exact(k, src):
+    """launch_mmvq_gguf_quantize_q8_1_<src> into the reference's scratch (rows * pad(k, 512) / 32 * 36 bytes) with a
+    guard region behind it: each slot holds BlockQ8K::from_float's d and qs, the int16 sums of each 32 values and a
+    zero tail; the padding to k_padded quantizes as zeros; nothing is written past the scratch."""
     rng = np.random.default_rng(100 + k)
     x = special_rows(rng, 5, k)
     tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[src]
     xt = to_dev(x).to(tdt)
     x_in = xt.float().cpu().numpy()  # the reference widens f16/bf16 to f32 before quantizing
-    vy, kp = qmm.quantize_decode(qmm.Q4K, xt)
-    got = vy.cpu().numpy()
+    kp = qmm.pad_to(k, 512)
+    size = 5 * kp // 32 * 36
+    buf = torch.full((size + 4096,), 0xA5, dtype=torch.uint8, device=DEV)
+    vy, kp2 = qmm.quantize_decode(qmm.Q4K, xt, out=buf)
+    assert kp2 == kp
+    got = buf.cpu().numpy()
+    assert np.all(got[size:] == 0xA5), "written past the reference's scratch size"
     xp = np.zeros((5, kp), np.float32)
     xp[:, :k] = x_in
     want = O.quantize(O.Q8K, xp).reshape(-1)
-    assert np.array_equal(got, want)
+    assert np.array_equal(decode_act_blocks(O.Q4K, got[:size], 5, kp), want)
 
 
 @pytest.mark.parametrize("k", [32, 96, 4096, 1056])
@@ -82,6 +93,19 @@ def test_mmvq_matches_the_cpu_qmatmul(gtype, n, k, b):
     want = O.matmul(gtype, x, wq, n)
     got = qmm.qmatmul_decode(gtype, to_dev(wq), to_dev(x), n).cpu().numpy()
     assert_parity(got, want, terms(gtype, x, wq, n), what=f"t{gtype} n{n} k{k} b{b}")
+
+
+@pytest.mark.parametrize("n,k,b", [(256, 512, 1), (300, 1024, 4), (48, 1056, 3), (17, 2688, 16), (64, 14336, 2)])
+def test_q8_0_reference_entries_over_q8_1_slots(n, k, b):
+    """The reference's own sequence for a Q8_0 weight: launch_mmvq_gguf_quantize_q8_1_f32 then
+    launch_mmvq_gguf_q8_0_f32_plain with stride_col_y = k_padded / 32.  The activation is Q8_K (one f32 scale per
+    256 values), so the result is the CPU QMatMul's arithmetic over Q8_K activations (oracle matmul_q8k_act)."""
+    rng = np.random.default_rng(3000 + n + k + b)
+    wq = O.quantize(O.Q8_0, weights(rng, n, k))
+    x = acts(rng, b, k)
+    x[:, ::64] *= 60.0
+    got = qmm.qmatmul_decode(O.Q8_0, to_dev(wq), to_dev(x), n, q8_1=True).cpu().numpy()
+    assert_parity(got, O.matmul_q8k_act(O.Q8_0, x, wq, n), terms(O.Q8_0, x, wq, n), what=f"n{n} k{k} b{b}")
 
 
 @pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])

@@ -7,7 +7,7 @@ import pytest
 
 import oracle as O
 import qmm
-from helpers import assert_parity, terms
+from helpers import assert_parity, decode_act_blocks, terms
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -32,8 +32,7 @@ def test_decode_against_fixture(gtype):
     for b in (1, 2, 4, 16):
         x = g["x"][:b]
         vy, kp = qmm.quantize_decode(gtype, dev(x))
-        bs = O.BLOCK_SIZE[O.ACT_TYPE[gtype]]
-        blocks = vy.cpu().numpy().reshape(b, kp // bs, -1)[:, : k // bs].reshape(-1)
+        blocks = decode_act_blocks(gtype, vy.cpu().numpy(), b, kp, k)
         assert np.array_equal(blocks, g["xq_bytes"][:b].reshape(-1)), f"b={b}"
         y = qmm.mmvq(gtype, dev(w), vy, k, n, b, kp).cpu().numpy()
         assert_parity(y, g["y"][:b], terms(gtype, x, w, n), what=f"{TYPES[gtype]} b={b}")

@@ -1,4 +1,5 @@
-"""GPU parity of the prefill path through the C ABI: the tile-layout Q8_K / Q8_0 quantizers (bit-exact) and the
+"""GPU parity of the prefill path through the C ABI: the tile-layout Q8_K / Q8_0 quantizers (bit-exact; the Q8_K
+tiles, launch_mmq_quantize_q8_1_*, fit the reference's MMQ scratch of M * k_padded / 128 * 144 + 128 * 144 bytes) and the
 int8-MFMA matmul for Q4_K / Q6_K / Q8_0 and, on the Q8_0 kernel, Q4_0 / Q5_0 (max rel. error <= 1e-3 against the
 oracle's CPU QMatMul)."""
 import numpy as np
@@ -6,7 +7,7 @@ import pytest
 
 import oracle as O
 import qmm
-from helpers import acts, assert_parity, terms, weights
+from helpers import acts, assert_parity, terms, tiles_to_blocks, weights
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -15,27 +16,6 @@ DEV = "cuda"
 
 def to_dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-
-
-def tiles_to_blocks(buf, rows, kp, at):
-    """Prefill tile layout -> the oracle's block array [rows, nsb] (bytes)."""
-    nsb = kp // 256
-    b = buf[: rows * nsb * (292 if at == O.Q8K else 272)]
-    qs = b[: nsb * rows * 256].reshape(nsb, rows, 256)
-    if at == O.Q8K:
-        d = b[nsb * rows * 256: nsb * rows * 260].view(np.float32).reshape(nsb, rows)
-        # bsums are stored as f16 (exact for |bsum| <= 2048)
-        bs = b[nsb * rows * 260:].view(np.float16).reshape(nsb, rows, 16).astype(np.int16)
-        out = np.zeros((rows, nsb), dtype=O.BLOCK_DTYPES[O.Q8K])
-        out["d"] = d.T
-        out["qs"] = qs.transpose(1, 0, 2)
-        out["bsums"] = bs.transpose(1, 0, 2)
-        return out.view(np.uint8).reshape(-1)
-    d8 = b[nsb * rows * 256:].view(np.uint16).reshape(nsb, rows, 8)
-    out = np.zeros((rows, nsb * 8), dtype=O.BLOCK_DTYPES[O.Q8_0])
-    out["d"] = d8.transpose(1, 0, 2).reshape(rows, nsb * 8)
-    out["qs"] = qs.transpose(1, 0, 2).reshape(rows, nsb * 8, 32)
-    return out.view(np.uint8).reshape(-1)
 
 
 @pytest.mark.parametrize("wtype", [O.Q4K, O.Q8_0])
@@ -51,7 +31,7 @@ def test_prefill_quantizer_is_bit_exact(wtype, m, k):
     xp = np.zeros((m, kp), np.float32)
     xp[:, :k] = x
     want = O.quantize(at, xp).reshape(-1)
-    got = tiles_to_blocks(y.cpu().numpy(), m, kp, at)
+    got = tiles_to_blocks(y.cpu().numpy(), m, kp, at == O.Q8K)
     assert np.array_equal(got, want)
 
 
@@ -61,7 +41,7 @@ def test_prefill_quantizer_row_gather():
     ids = np.array([7, 7, 0, 9, 3], dtype=np.int32)
     y, kp = qmm.quantize_prefill(O.Q4K, to_dev(x), ids=to_dev(ids))
     want = O.quantize(O.Q8K, x[ids]).reshape(-1)
-    assert np.array_equal(tiles_to_blocks(y.cpu().numpy(), 5, kp, O.Q8K), want)
+    assert np.array_equal(tiles_to_blocks(y.cpu().numpy(), 5, kp, True), want)
 
 
 CASES = [
@@ -159,7 +139,7 @@ def test_split_k_grouped_is_deterministic():
 @pytest.mark.parametrize("wtype", [O.Q4K, O.Q8_0])
 @pytest.mark.parametrize("activation", [2, 0])
 def test_glu_requantizer(wtype, activation):
-    """launch_mmq_quantize_glu_{q8k,q8_0}_f32: act(gate[r]) * up[r] for the gathered rows, quantized into the prefill
+    """launch_mmq_quantize_glu_q8_1_DS4_f32 / launch_mmq_quantize_glu_q8_0_f32: act(gate[r]) * up[r] for the gathered rows, quantized into the prefill
     layout.  ReLU (2) is exact in f32 (a select and one rounded product), so the blocks must equal the oracle's
     quantization of the same values byte for byte.  SiLU (0) goes through the device's expf: its blocks match those
     of the device-independent quantizer run on the same f32 products computed here, except where a product sits
@@ -179,7 +159,7 @@ def test_glu_requantizer(wtype, activation):
     hp[:, :k] = h
     at = O.ACT_TYPE[wtype]
     want = O.quantize(at, hp).reshape(-1)
-    got = tiles_to_blocks(y.cpu().numpy(), len(ids), kp, at)
+    got = tiles_to_blocks(y.cpu().numpy(), len(ids), kp, at == O.Q8K)
     if activation == 2:
         assert np.array_equal(got, want)
     else:
