@@ -205,11 +205,14 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     """Llama-3-8B linears, Q4_K for q/k/o/gate/up and Q6_K for v/down, 32 layers; one weight per shape is
     quantized and its bytes copied to every layer (distinct HBM copies, so every step streams 4.44 GB).
     Per layer, as the reference's decode path runs them: the attention input is quantized once and q, k, v read
-    that one activation; o and down quantize their own inputs (at b <= 2, o in one launch with its quantization,
-    launch_mmvq_gguf_q4_k_f32_quantize_plain); gate and up are one fused-GLU launch
-    (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  Each input takes QMatMul's route: the decode
-    launcher up to 32 rows, except the Q6_K down projection (K = 14336) above 16 rows, which takes the prefill
-    matmul; one quantized activation per distinct input.  The inputs are synthetic, one per projection group."""
+    that one activation; o and down quantize their own inputs; gate and up are one fused-GLU launch
+    (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  At b <= 2 the launches that can quantize their
+    own f32 input do: q, k and v in one launch (launch_mmvq_gguf_q4_k_q6_k_f32_fused_qkv_quantize), o
+    (launch_mmvq_gguf_q4_k_f32_quantize_plain) and gate / up (launch_mmvq_gguf_q4_k_f32_fused_glu_quantize), with the
+    same output bits as their two-launch forms; the down projection (K = 14336) keeps its quantizer.  Each input
+    takes QMatMul's route: the decode launcher up to 32 rows, except the Q6_K down projection (K = 14336) above 16
+    rows, which takes the prefill matmul; one quantized activation per distinct input.  The inputs are synthetic, one
+    per projection group."""
     shapes = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
               ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
     layers = 32
@@ -217,9 +220,9 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     dev = {name: [torch.from_numpy(base[name]).cuda() for _ in range(layers)] for name, _, _, _ in shapes}
     total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
     res = {"weight_bytes_per_step": total_bytes,
-           "launches_per_layer": "decode b <= 2: 3 quantize + q, k, v, o (quantizing its input), gate/up (fused GLU), "
-                                 "down = 9; b 3..16: 4 quantize + 6 = 10; b 17..32: the same with down on the "
-                                 "prefill matmul = 10; prefill: 4 quantize + 7 matmuls"}
+           "launches_per_layer": "decode b <= 2: q/k/v in one launch, o and gate/up each in one, all three "
+                                 "quantizing their input, down quantize + matvec = 5; b 3..16: 4 quantize + 6 = 10; "
+                                 "b 17..32: the same with down on the prefill matmul = 10"}
     import qmm as Q
     for b in batches:
         rng = np.random.default_rng(seed + 100 + b)
@@ -236,25 +239,32 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
         tdim = {name: t for name, t, _, _ in shapes}
         ndim = {name: n for name, _, n, _ in shapes}
 
-        one_launch_o = b <= 2
+        one_launch = b <= 2  # q/k/v, o and gate/up quantize their own f32 inputs
 
         def step(i):
             for layer in range(layers):
                 for g, x in xs.items():
                     vy, kp = bufs[g]
-                    if g == "o" and one_launch_o:
+                    if one_launch and g != "down":
                         continue
                     if dec_of[g]:
                         Q.quantize_decode(Q4K, x, kp=kp, out=vy)
                     else:
                         Q.quantize_prefill(Q4K, x, out=vy)
+                if one_launch:
+                    Q.mmvq_fused_qkv_quantize(Q4K, dev["q"][layer], dev["k"][layer], dev["v"][layer], xs["attn"],
+                                              4096, 1024, 1024, outs=(outs["q"], outs["k"], outs["v"]), vtype=Q6K)
+                    Q.mmvq_quantize(Q4K, dev["o"][layer], xs["o"], 4096, out=outs["o"])
+                    Q.mmvq_fused_glu_quantize(Q4K, dev["gate"][layer], dev["up"][layer], xs["ffn"], 14336,
+                                              out=outs["gate"])
+                    vy, kp = bufs["down"]
+                    Q.mmvq(Q6K, dev["down"][layer], vy, 14336, 4096, b, kp, out=outs["down"])
+                    continue
                 for name in ("q", "k", "v", "o", "gate", "down"):
                     vy, kp = bufs[group[name]]
                     t, n, k = tdim[name], ndim[name], kdim[name]
                     decode = dec_of[group[name]]
-                    if decode and name == "o" and one_launch_o:
-                        Q.mmvq_quantize(t, dev["o"][layer], xs["o"], n, out=outs["o"])
-                    elif decode and name == "gate":
+                    if decode and name == "gate":
                         Q.mmvq_fused_glu(Q4K, dev["gate"][layer], dev["up"][layer], vy, k, n, b, kp,
                                          out=outs["gate"])
                     elif decode:

@@ -154,6 +154,34 @@ QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q8_0)
 QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q4_k)
 QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(q6_k)
 
+/* launch_mmvq_gguf_<t>_<dt>_fused_glu_quantize and _fused_qkv_quantize (t = q8_0, q4_k, q6_k; no counterpart in the
+ * reference): the fused GLU / QKV decode forms over f32 activations x [b_size rows, stride_col_x apart] that the
+ * launch quantizes itself, once per workgroup into LDS (the decode quantizers' blocks, bit for bit), instead of the
+ * quantizer launch before them; the same output bits as that quantizer followed by _fused_glu / _fused_qkv.
+ * b_size 1 or 2, ncols_x <= 4096 (Q8_0: a multiple of 64).  _fused_glu_quantize: dst[j * stride_col_dst + row] =
+ * act(W_gate . x_j) * (W_up . x_j), activation as _fused_glu.  _fused_qkv_quantize: q_dst[j * nrows_q + row] and
+ * likewise k, v.  launch_mmvq_gguf_q4_k_q6_k_f32_fused_qkv_quantize: the same with Q4_K q / k and Q6_K v weights. */
+#define QMM_DECLARE_MMVQ_FUSED_QUANTIZE_DT(t, dt)                                                                 \
+  void launch_mmvq_gguf_##t##_##dt##_fused_glu_quantize(const void *vx_gate, const void *vx_up, const float *x,     \
+                                                        void *dst, int ncols_x, int nrows_x, int stride_col_x,      \
+                                                        int stride_col_dst, int b_size, int activation,             \
+                                                        void *stream);                                              \
+  void launch_mmvq_gguf_##t##_##dt##_fused_qkv_quantize(const void *vx_q, const void *vx_k, const void *vx_v,       \
+                                                        const float *x, void *q_dst, void *k_dst, void *v_dst,      \
+                                                        int ncols_x, int nrows_q, int nrows_k, int nrows_v,         \
+                                                        int stride_col_x, int b_size, void *stream);
+#define QMM_DECLARE_MMVQ_FUSED_QUANTIZE(t)     \
+  QMM_DECLARE_MMVQ_FUSED_QUANTIZE_DT(t, f32)   \
+  QMM_DECLARE_MMVQ_FUSED_QUANTIZE_DT(t, f16)   \
+  QMM_DECLARE_MMVQ_FUSED_QUANTIZE_DT(t, bf16)
+QMM_DECLARE_MMVQ_FUSED_QUANTIZE(q8_0)
+QMM_DECLARE_MMVQ_FUSED_QUANTIZE(q4_k)
+QMM_DECLARE_MMVQ_FUSED_QUANTIZE(q6_k)
+void launch_mmvq_gguf_q4_k_q6_k_f32_fused_qkv_quantize(const void *vx_q, const void *vx_k, const void *vx_v,
+                                                       const float *x, void *q_dst, void *k_dst, void *v_dst,
+                                                       int ncols_x, int nrows_q, int nrows_k, int nrows_v,
+                                                       int stride_col_x, int b_size, void *stream);
+
 /* ------------------------------------------------------------------ fused decode forms
  * launch_mmvq_gguf_<t>_{bf16,f16,f32}_fused_glu (gguf/ffi.rs:1032-1069; kernel mmvq_gguf.cuh:761-842):
  * dst[j * stride_col_dst + row] = act(W_gate[row] . Q(y_j)) * (W_up[row] . Q(y_j)) for j < b_size (1..16; 1..32 for

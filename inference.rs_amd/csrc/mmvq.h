@@ -15,6 +15,8 @@
 // Q8_0 blocks of their CPU dot product (the _q8_0 entries, 34 bytes per 32 values, stride_col_y in blocks).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "inferencequant.h"
 #include "q8.h"
@@ -425,6 +427,160 @@ __global__ __launch_bounds__(64 * NW) void k_mmvq_pq(const uint8_t *__restrict__
                                         act_row_bytes, dst, stride_col_dst);
 }
 
+// ------------------------------------------------------------------------------------------------ several weights
+
+// One-launch decode over up to three weights that share one f32 activation (q / k / v, or gate and up): the
+// workgroups are split between the segments in proportion to their bytes, and each workgroup quantizes the
+// activation into LDS, as k_mmvq_pq does, then walks its segment's rows with two in flight.  So the activation is
+// quantized in the launch that reads it, once per workgroup, and the segments share the chip in one launch.
+struct PqSeg {
+  const uint8_t *w;   // weight rows (GLU: the gate rows)
+  const uint8_t *w2;  // GLU: the up rows
+  void *dst;          // output, stride_col_dst elements per activation row
+  int nrows, stride_col_dst, wg0;  // wg0: the segment's first workgroup
+};
+struct PqSegs {
+  PqSeg s[3];
+};
+
+// pq_quantize: the f32 loads of this wave's activation blocks (step 1 of k_mmvq_pq), then, once the caller has
+// issued its first weight loads, their quantization into LDS (step 3).
+template <class U, int NC, int NW, int G>
+struct PqAct {
+  static constexpr bool kQ8K = U::kActBlockValues == 256;
+  static constexpr int kBlocksPerStep = kQ8K ? 1 : 8;
+  float v[G][4];
+  int blk[G];
+  int total;
+  __device__ __forceinline__ void load(const float *__restrict__ x, int64_t stride_x, int nblk, int lane, int wave) {
+    total = NC * nblk;
+#pragma unroll
+    for (int t = 0; t < G; t++) {
+      blk[t] = (wave + NW * t) * kBlocksPerStep + (kQ8K ? 0 : lane >> 3);
+      const int b = blk[t] < total ? blk[t] : 0;
+      const int j = NC > 1 && b >= nblk ? 1 : 0;
+      const int k0 = (b - j * nblk) * U::kActBlockValues + 4 * (kQ8K ? lane : lane & 7);
+      typedef float f32x4 __attribute__((ext_vector_type(4)));
+      f32x4 f;
+      __builtin_memcpy(&f, __builtin_assume_aligned(x + j * stride_x + k0, 4), 16);
+      v[t][0] = f.x, v[t][1] = f.y, v[t][2] = f.z, v[t][3] = f.w;
+    }
+  }
+  __device__ __forceinline__ void quantize(uint8_t *s_act, int lane) {
+    if constexpr (kQ8K) {
+      qmm_q8::q8k_dst d[G];
+      bool st[G];
+#pragma unroll
+      for (int t = 0; t < G; t++) {
+        st[t] = blk[t] < total;
+        d[t] = qmm_q8::q8k_decode_dst(s_act, st[t] ? blk[t] : 0);
+      }
+      qmm_q8::q8k_waves<G>(v, lane, d, st);
+    } else {
+#pragma unroll
+      for (int t = 0; t < G; t++) {
+        uint8_t *b = s_act + (int64_t)(blk[t] < total ? blk[t] : 0) * 34;
+        qmm_q8::q8_0_group(v[t], lane & 7, (int8_t *)(b + 2), (uint16_t *)b, blk[t] < total);
+      }
+    }
+  }
+};
+
+// The GLU form of row_pairs: buffers (ga, ua) hold row r's gate and up weights and (gb, ub) row r + tw's; each row
+// stores act(W_gate . y) * (W_up . y).
+template <class U, class Out, int NC, int S, bool FULL, bool kRegs>
+__device__ __forceinline__ void row_pairs_glu(const uint8_t *vg, const uint8_t *vu, int64_t row_bytes, int nunits,
+                                              int nrows, int row, int tw, int lane, typename U::W (&ga)[S],
+                                              typename U::W (&ua)[S], typename U::W (&gb)[S], typename U::W (&ub)[S],
+                                              const typename U::A *areg, const uint8_t *act, int64_t act_row_bytes,
+                                              typename Out::T *dst, int stride_col_dst, int activation) {
+  float g[NC], u[NC];
+  auto store = [&](int r) {
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+      const float gs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(g[j])), 63));
+      const float us = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(u[j])), 63));
+      Out::store(dst, (int64_t)j * stride_col_dst + r, glu_act(activation, gs) * us);
+    }
+  };
+  for (;;) {
+    row_dots<U, NC, S, FULL, kRegs>(ga, areg, act, act_row_bytes, nunits, lane, g);
+    row_dots<U, NC, S, FULL, kRegs>(ua, areg, act, act_row_bytes, nunits, lane, u);
+    load_row<U, S, FULL>(vg, row_bytes, nunits, nrows, row + 2 * tw, lane, ga);
+    load_row<U, S, FULL>(vu, row_bytes, nunits, nrows, row + 2 * tw, lane, ua);
+    store(row);
+    if (row + tw >= nrows) break;
+    row_dots<U, NC, S, FULL, kRegs>(gb, areg, act, act_row_bytes, nunits, lane, g);
+    row_dots<U, NC, S, FULL, kRegs>(ub, areg, act, act_row_bytes, nunits, lane, u);
+    load_row<U, S, FULL>(vg, row_bytes, nunits, nrows, row + 3 * tw, lane, gb);
+    load_row<U, S, FULL>(vu, row_bytes, nunits, nrows, row + 3 * tw, lane, ub);
+    store(row + tw);
+    row += 2 * tw;
+    if (row >= nrows) break;
+  }
+}
+
+// One segment's part of k_mmvq_pqs: the workgroup's rows are local_block * NW + wave + t * local_grid * NW.
+template <class U, class Out, int NC, bool FULL, int NW, int G, bool GLU>
+__device__ __forceinline__ void pqs_segment(const PqSeg &sg, int local_block, int local_grid,
+                                            const float *__restrict__ x, int64_t stride_x, int nunits,
+                                            uint8_t *s_act, int activation) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nblk = nunits * U::kValuesPerUnit / U::kActBlockValues;
+  const int64_t act_row_bytes = (int64_t)nblk * U::kActBlockBytes;
+  const int64_t row_bytes = U::row_bytes((int64_t)nunits * U::kValuesPerUnit);
+  PqAct<U, NC, NW, G> qa;
+  qa.load(x, stride_x, nblk, lane, wave);
+  const int tw = local_grid * NW;
+  int row = local_block * NW + wave;
+  typename U::W ga[1], gb[1], ua[1], ub[1];
+  load_row<U, 1, FULL>(sg.w, row_bytes, nunits, sg.nrows, row, lane, ga);
+  load_row<U, 1, FULL>(sg.w, row_bytes, nunits, sg.nrows, row + tw, lane, gb);
+  if (GLU) {
+    load_row<U, 1, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row, lane, ua);
+    load_row<U, 1, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row + tw, lane, ub);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  qa.quantize(s_act, lane);
+  __syncthreads();
+  if (row >= sg.nrows) return;  // whole wave
+  constexpr bool kRegs = NC <= 2;
+  typename U::A areg[kRegs ? NC : 1];
+  if (kRegs) {
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+      if (FULL || lane < nunits) U::load_a(s_act + j * act_row_bytes, lane, areg[kRegs ? j : 0]);
+  }
+  typename Out::T *dst = (typename Out::T *)sg.dst;
+  if constexpr (GLU)
+    row_pairs_glu<U, Out, NC, 1, FULL, kRegs>(sg.w, sg.w2, row_bytes, nunits, sg.nrows, row, tw, lane, ga, ua, gb, ub,
+                                              areg, s_act, act_row_bytes, dst, sg.stride_col_dst, activation);
+  else
+    row_pairs<U, Out, NC, 1, FULL, kRegs>(sg.w, row_bytes, nunits, sg.nrows, row, tw, lane, ga, gb, areg, s_act,
+                                          act_row_bytes, dst, sg.stride_col_dst);
+}
+
+// Segments [0, NA) take unit UA, the rest UB (which share UA's activation format); NS segments in all.
+template <class UA, class UB, int NA, int NS, class Out, int NC, bool FULL, int NW, int G, bool GLU>
+__global__ __launch_bounds__(64 * NW) void k_mmvq_pqs(PqSegs segs, const float *__restrict__ x, int64_t stride_x,
+                                                      int nunits, int activation) {
+  static_assert(UA::kActBlockValues == UB::kActBlockValues && UA::kActBlockBytes == UB::kActBlockBytes,
+                "segments share one quantized activation");
+  extern __shared__ __align__(16) uint8_t s_act[];
+  const int b = blockIdx.x;
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < NS; i++)
+    if (b >= segs.s[i].wg0) si = i;
+  const int end = si + 1 < NS ? segs.s[si + 1 < NS ? si + 1 : 0].wg0 : (int)gridDim.x;
+  const int local = b - segs.s[si].wg0, grid = end - segs.s[si].wg0;
+  // the segment is uniform over the workgroup
+  if (si < NA)
+    pqs_segment<UA, Out, NC, FULL, NW, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
+  else
+    pqs_segment<UB, Out, NC, FULL, NW, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
+}
+
 // MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's
 // weights through L2.  dst[p * nrows + row] = W_gate[ids[p]] . y[p / y_div]  (or act(gate) * up).
 template <class U, int R, bool GLU>
@@ -665,6 +821,66 @@ void launch_pq(const uint8_t *vx, const float *x, int64_t stride_x, typename Out
 }
 
 
+// Grid of k_mmvq_pqs: as launch_pq_nw, split between the segments in proportion to their weight bytes (each at least
+// one workgroup, and none more workgroups than its rows fill).  rows[i], w[i], w2[i], dst[i] per segment.
+template <class UA, class UB, int NA, int NS, class Out, int NC, bool GLU>
+void launch_pqs(const uint8_t *const *w, const uint8_t *const *w2, typename Out::T *const *dst, const int *rows,
+                const float *x, int64_t stride_x, int k, const int *stride_col_dst, int activation, hipStream_t s) {
+  const int nu = UA::units(k);
+  const bool full = nu % 64 == 0;
+  const int nblk = nu * UA::kValuesPerUnit / UA::kActBlockValues;
+  const int steps = (int)qmm_ceil_div((int64_t)NC * nblk, UA::kActBlockValues == 256 ? 1 : 8);  // <= 32
+  const size_t lds = (size_t)NC * nblk * UA::kActBlockBytes;
+  int64_t total_rows = 0;
+  double bytes[3] = {0, 0, 0}, all = 0;
+  for (int i = 0; i < NS; i++) {
+    total_rows += rows[i];
+    bytes[i] = (double)rows[i] * (double)(i < NA ? UA::row_bytes(k) : UB::row_bytes(k)) * (GLU ? 2 : 1);
+    all += bytes[i];
+  }
+  auto go = [&](auto nw_tag, auto g_tag, auto full_tag) {
+    constexpr int NW = decltype(nw_tag)::value, G = decltype(g_tag)::value;
+    constexpr bool FF = decltype(full_tag)::value;
+    auto kern = k_mmvq_pqs<UA, UB, NA, NS, Out, NC, FF, NW, G, GLU>;
+    const int per_cu = qmm_resident_per_cu<k_mmvq_pqs<UA, UB, NA, NS, Out, NC, FF, NW, G, GLU>>(64 * NW, lds);
+    const int kCap = NW == 8 ? 1 : 2;
+    const int wgs = (per_cu < kCap ? per_cu : kCap) * qmm_device_cus();
+    PqSegs segs = {};
+    int next = 0;
+    for (int i = 0; i < NS; i++) {
+      int n = (int)(wgs * bytes[i] / all + 0.5);
+      const int most = (int)qmm_ceil_div(rows[i], NW);
+      n = n < 1 ? 1 : (n > most ? most : n);
+      segs.s[i] = PqSeg{w[i], GLU ? w2[i] : nullptr, (void *)dst[i], rows[i], stride_col_dst[i], next};
+      next += n;
+    }
+    kern<<<dim3((unsigned)next), 64 * NW, lds, s>>>(segs, x, stride_x, nu, activation);
+  };
+  typedef std::integral_constant<int, 8> nw8;
+  typedef std::integral_constant<int, 16> nw16;
+  auto pick_g = [&](auto nw_tag, auto full_tag) {
+    constexpr int NW = decltype(nw_tag)::value;
+    if (steps <= NW)
+      go(nw_tag, std::integral_constant<int, 1>(), full_tag);
+    else if (steps <= 2 * NW)
+      go(nw_tag, std::integral_constant<int, 2>(), full_tag);
+    else
+      go(nw_tag, std::integral_constant<int, 4>(), full_tag);
+  };
+  // 8-wave workgroups for tall weights and the GLU form (two rows' weights per step; 16 waves would cap a wave at
+  // 128 registers), 16 below
+  auto pick_nw = [&](auto full_tag) {
+    if (GLU || total_rows >= 8192)
+      pick_g(nw8(), full_tag);
+    else
+      pick_g(nw16(), full_tag);
+  };
+  if (full)
+    pick_nw(std::true_type());
+  else
+    pick_nw(std::false_type());
+}
+
 template <class U>
 void moe_launch(const void *vx_gate, const void *vx_up, int64_t expert_stride, const void *vy, const void *ids,
                 float *dst, int ncols_x, int nrows_x, int64_t act_row_bytes, int y_div, int n_pairs, int activation,
@@ -813,6 +1029,115 @@ void quantize_plain_t(const void *vx, const float *x, void *dst, int ncols_x, in
 // below the few-row threshold, the few-row MFMA kernel from it, with the same integer dots as the plain entries.
 // cfg names one of the reference's CUDA tile shapes (fast_mmvq.rs:1845-1881); it is accepted and has no meaning here.
 // b_size 1..32 (the reference passes at most 16).
+// the unit of the one-launch forms (their activation is quantized into LDS in the 292- / 34-byte block layouts)
+template <int T>
+using pq_unit = typename std::conditional<T == QMM_TYPE_Q4K, unit_q4k,
+                                          typename std::conditional<T == QMM_TYPE_Q6K, unit_q6k, unit_q8_0>::type>::type;
+
+// the argument checks of the one-launch forms: b 1 or 2, ncols_x <= 4096 (one unit per lane), aligned weights
+// (a null weight among ws is skipped: the caller's empty projection)
+inline bool check_pq(const char *who, int type, std::initializer_list<const void *> ws, const float *x, int ncols_x,
+                     int stride_col_x, int b, bool null_ok = false) {
+  const int bs = (int)qmm_block_size(type);
+  if (ncols_x <= 0 || ncols_x % bs != 0 || (type == QMM_TYPE_Q8_0 && ncols_x % 64 != 0) || ncols_x > 64 * 64) {
+    qmm_set_error("%s: ncols_x=%d (a positive multiple of %d, at most 4096)", who, ncols_x,
+                  type == QMM_TYPE_Q8_0 ? 64 : bs);
+    return false;
+  }
+  if (b < 0 || b > 2 || (b > 1 && stride_col_x < ncols_x)) {
+    qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
+    return false;
+  }
+  const uintptr_t align = type == QMM_TYPE_Q6K ? 2 : (type == QMM_TYPE_Q8_0 ? 4 : 16);
+  for (const void *w : ws)
+    if ((!w && !null_ok) || (uintptr_t)w % align != 0) {
+      qmm_set_error("%s: weights must be non-null and %zu-byte aligned", who, (size_t)align);
+      return false;
+    }
+  if (!x || (uintptr_t)x % 4 != 0) {
+    qmm_set_error("%s: x must be non-null and 4-byte aligned", who);
+    return false;
+  }
+  return true;
+}
+
+// launch_mmvq_gguf_<t>_<dt>_fused_glu_quantize: dst = act(W_gate . Q(x)) * (W_up . Q(x)), x quantized in the launch
+template <int T, class Out>
+void fused_glu_quantize_t(const void *vx_gate, const void *vx_up, const float *x, void *dst, int ncols_x,
+                          int nrows_x, int stride_col_x, int stride_col_dst, int b, int activation, void *stream,
+                          const char *who) {
+  if (!check_pq(who, T, {vx_gate, vx_up}, x, ncols_x, stride_col_x, b)) return;
+  if (nrows_x < 0 || stride_col_dst < nrows_x || activation < 0 || activation >= kGluActivations) {
+    qmm_set_error("%s: nrows_x=%d stride_col_dst=%d activation=%d", who, nrows_x, stride_col_dst, activation);
+    return;
+  }
+  if (b == 0 || nrows_x == 0) return;
+  typedef pq_unit<T> U;
+  const uint8_t *w[1] = {(const uint8_t *)vx_gate}, *w2[1] = {(const uint8_t *)vx_up};
+  typename Out::T *d[1] = {(typename Out::T *)dst};
+  const int rows[1] = {nrows_x}, ldd[1] = {stride_col_dst};
+  if (b == 1)
+    launch_pqs<U, U, 1, 1, Out, 1, true>(w, w2, d, rows, x, stride_col_x, ncols_x, ldd, activation, (hipStream_t)stream);
+  else
+    launch_pqs<U, U, 1, 1, Out, 2, true>(w, w2, d, rows, x, stride_col_x, ncols_x, ldd, activation, (hipStream_t)stream);
+}
+
+// launch_mmvq_gguf_<t>_<dt>_fused_qkv_quantize (TV = T) and the mixed form with Q6_K v weights (T = Q4_K):
+// q / k / v = W_q / W_k / W_v . Q(x), x quantized in the launch; each output row holds nrows_* values
+template <int T, int TV, class Out>
+void fused_qkv_quantize_t(const void *vx_q, const void *vx_k, const void *vx_v, const float *x, void *q_dst,
+                          void *k_dst, void *v_dst, int ncols_x, int nrows_q, int nrows_k, int nrows_v,
+                          int stride_col_x, int b, void *stream, const char *who) {
+  // the weights and outputs of an empty projection are not read and may be null
+  const void *none = nullptr;
+  if (!check_pq(who, T, {nrows_q ? vx_q : none, nrows_k ? vx_k : none}, x, ncols_x, stride_col_x, b, true)) return;
+  if (!check_pq(who, TV, {nrows_v ? vx_v : none}, x, ncols_x, stride_col_x, b, true)) return;
+  if ((nrows_q && !vx_q) || (nrows_k && !vx_k) || (nrows_v && !vx_v)) {
+    qmm_set_error("%s: weights of non-empty projections must be non-null", who);
+    return;
+  }
+  if (nrows_q < 0 || nrows_k < 0 || nrows_v < 0 || (nrows_q && !q_dst) || (nrows_k && !k_dst) ||
+      (nrows_v && !v_dst)) {
+    qmm_set_error("%s: nrows_q=%d nrows_k=%d nrows_v=%d (outputs of non-empty projections non-null)", who, nrows_q,
+                  nrows_k, nrows_v);
+    return;
+  }
+  if (b == 0) return;
+  typedef pq_unit<T> UA;
+  typedef pq_unit<TV> UB;
+  // empty segments are left out
+  const uint8_t *w[3];
+  typename Out::T *d[3];
+  int rows[3], ldd[3], n = 0, na = 0;
+  const void *ws[3] = {vx_q, vx_k, vx_v};
+  void *ds[3] = {q_dst, k_dst, v_dst};
+  const int rs[3] = {nrows_q, nrows_k, nrows_v};
+  for (int i = 0; i < 3; i++) {
+    if (rs[i] == 0) continue;
+    w[n] = (const uint8_t *)ws[i];
+    d[n] = (typename Out::T *)ds[i];
+    rows[n] = ldd[n] = rs[i];
+    n++;
+    if (i < 2) na = n;
+  }
+  if (n == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+#define QMM_PQS(NA, NS)                                                                                          \
+  (b == 1 ? launch_pqs<UA, UB, NA, NS, Out, 1, false>(w, nullptr, d, rows, x, stride_col_x, ncols_x, ldd, 0, s)  \
+          : launch_pqs<UA, UB, NA, NS, Out, 2, false>(w, nullptr, d, rows, x, stride_col_x, ncols_x, ldd, 0, s))
+  if (n == 3)
+    QMM_PQS(2, 3);
+  else if (n == 2 && na == 2)
+    QMM_PQS(2, 2);
+  else if (n == 2)
+    QMM_PQS(1, 2);
+  else if (na == 1)
+    QMM_PQS(1, 1);
+  else
+    QMM_PQS(0, 1);
+#undef QMM_PQS
+}
+
 template <int T, class Out>
 void tc_plain_t(const void *vx, const void *vy, void *dst, int ncols_x, int nrows_x, int stride_col_dst, int b,
                 int cfg, void *stream, const char *who) {
@@ -970,6 +1295,27 @@ void moe_gemv_down_aggregate_t(const void *w, const void *x, const uint32_t *ids
   QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, f32, out_f32)    \
   QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, f16, out_f16)    \
   QMM_MMVQ_QUANTIZE_PLAIN_DT(t, T, bf16, out_bf16)
+
+#define QMM_MMVQ_FUSED_QUANTIZE_DT(t, T, dt, Out)                                                                  \
+  void launch_mmvq_gguf_##t##_##dt##_fused_glu_quantize(const void *vx_gate, const void *vx_up, const float *x,      \
+                                                        void *dst, int ncols_x, int nrows_x, int stride_col_x,       \
+                                                        int stride_col_dst, int b_size, int activation,              \
+                                                        void *stream) {                                              \
+    fused_glu_quantize_t<T, Out>(vx_gate, vx_up, x, dst, ncols_x, nrows_x, stride_col_x, stride_col_dst, b_size,     \
+                                 activation, stream, "mmvq_" #t "_" #dt "_fused_glu_quantize");                      \
+  }                                                                                                                  \
+  void launch_mmvq_gguf_##t##_##dt##_fused_qkv_quantize(const void *vx_q, const void *vx_k, const void *vx_v,        \
+                                                        const float *x, void *q_dst, void *k_dst, void *v_dst,       \
+                                                        int ncols_x, int nrows_q, int nrows_k, int nrows_v,          \
+                                                        int stride_col_x, int b_size, void *stream) {                \
+    fused_qkv_quantize_t<T, T, Out>(vx_q, vx_k, vx_v, x, q_dst, k_dst, v_dst, ncols_x, nrows_q, nrows_k, nrows_v,    \
+                                    stride_col_x, b_size, stream, "mmvq_" #t "_" #dt "_fused_qkv_quantize");         \
+  }
+// launch_mmvq_gguf_<t>_{f32,f16,bf16}_fused_{glu,qkv}_quantize
+#define QMM_MMVQ_FUSED_QUANTIZE(t, T)               \
+  QMM_MMVQ_FUSED_QUANTIZE_DT(t, T, f32, out_f32)    \
+  QMM_MMVQ_FUSED_QUANTIZE_DT(t, T, f16, out_f16)    \
+  QMM_MMVQ_FUSED_QUANTIZE_DT(t, T, bf16, out_bf16)
 
 // launch_mmvq_gguf_<t>_moe<sfx> and launch_mmvq_gguf_<t>_moe_wsum<sfx>
 #define QMM_MMVQ_MOE(t, T, F, sfx)                                                                                 \

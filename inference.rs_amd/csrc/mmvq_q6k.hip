@@ -4,6 +4,7 @@
 extern "C" {
 QMM_MMVQ_PLAIN(q6_k, QMM_TYPE_Q6K, kActSlots, )
 QMM_MMVQ_QUANTIZE_PLAIN(q6_k, QMM_TYPE_Q6K)
+QMM_MMVQ_FUSED_QUANTIZE(q6_k, QMM_TYPE_Q6K)
 QMM_MMVQ_MOE(q6_k, QMM_TYPE_Q6K, kActSlots, )
 QMM_MMVQ_INDEXED(q6k, QMM_TYPE_Q6K, kActSlots, q8_1)
 QMM_MOE_GEMV(q6k, QMM_TYPE_Q6K)

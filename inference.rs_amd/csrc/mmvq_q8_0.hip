@@ -10,4 +10,5 @@ QMM_MMVQ_PLAIN(q8_0, QMM_TYPE_Q8_0, kActQ8_0, _q8_0)
 QMM_MMVQ_MOE(q8_0, QMM_TYPE_Q8_0, kActQ8_0, _q8_0)
 QMM_MMVQ_INDEXED(q8_0, QMM_TYPE_Q8_0, kActQ8_0, q8_0)
 QMM_MMVQ_QUANTIZE_PLAIN(q8_0, QMM_TYPE_Q8_0)
+QMM_MMVQ_FUSED_QUANTIZE(q8_0, QMM_TYPE_Q8_0)
 }

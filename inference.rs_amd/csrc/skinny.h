@@ -8,7 +8,15 @@
 
 // From this many activation rows on, K-quant weights go through the MFMA few-row kernel, which decodes each weight
 // block once for all rows (measured crossover on MI355X: Q4_K 4 rows, Q6_K 3).
-inline int qmm_skinny_min_rows(int type) { return type == QMM_TYPE_Q6K ? 3 : 4; }
+#ifndef QMM_SKINNY_MIN_ROWS_Q4K
+#define QMM_SKINNY_MIN_ROWS_Q4K 4
+#endif
+#ifndef QMM_SKINNY_MIN_ROWS_Q6K
+#define QMM_SKINNY_MIN_ROWS_Q6K 3
+#endif
+inline int qmm_skinny_min_rows(int type) {
+  return type == QMM_TYPE_Q6K ? QMM_SKINNY_MIN_ROWS_Q6K : QMM_SKINNY_MIN_ROWS_Q4K;
+}
 
 // Decode-layout activations (b rows of Q8_K blocks, stride_col_y blocks apart) against Q4_K / Q6_K weights;
 // dst[j * stride_col_dst + row] of element type out_type (QMM_TYPE_F32 / F16 / BF16).  Returns false, launching

@@ -21,6 +21,10 @@
 
 #include "common.h"
 
+// No multiply is fused into an add here: each unit's f32 arithmetic is the same instructions in every kernel that
+// inlines it, whatever the code around it, so the decode entries that share a unit give the same bits.
+#pragma clang fp contract(off)
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16 bytes from a 16-byte aligned address
@@ -865,3 +869,4 @@ inline bool reads_pairs(int ncols_x, int stride_col_y, const void *vy, std::init
   return ok;
 }
 
+#pragma clang fp contract(fast)

@@ -253,6 +253,39 @@ def mmvq_quantize(wtype: int, w, x, n: int, out_dtype=None, out=None):
     return out
 
 
+def mmvq_fused_glu_quantize(wtype: int, w_gate, w_up, x, n: int, activation: int = 0, out_dtype=None, out=None):
+    """act(W_gate . Q(x)) * (W_up . Q(x)) for f32 x [b, k] (b <= 2, k <= 4096), quantized inside the launch:
+    launch_mmvq_gguf_<t>_<dtype>_fused_glu_quantize."""
+    torch = _torch()
+    b, k = x.shape
+    if out is None:
+        out = torch.empty((b, n), dtype=out_dtype or torch.float32, device=w_gate.device)
+    getattr(lib(), f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{_oname(out)}_fused_glu_quantize")(
+        _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(out), k, n, x.stride(0), out.stride(0), b, activation, _stream())
+    check()
+    return out
+
+
+def mmvq_fused_qkv_quantize(wtype: int, wq, wk, wv, x, nq: int, nk: int, nv: int, out_dtype=None, outs=None,
+                            vtype=None):
+    """(q, k, v) = W . Q(x) for f32 x [b, k] (b <= 2, k <= 4096), quantized inside the launch:
+    launch_mmvq_gguf_<t>_<dtype>_fused_qkv_quantize, or with vtype = Q6K for Q4_K q / k,
+    launch_mmvq_gguf_q4_k_q6_k_f32_fused_qkv_quantize."""
+    torch = _torch()
+    b, k = x.shape
+    if outs is None:
+        dt = out_dtype or torch.float32
+        outs = tuple(torch.empty((b, n), dtype=dt, device=x.device) for n in (nq, nk, nv))
+    if vtype is not None and vtype != wtype:
+        name = f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{TYPE_NAME[vtype]}_{_oname(outs[0])}_fused_qkv_quantize"
+    else:
+        name = f"launch_mmvq_gguf_{TYPE_NAME[wtype]}_{_oname(outs[0])}_fused_qkv_quantize"
+    getattr(lib(), name)(_ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), k, nq,
+                         nk, nv, x.stride(0), b, _stream())
+    check()
+    return outs
+
+
 def mmvq_fused_glu(wtype: int, w_gate, w_up, vy, k: int, n: int, b: int, kp: int, activation: int = 0,
                    out_dtype=None, out=None, q8_1=None):
     """dst [b, n] = act(Q(y) . W_gate^T) * (Q(y) . W_up^T) through launch_mmvq_gguf_<t>_<dtype>_fused_glu."""

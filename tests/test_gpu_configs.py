@@ -40,12 +40,12 @@ def stack():
     return ws, {name: dev(w) for name, w in ws.items()}
 
 
-@pytest.mark.parametrize("b", [1, 8, 24, 32])
+@pytest.mark.parametrize("b", [1, 2, 8, 24, 32])
 def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
     """Each projection of one layer through the launch sequence bench.py's stack workload times, on QMatMul's route:
-    the decode quantizer once per input and the matvec up to 32 rows (o in one launch with its own quantization at
-    b <= 2; gate and up as one fused-GLU launch, SiLU), except the Q6_K down projection (K = 14336), which takes
-    the prefill quantizer and matmul above 16 rows."""
+    the decode quantizer once per input and the matvec up to 32 rows (gate and up as one fused-GLU launch, SiLU),
+    except the Q6_K down projection (K = 14336), which takes the prefill quantizer and matmul above 16 rows; at
+    b <= 2, q / k / v in one launch and o and gate / up each in one, all three quantizing their own inputs."""
     ws, wd = stack
     rng = np.random.default_rng(40 + b)
     x = {"attn": acts(rng, b, 4096), "o": acts(rng, b, 4096), "ffn": acts(rng, b, 4096), "down": acts(rng, b, 14336)}
@@ -55,6 +55,12 @@ def test_llama3_stack_projections_as_the_bench_runs_them(stack, b):
     xd = {g: dev(v) for g, v in x.items()}
     dec_of = {"attn": b <= 32, "o": b <= 32, "ffn": b <= 32, "down": b <= 16}
     bufs = {g: (qmm.quantize_decode(O.Q4K, v) if dec_of[g] else qmm.quantize_prefill(O.Q4K, v)) for g, v in xd.items()}
+    if b <= 2:
+        outs = qmm.mmvq_fused_qkv_quantize(O.Q4K, wd["q"], wd["k"], wd["v"], xd["attn"], 4096, 1024, 1024, vtype=O.Q6K)
+        for name, got in zip("qkv", outs):
+            assert_parity(got.cpu().numpy(), want[name], what=f"b={b} one-launch {name}")
+        got = qmm.mmvq_fused_glu_quantize(O.Q4K, wd["gate"], wd["up"], xd["ffn"], 14336, activation=0).cpu().numpy()
+        assert_parity(got, silu(want["gate"]) * want["up"], what=f"b={b} one-launch gate/up")
     for name in ("q", "k", "v", "o", "down"):
         t, n, k = spec[name]
         vy, kp = bufs[group[name]]

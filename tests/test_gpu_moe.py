@@ -163,15 +163,19 @@ def test_grouped_down_with_folded_weighted_sum(gtype, case):
         ids = skewed_routing(rng, tokens, E, topk)
     w[3, 1] = 0.0  # a zero-weight route: skipped by the sum
     x = acts(rng, tokens, k)
-    routes_want = O.indexed_moe(gtype, wq, E, n, k, x[:, None], ids.astype(np.uint32))
+    if gtype in (O.Q8_0, O.Q4_0):  # the entry reads Q8_K tiles: the oracle's matmul over Q8_K activations per route
+        routes_want = np.stack([np.stack([O.matmul_q8k_act(gtype, x[t: t + 1], wq[ids[t, s]], n)[0]
+                                          for s in range(topk)]) for t in range(tokens)])
+    else:
+        routes_want = O.indexed_moe(gtype, wq, E, n, k, x[:, None], ids.astype(np.uint32))
     want = O.moe_weighted_reduce(routes_want, w)
     bounds, tok, src, counts, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
-    y, kp = qmm.quantize_prefill(gtype, to_dev(x), ids=src)
+    y, kp = qmm.quantize_prefill(gtype, to_dev(x), ids=src, q8_1=True)
     ncols_max = int(counts.max().item())
     wd, wt = to_dev(wq), to_dev(w.reshape(-1))
     # the two launches: grouped matmul without split K, then the reduce
     routes = torch.full((tokens * topk, n), float("nan"), device=DEV)
-    qmm.mmq_moe(gtype, wd, y, tok, bounds, E, k, n, tokens * topk, ncols_max, routes, tmp_fixup=False)
+    qmm.mmq_moe(gtype, wd, y, tok, bounds, E, k, n, tokens * topk, ncols_max, routes, tmp_fixup=False, q8_1=True)
     two = qmm.moe_weighted_reduce(routes.reshape(tokens, topk, n), wt).cpu().numpy()
     counters = torch.zeros(tokens * ((n + 31) // 32), dtype=torch.int32, device=DEV)
     for call in range(2):

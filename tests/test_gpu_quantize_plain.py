@@ -86,3 +86,62 @@ def test_rejected_shapes_launch_nothing(gtype, k, b):
         qmm.mmvq_quantize(gtype, wd, to_dev(acts(rng, b, k)), n, out=out)
     torch.cuda.synchronize()
     assert bool((out == 5.0).all())
+
+
+# ------------------------------------------------------------------------------------------------ several weights
+
+QK = {O.Q4K: 4096, O.Q6K: 2048, O.Q8_0: 1024}
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q8_0])
+@pytest.mark.parametrize("b", [1, 2])
+@pytest.mark.parametrize("activation", [0, 2])
+def test_fused_glu_quantize_same_bits_as_two_launches(gtype, b, activation):
+    """launch_mmvq_gguf_<t>_f32_fused_glu_quantize: the bits of the decode quantizer followed by _fused_glu, and the
+    oracle's act(gate) * up within the north-star bound."""
+    rng = np.random.default_rng(300 + gtype + b + activation)
+    n, k = 300, QK[gtype]
+    wg, wu = O.quantize(gtype, weights(rng, n, k)), O.quantize(gtype, weights(rng, n, k))
+    x = rows(rng, b, k)
+    xd = to_dev(x)
+    got = qmm.mmvq_fused_glu_quantize(gtype, to_dev(wg), to_dev(wu), xd, n, activation).cpu().numpy()
+    vy, kp = qmm.quantize_decode(gtype, xd)
+    two = qmm.mmvq_fused_glu(gtype, to_dev(wg), to_dev(wu), vy, k, n, b, kp, activation=activation).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), two.view(np.uint32))
+    g = O.matmul(gtype, x, wg, n).astype(np.float64)
+    u = O.matmul(gtype, x, wu, n).astype(np.float64)
+    f = (lambda v: v / (1 + np.exp(-v))) if activation == 0 else (lambda v: np.maximum(v, 0))
+    assert_parity(got, f(g) * u)
+
+
+@pytest.mark.parametrize("gtype,vtype", [(O.Q4K, O.Q4K), (O.Q6K, O.Q6K), (O.Q8_0, O.Q8_0), (O.Q4K, O.Q6K)])
+@pytest.mark.parametrize("b", [1, 2])
+@pytest.mark.parametrize("ns", [(4096, 1024, 1024), (128, 0, 48), (0, 0, 64), (200, 33, 0)])
+def test_fused_qkv_quantize(gtype, vtype, b, ns):
+    """launch_mmvq_gguf_<t>_f32_fused_qkv_quantize (and the Q4_K / Q6_K mix): each output the bits of the decode
+    quantizer followed by that weight's plain matvec (an empty projection is left out), and the oracle's."""
+    rng = np.random.default_rng(400 + gtype + vtype + b + sum(ns))
+    k = QK[gtype] if gtype == vtype else 4096
+    types = (gtype, gtype, vtype)
+    ws = [O.quantize(t, weights(rng, max(n, 1), k)) for t, n in zip(types, ns)]
+    x = rows(rng, b, k)
+    xd = to_dev(x)
+    outs = qmm.mmvq_fused_qkv_quantize(gtype, *(to_dev(w) for w in ws), xd, *ns, vtype=vtype)
+    for t, w, n, got in zip(types, ws, ns, outs):
+        if n == 0:
+            continue
+        vy, kp = qmm.quantize_decode(t, xd)
+        two = qmm.mmvq(t, to_dev(w), vy, k, n, b, kp).cpu().numpy()
+        g = got.cpu().numpy()
+        assert np.array_equal(g.view(np.uint32), two.view(np.uint32)), f"type {t} n={n}"
+        assert_parity(g, O.matmul(t, x, w, n), what=f"type {t} n={n}")
+
+
+def test_fused_quantize_rejects_bad_shapes():
+    w = torch.zeros(144 * 64, dtype=torch.uint8, device=DEV)
+    x = torch.zeros((3, 256), device=DEV)
+    with pytest.raises(qmm.QmmError, match="b_size"):
+        qmm.mmvq_fused_glu_quantize(O.Q4K, w, w, x, 4)
+    x = torch.zeros((1, 8192), device=DEV)
+    with pytest.raises(qmm.QmmError, match="4096"):
+        qmm.mmvq_fused_qkv_quantize(O.Q4K, w, w, w, x, 1, 1, 1)

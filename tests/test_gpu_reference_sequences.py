@@ -112,9 +112,9 @@ def test_indexed_moe_forward_sequence(gtype, xdim1):
     x = acts(rng, batch * xdim1, k)
     vy, kp, nbytes = decode_quantize(to_dev(x), k)
     out = torch.full((batch * topk, n), float("nan"), device=DEV)
+    wd, idd = to_dev(wq), to_dev(ids)  # held until the launch has run
     getattr(qmm.lib(), f"launch_indexed_moe_forward_{qmm.MOE_TYPE[gtype]}_q8_1")(
-        qmm._ptr(to_dev(wq)), qmm._ptr(vy), qmm._ptr(to_dev(ids)), qmm._ptr(out), n, k, batch, topk, kp, xdim1,
-        qmm._stream())
+        qmm._ptr(wd), qmm._ptr(vy), qmm._ptr(idd), qmm._ptr(out), n, k, batch, topk, kp, xdim1, qmm._stream())
     qmm.check()
     assert_guard(vy, nbytes, "quantize_q8_1")
     want = np.zeros((batch * topk, n), np.float32)
@@ -152,11 +152,13 @@ def test_moe_gemv_fused_decode_sequence(gtype, act_type):
     L = qmm.lib()
     t = qmm.MOE_TYPE[gtype]
 
+    # device copies held until the launches have run (a temporary freed at once could be reused by the next copy)
+    gd, ud, dd, idd, twd = (to_dev(a) for a in (gate, up, down, ids.reshape(-1), tw.reshape(-1)))
     vy, kp, nbytes = decode_quantize(to_dev(x), hidden)
     h = torch.full((batch * topk, inter), float("nan"), device=DEV)
     getattr(L, f"launch_moe_gemv_fused_gate_up_{t}_q8_1")(
-        qmm._ptr(to_dev(gate)), qmm._ptr(to_dev(up)), qmm._ptr(vy), qmm._ptr(to_dev(ids.reshape(-1))), qmm._ptr(h),
-        inter, hidden, batch, topk, kp, act_type, qmm._stream())
+        qmm._ptr(gd), qmm._ptr(ud), qmm._ptr(vy), qmm._ptr(idd), qmm._ptr(h), inter, hidden, batch, topk, kp, act_type,
+        qmm._stream())
     qmm.check()
     assert_guard(vy, nbytes, "quantize_q8_1 (hidden)")
     act = gelu_tanh if act_type == 0 else silu
@@ -175,8 +177,8 @@ def test_moe_gemv_fused_decode_sequence(gtype, act_type):
     for start in (np.zeros_like(init), init):
         out = to_dev(start)
         getattr(L, f"launch_moe_gemv_down_aggregate_{t}_q8_1")(
-            qmm._ptr(to_dev(down)), qmm._ptr(vh), qmm._ptr(to_dev(ids.reshape(-1))), qmm._ptr(to_dev(tw.reshape(-1))),
-            qmm._ptr(out), hidden, inter, batch, topk, kp2, qmm._stream())
+            qmm._ptr(dd), qmm._ptr(vh), qmm._ptr(idd), qmm._ptr(twd), qmm._ptr(out), hidden, inter, batch, topk, kp2,
+            qmm._stream())
         qmm.check()
         assert_guard(vh, nbytes2, "quantize_q8_1 (intermediate)")
         want = np.zeros((batch, hidden), np.float64)
