@@ -520,11 +520,14 @@ __device__ __forceinline__ void row_pairs_glu(const uint8_t *vg, const uint8_t *
   }
 }
 
-// One segment's part of k_mmvq_pqs: the workgroup's rows are local_block * NW + wave + t * local_grid * NW.
-template <class U, class Out, int NC, bool FULL, int NW, int G, bool GLU>
+// One segment's part of k_mmvq_pqs: the workgroup's rows are local_block * kPqsWaves + wave + t * local_grid *
+// kPqsWaves.  S units per lane (FULL: all of them in every lane).
+constexpr int kPqsWaves = 8;
+template <class U, class Out, int NC, int S, bool FULL, int G, bool GLU>
 __device__ __forceinline__ void pqs_segment(const PqSeg &sg, int local_block, int local_grid,
                                             const float *__restrict__ x, int64_t stride_x, int nunits,
                                             uint8_t *s_act, int activation) {
+  constexpr int NW = kPqsWaves;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nblk = nunits * U::kValuesPerUnit / U::kActBlockValues;
   const int64_t act_row_bytes = (int64_t)nblk * U::kActBlockBytes;
@@ -533,37 +536,39 @@ __device__ __forceinline__ void pqs_segment(const PqSeg &sg, int local_block, in
   qa.load(x, stride_x, nblk, lane, wave);
   const int tw = local_grid * NW;
   int row = local_block * NW + wave;
-  typename U::W ga[1], gb[1], ua[1], ub[1];
-  load_row<U, 1, FULL>(sg.w, row_bytes, nunits, sg.nrows, row, lane, ga);
-  load_row<U, 1, FULL>(sg.w, row_bytes, nunits, sg.nrows, row + tw, lane, gb);
-  if (GLU) {
-    load_row<U, 1, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row, lane, ua);
-    load_row<U, 1, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row + tw, lane, ub);
+  typename U::W ga[S], gb[S], ua[GLU ? S : 1], ub[GLU ? S : 1];
+  load_row<U, S, FULL>(sg.w, row_bytes, nunits, sg.nrows, row, lane, ga);
+  load_row<U, S, FULL>(sg.w, row_bytes, nunits, sg.nrows, row + tw, lane, gb);
+  if constexpr (GLU) {
+    load_row<U, S, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row, lane, ua);
+    load_row<U, S, FULL>(sg.w2, row_bytes, nunits, sg.nrows, row + tw, lane, ub);
   }
   __builtin_amdgcn_sched_barrier(0);
   qa.quantize(s_act, lane);
   __syncthreads();
   if (row >= sg.nrows) return;  // whole wave
-  constexpr bool kRegs = NC <= 2;
-  typename U::A areg[kRegs ? NC : 1];
+  constexpr bool kRegs = NC * S <= 2;
+  typename U::A areg[kRegs ? NC * S : 1];
   if (kRegs) {
 #pragma unroll
-    for (int j = 0; j < NC; j++)
-      if (FULL || lane < nunits) U::load_a(s_act + j * act_row_bytes, lane, areg[kRegs ? j : 0]);
+    for (int s = 0; s < S; s++)
+#pragma unroll
+      for (int j = 0; j < NC; j++)
+        if (FULL || lane + 64 * s < nunits) U::load_a(s_act + j * act_row_bytes, lane + 64 * s, areg[kRegs ? s * NC + j : 0]);
   }
   typename Out::T *dst = (typename Out::T *)sg.dst;
   if constexpr (GLU)
-    row_pairs_glu<U, Out, NC, 1, FULL, kRegs>(sg.w, sg.w2, row_bytes, nunits, sg.nrows, row, tw, lane, ga, ua, gb, ub,
+    row_pairs_glu<U, Out, NC, S, FULL, kRegs>(sg.w, sg.w2, row_bytes, nunits, sg.nrows, row, tw, lane, ga, ua, gb, ub,
                                               areg, s_act, act_row_bytes, dst, sg.stride_col_dst, activation);
   else
-    row_pairs<U, Out, NC, 1, FULL, kRegs>(sg.w, row_bytes, nunits, sg.nrows, row, tw, lane, ga, gb, areg, s_act,
+    row_pairs<U, Out, NC, S, FULL, kRegs>(sg.w, row_bytes, nunits, sg.nrows, row, tw, lane, ga, gb, areg, s_act,
                                           act_row_bytes, dst, sg.stride_col_dst);
 }
 
 // Segments [0, NA) take unit UA, the rest UB (which share UA's activation format); NS segments in all.
-template <class UA, class UB, int NA, int NS, class Out, int NC, bool FULL, int NW, int G, bool GLU>
-__global__ __launch_bounds__(64 * NW) void k_mmvq_pqs(PqSegs segs, const float *__restrict__ x, int64_t stride_x,
-                                                      int nunits, int activation) {
+template <class UA, class UB, int NA, int NS, class Out, int NC, int S, bool FULL, int G, bool GLU>
+__global__ __launch_bounds__(64 * kPqsWaves) void k_mmvq_pqs(PqSegs segs, const float *__restrict__ x,
+                                                             int64_t stride_x, int nunits, int activation) {
   static_assert(UA::kActBlockValues == UB::kActBlockValues && UA::kActBlockBytes == UB::kActBlockBytes,
                 "segments share one quantized activation");
   extern __shared__ __align__(16) uint8_t s_act[];
@@ -576,9 +581,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmvq_pqs(PqSegs segs, const float *
   const int local = b - segs.s[si].wg0, grid = end - segs.s[si].wg0;
   // the segment is uniform over the workgroup
   if (si < NA)
-    pqs_segment<UA, Out, NC, FULL, NW, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
+    pqs_segment<UA, Out, NC, S, FULL, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
   else
-    pqs_segment<UB, Out, NC, FULL, NW, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
+    pqs_segment<UB, Out, NC, S, FULL, G, GLU>(segs.s[si], local, grid, x, stride_x, nunits, s_act, activation);
 }
 
 // MoE matvec: grid (pairs, row groups) -- pairs innermost so the pairs of one expert share the row group's
@@ -821,30 +826,30 @@ void launch_pq(const uint8_t *vx, const float *x, int64_t stride_x, typename Out
 }
 
 
-// Grid of k_mmvq_pqs: as launch_pq_nw, split between the segments in proportion to their weight bytes (each at least
-// one workgroup, and none more workgroups than its rows fill).  rows[i], w[i], w2[i], dst[i] per segment.
+// Grid of k_mmvq_pqs: 8-wave workgroups, two per CU (one for the GLU form, whose waves hold two rows' weights per
+// step; measured on MI355X at the Llama-3 shapes: q/k/v 8.5 us at two per CU against 10.3 us for one 16-wave
+// workgroup per CU, gate/up 15.2 against 16.1 us at two), split between the segments in proportion to their weight
+// bytes (each at least one workgroup, and none more workgroups than its rows fill).  rows[i], w[i], w2[i], dst[i] per
+// segment.  One unit per lane (k <= 4096).
 template <class UA, class UB, int NA, int NS, class Out, int NC, bool GLU>
 void launch_pqs(const uint8_t *const *w, const uint8_t *const *w2, typename Out::T *const *dst, const int *rows,
                 const float *x, int64_t stride_x, int k, const int *stride_col_dst, int activation, hipStream_t s) {
+  constexpr int NW = kPqsWaves;
   const int nu = UA::units(k);
-  const bool full = nu % 64 == 0;
   const int nblk = nu * UA::kValuesPerUnit / UA::kActBlockValues;
-  const int steps = (int)qmm_ceil_div((int64_t)NC * nblk, UA::kActBlockValues == 256 ? 1 : 8);  // <= 32
+  const int steps = (int)qmm_ceil_div((int64_t)NC * nblk, UA::kActBlockValues == 256 ? 1 : 8);
   const size_t lds = (size_t)NC * nblk * UA::kActBlockBytes;
-  int64_t total_rows = 0;
   double bytes[3] = {0, 0, 0}, all = 0;
   for (int i = 0; i < NS; i++) {
-    total_rows += rows[i];
     bytes[i] = (double)rows[i] * (double)(i < NA ? UA::row_bytes(k) : UB::row_bytes(k)) * (GLU ? 2 : 1);
     all += bytes[i];
   }
-  auto go = [&](auto nw_tag, auto g_tag, auto full_tag) {
-    constexpr int NW = decltype(nw_tag)::value, G = decltype(g_tag)::value;
+  auto go = [&](auto s_tag, auto g_tag, auto full_tag) {
+    constexpr int S = decltype(s_tag)::value, G = decltype(g_tag)::value;
     constexpr bool FF = decltype(full_tag)::value;
-    auto kern = k_mmvq_pqs<UA, UB, NA, NS, Out, NC, FF, NW, G, GLU>;
-    const int per_cu = qmm_resident_per_cu<k_mmvq_pqs<UA, UB, NA, NS, Out, NC, FF, NW, G, GLU>>(64 * NW, lds);
-    const int kCap = NW == 8 ? 1 : 2;
-    const int wgs = (per_cu < kCap ? per_cu : kCap) * qmm_device_cus();
+    const int per_cu = qmm_resident_per_cu<k_mmvq_pqs<UA, UB, NA, NS, Out, NC, S, FF, G, GLU>>(64 * NW, lds);
+    const int cap = GLU ? 1 : 2;
+    const int wgs = (per_cu < cap ? per_cu : cap) * qmm_device_cus();
     PqSegs segs = {};
     int next = 0;
     for (int i = 0; i < NS; i++) {
@@ -854,31 +859,24 @@ void launch_pqs(const uint8_t *const *w, const uint8_t *const *w2, typename Out:
       segs.s[i] = PqSeg{w[i], GLU ? w2[i] : nullptr, (void *)dst[i], rows[i], stride_col_dst[i], next};
       next += n;
     }
-    kern<<<dim3((unsigned)next), 64 * NW, lds, s>>>(segs, x, stride_x, nu, activation);
+    k_mmvq_pqs<UA, UB, NA, NS, Out, NC, S, FF, G, GLU><<<dim3((unsigned)next), 64 * NW, lds, s>>>(segs, x, stride_x,
+                                                                                                 nu, activation);
   };
-  typedef std::integral_constant<int, 8> nw8;
-  typedef std::integral_constant<int, 16> nw16;
-  auto pick_g = [&](auto nw_tag, auto full_tag) {
-    constexpr int NW = decltype(nw_tag)::value;
-    if (steps <= NW)
-      go(nw_tag, std::integral_constant<int, 1>(), full_tag);
-    else if (steps <= 2 * NW)
-      go(nw_tag, std::integral_constant<int, 2>(), full_tag);
+  typedef std::integral_constant<int, 1> i1;
+  typedef std::integral_constant<int, 2> i2;
+  typedef std::integral_constant<int, 4> i4;
+  auto pick_full = [&](auto s_tag, auto g_tag) {
+    if (nu == 64 * decltype(s_tag)::value)
+      go(s_tag, g_tag, std::true_type());
     else
-      go(nw_tag, std::integral_constant<int, 4>(), full_tag);
+      go(s_tag, g_tag, std::false_type());
   };
-  // 8-wave workgroups for tall weights and the GLU form (two rows' weights per step; 16 waves would cap a wave at
-  // 128 registers), 16 below
-  auto pick_nw = [&](auto full_tag) {
-    if (GLU || total_rows >= 8192)
-      pick_g(nw8(), full_tag);
-    else
-      pick_g(nw16(), full_tag);
-  };
-  if (full)
-    pick_nw(std::true_type());
+  if (steps <= NW)
+    pick_full(i1(), i1());
+  else if (steps <= 2 * NW)
+    pick_full(i1(), i2());
   else
-    pick_nw(std::false_type());
+    pick_full(i1(), i4());
 }
 
 template <class U>
@@ -1001,7 +999,9 @@ void quantize_plain_t(const void *vx, const float *x, void *dst, int ncols_x, in
     qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
     return;
   }
-  // one unit per lane; every activation block of the b rows within kPqSteps wave steps of one workgroup
+  // one unit per lane; every activation block of the b rows within a few wave steps of one workgroup.  (Rows of
+  // four units per lane, K = 14336, quantized per workgroup the same way, measured slower on MI355X than the two
+  // launches: Q6_K 4096 x 14336 26.3 against 17.2 us, the 14336 values quantized again by every workgroup.)
   if (ncols_x > 64 * 64) {
     qmm_set_error("%s: ncols_x=%d (at most 4096)", who, ncols_x);
     return;
