@@ -21,12 +21,13 @@ __global__ __launch_bounds__(256) void k_quantize_q8ks_rows(const typename In::T
                                                             uint8_t *__restrict__ vy, int kx, int kx_padded,
                                                             int num_rows) {
   const int lane = threadIdx.x & 63;
-  const int64_t nsb = kx_padded / 256;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= nsb * num_rows) return;  // whole wave
-  const int64_t row = blk / nsb, sb = blk % nsb;
+  // 32-bit index arithmetic: blocks = kx_padded / 256 * num_rows fits an int (the launcher checks)
+  const unsigned nsb = (unsigned)kx_padded / 256;
+  const unsigned blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nsb * (unsigned)num_rows) return;  // whole wave
+  const unsigned row = blk / nsb, sb = blk - row * nsb;
   float v[4];
-  load4<In>(x + row * (int64_t)kx, sb * 256 + lane * 4, kx, v);
+  load4<In>(x + (int64_t)row * kx, (int64_t)sb * 256 + lane * 4, kx, v);
   q8k_wave(v, lane, q8k_slot_dst(vy, blk));
 }
 
@@ -35,12 +36,12 @@ template <class In>
 __global__ __launch_bounds__(256) void k_quantize_q8k_tc_rows(const typename In::T *__restrict__ x,
                                                               uint8_t *__restrict__ vy, int kx, int num_rows) {
   const int lane = threadIdx.x & 63;
-  const int64_t nsb = kx / 256;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= nsb * num_rows) return;  // whole wave
-  const int64_t row = blk / nsb, sb = blk % nsb;
+  const unsigned nsb = (unsigned)kx / 256;
+  const unsigned blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nsb * (unsigned)num_rows) return;  // whole wave
+  const unsigned row = blk / nsb, sb = blk - row * nsb;
   float v[4];
-  load4<In>(x + row * (int64_t)kx, sb * 256 + lane * 4, kx, v);
+  load4<In>(x + (int64_t)row * kx, (int64_t)sb * 256 + lane * 4, kx, v);
   q8k_wave(v, lane, q8k_tc_dst(vy, blk));
 }
 
@@ -62,23 +63,22 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_rows(const typename In::T
 
 // ------------------------------------------------------------------ prefill (tile) layout kernels
 
+// Grid (row groups of 4, superblock columns, channels): one block per wave, its indices from the grid with no
+// division (the 64-bit index divisions of a flat grid were a large share of each wave's few hundred instructions).
 template <class In>
 __global__ __launch_bounds__(256) void k_quantize_q8k_tiles(const typename In::T *__restrict__ x,
                                                             const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
                                                             int64_t ne00, int64_t s01, int64_t s02, int64_t s03,
-                                                            int64_t ne0, int64_t ne1, int64_t ne2, int64_t nblk) {
+                                                            int64_t ne0, int64_t ne1, int ne2) {
   const int lane = threadIdx.x & 63;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= nblk) return;
-  const int64_t nsb = ne0 / 256;
-  const int64_t per_chan = nsb * ne1;
-  const int64_t ch = blk / per_chan, rem = blk % per_chan;
-  const int64_t sb = rem / ne1, r = rem % ne1;
-  const int64_t i2 = ch % ne2, i3 = ch / ne2;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= ne1) return;  // whole wave
+  const int64_t sb = blockIdx.y, nsb = ne0 / 256;
+  const int ch = blockIdx.z, i2 = ch % ne2, i3 = ch / ne2;
   const int64_t src_row = ids ? ids[r] : r;
   float v[4];
   load4<In>(x + i3 * s03 + i2 * s02 + src_row * s01, sb * 256 + lane * 4, ne00, v);
-  q8k_wave(v, lane, q8k_tile_dst(vy + ch * per_chan * 276, ne1, nsb, sb, r));
+  q8k_wave(v, lane, q8k_tile_dst(vy + (int64_t)ch * nsb * ne1 * 276, ne1, nsb, sb, r));
 }
 
 template <class In>
@@ -131,12 +131,12 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const typename I
                                                                 const typename In::T *__restrict__ up,
                                                                 const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
                                                                 int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1,
-                                                                int activation, int64_t nblk) {
+                                                                int activation) {
+  // grid (row groups of 4, superblock columns), as k_quantize_q8k_tiles
   const int lane = threadIdx.x & 63;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= nblk) return;
-  const int64_t nsb = ne0 / 256;
-  const int64_t sb = blk / ne1, r = blk % ne1;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= ne1) return;  // whole wave
+  const int64_t nsb = ne0 / 256, sb = blockIdx.y;
   const int64_t src = (ids ? ids[r] : r) * s01;
   float v[4];
 #pragma unroll
@@ -180,6 +180,10 @@ void decode_q8ks(const void *x, void *vy, int kx, int kx_padded, int num_rows, v
   }
   const int64_t blocks = (int64_t)kx_padded / 256 * num_rows;
   if (blocks == 0) return;
+  if (blocks > INT32_MAX) {
+    qmm_set_error("quantize_q8_1: %lld blocks (at most 2^31 - 1)", (long long)blocks);
+    return;
+  }
   k_quantize_q8ks_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
       (const typename In::T *)x, (uint8_t *)vy, kx, kx_padded, num_rows);
 }
@@ -192,6 +196,10 @@ void tc_q8k(const void *x, void *vy, int kx, int num_rows, void *stream) {
   }
   const int64_t blocks = (int64_t)kx / 256 * num_rows;
   if (blocks == 0) return;
+  if (blocks > INT32_MAX) {
+    qmm_set_error("mmvq_tc_quantize: %lld blocks (at most 2^31 - 1)", (long long)blocks);
+    return;
+  }
   k_quantize_q8k_tc_rows<In><<<dim3((unsigned)qmm_ceil_div(blocks, 4)), 256, 0, (hipStream_t)stream>>>(
       (const typename In::T *)x, (uint8_t *)vy, kx, num_rows);
 }
@@ -264,22 +272,26 @@ void mmq_quantize_q8ks(const void *x, const int32_t *ids, void *vy, int type_x, 
                        int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, void *stream) {
   if (!tile_args_ok("mmq_quantize_q8_1", ne00, ne0, ne1, ne2, ne3)) return;
   const int64_t kt = tile_width(ne00);
-  const int64_t nblk = kt / 256 * ne1 * ne2 * ne3;
-  if (nblk == 0) return;
-  const dim3 grid((unsigned)qmm_ceil_div(nblk, 4));
+  if (kt == 0 || ne1 == 0) return;
+  if (kt / 256 > 65535 || ne2 * ne3 > 65535 || qmm_ceil_div(ne1, 4) > INT32_MAX) {
+    qmm_set_error("mmq_quantize_q8_1: ne0=%lld ne1=%lld ne2*ne3=%lld beyond the grid", (long long)ne0, (long long)ne1,
+                  (long long)(ne2 * ne3));
+    return;
+  }
+  const dim3 grid((unsigned)qmm_ceil_div(ne1, 4), (unsigned)(kt / 256), (unsigned)(ne2 * ne3));
   hipStream_t s = (hipStream_t)stream;
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
-      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, ne2, nblk);
+      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, (int)ne2);
       break;
     case QMM_TYPE_F16:
-      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1, ne2,
-                                                        nblk);
+      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
+                                                        (int)ne2);
       break;
     case QMM_TYPE_BF16:
       k_quantize_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
-                                                         ne2, nblk);
+                                                         (int)ne2);
       break;
     default: qmm_set_error("mmq_quantize_q8_1: unsupported input type %d", type_x);
   }
@@ -293,23 +305,26 @@ void mmq_quantize_glu_q8ks(const void *gate, const void *up, const int32_t *ids,
     qmm_set_error("mmq_quantize_glu_q8_1: activation %d", activation);
     return;
   }
-  const int64_t nblk = kt / 256 * ne1;
-  if (nblk == 0) return;
-  const dim3 grid((unsigned)qmm_ceil_div(nblk, 4));
+  if (kt == 0 || ne1 == 0) return;
+  if (kt / 256 > 65535 || qmm_ceil_div(ne1, 4) > INT32_MAX) {
+    qmm_set_error("mmq_quantize_glu_q8_1: ne0=%lld ne1=%lld beyond the grid", (long long)ne0, (long long)ne1);
+    return;
+  }
+  const dim3 grid((unsigned)qmm_ceil_div(ne1, 4), (unsigned)(kt / 256));
   hipStream_t s = (hipStream_t)stream;
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
       k_quantize_glu_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)gate, (const float *)up, ids, y, ne00, s01,
-                                                            kt, ne1, activation, nblk);
+                                                            kt, ne1, activation);
       break;
     case QMM_TYPE_F16:
       k_quantize_glu_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y, ne00,
-                                                            s01, kt, ne1, activation, nblk);
+                                                            s01, kt, ne1, activation);
       break;
     case QMM_TYPE_BF16:
       k_quantize_glu_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y,
-                                                             ne00, s01, kt, ne1, activation, nblk);
+                                                             ne00, s01, kt, ne1, activation);
       break;
     default: qmm_set_error("mmq_quantize_glu_q8_1: unsupported input type %d", type_x);
   }
