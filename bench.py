@@ -183,15 +183,18 @@ def prefill_workload(torch, qmm, gtype, n, k, m, copies, steps, warmup, seed):
     ws = device_copies(torch, wq, copies)
     rng = np.random.default_rng(seed + 1)
     x = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).cuda()
-    y, kp = qmm.quantize_prefill(gtype, x)
+    # QMatMul::forward's prefill route: Q4_K and Q5_K read the `_q8k` tiles (launch_mmq_quantize_q8k and the _q8k
+    # entries), Q6_K the Q8_K tiles, the 32-value types the Q8_0 tiles
+    q8k = gtype in (Q4K, Q5K)
+    y, kp = qmm.quantize_prefill(gtype, x, q8k=q8k)
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
 
     def step(i):
-        qmm.quantize_prefill(gtype, x, out=y)
-        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out)
+        qmm.quantize_prefill(gtype, x, out=y, q8k=q8k)
+        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out, q8k=q8k)
 
     def mmq_only(i):
-        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out)
+        qmm.mmq(gtype, ws[i % copies], y, k, n, m, out=out, q8k=q8k)
 
     t = graph_time(torch, step, steps, warmup)
     tk = graph_time(torch, mmq_only, steps, warmup)
@@ -535,8 +538,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no extra workloads, no CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs: one dispatch per launch (for rocprofv3 --pmc)")
-    ap.add_argument("--only", choices=sorted(EXTRA_NAMES), default=None,
-                    help="run only this extra workload (no headline, no CPU baseline) and print its JSON")
+    ap.add_argument("--only", choices=sorted(EXTRA_NAMES), default=None, nargs="+",
+                    help="run only these extra workloads (no headline, no CPU baseline) and print their JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only copy MB megabytes device-to-device 20 times (the known-size kernel that scales HBM "
                          "counters), then exit")
@@ -607,8 +610,11 @@ def main():
     }
     assert set(extra_runs) == EXTRA_NAMES
     if args.only:
-        log(f"only: {args.only}")
-        print(json.dumps({args.only: extra_runs[args.only]()}), flush=True)
+        res = {}
+        for name in args.only:
+            log(f"only: {name}")
+            res[name] = extra_runs[name]()
+        print(json.dumps(res), flush=True)
         return
 
     log("headline: Q4_K 14336x4096 decode b=1")

@@ -299,6 +299,13 @@ void launch_mmq_quantize_q8_1_DS4(const void *x, const int32_t *ids, void *vy, i
 void launch_mmq_quantize_q8_1_D2S6(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00,
                                    int64_t s01, int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2,
                                    int64_t ne3, void *stream);
+/* launch_mmq_quantize_q8k: no counterpart in the reference; the same arguments, writing `_q8k` tiles: the Q8_K tile
+ * layout with the sums of each 16 values as f16 in place of the int16 sums of 32 (qs[nsb][ne1][256], d[nsb][ne1] f32,
+ * h16[nsb][ne1][16] f16; 292 bytes per 256 values, more than the reference's MMQ scratch holds), which the `_q8k`
+ * prefill entries of Q4_K and Q5_K read with no conversion of the sums. */
+void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                             void *stream);
 /* launch_mmq_quantize_q8_0: no counterpart in the reference; the same arguments, writing the Q8_0 tile layout
  * (quantize_block32 per 32 values, bit-exact): the activations of the 32-value types' _q8_0 prefill entries. */
 void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
@@ -311,7 +318,9 @@ void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int t
  * 2 ReLU, 3 GELU (erf), 4 sigmoid (glu_activation.cuh).  The _f32 forms take f32 gate / up; the others gate / up of
  * type_x (0 f32, 1 f16, 30 bf16), where act(gate) is rounded to that type and multiplied by up in it, as the
  * reference's mmq_glu_product does (mmq_quantize.cu:230-235).
- * launch_mmq_quantize_glu_q8_0_f32 (no counterpart in the reference): f32 gate / up into the Q8_0 tile layout. */
+ * launch_mmq_quantize_glu_q8_0_f32 (no counterpart in the reference): f32 gate / up into the Q8_0 tile layout.
+ * launch_mmq_quantize_glu_q8k_f32 (no counterpart in the reference): f32 gate / up into the `_q8k` tile layout of
+ * launch_mmq_quantize_q8k, for the `_q8k` prefill entries. */
 #define QMM_DECLARE_MMQ_GLU(L)                                                                                    \
   void launch_mmq_quantize_glu_q8_1_##L##_f32(const float *gate, const float *up, const int32_t *ids, void *vy,   \
                                               int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1, int activation, \
@@ -324,6 +333,8 @@ QMM_DECLARE_MMQ_GLU(DS4)
 QMM_DECLARE_MMQ_GLU(D2S6)
 void launch_mmq_quantize_glu_q8_0_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
                                       int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream);
+void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                     int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream);
 
 /* ------------------------------------------------------------------ prefill matmul
  * launch_mmq_gguf_<t> (gguf/ffi.rs:902-918; host fast_mmq.rs:446-524, 604-715; kernel mmq_instance.cuh:
@@ -380,6 +391,15 @@ QMM_DECLARE_MMQ(iq4_xs)
 QMM_DECLARE_MMQ_Q8_0(q8_0)
 QMM_DECLARE_MMQ_Q8_0(q4_0)
 QMM_DECLARE_MMQ_Q8_0(q5_0)
+/* launch_mmq_gguf_{q4_k,q5_k}_q8k: no counterpart in the reference; launch_mmq_gguf_<t> over `_q8k` tiles
+ * (launch_mmq_quantize_q8k): the min term's activation sums come in the f16 form its MFMA takes, so the kernel skips
+ * converting them (the same result, about 9% fewer vector instructions per superblock) */
+void launch_mmq_gguf_q4_k_q8k(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,
+                              int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc,
+                              int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream);
+void launch_mmq_gguf_q5_k_q8k(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,
+                              int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc,
+                              int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream);
 /* launch_mmq_gguf_<t>_moe_wsum: no counterpart in the reference, whose grouped MoE runs launch_mmq_gguf_<t>_moe for
  * the down projection and then launch_moe_weighted_reduce_flat (inference-nn/src/moe/experts/backends.rs:2304-2334,
  * 2418-2446).  The same grouped matmul, with the routes' rows stored to routes[p * nrows_x + row] (p = ids_dst[c],

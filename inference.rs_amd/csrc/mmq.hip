@@ -62,7 +62,8 @@ struct ActTile {
 // way from global memory to an LDS slot.  The prefill layout keeps a superblock's rows contiguous, so thread t
 // moves 16-byte chunks t, t + NT, ... of each section (NT threads); every address is a per-thread constant plus a
 // scalar.
-template <int BMt, bool MIN, int NT>
+// SB: bytes of sums per row and superblock, 16 (int16 sums of 32) or 32 (the `_q8k` tiles' f16 sums of 16).
+template <int BMt, bool MIN, int NT, int SB = 16>
 struct ActStage {
   static_assert(BMt * 16 % NT == 0, "whole qs chunks per thread");
   static constexpr int NQ = BMt * 16 / NT;  // qs chunks per thread
@@ -81,7 +82,7 @@ struct ActStage {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NQ; i++) q[i] = __builtin_amdgcn_raw_buffer_load_b128(r, voff[0] + s_qs + 16 * NT * i, 0, 0);
-    if (MIN && tid < BMt) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
+    if (MIN && tid < BMt * SB / 16) bs = __builtin_amdgcn_raw_buffer_load_b128(r, voff[1] + s_bs, 0, 0);
     if (tid < BMt / 4) d = __builtin_amdgcn_raw_buffer_load_b128(r, voff[2] + s_d, 0, 0);
   }
   __device__ __forceinline__ void store(uint8_t *slot) const {
@@ -89,7 +90,7 @@ struct ActStage {
     const int swz = (tid & 15) ^ ((tid >> 4) & 15);
 #pragma unroll
     for (int i = 0; i < NQ; i++) *(u32x4 *)(slot + 16 * NT * i + 256 * (tid >> 4) + 16 * swz) = q[i];
-    if (MIN && tid < BMt) *(u32x4 *)(slot + QS + 16 * tid) = bs;
+    if (MIN && tid < BMt * SB / 16) *(u32x4 *)(slot + QS + 16 * tid) = bs;
     if (tid < BMt / 4) *(u32x4 *)(slot + QS + BSB + 16 * tid) = d;
   }
 };
@@ -100,7 +101,7 @@ struct ActStage {
 // the swizzled layout.  Every one of the NW waves issues kLoads loads per superblock (the same count: the tile loop's
 // wait counts on it).  The compiler does not order LDS reads after these writes: the tile loop waits for them with an
 // explicit vmcnt before its barrier.
-template <int BMt, bool MIN, int NW>
+template <int BMt, bool MIN, int NW, int SB = 16>
 struct ActDma {
   static_assert(BMt % (4 * NW) == 0 && (!MIN || BMt % (8 * NW) == 0), "the same load count in every wave");
   static constexpr int QS = BMt * 256;
@@ -124,8 +125,8 @@ struct ActDma {
     }
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-      const int D = 64 * (NW * i + wave) + lane, r = D >> 2, k = D & 3;
-      ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * 16 + 4 * k);
+      const int D = 64 * (NW * i + wave) + lane, r = SB == 32 ? D >> 3 : D >> 2, k = SB == 32 ? D & 7 : D & 3;
+      ob[i] = (uint32_t)(nsb * rows * 260 + (m0 + r) * SB + 4 * k);
     }
     od = (uint32_t)(nsb * rows * 256 + (m0 + ND * wave + lane) * 4);
   }
@@ -139,7 +140,7 @@ struct ActDma {
 #pragma unroll
     for (int i = 0; i < NB; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (NW * i + wave)), 4, ob[i] + 16 * sb_rows, 0,
+          r, (__attribute__((address_space(3))) void *)(slot + QS + 256 * (NW * i + wave)), 4, ob[i] + SB * sb_rows, 0,
           0, 0);
     if (lane < ND)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -174,7 +175,9 @@ __device__ __forceinline__ void lds_barrier() {
 // register sets rotate: during superblock s the workgroup computes from slot s, writes the activations of s + 1
 // (loaded one step earlier) into slot s + 1, and has the activations and weights of s + 2 in flight, so global
 // latency is covered by two steps of MFMA work.  One LDS barrier per superblock.
-template <class WT, class Out, int TM, int NW>
+// S16: the activations are `_q8k` tiles (f16 sums of 16, the min term's A operand as it is), else the reference-named
+// tiles (int16 sums of 32, split for the f16 MFMA here: planes.h min_frag).
+template <class WT, class Out, int TM, int NW, bool S16 = false>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
@@ -192,8 +195,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   // Without kLw, Q4_K stages its activations by DMA (its register budget at two waves per SIMD has no room for a
   // register ring); Q6_K, at one wave per SIMD, through registers.  Both write the same LDS layout.
   constexpr bool kDma = WT::kDma || kLw;
-  typedef ActStage<BMt, WT::kMin, 64 * NW> AS;
-  typedef ActDma<BMt, WT::kMin, NW> AD;
+  constexpr int SB = S16 ? 32 : 16;
+  typedef ActStage<BMt, WT::kMin, 64 * NW, SB> AS;
+  typedef ActDma<BMt, WT::kMin, NW, SB> AD;
   static_assert(AS::STAGE == AD::STAGE, "one LDS layout");
   // Superblocks of a multiple of 16 bytes (Q4_K: 16-byte aligned) are copied as their own pieces and kept row after
   // row.  Others (Q6_K: 210 bytes, 2-byte aligned) are copied as the 16-byte pieces of a window that starts at the
@@ -227,9 +231,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 
   // activations: one resource over the channel; the scalar part of each address moves with the superblock
   const int64_t rows = a.rows, nsb = a.nsb;
-  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * 276);
+  const rsrc_t ra = make_rsrc(a.qs, nsb * rows * (260 + SB));
   const uint32_t voff[3] = {(uint32_t)(m0 * 256 + 16 * tid),
-                            (uint32_t)(nsb * rows * 260 + m0 * 16 + 16 * tid),
+                            (uint32_t)(nsb * rows * 260 + m0 * SB + 16 * tid),
                             (uint32_t)(nsb * rows * 256 + m0 * 4 + 16 * tid)};
   // weights: one resource over the tile's rows, from the dword that holds the tile's first byte (wdelta bytes
   // before it), so offsets that are multiples of 4 from the resource are dword aligned in memory, to the end of the
@@ -296,7 +300,7 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
       WT::load(rw, wrow, (uint32_t)sb, g, rr);
       __builtin_amdgcn_sched_barrier(0);
     } else {
-      as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * 16), (uint32_t)(sb * rows * 4));
+      as.load(ra, voff, (uint32_t)(sb * rows * 256), (uint32_t)(sb * rows * SB), (uint32_t)(sb * rows * 4));
       WT::load(rw, wrow, (uint32_t)sb, g, rr);
     }
   };
@@ -305,7 +309,10 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   // matrix work.
   auto compute = [&](const uint8_t *slot, const typename WT::Raw &rr) {
     typename WT::Prep p;
-    WT::prepare(rr, g, p);
+    if constexpr (WT::kMin)
+      WT::template prepare<S16>(rr, g, p);
+    else
+      WT::prepare(rr, g, p);
     v16i acc1[TM], acc2[TM], acc3[TM];  // acc3: Q5_K's fifth-bit plane
 #pragma unroll
     for (int t = 0; t < TM; t++) acc1[t] = acc2[t] = acc3[t] = (v16i){};
@@ -341,7 +348,10 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       v16f fmin = (v16f){};
-      if (WT::kMin) {  // the sums of sub-blocks 4g .. 4g + 3 of row 32t + li
+      if (WT::kMin && S16) {  // the f16 sums of 16 of sub-blocks 4g .. 4g + 3 of row 32t + li
+        const v8h bs = *(const v8h *)(slot + AS::QS + (32 * t + li) * 32 + 16 * g);
+        fmin = mfma_f16(bs, p.bmin, fmin);
+      } else if (WT::kMin) {  // the sums of 32 of sub-blocks 4g .. 4g + 3 of row 32t + li
         const u32x2 sm = *(const u32x2 *)(slot + AS::QS + (32 * t + li) * 16 + 8 * g);
         fmin = mfma_f16(min_frag(sm.x, sm.y), p.bmin, fmin);
       }
@@ -918,7 +928,7 @@ constexpr int kq_waves() {
 
 // grid: tiles x splits; split s of a tile sums superblocks [s * per, min((s + 1) * per, nsb)) into dst, or with more
 // than one split into plane s of `part` (mrows x nrows_w f32 per plane)
-template <class WT, class Out, int TMv, int NW>
+template <class WT, class Out, int TMv, int NW, bool S16 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq(
     const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes, ActTile a, int64_t mrows, int64_t nsb,
     int64_t splits, typename Out::T *__restrict__ dst, int64_t ldd, float *__restrict__ part) {
@@ -928,8 +938,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kq_wave
   const int64_t per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, Out, TMv, NW>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BNt, sb0, sb1, dst, ldd, nullptr,
-                                part ? part + split * mrows * nrows_w : nullptr);
+  mmq_kq_tile<WT, Out, TMv, NW, S16>(W, nrows_w, w_row_bytes, a, mt * BMt, mrows, nt * BNt, sb0, sb1, dst, ldd,
+                                     nullptr, part ? part + split * mrows * nrows_w : nullptr);
 }
 
 template <class WB, class Out, bool F32D>
@@ -1054,7 +1064,7 @@ int64_t k_splits(int64_t tiles, int64_t nsb, int64_t rows, int64_t cols, const v
 #define QMM_KQ_WAVES 4
 #endif
 
-template <class WT, class Out>
+template <class WT, class Out, bool S16 = false>
 void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const ActTile &a, int64_t ncols_y, int64_t nsb,
                typename Out::T *d, int64_t ldd, void *fixup, int nsm, hipStream_t s) {
   // activation rows per wave: the smallest of 32, 64, 128 that covers the batch
@@ -1069,11 +1079,13 @@ void launch_kq(const uint8_t *w, int64_t nrows_x, int64_t w_row_bytes, const Act
   float *part = splits > 1 ? (float *)fixup : nullptr;
   const dim3 grid((unsigned)(tiles * splits));
   if (tm == 1) {
-    k_mmq_kq<WT, Out, 1, 4><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 1, 4, S16><<<grid, 256, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
   } else if (tm == 2) {
-    k_mmq_kq<WT, Out, 2, NW><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 2, NW, S16><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd,
+                                                          part);
   } else if constexpr (kq_tm_max<WT>() >= 4) {  // (not instantiated where it cannot be chosen)
-    k_mmq_kq<WT, Out, 4, NW><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd, part);
+    k_mmq_kq<WT, Out, 4, NW, S16><<<grid, 64 * NW, 0, s>>>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, splits, d, ldd,
+                                                          part);
   }
   if (part) split_sum<Out>(part, splits, ncols_y, nrows_x, d, ldd, nullptr, s);
 }
@@ -1158,8 +1170,8 @@ void mmq_plain(int type, const void *x, const void *y, void *dst, int64_t ncols_
 }
 
 // The kernels address one activation channel with 32-bit offsets.
-bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows) {
-  if ((ncols_x + 255) / 256 * rows * 276 > 0x7ffffff0) {
+bool check_act_bytes(const char *who, int64_t ncols_x, int64_t rows, int bytes_per_256 = 276) {
+  if ((ncols_x + 255) / 256 * rows * bytes_per_256 > 0x7ffffff0) {
     qmm_set_error("%s: activation channel of %lld x %lld values exceeds 2 GiB", who, (long long)rows,
                   (long long)ncols_x);
     return false;
@@ -1190,6 +1202,35 @@ void mmq(int type, bool q8_0, void *tmp_fixup, const void *x, const void *y, voi
     default: qmm_set_error("%s: type_dst=%d (0 f32, 1 f16, 30 bf16)", who, type_dst);
   }
 #undef QMM_MMQ_P
+}
+
+// launch_mmq_gguf_{q4_k,q5_k}_q8k: the plain prefill over `_q8k` tiles (f16 sums of 16)
+void mmq_q8k(int type, void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x, int64_t nrows_x,
+             int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int nsm, int type_dst, void *stream,
+             const char *who) {
+  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_y, 292)) return;
+  if (ncols_y < 0 || stride_col_dst < nrows_x) {
+    qmm_set_error("%s: ncols_y=%lld stride_col_dst=%lld", who, (long long)ncols_y, (long long)stride_col_dst);
+    return;
+  }
+  if (ncols_y == 0) return;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t nsb = (ncols_x + 255) / 256;
+  const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
+  const ActTile a = act_tile(y, ncols_y, nsb);
+  const uint8_t *w = (const uint8_t *)x;
+#define QMM_Q8K(Out)                                                                                                 \
+  (type == QMM_TYPE_Q4K ? launch_kq<wq4k, Out, true>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, (Out::T *)dst,       \
+                                                     stride_col_dst, tmp_fixup, nsm, s)                              \
+                        : launch_kq<wq5k, Out, true>(w, nrows_x, w_row_bytes, a, ncols_y, nsb, (Out::T *)dst,       \
+                                                     stride_col_dst, tmp_fixup, nsm, s))
+  switch (type_dst) {
+    case QMM_TYPE_F32: QMM_Q8K(out_f32); break;
+    case QMM_TYPE_F16: QMM_Q8K(out_f16); break;
+    case QMM_TYPE_BF16: QMM_Q8K(out_bf16); break;
+    default: qmm_set_error("%s: type_dst=%d (0 f32, 1 f16, 30 bf16)", who, type_dst);
+  }
+#undef QMM_Q8K
 }
 
 template <class WT, int TMv>
@@ -1384,4 +1425,16 @@ QMM_DEFINE_MMQ(iq4_xs, QMM_TYPE_IQ4_XS)
 QMM_DEFINE_MMQ_ENTRIES(q8_0, QMM_TYPE_Q8_0, true, _q8_0)
 QMM_DEFINE_MMQ_ENTRIES(q4_0, QMM_TYPE_Q4_0, true, _q8_0)
 QMM_DEFINE_MMQ_ENTRIES(q5_0, QMM_TYPE_Q5_0, true, _q8_0)
+
+#define QMM_DEFINE_MMQ_Q8K(t, TYPE)                                                                                \
+  void launch_mmq_gguf_##t##_q8k(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,       \
+                                 int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst,  \
+                                 int cc, int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream) {     \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq_q8k(TYPE, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, nsm, type_dst,     \
+            stream, "mmq_" #t "_q8k");                                                                             \
+  }
+QMM_DEFINE_MMQ_Q8K(q4_k, QMM_TYPE_Q4K)
+QMM_DEFINE_MMQ_Q8K(q5_k, QMM_TYPE_Q5K)
+#undef QMM_DEFINE_MMQ_Q8K
 }

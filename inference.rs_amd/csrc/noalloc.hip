@@ -57,11 +57,13 @@ typedef void (*mmq_fn)(void *, const void *, const void *, void *, int64_t, int6
                        int, int64_t, int, int, void *);
 
 // activation geometry as the host layer's: Q8_0 blocks (34 bytes per 32 values) for the 32-value types, Q8_1 slots
-// (288 bytes per 256) for the rest; stride_col_y in 32-value blocks either way; prefill tiles 272 or 276 bytes per 256
+// (288 bytes per 256) for the rest; stride_col_y in 32-value blocks either way; prefill tiles: Q8_0 (272 bytes per 256)
+// for the 32-value types, `_q8k` (292) for Q4_K and Q5_K, Q8_K (276) for Q6_K
 bool act_q8_0(int w) { return qmm_vec_dot_type(w) == QMM_TYPE_Q8_0; }
+bool prefill_q8k(int w) { return w == QMM_TYPE_Q4K || w == QMM_TYPE_Q5K; }
 int64_t act_block(int w) { return act_q8_0(w) ? 32 : 256; }
 int64_t act_row_bytes(int w, int64_t kp) { return act_q8_0(w) ? kp / 32 * 34 : kp / 256 * 288; }
-int64_t tile_bytes_per_256(int w) { return act_q8_0(w) ? 272 : 276; }
+int64_t tile_bytes_per_256(int w) { return act_q8_0(w) ? 272 : prefill_q8k(w) ? 292 : 276; }
 int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 bool has_all_routes(int t) { return t == QMM_TYPE_Q8_0 || t == QMM_TYPE_Q4K || t == QMM_TYPE_Q6K; }
 
@@ -101,11 +103,11 @@ mmvq_q_fn decode_matvec_quantize(int w) {
 mmq_fn prefill_matmul(int w) {
   switch (w) {
     case QMM_TYPE_Q8_0: return launch_mmq_gguf_q8_0_q8_0;
-    case QMM_TYPE_Q4K: return launch_mmq_gguf_q4_k;
+    case QMM_TYPE_Q4K: return launch_mmq_gguf_q4_k_q8k;
     case QMM_TYPE_Q6K: return launch_mmq_gguf_q6_k;
     case QMM_TYPE_Q4_0: return launch_mmq_gguf_q4_0_q8_0;
     case QMM_TYPE_Q5_0: return launch_mmq_gguf_q5_0_q8_0;
-    default: return launch_mmq_gguf_q5_k;
+    default: return launch_mmq_gguf_q5_k_q8k;
   }
 }
 
@@ -167,9 +169,10 @@ int forward(const void *w, int wtype, int64_t n, int64_t k, const void *xs, int 
                   (long long)rows, (long long)k, (long long)act, kActBytes);
     return -1;
   }
-  (act_q8_0(wtype) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(xs, nullptr, ptr, in_dtype, k, k,
-                                                                               k * rows, k * rows, kp, rows, 1, 1,
-                                                                               stream);
+  (act_q8_0(wtype)      ? launch_mmq_quantize_q8_0
+   : prefill_q8k(wtype) ? launch_mmq_quantize_q8k
+                        : launch_mmq_quantize_q8_1_DS4)(xs, nullptr, ptr, in_dtype, k, k, k * rows, k * rows, kp, rows, 1,
+                                                        1, stream);
   // the fixup region holds nsm * 128 * 128 f32 for nsm up to 256 (MI355X has 256 compute units); a device with more
   // would split K less than the host layer does, and its output would then differ from QMatMul::forward's in the f32
   // summation order

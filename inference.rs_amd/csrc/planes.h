@@ -120,20 +120,28 @@ struct wq4k {
     auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
     return j < 4 ? byte(j) & 63 : (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
   }
+  // S16: the A operand is the f16 sums of 16 values (`_q8k` tiles): k = 8g + 2i + h holds sub-block 4g + i's min m
+  // for both of its halves.  Otherwise the sums of 32 split as 64 h + l (min_frag's order): k = 8g + 4 (i / 2) + i % 2
+  // holds 64 m, two further on m.  Sub-block 4g + i's 6-bit min is byte(4 + i) & 63 (g = 0) or
+  // (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4) (g = 1).
+  template <bool S16 = false>
   static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
     const uint32_t s[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
     auto byte = [&](int i) { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
     p.d = f16_bits_to_f32(r.hdr.x & 0xffff);
     p.dmin = f16_bits_to_f32(r.hdr.x >> 16);
-    // B operand of the min-term MFMA for sub-blocks 4g + i (i = 0..3), whose 6-bit min is byte(4 + i) & 63 (g = 0)
-    // or (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4) (g = 1): k = 8g + 4 (i / 2) + i % 2 holds 64 m, two further
-    // on m (min_frag's order)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t lo = byte(4 + i) & 63, hi = (byte(8 + i) >> 4) | ((byte(4 + i) >> 6) << 4);
       const uint32_t m = g ? hi : lo;
-      p.bmin[4 * (i >> 1) + (i & 1)] = (_Float16)(float)(64 * m);
-      p.bmin[4 * (i >> 1) + (i & 1) + 2] = (_Float16)(float)m;
+      if constexpr (S16) {
+        const _Float16 mh = (_Float16)(float)m;
+        p.bmin[2 * i] = mh;
+        p.bmin[2 * i + 1] = mh;
+      } else {
+        p.bmin[4 * (i >> 1) + (i & 1)] = (_Float16)(float)(64 * m);
+        p.bmin[4 * (i >> 1) + (i & 1) + 2] = (_Float16)(float)m;
+      }
     }
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2) {
@@ -186,10 +194,11 @@ struct wq5k {
 #pragma unroll
     for (int c = 0; c < 4; c++) r.q[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 48 + 32 * c + 16 * g, 0, 0);
   }
+  template <bool S16 = false>
   static __device__ __forceinline__ void prepare(const Raw &r, int g, Prep &p) {
     wq4k::Raw h;
     h.hdr = r.hdr;
-    wq4k::prepare(h, g, p);
+    wq4k::prepare<S16>(h, g, p);
   }
   static __device__ __forceinline__ void planes(const Raw &r, const Prep &p, int j, v4i &b1, v4i &b2, v4i &b3) {
     (void)p;

@@ -16,27 +16,30 @@ namespace qmm_q8 {
 //   slot     the 288-byte qmm_block_q8ks of the reference-named decode entries: int16 sums of each 32, 12 zero bytes
 //   tile     the prefill layout of one channel: qs[nsb][rows][256], d[nsb][rows] f32, s32[nsb][rows][8] int16 sums of
 //            each 32 (276 bytes per 256 values)
+//   tile16   the same with h16[nsb][rows][16], the sums of each 16 as f16 (exact: |sum| <= 2032), for the
+//            `_q8k` prefill entries (292 bytes per 256 values)
 struct q8k_dst {
   uint8_t *qs;
   float *d;
   uint16_t *bsums;  // int16 sums of 16 values
   int16_t *s32;     // int16 sums of 32 values
   uint32_t *pad;    // three dwords set to zero
+  uint16_t *h16;    // f16 sums of 16 values
 };
 
 __device__ __forceinline__ q8k_dst q8k_decode_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8k);
-  return {b + 4, (float *)b, (uint16_t *)(b + 260), nullptr, nullptr};
+  return {b + 4, (float *)b, (uint16_t *)(b + 260), nullptr, nullptr, nullptr};
 }
 
 __device__ __forceinline__ q8k_dst q8k_tc_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * 260;
-  return {b + 4, (float *)b, nullptr, nullptr, nullptr};
+  return {b + 4, (float *)b, nullptr, nullptr, nullptr, nullptr};
 }
 
 __device__ __forceinline__ q8k_dst q8k_slot_dst(uint8_t *vy, int64_t block) {
   uint8_t *b = vy + block * (int64_t)sizeof(qmm_block_q8ks);
-  return {b + 4, (float *)b, nullptr, (int16_t *)(b + 260), (uint32_t *)(b + 276)};
+  return {b + 4, (float *)b, nullptr, (int16_t *)(b + 260), (uint32_t *)(b + 276), nullptr};
 }
 
 __device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
@@ -44,7 +47,15 @@ __device__ __forceinline__ q8k_dst q8k_tile_dst(uint8_t *chan, int64_t rows, int
   uint8_t *qs = chan + i * 256;
   float *d = (float *)(chan + nsb * rows * 256) + i;
   int16_t *s32 = (int16_t *)(chan + nsb * rows * 260) + i * 8;
-  return {qs, d, nullptr, s32, nullptr};
+  return {qs, d, nullptr, s32, nullptr, nullptr};
+}
+
+__device__ __forceinline__ q8k_dst q8k_tile16_dst(uint8_t *chan, int64_t rows, int64_t nsb, int64_t sb, int64_t r) {
+  const int64_t i = sb * rows + r;
+  uint8_t *qs = chan + i * 256;
+  float *d = (float *)(chan + nsb * rows * 256) + i;
+  uint16_t *h16 = (uint16_t *)(chan + nsb * rows * 260) + i * 16;
+  return {qs, d, nullptr, nullptr, nullptr, h16};
 }
 
 // One wave quantizes G blocks: v[t][0..3] of lanes 0..63 are values 4*lane .. 4*lane+3 of block t, written to
@@ -94,6 +105,7 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     *(uint32_t *)(dst[t].qs + 4 * lane) = packed;
     if ((lane & 3) == 0 && dst[t].bsums) dst[t].bsums[lane >> 2] = (uint16_t)(int16_t)s;  // +0 for a zero block
+    if ((lane & 3) == 0 && dst[t].h16) dst[t].h16[lane >> 2] = f32_to_f16_bits((float)s);
     if ((lane & 7) == 4 && dst[t].s32) dst[t].s32[lane >> 3] = (int16_t)s32;
     if (lane < 3 && dst[t].pad) dst[t].pad[lane] = 0u;
     if (lane == 0) *dst[t].d = nz ? 1.0f / iscale : 0.0f;

@@ -65,7 +65,8 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_rows(const typename In::T
 
 // Grid (row groups of 4, superblock columns, channels): one block per wave, its indices from the grid with no
 // division (the 64-bit index divisions of a flat grid were a large share of each wave's few hundred instructions).
-template <class In>
+// S16: the `_q8k` tiles (f16 sums of 16, 292 bytes per 256 values), else the reference-named tiles (int16 sums of 32).
+template <class In, bool S16>
 __global__ __launch_bounds__(256) void k_quantize_q8k_tiles(const typename In::T *__restrict__ x,
                                                             const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
                                                             int64_t ne00, int64_t s01, int64_t s02, int64_t s03,
@@ -78,7 +79,8 @@ __global__ __launch_bounds__(256) void k_quantize_q8k_tiles(const typename In::T
   const int64_t src_row = ids ? ids[r] : r;
   float v[4];
   load4<In>(x + i3 * s03 + i2 * s02 + src_row * s01, sb * 256 + lane * 4, ne00, v);
-  q8k_wave(v, lane, q8k_tile_dst(vy + (int64_t)ch * nsb * ne1 * 276, ne1, nsb, sb, r));
+  uint8_t *chan = vy + (int64_t)ch * nsb * ne1 * (S16 ? 292 : 276);
+  q8k_wave(v, lane, S16 ? q8k_tile16_dst(chan, ne1, nsb, sb, r) : q8k_tile_dst(chan, ne1, nsb, sb, r));
 }
 
 template <class In>
@@ -126,7 +128,7 @@ __device__ __forceinline__ float glu_product<in_bf16>(float g, float u, int acti
   return bf16_bits_to_f32(f32_to_bf16_bits(a * u));
 }
 
-template <class In>
+template <class In, bool S16>
 __global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const typename In::T *__restrict__ gate,
                                                                 const typename In::T *__restrict__ up,
                                                                 const int32_t *__restrict__ ids, uint8_t *__restrict__ vy,
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const typename I
     const int64_t k = sb * 256 + lane * 4 + i;
     v[i] = k < ne00 ? glu_product<In>(In::load(gate, src + k), In::load(up, src + k), activation) : 0.0f;
   }
-  q8k_wave(v, lane, q8k_tile_dst(vy, ne1, nsb, sb, r));
+  q8k_wave(v, lane, S16 ? q8k_tile16_dst(vy, ne1, nsb, sb, r) : q8k_tile_dst(vy, ne1, nsb, sb, r));
 }
 
 __global__ __launch_bounds__(256) void k_quantize_glu_q8_0_tiles(const float *__restrict__ gate,
@@ -268,9 +270,10 @@ void launch_mmvq_gguf_quantize_q8_0_bf16(const void *x, void *vy, int kx, int kx
 }  // extern "C"
 
 namespace {
+template <bool S16>
 void mmq_quantize_q8ks(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01, int64_t s02,
                        int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, void *stream) {
-  if (!tile_args_ok("mmq_quantize_q8_1", ne00, ne0, ne1, ne2, ne3)) return;
+  if (!tile_args_ok(S16 ? "mmq_quantize_q8k" : "mmq_quantize_q8_1", ne00, ne0, ne1, ne2, ne3)) return;
   const int64_t kt = tile_width(ne00);
   if (kt == 0 || ne1 == 0) return;
   if (kt / 256 > 65535 || ne2 * ne3 > 65535 || qmm_ceil_div(ne1, 4) > INT32_MAX) {
@@ -283,20 +286,21 @@ void mmq_quantize_q8ks(const void *x, const int32_t *ids, void *vy, int type_x, 
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
-      k_quantize_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, (int)ne2);
+      k_quantize_q8k_tiles<in_f32, S16><<<grid, 256, 0, s>>>((const float *)x, ids, y, ne00, s01, s02, s03, kt, ne1, (int)ne2);
       break;
     case QMM_TYPE_F16:
-      k_quantize_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
+      k_quantize_q8k_tiles<in_f16, S16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
                                                         (int)ne2);
       break;
     case QMM_TYPE_BF16:
-      k_quantize_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
+      k_quantize_q8k_tiles<in_bf16, S16><<<grid, 256, 0, s>>>((const uint16_t *)x, ids, y, ne00, s01, s02, s03, kt, ne1,
                                                          (int)ne2);
       break;
     default: qmm_set_error("mmq_quantize_q8_1: unsupported input type %d", type_x);
   }
 }
 
+template <bool S16>
 void mmq_quantize_glu_q8ks(const void *gate, const void *up, const int32_t *ids, void *vy, int type_x, int64_t ne00,
                            int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
   if (!tile_args_ok("mmq_quantize_glu_q8_1", ne00, ne0, ne1, 1, 1)) return;
@@ -315,15 +319,15 @@ void mmq_quantize_glu_q8ks(const void *gate, const void *up, const int32_t *ids,
   uint8_t *y = (uint8_t *)vy;
   switch (type_x) {
     case QMM_TYPE_F32:
-      k_quantize_glu_q8k_tiles<in_f32><<<grid, 256, 0, s>>>((const float *)gate, (const float *)up, ids, y, ne00, s01,
+      k_quantize_glu_q8k_tiles<in_f32, S16><<<grid, 256, 0, s>>>((const float *)gate, (const float *)up, ids, y, ne00, s01,
                                                             kt, ne1, activation);
       break;
     case QMM_TYPE_F16:
-      k_quantize_glu_q8k_tiles<in_f16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y, ne00,
+      k_quantize_glu_q8k_tiles<in_f16, S16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y, ne00,
                                                             s01, kt, ne1, activation);
       break;
     case QMM_TYPE_BF16:
-      k_quantize_glu_q8k_tiles<in_bf16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y,
+      k_quantize_glu_q8k_tiles<in_bf16, S16><<<grid, 256, 0, s>>>((const uint16_t *)gate, (const uint16_t *)up, ids, y,
                                                              ne00, s01, kt, ne1, activation);
       break;
     default: qmm_set_error("mmq_quantize_glu_q8_1: unsupported input type %d", type_x);
@@ -339,22 +343,33 @@ extern "C" {
   void launch_mmq_quantize_q8_1_##L(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00,         \
                                     int64_t s01, int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2,  \
                                     int64_t ne3, void *stream) {                                                   \
-    mmq_quantize_q8ks(x, ids, vy, type_x, ne00, s01, s02, s03, ne0, ne1, ne2, ne3, stream);                        \
+    mmq_quantize_q8ks<false>(x, ids, vy, type_x, ne00, s01, s02, s03, ne0, ne1, ne2, ne3, stream);                 \
   }                                                                                                                \
   void launch_mmq_quantize_glu_q8_1_##L##_f32(const float *gate, const float *up, const int32_t *ids, void *vy,    \
                                               int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1, int activation, \
                                               void *stream) {                                                      \
-    mmq_quantize_glu_q8ks(gate, up, ids, vy, QMM_TYPE_F32, ne00, s01, ne0, ne1, activation, stream);               \
+    mmq_quantize_glu_q8ks<false>(gate, up, ids, vy, QMM_TYPE_F32, ne00, s01, ne0, ne1, activation, stream);        \
   }                                                                                                                \
   void launch_mmq_quantize_glu_q8_1_##L(const void *gate, const void *up, const int32_t *ids, void *vy, int type_x, \
                                         int64_t ne00, int64_t s01, int64_t ne0, int64_t ne1, int activation,       \
                                         void *stream) {                                                            \
-    mmq_quantize_glu_q8ks(gate, up, ids, vy, type_x, ne00, s01, ne0, ne1, activation, stream);                     \
+    mmq_quantize_glu_q8ks<false>(gate, up, ids, vy, type_x, ne00, s01, ne0, ne1, activation, stream);              \
   }
 QMM_DEFINE_MMQ_Q8_1(D4)
 QMM_DEFINE_MMQ_Q8_1(DS4)
 QMM_DEFINE_MMQ_Q8_1(D2S6)
 #undef QMM_DEFINE_MMQ_Q8_1
+
+void launch_mmq_quantize_q8k(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
+                             int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                             void *stream) {
+  mmq_quantize_q8ks<true>(x, ids, vy, type_x, ne00, s01, s02, s03, ne0, ne1, ne2, ne3, stream);
+}
+
+void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const int32_t *ids, void *vy, int64_t ne00,
+                                     int64_t s01, int64_t ne0, int64_t ne1, int activation, void *stream) {
+  mmq_quantize_glu_q8ks<true>(gate, up, ids, vy, QMM_TYPE_F32, ne00, s01, ne0, ne1, activation, stream);
+}
 
 void launch_mmq_quantize_q8_0(const void *x, const int32_t *ids, void *vy, int type_x, int64_t ne00, int64_t s01,
                               int64_t s02, int64_t s03, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,

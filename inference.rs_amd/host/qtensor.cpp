@@ -161,9 +161,9 @@ mmq_fn prefill_matmul(GgmlDType w) {
     case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_q8_0;
     case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_q8_0;
     case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_q8_0;
-    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k;
+    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_q8k;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k;
-    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k;
+    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k_q8k;
     default: throw Error("QMatMul: unsupported weight type");
   }
 }
@@ -219,6 +219,16 @@ bool act_q8_0(GgmlDType w) { return qmm_vec_dot_type((int)w) == QMM_TYPE_Q8_0; }
 int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
 int64_t act_row_bytes(GgmlDType w, int64_t kp) { return act_q8_0(w) ? kp / 32 * 34 : kp / 256 * 288; }
 int64_t tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : 276; }
+
+// the plain prefill matmul's activations (prefill_matmul): Q8_0 tiles for the 32-value types, the `_q8k` tiles (f16
+// sums of 16, which the min term reads as they are) for Q4_K and Q5_K, the reference-named Q8_K tiles otherwise
+bool prefill_q8k(GgmlDType w) { return w == GgmlDType::Q4K || w == GgmlDType::Q5K; }
+int64_t prefill_tile_bytes_per_256(GgmlDType w) { return prefill_q8k(w) ? 292 : tile_bytes_per_256(w); }
+typedef void (*tile_quant_fn)(const void *, const int32_t *, void *, int, int64_t, int64_t, int64_t, int64_t, int64_t,
+                              int64_t, int64_t, int64_t, void *);
+tile_quant_fn prefill_quantizer(GgmlDType w) {
+  return act_q8_0(w) ? launch_mmq_quantize_q8_0 : prefill_q8k(w) ? launch_mmq_quantize_q8k : launch_mmq_quantize_q8_1_DS4;
+}
 
 // matvec_only: the route needs the decode matvec kernels alone (QMatMul::forward, gather_forward); else every route
 void check_weight(const QTensor &w, const char *who, bool matvec_only = false) {
@@ -424,11 +434,10 @@ void QMatMul::forward(const void *xs, GgmlDType in_dtype, int64_t rows, void *ys
     const int64_t kp = pad_to(k, 256);
     const int nsm = device_cus(w.device().ordinal);
     Carver c;
-    const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+    const size_t o_y = c.add((size_t)(rows * kp / 256 * prefill_tile_bytes_per_256(t)));
     const size_t o_fix = c.add(fixup_bytes(nsm));
     uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
-    (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(
-        xs, nullptr, ws + o_y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
+    prefill_quantizer(t)(xs, nullptr, ws + o_y, (int)in_dtype, k, k, k * rows, k * rows, kp, rows, 1, 1, stream);
     abi_check("QMatMul::forward (quantize)");
     prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
                       160 * 1024, 64, (int)in_dtype, stream);
@@ -452,11 +461,13 @@ void QMatMul::down_from_glu(const float *gate, const float *up, int64_t rows, in
   const int64_t kp = pad_to(k, 256);
   const int nsm = device_cus(w.device().ordinal);
   Carver c;
-  const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+  const size_t o_y = c.add((size_t)(rows * kp / 256 * prefill_tile_bytes_per_256(t)));
   const size_t o_fix = c.add(fixup_bytes(nsm));
   uint8_t *ws = (uint8_t *)workspace().get(w.device().ordinal, c.total, stream);
-  (act_q8_0(t) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8_1_DS4_f32)(
-      gate, up, nullptr, ws + o_y, k, k, kp, rows, activation, stream);
+  (act_q8_0(t)      ? launch_mmq_quantize_glu_q8_0_f32
+   : prefill_q8k(t) ? launch_mmq_quantize_glu_q8k_f32
+                    : launch_mmq_quantize_glu_q8_1_DS4_f32)(gate, up, nullptr, ws + o_y, k, k, kp, rows, activation,
+                                                            stream);
   abi_check("QMatMul::down_from_glu (GLU + quantize)");
   prefill_matmul(t)(ws + o_fix, w.device_ptr(), ws + o_y, ys, k, n, rows, k / (int64_t)block_size(t), n, 0, nsm,
                     160 * 1024, 64, 0, stream);
@@ -501,14 +512,12 @@ void fused_ffn(const QMatMul &gate, const QMatMul &up, const QMatMul &down, cons
   const int64_t kp = pad_to(hidden, 256);
   const int nsm = device_cus(ordinal);
   Carver c;
-  const size_t o_y = c.add((size_t)(rows * kp / 256 * tile_bytes_per_256(t)));
+  const size_t o_y = c.add((size_t)(rows * kp / 256 * prefill_tile_bytes_per_256(t)));
   const size_t o_fix = c.add(fixup_bytes(nsm));
   const size_t o_g = c.add((size_t)(rows * inter * 4));
   const size_t o_u = c.add((size_t)(rows * inter * 4));
   uint8_t *ws = (uint8_t *)ffn_workspace().get(ordinal, c.total, stream);
-  (act_q8_0(t) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(xs, nullptr, ws + o_y, 0, hidden, hidden,
-                                                                         hidden * rows, hidden * rows, kp, rows, 1, 1,
-                                                                         stream);
+  prefill_quantizer(t)(xs, nullptr, ws + o_y, 0, hidden, hidden, hidden * rows, hidden * rows, kp, rows, 1, 1, stream);
   abi_check("fused_ffn (quantize)");
   for (int which = 0; which < 2; which++) {
     const QTensor &w = which == 0 ? g : u;

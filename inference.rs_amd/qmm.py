@@ -458,21 +458,22 @@ def moe_weighted_reduce(inp, weights, out_dtype=None):
 
 # ------------------------------------------------------------------------------------------------ prefill
 
-def mmq_act_bytes(wtype: int, rows: int, kp: int, q8_1=None) -> int:
-    return rows * kp // 256 * (276 if _q8_1(wtype, q8_1) else 272)
+def mmq_act_bytes(wtype: int, rows: int, kp: int, q8_1=None, q8k=False) -> int:
+    return rows * kp // 256 * (292 if q8k else 276 if _q8_1(wtype, q8_1) else 272)
 
 
-def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None, q8_1=None):
+def quantize_prefill(wtype: int, x, ids=None, rows: int | None = None, out=None, q8_1=None, q8k=False):
     """Quantize x [rows, k] (or the rows ids selects) into wtype's prefill tile layout: launch_mmq_quantize_q8_1_DS4
-    (Q8_K tiles) or launch_mmq_quantize_q8_0.  Returns (uint8 tensor, kp)."""
+    (Q8_K tiles), launch_mmq_quantize_q8_0, or with q8k launch_mmq_quantize_q8k (the `_q8k` tiles of the Q4_K / Q5_K
+    _q8k entries).  Returns (uint8 tensor, kp)."""
     torch = _torch()
     k = x.shape[-1]
     kp = pad_to(k, 256)
     ne1 = rows if rows is not None else (ids.numel() if ids is not None else x.shape[0])
     if out is None:
-        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1), 1), dtype=torch.uint8, device=x.device)
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1, q8k), 1), dtype=torch.uint8, device=x.device)
     type_x = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[x.dtype]
-    name = "q8_1_DS4" if _q8_1(wtype, q8_1) else "q8_0"
+    name = "q8k" if q8k else "q8_1_DS4" if _q8_1(wtype, q8_1) else "q8_0"
     getattr(lib(), f"launch_mmq_quantize_{name}")(_ptr(x), _ptr(ids), _ptr(out), type_x, k, x.stride(0),
                                                   x.stride(0) * x.shape[0], x.stride(0) * x.shape[0], kp, ne1, 1, 1,
                                                   _stream())
@@ -494,17 +495,20 @@ def fixup(device):
     return _fixups[idx]
 
 
-def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, out=None, q8_1=None):
+def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, out=None, q8_1=None, q8k=False):
     """act(gate[r]) * up[r] for r = ids[i] (or i), [rows, k] inputs, quantized into the prefill tile layout through
-    launch_mmq_quantize_glu_q8_1_DS4_f32 (f32 inputs) / launch_mmq_quantize_glu_q8_1_DS4 (f16 / bf16 inputs) or
-    launch_mmq_quantize_glu_q8_0_f32.  Returns (uint8 tensor, kp)."""
+    launch_mmq_quantize_glu_q8_1_DS4_f32 (f32 inputs) / launch_mmq_quantize_glu_q8_1_DS4 (f16 / bf16 inputs),
+    launch_mmq_quantize_glu_q8_0_f32, or with q8k launch_mmq_quantize_glu_q8k_f32.  Returns (uint8 tensor, kp)."""
     torch = _torch()
     k = gate.shape[-1]
     kp = pad_to(k, 256)
     ne1 = ids.numel() if ids is not None else gate.shape[0]
     if out is None:
-        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1), 1), dtype=torch.uint8, device=gate.device)
-    if not _q8_1(wtype, q8_1):
+        out = torch.empty(max(mmq_act_bytes(wtype, ne1, kp, q8_1, q8k), 1), dtype=torch.uint8, device=gate.device)
+    if q8k:
+        lib().launch_mmq_quantize_glu_q8k_f32(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0), kp, ne1,
+                                              activation, _stream())
+    elif not _q8_1(wtype, q8_1):
         lib().launch_mmq_quantize_glu_q8_0_f32(_ptr(gate), _ptr(up), _ptr(ids), _ptr(out), k, gate.stride(0), kp, ne1,
                                                activation, _stream())
     elif gate.dtype == torch.float32:
@@ -518,25 +522,25 @@ def quantize_prefill_glu(wtype: int, gate, up, ids=None, activation: int = 0, ou
     return out, kp
 
 
-def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None, tmp_fixup=True, q8_1=None):
-    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t> (or _q8_0).  tmp_fixup=False passes no fixup buffer
-    (no split-K)."""
+def mmq(wtype: int, w, y, k: int, n: int, m: int, out_dtype=None, out=None, tmp_fixup=True, q8_1=None, q8k=False):
+    """Prefill matmul: dst [m, n] through launch_mmq_gguf_<t> (or _q8_0, or with q8k the Q4_K / Q5_K _q8k entries over
+    `_q8k` tiles).  tmp_fixup=False passes no fixup buffer (no split-K)."""
     torch = _torch()
     out_dtype = out_dtype or torch.float32
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=w.device)
     type_dst = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[out.dtype]
     fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
-    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}{_sfx(wtype, q8_1)}")(
+    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}{'_q8k' if q8k else _sfx(wtype, q8_1)}")(
         _ptr(fx), _ptr(w), _ptr(y), _ptr(out), k, n, m, k // BLOCK_SIZE[wtype], n, 0, nsm, 160 * 1024, 64, type_dst,
         _stream())
     check()
     return out
 
 
-def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None, q8_1=None):
-    y, _ = quantize_prefill(wtype, x, q8_1=q8_1)
-    return mmq(wtype, w, y, x.shape[1], n, x.shape[0], out_dtype=out_dtype, q8_1=q8_1)
+def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None, q8_1=None, q8k=False):
+    y, _ = quantize_prefill(wtype, x, q8_1=q8_1, q8k=q8k)
+    return mmq(wtype, w, y, x.shape[1], n, x.shape[0], out_dtype=out_dtype, q8_1=q8_1, q8k=q8k)
 
 
 def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,

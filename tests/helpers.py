@@ -84,17 +84,24 @@ def decode_act_blocks(gtype, buf, m, kp, k=None, q8_1=None):
     return np.ascontiguousarray(raw[: m * kp // 32 * 34].reshape(m, kp // 32, 34)[:, : -(-k // 32)]).reshape(-1)
 
 
-def tiles_to_blocks(buf, rows, kp, q8k):
+def tiles_to_blocks(buf, rows, kp, q8k, s16=False):
     """Prefill tile bytes -> the oracle's block bytes [rows, kp / block]: Q8_K tiles (qs [nsb][rows][256] | f32 d
-    [nsb][rows] | int16 per-32 sums [nsb][rows][8], 276 bytes per 256 values; the sums are checked) or Q8_0 tiles
-    (qs | f16 d [nsb][rows][8], 272 per 256)."""
+    [nsb][rows] | int16 per-32 sums [nsb][rows][8], 276 bytes per 256 values; the sums are checked), with s16 the
+    `_q8k` tiles (the same qs and d, then f16 per-16 sums [nsb][rows][16], 292 per 256; the sums are checked), or
+    Q8_0 tiles (qs | f16 d [nsb][rows][8], 272 per 256)."""
     nsb = kp // 256
-    b = np.ascontiguousarray(buf).reshape(-1)[: rows * nsb * (276 if q8k else 272)]
+    b = np.ascontiguousarray(buf).reshape(-1)[: rows * nsb * (292 if s16 else 276 if q8k else 272)]
     qs = b[: nsb * rows * 256].view(np.int8).reshape(nsb, rows, 256).transpose(1, 0, 2).reshape(-1, 256)
-    if q8k:
+    if q8k or s16:
         d = b[nsb * rows * 256: nsb * rows * 260].view(np.float32).reshape(nsb, rows).T.reshape(-1)
-        s32 = b[nsb * rows * 260:].view(np.int16).reshape(nsb, rows, 8).transpose(1, 0, 2)
-        _check_s32(qs, s32, "tile")
+        if s16:
+            # sums of 16 int8 lie within +-2048, where f16 holds every integer: they must be exact
+            h = b[nsb * rows * 260:].view(np.float16).reshape(nsb, rows, 16).transpose(1, 0, 2).reshape(-1, 16)
+            want = qs.reshape(-1, 16, 16).astype(np.int32).sum(axis=2)
+            assert np.array_equal(h.astype(np.float32), want.astype(np.float32)), "tile f16 sums of 16"
+        else:
+            s32 = b[nsb * rows * 260:].view(np.int16).reshape(nsb, rows, 8).transpose(1, 0, 2)
+            _check_s32(qs, s32, "tile")
         return _q8k(d, qs).view(np.uint8).reshape(-1)
     d8 = b[nsb * rows * 256:].view(np.uint16).reshape(nsb, rows, 8)
     out = np.zeros((rows, nsb * 8), dtype=O.BLOCK_DTYPES[O.Q8_0])

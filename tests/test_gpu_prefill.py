@@ -35,6 +35,20 @@ def test_prefill_quantizer_is_bit_exact(wtype, m, k):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("m,k", [(5, 256), (130, 1024), (3, 300), (64, 4096)])
+def test_q8k_tile_quantizer_is_bit_exact(m, k):
+    """launch_mmq_quantize_q8k: the Q8_K quantization of the reference-named tiles, with exact f16 sums of 16."""
+    rng = np.random.default_rng(m * 5 + k)
+    x = acts(rng, m, k)
+    y, kp = qmm.quantize_prefill(O.Q4K, to_dev(x), q8k=True)
+    xp = np.zeros((m, kp), np.float32)
+    xp[:, :k] = x
+    got = tiles_to_blocks(y.cpu().numpy(), m, kp, True, s16=True)
+    assert np.array_equal(got, O.quantize(O.Q8K, xp).reshape(-1))
+    y1, _ = qmm.quantize_prefill(O.Q4K, to_dev(x))
+    assert np.array_equal(y.cpu().numpy()[: m * kp // 256 * 260], y1.cpu().numpy()[: m * kp // 256 * 260])
+
+
 def test_prefill_quantizer_row_gather():
     rng = np.random.default_rng(3)
     x = acts(rng, 10, 512)
@@ -136,6 +150,27 @@ def test_split_k_grouped_is_deterministic():
     assert_parity(outs[0], want)
 
 
+# (gtype, m, n, k): the K-quant kernel's tile shapes, split K, ragged edges and K not a multiple of 512
+Q8K_CASES = [(O.Q4K, 40, 64, 512), (O.Q4K, 130, 200, 1024), (O.Q4K, 17, 300, 4096), (O.Q4K, 512, 256, 4096),
+             (O.Q4K, 3, 33, 768), (O.Q5K, 40, 64, 512), (O.Q5K, 255, 129, 256), (O.Q5K, 17, 300, 4096)]
+
+
+@pytest.mark.parametrize("gtype,m,n,k", Q8K_CASES)
+def test_mmq_q8k_twin(gtype, m, n, k):
+    """launch_mmq_gguf_{q4_k,q5_k}_q8k over `_q8k` tiles: the min term's per-superblock sums are exact integers on
+    both activation forms (f16 sums of 16 here, the int16 sums of 32 split into two f16 halves on the reference
+    names), so the output equals the reference-named entry's bit for bit, and the oracle's within the bound."""
+    rng = np.random.default_rng(gtype * 77 + m + n + k)
+    wq = O.quantize(gtype, weights(rng, n, k))
+    x = acts(rng, m, k)
+    x[:, ::64] *= 60.0
+    wd, xd = to_dev(wq), to_dev(x)
+    got = qmm.qmatmul_prefill(gtype, wd, xd, n, q8k=True).cpu().numpy()
+    ref = qmm.qmatmul_prefill(gtype, wd, xd, n).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"t{gtype} m{m} n{n} k{k}"
+    assert_parity(got, O.matmul(gtype, x, wq, n), terms(gtype, x, wq, n), what=f"t{gtype} m{m} n{n} k{k}")
+
+
 @pytest.mark.parametrize("wtype", [O.Q4K, O.Q8_0])
 @pytest.mark.parametrize("activation", [2, 0])
 def test_glu_requantizer(wtype, activation):
@@ -160,6 +195,10 @@ def test_glu_requantizer(wtype, activation):
     at = O.ACT_TYPE[wtype]
     want = O.quantize(at, hp).reshape(-1)
     got = tiles_to_blocks(y.cpu().numpy(), len(ids), kp, at == O.Q8K)
+    if wtype == O.Q4K:
+        y16, _ = qmm.quantize_prefill_glu(wtype, to_dev(gate), to_dev(up), ids=to_dev(ids), activation=activation,
+                                          q8k=True)
+        assert np.array_equal(tiles_to_blocks(y16.cpu().numpy(), len(ids), kp, True, s16=True), got)
     if activation == 2:
         assert np.array_equal(got, want)
     else:
