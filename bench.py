@@ -626,7 +626,7 @@ def main():
     extra = {"q4_k_decode_b1_two_launch": {
         "ms_per_step": head["ms_per_step"], "gb_s": head["gb_s"],
         "step": "launch_mmvq_gguf_quantize_q8_1_f32 + launch_mmvq_gguf_q4_k_f32_plain",
-        "matvec": {"kernel": "k_mmvq_p<unit_q4k, out_f32, 1, 1, true>", "kernel_us": head["kernel_us"],
+        "matvec": {"kernel": "k_mmvq_p<unit_q4k_s, out_f32, 1, 1, true>", "kernel_us": head["kernel_us"],
                    "gb_s": head["kernel_gb_s"], "algorithmic_bytes": head["kernel_bytes"],
                    "frac_hbm_peak": head["kernel_gb_s"] / HBM_PEAK_GBS}}}
     if not args.quick:
