@@ -358,12 +358,7 @@ void launch_mmq_quantize_glu_q8k_f32(const float *gate, const float *up, const i
                                  const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,     \
                                  int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,               \
                                  int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,        \
-                                 int warp_size, void *stream);                                                  \
-  void launch_mmq_gguf_##t##_moe_wsum(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,  \
-                                      const int32_t *expert_bounds, float *routes, const float *topk_weights, \
-                                      int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,        \
-                                      int64_t ncols_dst, int64_t stride_row_x, int64_t num_experts,           \
-                                      int64_t ncols_max, int topk, int nsm, void *stream);
+                                 int warp_size, void *stream);
 QMM_DECLARE_MMQ(q8_0)
 QMM_DECLARE_MMQ(q4_k)
 QMM_DECLARE_MMQ(q6_k)
@@ -400,19 +395,6 @@ void launch_mmq_gguf_q4_k_q8k(void *tmp_fixup, const void *x, const void *y, voi
 void launch_mmq_gguf_q5_k_q8k(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,
                               int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc,
                               int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream);
-/* launch_mmq_gguf_<t>_moe_wsum: no counterpart in the reference, whose grouped MoE runs launch_mmq_gguf_<t>_moe for
- * the down projection and then launch_moe_weighted_reduce_flat (inference-nn/src/moe/experts/backends.rs:2304-2334,
- * 2418-2446).  The same grouped matmul, with the routes' rows stored to routes[p * nrows_x + row] (p = ids_dst[c],
- * f32, ncols_dst = tokens * topk rows) and the weighted sum over each token's routes folded in:
- * out[t * nrows_x + row] = sum_s topk_weights[t * topk + s] * routes[(t * topk + s) * nrows_x + row], in slot order
- * with the reduce's arithmetic (zero-weight routes not read), so out is bit for bit that of launch_mmq_gguf_<t>_moe
- * without a fixup buffer (no split K; tmp_fixup is accepted and unused here) followed by the reduce.  The
- * workgroup that stores a token's last route row of a column tile adds the token's rows up (agent-scope release
- * before its count, acquire after); counters: int32[tokens * ceil(nrows_x / 32)], all zero before the first call and
- * left zero by every call.  Calls that overlap on one counters buffer race.  The K-quant types fold the sum into
- * the matmul's workgroups; the 32-value types (Q8_0, Q4_0, Q5_0) run the reduce as a second launch.  Measured on
- * MI355X it is slower than the two launches (the agent-scope release and acquire of every workgroup write back and
- * invalidate its XCD's L2): the C++ host's MoE block keeps the two. */
 /* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
  * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
  * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by

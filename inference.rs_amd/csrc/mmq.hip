@@ -23,7 +23,6 @@
 #include "common.h"
 #include "inferencequant.h"
 #include "planes.h"
-#include "routesum.h"
 #include "skinny.h"
 #include "units.h"
 
@@ -181,8 +180,7 @@ template <class WT, class Out, int TM, int NW, bool S16 = false>
 __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64_t nrows_w, int64_t w_row_bytes,
                                             const ActTile &a, int64_t m0, int64_t mrows, int64_t n0, int64_t sb0,
                                             int64_t sb1, typename Out::T *__restrict__ dst, int64_t ldd,
-                                            const int32_t *__restrict__ dst_rows, float *__restrict__ part,
-                                            const RouteSum &rsum = RouteSum{}) {
+                                            const int32_t *__restrict__ dst_rows, float *__restrict__ part) {
   constexpr int BMt = 32 * TM;
   constexpr int BNt = 32 * NW;
   // kLw: the weight superblocks go by DMA into LDS too, as the tile's rows' contiguous 16-byte pieces, and each wave
@@ -448,10 +446,6 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
         }
       }
   }
-  // grouped down projection with the weighted sum folded in (no split K there): every thread takes part
-  if (rsum.out)
-    route_sum_finish<64 * NW, BMt>(rsum, (const float *)(const void *)dst, ldd, dst_rows, m0, mrows, n0,
-                                   (int)(nrows_w - n0 < BNt ? nrows_w - n0 : BNt), (int)(n0 / BNt));
 }
 
 // Split K: split s of a tile writes its partial sums to plane s of the caller's fixup buffer (planes of rows x cols
@@ -953,15 +947,13 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W,
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
-// FUSED: the weighted sum over each token's routes folded in (rsum); a separate instantiation, so that the grouped
-// matmul without it keeps its register allocation
-template <class WT, int TMv, bool FUSED>
+template <class WT, int TMv>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
                                                     const int32_t *__restrict__ ids_dst, int64_t nsb, int64_t splits,
                                                     float *__restrict__ dst, int64_t ldd, float *__restrict__ part,
-                                                    int64_t ncols_dst, RouteSum rsum) {
+                                                    int64_t ncols_dst) {
   const int64_t e = blockIdx.z;
   const int64_t m0 = bounds[e] + (int64_t)blockIdx.y * (32 * TMv), m1 = bounds[e + 1];
   if (m0 >= m1) return;  // uniform over the workgroup
@@ -970,7 +962,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   if (sb0 >= sb1) return;
   mmq_kq_tile<WT, out_f32, TMv, 4>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
-                                part ? part + split * ncols_dst * nrows_w : nullptr, FUSED ? rsum : RouteSum{});
+                                part ? part + split * ncols_dst * nrows_w : nullptr);
 }
 
 template <class WB, bool F32D>
@@ -1236,20 +1228,16 @@ void mmq_q8k(int type, void *tmp_fixup, const void *x, const void *y, void *dst,
 template <class WT, int TMv>
 void kq_moe(dim3 grid, hipStream_t s, const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes,
             const ActTile &a, const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, int64_t splits, float *d,
-            int64_t ldd, float *part, int64_t ncols_dst, const RouteSum &rsum) {
-  if (rsum.out)
-    k_mmq_kq_moe<WT, TMv, true><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                     splits, d, ldd, part, ncols_dst, rsum);
-  else
-    k_mmq_kq_moe<WT, TMv, false><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
-                                                      splits, d, ldd, part, ncols_dst, rsum);
+            int64_t ldd, float *part, int64_t ncols_dst) {
+  k_mmq_kq_moe<WT, TMv><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits,
+                                             d, ldd, part, ncols_dst);
 }
 
 template <bool F32D>
 void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
                void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
-               int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream, const char *who,
-               RouteSum rsum) {
+               int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm, void *stream,
+               const char *who) {
   if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst)) return;
   if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
     qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
@@ -1266,14 +1254,8 @@ void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const in
   // a few rows per expert: the few-row kernel streams each expert's weights once, without 64-row tiles of padding
   const bool b32 = qmm_block_size(type) == 32;  // Q8_0, Q4_0, Q5_0: the Q8_0-layout kernel
   if (!b32 && F32D && qmm_skinny_moe(type, x, y, ids_dst, bounds, (float *)dst, ncols_x, nrows_x, w_row_bytes,
-                                              ncols_dst, stride_col_dst, num_experts, s, rsum))
+                                              ncols_dst, stride_col_dst, num_experts, s))
     return;
-  // the 32-value types store their route rows, then the weighted sum runs as its own launch (the same arithmetic)
-  auto separate_sum = [&] {
-    if (rsum.out)
-      launch_moe_weighted_reduce_flat(dst, rsum.weights, rsum.out, (int)(ncols_dst / rsum.topk), (int)nrows_x,
-                                      rsum.topk, stream);
-  };
   const uint8_t *w = (const uint8_t *)x;
   float *d = (float *)dst;
   if (b32 && b32_runs(w, ncols_x, w_row_bytes)) {
@@ -1286,7 +1268,6 @@ void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const in
     else
       launch_b32_moe<wr_q8_0, F32D>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, d, stride_col_dst,
                               ncols_dst, ncols_max, num_experts, tmp_fixup, nsm, s);
-    separate_sum();
     return;
   }
   // 32-row tiles for a few rows per expert, and always for Q5_K (its third plane does not fit two waves per SIMD at
@@ -1298,39 +1279,37 @@ void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const in
   const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
   // expected work: about ncols_dst / (32 tm) row tiles per n tile over all experts
   const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
-  // (no split K with the weighted sum folded in: each route row of a column tile is stored once, by one workgroup)
-  const int64_t splits = b32 || rsum.out ? 1 : k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
-  rsum.col_tiles = (int32_t)ntiles;
+  const int64_t splits = b32 ? 1 : k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
   float *part = splits > 1 ? (float *)tmp_fixup : nullptr;
   const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
   switch (F32D ? type : QMM_TYPE_Q8_0) {
     case QMM_TYPE_Q4K:
       if (small)
         kq_moe<wq4k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       else
         kq_moe<wq4k, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q5K:  // always 32-row tiles (small)
       kq_moe<wq5k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q6K:
       if (small)
         kq_moe<wq6k, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       else
         kq_moe<wq6k, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_IQ4_XS:
       if (small)
         kq_moe<wiq4xs, 1>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       else
         kq_moe<wiq4xs, 2>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
-                        stride_col_dst, part, ncols_dst, rsum);
+                        stride_col_dst, part, ncols_dst);
       break;
     case QMM_TYPE_Q4_0:
       k_mmq_q8_0_moe<wb_q4_0, F32D><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, ncols_x / 32, a, bounds,
@@ -1345,42 +1324,19 @@ void mmq_moe_t(int type, void *tmp_fixup, const void *x, const void *y, const in
                                                    ids_dst, nsb, d, stride_col_dst);
   }
   if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, stride_col_dst, ids_dst, s);
-  if (b32) separate_sum();  // (the Q8_0-layout kernel of rows that are not whole dword-aligned superblocks)
 }
 
 // q8_0: the activations are Q8_0 blocks (the 32-value types' _q8_0 entries), else Q8_K tiles
 void mmq_moe(int type, bool q8_0, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,
              const int32_t *bounds, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst,
              int64_t stride_row_x, int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm,
-             void *stream, const char *who, RouteSum rsum = RouteSum{}) {
+             void *stream, const char *who) {
   if (q8_0)
     mmq_moe_t<false>(type, tmp_fixup, x, y, ids_dst, bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,
-                     stride_col_dst, num_experts, ncols_max, nsm, stream, who, rsum);
+                     stride_col_dst, num_experts, ncols_max, nsm, stream, who);
   else
     mmq_moe_t<true>(type, tmp_fixup, x, y, ids_dst, bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,
-                    stride_col_dst, num_experts, ncols_max, nsm, stream, who, rsum);
-}
-
-void moe_wsum(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds,
-              float *routes, const float *weights, int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,
-              int64_t ncols_dst, int64_t stride_row_x, int64_t num_experts, int64_t ncols_max, int topk, int nsm,
-              void *stream, const char *who) {
-  if (topk <= 0 || ncols_dst % topk != 0 || !routes || !weights || !counters || !out) {
-    qmm_set_error("%s: topk=%d ncols_dst=%lld (a multiple of topk), routes, topk_weights, counters and out required",
-                  who, topk, (long long)ncols_dst);
-    return;
-  }
-  RouteSum rs;
-  rs.out = out;
-  rs.weights = weights;
-  rs.counters = counters;
-  rs.ldo = nrows_x;
-  rs.topk = topk;
-  rs.col_tiles = 0;  // set by the kernel's launcher
-  // no split K (each route row of a column tile is stored once, by one workgroup), whatever tmp_fixup holds
-  (void)tmp_fixup;
-  mmq_moe(type, false, nullptr, x, y, ids_dst, bounds, routes, ncols_x, nrows_x, ncols_dst, stride_row_x, nrows_x,
-          num_experts, ncols_max, nsm, stream, who, rs);
+                    stride_col_dst, num_experts, ncols_max, nsm, stream, who);
 }
 
 }  // namespace
@@ -1403,16 +1359,7 @@ void moe_wsum(int type, void *tmp_fixup, const void *x, const void *y, const int
     mmq_moe(TYPE, Q8_0, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,   \
             stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe" #sfx);                           \
   }
-#define QMM_DEFINE_MMQ(t, TYPE)                                                                                    \
-  QMM_DEFINE_MMQ_ENTRIES(t, TYPE, false, )                                                                         \
-  void launch_mmq_gguf_##t##_moe_wsum(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,      \
-                                      const int32_t *expert_bounds, float *routes, const float *topk_weights,     \
-                                      int32_t *counters, float *out, int64_t ncols_x, int64_t nrows_x,            \
-                                      int64_t ncols_dst, int64_t stride_row_x, int64_t num_experts,               \
-                                      int64_t ncols_max, int topk, int nsm, void *stream) {                       \
-    moe_wsum(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, routes, topk_weights, counters, out, ncols_x, nrows_x, \
-             ncols_dst, stride_row_x, num_experts, ncols_max, topk, nsm, stream, "mmq_" #t "_moe_wsum");           \
-  }
+#define QMM_DEFINE_MMQ(t, TYPE) QMM_DEFINE_MMQ_ENTRIES(t, TYPE, false, )
 
 extern "C" {
 QMM_DEFINE_MMQ(q8_0, QMM_TYPE_Q8_0)

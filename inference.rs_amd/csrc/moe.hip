@@ -5,7 +5,6 @@
 // order inside an expert follows atomic arrival (as in the reference); only the grouping is contractual.
 // No memset/memcpy nodes, so the sequence can be captured in a HIP graph.
 #include "common.h"
-#include "routesum.h"
 #include "inferencequant.h"
 
 namespace {
@@ -79,7 +78,7 @@ __global__ __launch_bounds__(256) void k_weighted_reduce(const typename In::T *_
   for (int s = 0; s < topk; s++) {
     const float ws = w[(int64_t)t * topk + s];
     // a zero-weight route may be one the grouped kernels parked and never wrote: it is not read
-    if (ws != 0.0f) acc = route_acc(acc, In::load(in, base + (int64_t)s * hidden), ws);
+    if (ws != 0.0f) acc = __builtin_fmaf(In::load(in, base + (int64_t)s * hidden), ws, acc);
   }
   Out::store(out, (int64_t)t * hidden + h, acc);
 }

@@ -4,7 +4,6 @@
 #include <hip/hip_runtime.h>
 
 #include "qmm_blocks.h"
-#include "routesum.h"
 
 // From this many activation rows on, K-quant weights go through the MFMA few-row kernel, which decodes each weight
 // block once for all rows (measured crossover on MI355X: Q4_K 4 rows, Q6_K 3).
@@ -42,8 +41,6 @@ bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void 
 #ifndef QMM_SKINNY_MOE_ROWS
 #define QMM_SKINNY_MOE_ROWS 0
 #endif
-// With sum.out set, the workgroups also fold the weighted sum over each token's routes (routesum.h) into out; the
-// column tiles are 32 rows of the weight (sum.col_tiles is set here).
 bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                     int64_t ncols_x, int64_t nrows_x, int64_t w_row_bytes, int64_t ncols_dst, int64_t ldd,
-                    int64_t num_experts, hipStream_t s, RouteSum sum = RouteSum{});
+                    int64_t num_experts, hipStream_t s);

@@ -138,7 +138,6 @@ struct moe_route {
   const int32_t *bounds;
   const int32_t *ids_dst;
   int64_t expert_bytes;
-  RouteSum sum;  // sum.out set: fold the weighted sum over each token's routes into sum.out (routesum.h)
 };
 
 // The NW waves' partial 32x32 tiles, summed through LDS.  Plain: lane (g, li) of wave w stores output registers
@@ -178,9 +177,7 @@ __device__ __forceinline__ void reduce_store(const v16f &fa, int wave, int lane,
 // 16..31 load nothing and their columns come out zero)
 // GLU: W2 holds the up weights; waves [0, NW/2) take the gate rows and [NW/2, NW) the up rows.
 // MOE: the activation rows and weights of expert blockIdx.z (moe_route); otherwise rows [0, mrows).
-// FUSED (MOE only): fold the weighted sum over each token's routes into route.sum.out (a separate instantiation, so
-// that the grouped matmul without it keeps its register allocation)
-template <class WT, class AP, class Out, int NW, int TR, bool GLU, bool MOE = false, bool FUSED = false>
+template <class WT, class AP, class Out, int NW, int TR, bool GLU, bool MOE = false>
 __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                                     int64_t nrows_w, int64_t w_row_bytes, AP ap, int mrows,
                                                     int64_t nsb, typename Out::T *__restrict__ dst, int64_t ldd,
@@ -265,9 +262,6 @@ __global__ __launch_bounds__(64 * NW) void k_skinny(const uint8_t *__restrict__ 
       }
     }
     reduce_store<Out, NW, GLU>(fa, wave, lane, g, li, n0, n0 + rows_here, m0, m_end, ids, dst, ldd, activation);
-    if constexpr (MOE && FUSED)
-      route_sum_finish<64 * NW, 32>(route.sum, (const float *)(const void *)dst, ldd, ids, m0, m_end, n0,
-                                    (int)rows_here, (int)blockIdx.x);
     if (!MOE) break;
     __syncthreads();  // the next chunk rewrites the reduction buffer
   }
@@ -450,25 +444,18 @@ void launch_tc(const void *vx, const void *vy, void *dst, int ncols_x, int nrows
 template <class WT>
 void launch_moe(const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                 int64_t nrows_x, int64_t w_row_bytes, int64_t nsb, int64_t ncols_dst, int64_t ldd, int64_t num_experts,
-                int64_t chunks, hipStream_t s, RouteSum sum) {
+                int64_t chunks, hipStream_t s) {
   act_tiles ap;
   ap.base = (const uint8_t *)y;
   ap.rows = (uint32_t)ncols_dst;
   ap.nsb = (uint32_t)nsb;
   ap.bytes = nsb * ncols_dst * 276;
-  sum.col_tiles = (int32_t)qmm_ceil_div(nrows_x, 32);
-  const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes, sum};
+  const moe_route rt{bounds, ids_dst, nrows_x * w_row_bytes};
   const dim3 grid((unsigned)qmm_ceil_div(nrows_x, 32), (unsigned)chunks, (unsigned)num_experts);
   const uint8_t *w = (const uint8_t *)x;
-  if (nsb >= 32 && sum.out)  // long rows: 8 waves split K
-    k_skinny<WT, act_tiles, out_f32, 8, 32, false, true, true><<<grid, 512, 0, s>>>(w, nullptr, nrows_x, w_row_bytes,
-                                                                                    ap, 0, nsb, dst, ldd, 0, rt);
-  else if (nsb >= 32)
+  if (nsb >= 32)  // long rows: 8 waves split K
     k_skinny<WT, act_tiles, out_f32, 8, 32, false, true><<<grid, 512, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
                                                                               nsb, dst, ldd, 0, rt);
-  else if (sum.out)
-    k_skinny<WT, act_tiles, out_f32, 4, 32, false, true, true><<<grid, 256, 0, s>>>(w, nullptr, nrows_x, w_row_bytes,
-                                                                                    ap, 0, nsb, dst, ldd, 0, rt);
   else
     k_skinny<WT, act_tiles, out_f32, 4, 32, false, true><<<grid, 256, 0, s>>>(w, nullptr, nrows_x, w_row_bytes, ap, 0,
                                                                               nsb, dst, ldd, 0, rt);
@@ -534,7 +521,7 @@ bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void 
 
 bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_dst, const int32_t *bounds, float *dst,
                     int64_t ncols_x, int64_t nrows_x, int64_t w_row_bytes, int64_t ncols_dst, int64_t ldd,
-                    int64_t num_experts, hipStream_t s, RouteSum sum) {
+                    int64_t num_experts, hipStream_t s) {
   if (ncols_x % 256 != 0 || ncols_dst <= 0 || num_experts <= 0 || num_experts > 65535) return false;
   if (ncols_dst > QMM_SKINNY_MOE_ROWS * num_experts) return false;
   const int64_t nsb = ncols_x / 256;
@@ -542,11 +529,9 @@ bool qmm_skinny_moe(int type, const void *x, const void *y, const int32_t *ids_d
   // enough 32-row chunks for an expert of average size; larger experts loop over theirs
   const int64_t chunks = qmm_ceil_div(qmm_ceil_div(ncols_dst, num_experts), 32);
   if (type == QMM_TYPE_Q4K)
-    launch_moe<wq4k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s,
-                     sum);
+    launch_moe<wq4k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
   else if (type == QMM_TYPE_Q6K)
-    launch_moe<wq6k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s,
-                     sum);
+    launch_moe<wq6k>(x, y, ids_dst, bounds, dst, nrows_x, w_row_bytes, nsb, ncols_dst, ldd, num_experts, chunks, s);
   else
     return false;
   return true;

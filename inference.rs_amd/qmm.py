@@ -553,22 +553,6 @@ def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n:
     return out
 
 
-def mmq_moe_wsum(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
-                 ncols_max: int, weights, topk: int, counters, out, routes=None):
-    """Grouped matmul with the weighted sum over each token's routes folded in (launch_mmq_gguf_<t>_moe_wsum, over
-    Q8_K tiles: quantize_prefill(..., q8_1=True)): out [ncols_dst / topk, n]; routes [ncols_dst, n] f32 receives the per-route rows; counters int32
-    [tokens * ceil(n / 32)], zero before the call and left zero.  Returns (out, routes)."""
-    torch = _torch()
-    if routes is None:
-        routes = torch.empty((ncols_dst, n), dtype=torch.float32, device=w.device)
-    fx, nsm = fixup(w.device)
-    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}_moe_wsum")(
-        _ptr(fx), _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(routes), _ptr(weights), _ptr(counters),
-        _ptr(out), k, n, ncols_dst, k // BLOCK_SIZE[wtype], n_experts, ncols_max, topk, nsm, _stream())
-    check()
-    return out, routes
-
-
 # ------------------------------------------------------------------------------------------------ dequantization
 
 def dequantize(wtype: int, w, n: int, out_dtype=None, out=None):

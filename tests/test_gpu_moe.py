@@ -143,50 +143,6 @@ def test_grouped_q6_k_experts_2_bytes_past_a_dword(tokens):
     assert_parity(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("case", ["uniform64", "skewed64", "uniform400", "top4"])
-@pytest.mark.parametrize("gtype", [O.Q4K, O.Q6K, O.Q5K, O.IQ4XS, O.Q8_0, O.Q4_0])
-def test_grouped_down_with_folded_weighted_sum(gtype, case):
-    """launch_mmq_gguf_<t>_moe_wsum: the same bits as the grouped matmul (unsplit) followed by
-    launch_moe_weighted_reduce_flat, on two calls in a row (the counters return to zero), whichever workgroup
-    finishes a token last; against the oracle's per-route matmuls and weighted reduce.  64 tokens take the few-row
-    kernel (32-column tiles; Q5_K / IQ4_XS the 128-column tile kernel), 400 tokens the tile kernel, top-4 more routes
-    per token; the 32-value types run the reduce as a second launch."""
-    rng = np.random.default_rng(60 + gtype)
-    E, n, k = 8, 160, 1024
-    topk = 4 if case == "top4" else 2
-    tokens = 400 if case == "uniform400" else 64
-    if case == "uniform400":
-        k = 512
-    wq = experts(rng, gtype, E, n, k)
-    ids, w = routing(rng, tokens, E, topk)
-    if case == "skewed64":
-        ids = skewed_routing(rng, tokens, E, topk)
-    w[3, 1] = 0.0  # a zero-weight route: skipped by the sum
-    x = acts(rng, tokens, k)
-    if gtype in (O.Q8_0, O.Q4_0):  # the entry reads Q8_K tiles: the oracle's matmul over Q8_K activations per route
-        routes_want = np.stack([np.stack([O.matmul_q8k_act(gtype, x[t: t + 1], wq[ids[t, s]], n)[0]
-                                          for s in range(topk)]) for t in range(tokens)])
-    else:
-        routes_want = O.indexed_moe(gtype, wq, E, n, k, x[:, None], ids.astype(np.uint32))
-    want = O.moe_weighted_reduce(routes_want, w)
-    bounds, tok, src, counts, _ = qmm.moe_dispatch(to_dev(ids.reshape(-1)), E, topk)
-    y, kp = qmm.quantize_prefill(gtype, to_dev(x), ids=src, q8_1=True)
-    ncols_max = int(counts.max().item())
-    wd, wt = to_dev(wq), to_dev(w.reshape(-1))
-    # the two launches: grouped matmul without split K, then the reduce
-    routes = torch.full((tokens * topk, n), float("nan"), device=DEV)
-    qmm.mmq_moe(gtype, wd, y, tok, bounds, E, k, n, tokens * topk, ncols_max, routes, tmp_fixup=False, q8_1=True)
-    two = qmm.moe_weighted_reduce(routes.reshape(tokens, topk, n), wt).cpu().numpy()
-    counters = torch.zeros(tokens * ((n + 31) // 32), dtype=torch.int32, device=DEV)
-    for call in range(2):
-        out = torch.full((tokens, n), float("nan"), device=DEV)
-        qmm.mmq_moe_wsum(gtype, wd, y, tok, bounds, E, k, n, tokens * topk, ncols_max, wt, topk, counters, out)
-        got = out.cpu().numpy()
-        assert np.array_equal(got.view(np.uint32), two.view(np.uint32)), f"call {call}: differs from the two launches"
-        assert int(counters.abs().sum().item()) == 0, f"call {call}: counters not returned to zero"
-    assert_parity(got, want, what=f"wsum t{gtype} {case}")
-
-
 @pytest.mark.parametrize("kind", ["f32", "bf16_out", "f16_in", "bf16_in"])
 def test_weighted_reduce(kind):
     rng = np.random.default_rng(9)
