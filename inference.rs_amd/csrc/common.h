@@ -58,17 +58,33 @@ __device__ __forceinline__ int32_t sat_i8(float v) {
 }
 
 // Element loads of the three activation dtypes.
+// load4: the four values at p, p + 1, p + 2, p + 3 in one vector load (p aligned to four values)
 struct in_f32 {
   typedef float T;
   static __device__ __forceinline__ float load(const float *p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void load4(const float *p, float v[4]) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 f = *(const f32x4 *)p;
+    v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+  }
 };
 struct in_f16 {
   typedef uint16_t T;
   static __device__ __forceinline__ float load(const uint16_t *p, int64_t i) { return f16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void load4(const uint16_t *p, float v[4]) {
+    const uint2 h = *(const uint2 *)p;
+    v[0] = f16_bits_to_f32(h.x & 0xffffu), v[1] = f16_bits_to_f32(h.x >> 16);
+    v[2] = f16_bits_to_f32(h.y & 0xffffu), v[3] = f16_bits_to_f32(h.y >> 16);
+  }
 };
 struct in_bf16 {
   typedef uint16_t T;
   static __device__ __forceinline__ float load(const uint16_t *p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void load4(const uint16_t *p, float v[4]) {
+    const uint2 h = *(const uint2 *)p;
+    v[0] = bf16_bits_to_f32(h.x & 0xffffu), v[1] = bf16_bits_to_f32(h.x >> 16);
+    v[2] = bf16_bits_to_f32(h.y & 0xffffu), v[3] = bf16_bits_to_f32(h.y >> 16);
+  }
 };
 
 // Output stores.

@@ -140,8 +140,15 @@ __device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs
   if (sub == 0) *d_out = f32_to_f16_bits(d);
 }
 
+// values k0 .. k0 + 3 of a row of kx values, zero past its end: one vector load where all four are in the row and
+// aligned (every row of an aligned, padded activation), else four element loads
 template <class In>
 __device__ __forceinline__ void load4(const typename In::T *row, int64_t k0, int64_t kx, float v[4]) {
+  const typename In::T *p = row + k0;
+  if (k0 + 4 <= kx && ((uintptr_t)p & (4 * sizeof(typename In::T) - 1)) == 0) {
+    In::load4(p, v);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++) v[i] = (k0 + i < kx) ? In::load(row, k0 + i) : 0.0f;
 }
