@@ -38,6 +38,12 @@ bool qmm_skinny_tc(int type, int out_type, const void *vx, const void *vy, void 
 // nothing, for a case it does not serve.  0 (the default): never -- the grouped tile kernel's 32-row tiles with
 // weights staged in LDS measured faster (MI355X, 8 x Q4_K 14336x4096 / 4096x14336 experts, 64 tokens top-2: 307
 // against 319 us for the MoE step)
+// Waves per workgroup of the GLU form (half on the gate rows, half on the up rows, each half splitting K).  Measured on
+// MI355X, 2 x Q4_K 14336x4096: 4 waves 28.7 / 30.0 / 33.9 / 41.2 us at b = 4 / 8 / 16 / 32, against 31.0 / 32.5 /
+// 36.5 / 42.9 us with 8 and 35.7 / 36.0 / 36.2 / 41.0 us with 2.
+#ifndef QMM_SKINNY_GLU_NW
+#define QMM_SKINNY_GLU_NW 4
+#endif
 #ifndef QMM_SKINNY_MOE_ROWS
 #define QMM_SKINNY_MOE_ROWS 0
 #endif

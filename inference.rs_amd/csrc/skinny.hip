@@ -385,9 +385,10 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
   const uint8_t *w = (const uint8_t *)vx, *w2 = (const uint8_t *)vx2;
   typename Out::T *d = (typename Out::T *)dst;
   const int64_t wrb = nsb * WT::kBytes;
-  if (w2) {  // gate and up in one workgroup: 4 waves each
+  if (w2) {  // gate and up in one workgroup: QMM_SKINNY_GLU_NW / 2 waves each
     if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
-      k_skinny<WT, act_slot, Out, 8, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 512, 0, s>>>(
+      k_skinny<WT, act_slot, Out, QMM_SKINNY_GLU_NW, 32, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)),
+                                                                  64 * QMM_SKINNY_GLU_NW, 0, s>>>(
           w, w2, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, activation, moe_route{});
     else
       k_skinny<WT, act_slot, Out, 8, 16, true><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
