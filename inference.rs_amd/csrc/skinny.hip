@@ -28,6 +28,11 @@ namespace {
 #ifndef QMM_SKINNY16_WIDE
 #define QMM_SKINNY16_WIDE 0
 #endif
+// from this many activation rows on, short weights split K over 8 waves as long rows do (MI355X, b = 24 / 32:
+// Q6_K 1024x4096 10.8 / 11.4 -> 10.1 / 10.9 us, Q4_K 4096x4096 10.0 / 11.0 -> 10.0 / 10.8 us)
+#ifndef QMM_SKINNY_K8_B
+#define QMM_SKINNY_K8_B 17
+#endif
 // weights with fewer 32-row tiles than this go in 16-row tiles (twice the workgroups)
 #ifndef QMM_SKINNY_WIDE_TILES
 #define QMM_SKINNY_WIDE_TILES 384
@@ -411,7 +416,7 @@ void launch_decode(const void *vx, const void *vx2, const void *vy, void *dst, i
   if (qmm_ceil_div(nrows_x, 32) >= QMM_SKINNY_WIDE_TILES)
     k_skinny<WT, act_slot, Out, 4, 32, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 32)), 256, 0, s>>>(
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
-  else if (nsb >= 32)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
+  else if (nsb >= 32 || b >= QMM_SKINNY_K8_B)  // long rows: 8 waves split K, so each wave's chain of superblocks stays short
     k_skinny<WT, act_slot, Out, 8, 16, false><<<dim3((unsigned)qmm_ceil_div(nrows_x, 16)), 512, 0, s>>>(
         w, nullptr, nrows_x, wrb, ap, b, nsb, d, stride_col_dst, 0, moe_route{});
   else
