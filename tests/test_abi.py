@@ -106,6 +106,19 @@ def test_bad_arguments_are_rejected_before_any_launch():
     L.launch_mmq_quantize_q8_1_D4(None, None, None, 0, 300, 300, 300, 300, 300, 1, 1, 1, None)
     assert "multiple of 256" in qmm.last_error()
     L.qmm_clear_error()
+    # the `_q8k` prefill entries
+    L.launch_mmq_quantize_q8k(None, None, None, 0, 300, 300, 300, 300, 300, 1, 1, 1, None)
+    assert "mmq_quantize_q8k" in qmm.last_error() and "multiple of 256" in qmm.last_error()
+    L.qmm_clear_error()
+    L.launch_mmq_quantize_glu_q8k_f32(None, None, None, None, 256, 256, 256, 1, 5, None)
+    assert "activation" in qmm.last_error()
+    L.qmm_clear_error()
+    L.launch_mmq_gguf_q4_k_q8k(None, 8, None, None, 256, 8, 1, 1, 8, 0, 256, 0, 64, 0, None)
+    assert "16-byte aligned" in qmm.last_error()
+    L.qmm_clear_error()
+    L.launch_mmq_gguf_q5_k_q8k(None, None, None, None, 300, 8, 1, 1, 8, 0, 256, 0, 64, 0, None)
+    assert "ncols_x" in qmm.last_error()
+    L.qmm_clear_error()
 
 
 def test_host_library_exports_its_header():
