@@ -395,6 +395,16 @@ void launch_mmq_gguf_q4_k_q8k(void *tmp_fixup, const void *x, const void *y, voi
 void launch_mmq_gguf_q5_k_q8k(void *tmp_fixup, const void *x, const void *y, void *dst, int64_t ncols_x,
                               int64_t nrows_x, int64_t ncols_y, int64_t stride_row_x, int64_t stride_col_dst, int cc,
                               int nsm, int64_t smpbo, int warp_size, int type_dst, void *stream);
+/* launch_mmq_gguf_{q4_k,q5_k}_moe_q8k: no counterpart in the reference; launch_mmq_gguf_<t>_moe over `_q8k` tiles
+ * (launch_mmq_quantize_q8k with the dispatch's row ids, or launch_mmq_quantize_glu_q8k_f32), the same results. */
+void launch_mmq_gguf_q4_k_moe_q8k(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,
+                                  const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,
+                                  int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst, int64_t num_experts,
+                                  int64_t ncols_max, int cc, int nsm, int64_t smpbo, int warp_size, void *stream);
+void launch_mmq_gguf_q5_k_moe_q8k(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,
+                                  const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,
+                                  int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst, int64_t num_experts,
+                                  int64_t ncols_max, int cc, int nsm, int64_t smpbo, int warp_size, void *stream);
 /* launch_mmq_gguf_<t>_moe (gguf/ffi.rs:919-938; mmq_gguf.cuh:4020-4061): expert e's weights are
  * x + e * nrows_x * stride_row_x blocks; its activation columns are [expert_bounds[e], expert_bounds[e+1])
  * of y (the prefill layout with ne1 = expert_bounds[num_experts] rows, rows gathered in expert order by

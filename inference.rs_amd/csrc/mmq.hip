@@ -947,7 +947,8 @@ __global__ __launch_bounds__(256) void k_mmq_q8_0(const uint8_t *__restrict__ W,
 
 // Expert-grouped: grid (n tiles, m tiles of the largest expert, experts).  Expert e's rows of `a` are
 // [bounds[e], bounds[e+1]); its weights start at W + e * expert_bytes; row m is written to dst row ids_dst[m].
-template <class WT, int TMv>
+// S16: `_q8k` activation tiles.
+template <class WT, int TMv, bool S16 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT, TMv>()))) void k_mmq_kq_moe(const uint8_t *__restrict__ W, int64_t expert_bytes,
                                                     int64_t nrows_w, int64_t w_row_bytes, ActTile a,
                                                     const int32_t *__restrict__ bounds,
@@ -960,7 +961,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves<WT
   const int64_t split = blockIdx.x % splits, per = (nsb + splits - 1) / splits;
   const int64_t sb0 = split * per, sb1 = sb0 + per < nsb ? sb0 + per : nsb;
   if (sb0 >= sb1) return;
-  mmq_kq_tile<WT, out_f32, TMv, 4>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
+  mmq_kq_tile<WT, out_f32, TMv, 4, S16>(W + e * expert_bytes, nrows_w, w_row_bytes, a, m0, m1,
                                 (int64_t)(blockIdx.x / splits) * BN, sb0, sb1, dst, ldd, ids_dst,
                                 part ? part + split * ncols_dst * nrows_w : nullptr);
 }
@@ -1225,12 +1226,12 @@ void mmq_q8k(int type, void *tmp_fixup, const void *x, const void *y, void *dst,
 #undef QMM_Q8K
 }
 
-template <class WT, int TMv>
+template <class WT, int TMv, bool S16 = false>
 void kq_moe(dim3 grid, hipStream_t s, const uint8_t *w, int64_t expert_bytes, int64_t nrows_x, int64_t w_row_bytes,
             const ActTile &a, const int32_t *bounds, const int32_t *ids_dst, int64_t nsb, int64_t splits, float *d,
             int64_t ldd, float *part, int64_t ncols_dst) {
-  k_mmq_kq_moe<WT, TMv><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits,
-                                             d, ldd, part, ncols_dst);
+  k_mmq_kq_moe<WT, TMv, S16><<<grid, 256, 0, s>>>(w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb,
+                                                  splits, d, ldd, part, ncols_dst);
 }
 
 template <bool F32D>
@@ -1339,6 +1340,46 @@ void mmq_moe(int type, bool q8_0, void *tmp_fixup, const void *x, const void *y,
                     stride_col_dst, num_experts, ncols_max, nsm, stream, who);
 }
 
+// launch_mmq_gguf_{q4_k,q5_k}_moe_q8k: the grouped prefill over `_q8k` tiles, with mmq_moe_t's tile and split choice
+void mmq_moe_q8k(int type, void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,
+                 const int32_t *bounds, void *dst, int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst,
+                 int64_t stride_row_x, int64_t stride_col_dst, int64_t num_experts, int64_t ncols_max, int nsm,
+                 void *stream, const char *who) {
+  if (!check_mmq(who, type, x, ncols_x, nrows_x, stride_row_x) || !check_act_bytes(who, ncols_x, ncols_dst, 292))
+    return;
+  if (num_experts <= 0 || ncols_max < 0 || ncols_dst < 0 || stride_col_dst < nrows_x || num_experts > 65535) {
+    qmm_set_error("%s: num_experts=%lld ncols_max=%lld ncols_dst=%lld stride_col_dst=%lld", who,
+                  (long long)num_experts, (long long)ncols_max, (long long)ncols_dst, (long long)stride_col_dst);
+    return;
+  }
+  if (ncols_max == 0 || ncols_dst == 0) return;
+  const int64_t nsb = (ncols_x + 255) / 256;
+  const int64_t w_row_bytes = stride_row_x * (int64_t)qmm_type_size(type);
+  const int64_t expert_bytes = nrows_x * w_row_bytes;
+  const ActTile a = act_tile(y, ncols_dst, nsb);
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *w = (const uint8_t *)x;
+  float *d = (float *)dst;
+  const bool small = (QMM_MOE_SMALL_AVG ? (ncols_dst + num_experts - 1) / num_experts : ncols_max) <= 32 ||
+                     type == QMM_TYPE_Q5K;
+  const int64_t ntiles = (nrows_x + BN - 1) / BN;
+  const int64_t mt = small ? (ncols_max + 31) / 32 : (ncols_max + 63) / 64;
+  const int64_t busy = ntiles * (small ? (ncols_dst + 31) / 32 : (ncols_dst + 63) / 64);
+  const int64_t splits = k_splits(busy, nsb, ncols_dst, nrows_x, tmp_fixup, nsm);
+  float *part = splits > 1 ? (float *)tmp_fixup : nullptr;
+  const dim3 gridk((unsigned)(ntiles * splits), (unsigned)mt, (unsigned)num_experts);
+  if (type == QMM_TYPE_Q5K)
+    kq_moe<wq5k, 1, true>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                          stride_col_dst, part, ncols_dst);
+  else if (small)
+    kq_moe<wq4k, 1, true>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                          stride_col_dst, part, ncols_dst);
+  else
+    kq_moe<wq4k, 2, true>(gridk, s, w, expert_bytes, nrows_x, w_row_bytes, a, bounds, ids_dst, nsb, splits, d,
+                          stride_col_dst, part, ncols_dst);
+  if (part) split_sum<out_f32>(part, splits, ncols_dst, nrows_x, d, stride_col_dst, ids_dst, s);
+}
+
 }  // namespace
 
 // launch_mmq_gguf_<t><sfx> and launch_mmq_gguf_<t>_moe<sfx> (sfx _q8_0: Q8_0-block activations)
@@ -1380,6 +1421,15 @@ QMM_DEFINE_MMQ_ENTRIES(q5_0, QMM_TYPE_Q5_0, true, _q8_0)
     (void)cc, (void)smpbo, (void)warp_size;                                                                        \
     mmq_q8k(TYPE, tmp_fixup, x, y, dst, ncols_x, nrows_x, ncols_y, stride_row_x, stride_col_dst, nsm, type_dst,     \
             stream, "mmq_" #t "_q8k");                                                                             \
+  }                                                                                                                \
+  void launch_mmq_gguf_##t##_moe_q8k(void *tmp_fixup, const void *x, const void *y, const int32_t *ids_dst,       \
+                                     const int32_t *expert_bounds, void *dst, int64_t ncols_x, int64_t nrows_x,    \
+                                     int64_t ncols_dst, int64_t stride_row_x, int64_t stride_col_dst,              \
+                                     int64_t num_experts, int64_t ncols_max, int cc, int nsm, int64_t smpbo,       \
+                                     int warp_size, void *stream) {                                                \
+    (void)cc, (void)smpbo, (void)warp_size;                                                                        \
+    mmq_moe_q8k(TYPE, tmp_fixup, x, y, ids_dst, expert_bounds, dst, ncols_x, nrows_x, ncols_dst, stride_row_x,     \
+                stride_col_dst, num_experts, ncols_max, nsm, stream, "mmq_" #t "_moe_q8k");                        \
   }
 QMM_DEFINE_MMQ_Q8K(q4_k, QMM_TYPE_Q4K)
 QMM_DEFINE_MMQ_Q8K(q5_k, QMM_TYPE_Q5K)

@@ -173,9 +173,9 @@ mmq_moe_fn prefill_matmul_moe(GgmlDType w) {
     case GgmlDType::Q8_0: return launch_mmq_gguf_q8_0_moe_q8_0;
     case GgmlDType::Q4_0: return launch_mmq_gguf_q4_0_moe_q8_0;
     case GgmlDType::Q5_0: return launch_mmq_gguf_q5_0_moe_q8_0;
-    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe;
+    case GgmlDType::Q4K: return launch_mmq_gguf_q4_k_moe_q8k;
     case GgmlDType::Q6K: return launch_mmq_gguf_q6_k_moe;
-    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k_moe;
+    case GgmlDType::Q5K: return launch_mmq_gguf_q5_k_moe_q8k;
     default: throw Error("MoE: unsupported weight type");
   }
 }
@@ -605,10 +605,10 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   const size_t o_src = c.add((size_t)pairs * 4);
   const size_t o_cnt = c.add((size_t)E * 4);
   const size_t o_cur = c.add((size_t)E * 4);
-  const size_t o_x = c.add((size_t)(pairs * kp1 / 256 * tile_bytes_per_256(tg)));
+  const size_t o_x = c.add((size_t)(pairs * kp1 / 256 * prefill_tile_bytes_per_256(tg)));
   const size_t o_g = c.add((size_t)(pairs * inter * 4));
   const size_t o_u = c.add((size_t)(pairs * inter * 4));
-  const size_t o_mq = c.add((size_t)(pairs * kp2 / 256 * tile_bytes_per_256(td)));
+  const size_t o_mq = c.add((size_t)(pairs * kp2 / 256 * prefill_tile_bytes_per_256(td)));
   const size_t o_y = c.add((size_t)(pairs * hidden * 4));
   const int nsm = device_cus(ordinal);
   const size_t o_fix = c.add(fixup_bytes(nsm));
@@ -617,8 +617,8 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
   launch_moe_dispatch(ids, bounds, tok, src, (int)pairs, (int)E, (int)topk, (int32_t *)(ws + o_cnt),
                       (int32_t *)(ws + o_cur), stream);
   abi_check("MoE grouped (dispatch)");
-  (act_q8_0(tg) ? launch_mmq_quantize_q8_0 : launch_mmq_quantize_q8_1_DS4)(
-      xs, src, ws + o_x, 0, hidden, hidden, hidden * tokens, hidden * tokens, kp1, pairs, 1, 1, stream);
+  prefill_quantizer(tg)(xs, src, ws + o_x, 0, hidden, hidden, hidden * tokens, hidden * tokens, kp1, pairs, 1, 1,
+                        stream);
   abi_check("MoE grouped (quantize x)");
   for (int which = 0; which < 2; which++) {
     const QTensor &w = which == 0 ? *gate_ : *up_;
@@ -627,9 +627,10 @@ void MoeExperts::forward(const float *xs, int64_t tokens, const int32_t *ids, co
                            stream);
     abi_check("MoE grouped (gate/up)");
   }
-  (act_q8_0(td) ? launch_mmq_quantize_glu_q8_0_f32 : launch_mmq_quantize_glu_q8_1_DS4_f32)(
-      (const float *)(ws + o_g), (const float *)(ws + o_u), tok, ws + o_mq, inter, inter, kp2, pairs, activation_,
-      stream);
+  (act_q8_0(td)      ? launch_mmq_quantize_glu_q8_0_f32
+   : prefill_q8k(td) ? launch_mmq_quantize_glu_q8k_f32
+                     : launch_mmq_quantize_glu_q8_1_DS4_f32)((const float *)(ws + o_g), (const float *)(ws + o_u), tok,
+                                                             ws + o_mq, inter, inter, kp2, pairs, activation_, stream);
   abi_check("MoE grouped (GLU + quantize)");
   // down, then the weighted sum over each token's routes as its own launch: folded into the down projection (a
   // counter per token and column tile, the workgroup completing it summing the routes) it measured 381 us against

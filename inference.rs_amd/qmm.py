@@ -544,9 +544,11 @@ def qmatmul_prefill(wtype: int, w, x, n: int, out_dtype=None, q8_1=None, q8k=Fal
 
 
 def mmq_moe(wtype: int, w, y, ids_dst, expert_bounds, n_experts: int, k: int, n: int, ncols_dst: int,
-            ncols_max: int, out, tmp_fixup=True, q8_1=None):
+            ncols_max: int, out, tmp_fixup=True, q8_1=None, q8k=False):
+    """Expert-grouped prefill matmul through launch_mmq_gguf_<t>_moe (or _q8_0, or with q8k the Q4_K / Q5_K
+    _moe_q8k entries over `_q8k` tiles)."""
     fx, nsm = fixup(w.device) if tmp_fixup else (None, 256)
-    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}_moe{_sfx(wtype, q8_1)}")(
+    getattr(lib(), f"launch_mmq_gguf_{tname(wtype)}_moe{'_q8k' if q8k else _sfx(wtype, q8_1)}")(
         _ptr(fx), _ptr(w), _ptr(y), _ptr(ids_dst), _ptr(expert_bounds), _ptr(out), k, n, ncols_dst,
         k // BLOCK_SIZE[wtype], n, n_experts, ncols_max, 0, nsm, 160 * 1024, 64, _stream())
     check()

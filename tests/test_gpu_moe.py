@@ -123,6 +123,13 @@ def test_grouped_prefill_matches_the_oracle(gtype, case):
     ncols_max = int(counts.max().item())
     qmm.mmq_moe(gtype, to_dev(wq), y, tok, bounds, E, k, n, tokens * topk, ncols_max, out)
     assert_parity(out.cpu().numpy(), want)
+    if gtype in (O.Q4K, O.Q5K):
+        # launch_mmq_gguf_<t>_moe_q8k over `_q8k` tiles: the min term's sums are exact integers on both tile forms,
+        # so the same bits
+        y16, _ = qmm.quantize_prefill(gtype, to_dev(x), ids=src, q8k=True)
+        out16 = torch.full((tokens * topk, n), float("nan"), device=DEV)
+        qmm.mmq_moe(gtype, to_dev(wq), y16, tok, bounds, E, k, n, tokens * topk, ncols_max, out16, q8k=True)
+        assert np.array_equal(out16.cpu().numpy().view(np.uint32), out.cpu().numpy().view(np.uint32)), case
 
 
 # Q6_K experts of an odd row count with an odd superblock count per row: every other expert starts 2 bytes past a
