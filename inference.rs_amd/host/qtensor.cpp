@@ -212,18 +212,17 @@ indexed_fn indexed_moe(GgmlDType w) {
   }
 }
 
-// activation geometry of a weight type (GgmlType::VecDotType): Q8_0 blocks of 34 bytes per 32 values, or Q8_1 slots of
-// 288 bytes per 256 (qmm_block_q8ks); stride_col_y counts 32-value blocks either way; prefill tiles 272 or 276 bytes
-// per 256 values
+// decode activation geometry of a weight type (GgmlType::VecDotType): Q8_0 blocks of 34 bytes per 32 values, or Q8_1
+// slots of 288 bytes per 256 (qmm_block_q8ks); stride_col_y counts 32-value blocks either way
 bool act_q8_0(GgmlDType w) { return qmm_vec_dot_type((int)w) == QMM_TYPE_Q8_0; }
 int64_t act_block(GgmlDType w) { return act_q8_0(w) ? 32 : 256; }
 int64_t act_row_bytes(GgmlDType w, int64_t kp) { return act_q8_0(w) ? kp / 32 * 34 : kp / 256 * 288; }
-int64_t tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : 276; }
 
-// the plain prefill matmul's activations (prefill_matmul): Q8_0 tiles for the 32-value types, the `_q8k` tiles (f16
-// sums of 16, which the min term reads as they are) for Q4_K and Q5_K, the reference-named Q8_K tiles otherwise
+// prefill activations (prefill_matmul, prefill_matmul_moe and their quantizers): Q8_0 tiles for the 32-value types (272
+// bytes per 256 values), the `_q8k` tiles (f16 sums of 16, which the min term reads as they are; 292) for Q4_K and
+// Q5_K, the reference-named Q8_K tiles (276) for Q6_K
 bool prefill_q8k(GgmlDType w) { return w == GgmlDType::Q4K || w == GgmlDType::Q5K; }
-int64_t prefill_tile_bytes_per_256(GgmlDType w) { return prefill_q8k(w) ? 292 : tile_bytes_per_256(w); }
+int64_t prefill_tile_bytes_per_256(GgmlDType w) { return act_q8_0(w) ? 272 : prefill_q8k(w) ? 292 : 276; }
 typedef void (*tile_quant_fn)(const void *, const int32_t *, void *, int, int64_t, int64_t, int64_t, int64_t, int64_t,
                               int64_t, int64_t, int64_t, void *);
 tile_quant_fn prefill_quantizer(GgmlDType w) {
