@@ -618,15 +618,24 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
 // loads blocks 4g .. 4g + 3 with 16-byte loads, decodes both 16-value halves of each, and one v_permlane32_swap per
 // dword trades halves with the partner lane, so that half g of all eight blocks ends in lane half g (the MFMA B
 // layout used by the Q8_0 kernel above).  Per block, the scale products da * dw (exact in f32: two f16 factors)
-// come from an f32 outer-product MFMA in the accumulator layout, leaving one convert and one FMA per output.
+// come from an outer-product MFMA in the accumulator layout, leaving one convert and one FMA per output: an f16 MFMA
+// on the scales' f16 bits (half the matrix-core cycles of the f32 one; the f16 MFMA keeps subnormal inputs, so the
+// products are the same bits) over Q8_0 activation tiles where the weight type's kHalfScales says so, else the f32
+// MFMA.
 __device__ __forceinline__ uint32_t run_dw(const uint32_t *R, int o) {  // dword at byte offset o of the run
   return o % 4 == 0 ? R[o / 4] : __builtin_amdgcn_alignbyte(R[o / 4 + 1], R[o / 4], (uint32_t)(o % 4));
 }
 __device__ __forceinline__ uint32_t run_u16(const uint32_t *R, int o) { return (R[o / 4] >> (8 * (o % 4))) & 0xffffu; }
 
 // decode(R, i, d, h0, h1): block i of the run: f16 scale bits d, values 0..15 (h0) and 16..31 (h1) as signed bytes
+// kSets: weight register sets (two: the weights of s + 2 are in flight while s is computed; one: those of s + 1).
+// Q8_0's 34-dword runs take one, which leaves room for the f16 scale MFMA's operands: with two sets and the f16 MFMA
+// the kernel spilled (172.7 us at M = 512, 14336x4096), with two and the f32 MFMA it took 152.9 us, with one and the
+// f16 MFMA 137.1 us.  Q4_0 / Q5_0 keep two (one: 114.4 -> 122.5 us, 127.5 -> 138.1 us).
 struct wr_q8_0 {
   static constexpr int kBytes = 34, kDwords = 34;  // run: 136 bytes
+  static constexpr bool kHalfScales = true;
+  static constexpr int kSets = 1;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
     const int o = 34 * i;
@@ -640,6 +649,8 @@ struct wr_q8_0 {
 };
 struct wr_q4_0 {
   static constexpr int kBytes = 18, kDwords = 18;  // run: 72 bytes
+  static constexpr bool kHalfScales = true;
+  static constexpr int kSets = 2;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
     const int o = 18 * i;
@@ -655,6 +666,8 @@ struct wr_q4_0 {
 };
 struct wr_q5_0 {
   static constexpr int kBytes = 22, kDwords = 22;  // run: 88 bytes
+  static constexpr bool kHalfScales = true;
+  static constexpr int kSets = 2;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
     const int o = 22 * i;
@@ -741,14 +754,26 @@ __device__ __forceinline__ v16f mfma_f32x2(float a, float b) {
 }
 
 // Group k = (tile k / 8, block j = k % 8): the integer block dot and the scale outer product on A fragment av.
-// Block j's scales live in lane half j / 4; the other half contributes 0 * 0 at k = 1.
-__device__ __forceinline__ void b32_group(v4i av, const v4i (&b)[8], const float (&da)[4], const float (&dw)[4],
-                                          int g, int k, v16i &acc, v16f &sc) {
+// Block j's scales live in lane half j / 4; the other half contributes zeros.  F32S: the scales as f32 (da, dw) and
+// the f32 MFMA (k = g); else their f16 bits, two to a dword (blocks 2p and 2p + 1 of the half in dword p of dah, dwh),
+// and the f16 MFMA (k = 4g, the rest of each half zero).
+template <bool F32S>
+__device__ __forceinline__ void b32_group(v4i av, const v4i (&b)[8], const float (&da)[4], const uint32_t (&dah)[2],
+                                          const float (&dw)[4], const uint32_t (&dwh)[2], int g, int k, v16i &acc,
+                                          v16f &sc) {
   const int j = k & 7, i = j & 3;
   const bool mine = g == (j >> 2);
   order_point(av);
   acc = mfma_i8(av, b[j], (v16i){});
-  sc = mfma_f32x2(mine ? da[i] : 0.0f, mine ? dw[i] : 0.0f);
+  if constexpr (F32S) {
+    sc = mfma_f32x2(mine ? da[i] : 0.0f, mine ? dw[i] : 0.0f);
+  } else {
+    const uint32_t a = (i & 1) ? dah[i >> 1] >> 16 : dah[i >> 1] & 0xffffu;
+    const uint32_t w = (i & 1) ? dwh[i >> 1] >> 16 : dwh[i >> 1] & 0xffffu;
+    const u32x2 A = {mine ? a : 0u, 0u}, B = {mine ? w : 0u, 0u};
+    sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, A), __builtin_bit_cast(v4h, B), (v16f){}, 0, 0,
+                                              0);
+  }
 }
 
 // One workgroup: 4 waves x 32 weight rows (BN = 128) against BMt = 32 TM activation rows, superblocks [sb0, sb1).
@@ -784,23 +809,38 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
 
   AD dma;
   dma.init(wave, lane, m0, rows, nsb);
-  // two weight register sets: step s decodes set s % 2 into B operands, then reloads it with superblock s + 2
-  uint32_t raw[2][WR::kDwords];
-  auto issue = [&](int64_t sb, int u, int v) {
+  // WR::kSets weight register sets: with two, step s decodes set s % 2 into B operands, then reloads it with
+  // superblock s + 2; with one, it reloads the set with superblock s + 1
+  constexpr int kSets = WR::kSets;
+  static_assert(kSets == 1 || kSets == 2, "one or two weight sets");
+  uint32_t raw[kSets][WR::kDwords];
+  auto issue_a = [&](int64_t sb, int u) {
     __builtin_amdgcn_sched_barrier(0);
     dma.issue(ra, lds + u * AD::STAGE, wave, lane, (uint32_t)(sb * rows));
-    RL::load(rw, wrun + (uint32_t)(sb * 8 * WR::kBytes), raw[v]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto issue_w = [&](int64_t sb, int v) {
+    __builtin_amdgcn_sched_barrier(0);
+    RL::load(rw, wrun + (uint32_t)(sb * 8 * WR::kBytes), raw[v % kSets]);
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // the scales take the f32 MFMA with Q8_K tiles (an f32 da) or where the weight type asks for it
+  constexpr bool F32S = F32D || !WR::kHalfScales;
   v4i b[8];
   float dw[4];
+  uint32_t dwh[2];
   auto decode = [&](const uint32_t (&R)[WR::kDwords]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       uint32_t d, h0[4], h1[4];
       WR::decode(R, i, d, h0, h1);
-      dw[i] = f16_bits_to_f32(d);
+      if constexpr (F32S)
+        dw[i] = f16_bits_to_f32(d);
+      else if (i & 1)
+        dwh[i >> 1] |= d << 16;
+      else
+        dwh[i >> 1] = d;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         swap_lane_halves(h0[q], h1[q]);
@@ -819,6 +859,7 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
   auto compute = [&](const uint8_t *slot) {
     // this lane's activation rows 32t + li: scales of blocks 4g .. 4g + 3 (Q8_K tiles: the row's one scale)
     float da[TM][4];
+    uint32_t dah[TM][2];
 #pragma unroll
     for (int t = 0; t < TM; t++) {
       if constexpr (F32D) {
@@ -826,8 +867,12 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
         da[t][0] = da[t][1] = da[t][2] = da[t][3] = d;
       } else {
         const uint2 d4 = *(const uint2 *)(slot + AD::QS + 16 * (32 * t + li) + 8 * g);
-        da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
-        da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
+        if constexpr (F32S) {
+          da[t][0] = f16_bits_to_f32(d4.x & 0xffffu), da[t][1] = f16_bits_to_f32(d4.x >> 16);
+          da[t][2] = f16_bits_to_f32(d4.y & 0xffffu), da[t][3] = f16_bits_to_f32(d4.y >> 16);
+        } else {
+          dah[t][0] = d4.x, dah[t][1] = d4.y;
+        }
       }
     }
     auto frag = [&](int k) { return *(const v4i *)(slot + 8192 * (k >> 3) + qoff[k & 7]); };
@@ -836,10 +881,12 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
     v4i av[2];
     av[0] = frag(0);
     av[1] = frag(1);
-    b32_group(av[0], b, da[0], dw, g, 0, acc[0], sc[0]);
+    b32_group<F32S>(av[0], b, da[0], dah[0], dw, dwh, g, 0, acc[0], sc[0]);
 #pragma unroll
     for (int k = 0; k < 8 * TM; k++) {
-      if (k + 1 < 8 * TM) b32_group(av[(k + 1) & 1], b, da[(k + 1) >> 3], dw, g, k + 1, acc[(k + 1) & 1], sc[(k + 1) & 1]);
+      if (k + 1 < 8 * TM)
+        b32_group<F32S>(av[(k + 1) & 1], b, da[(k + 1) >> 3], dah[(k + 1) >> 3], dw, dwh, g, k + 1, acc[(k + 1) & 1],
+                        sc[(k + 1) & 1]);
       if (k + 2 < 8 * TM) av[k & 1] = frag(k + 2);
       const int t = k >> 3;
 #pragma unroll
@@ -848,19 +895,38 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
     }
   };
 
-  // u = (s - sb0) % 3 selects the LDS slot, v = (s - sb0) % 2 the weight set; both constant after unrolling
+  // u = (s - sb0) % 3 selects the LDS slot, v = (s - sb0) % 2 the weight set; both constant after unrolling.  Two
+  // sets: step s waits for the activations and weights of s (issued together two steps earlier; those of s + 1 may
+  // still be in flight), decodes, and issues both for s + 2.  One set: step s waits for its weights (issued in step
+  // s - 1) and activations (step s - 2), decodes, then issues the weights of s + 1 and the activations of s + 2, in
+  // that order, so that only the newest activations may still be in flight at the next step's wait.  Past the end
+  // the last superblock is loaded again, into places that are not read, so every wait count stays exact.
   auto step = [&](int64_t s, int u, int v) {
     __builtin_amdgcn_sched_barrier(0);
-    dma_barrier<AD::kLoads + RL::kLoads>();
-    decode(raw[v]);
-    const int64_t sn = s + 2 < sb1 ? s + 2 : sb1 - 1;
-    issue(sn, (u + 2) % 3, v);
+    dma_barrier<kSets == 2 ? AD::kLoads + RL::kLoads : AD::kLoads>();
+    decode(raw[v % kSets]);
+    if constexpr (kSets == 2) {
+      const int64_t sn = s + 2 < sb1 ? s + 2 : sb1 - 1;
+      issue_a(sn, (u + 2) % 3);
+      issue_w(sn, v);
+    } else {
+      issue_w(s + 1 < sb1 ? s + 1 : sb1 - 1, 0);
+      issue_a(s + 2 < sb1 ? s + 2 : sb1 - 1, (u + 2) % 3);
+    }
     if (s < sb1) compute(lds + u * AD::STAGE);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue(sb0, 0, 0);
-  issue(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1, 1);
+  if constexpr (kSets == 2) {
+    issue_a(sb0, 0);
+    issue_w(sb0, 0);
+    issue_a(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1);
+    issue_w(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1);
+  } else {
+    issue_w(sb0, 0);
+    issue_a(sb0, 0);
+    issue_a(sb0 + 1 < sb1 ? sb0 + 1 : sb1 - 1, 1);
+  }
   for (int64_t sb = sb0; sb < sb1; sb += 6) {
     step(sb, 0, 0);
     step(sb + 1, 1, 1);

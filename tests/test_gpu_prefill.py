@@ -86,6 +86,27 @@ def test_mmq_matches_the_cpu_qmatmul(gtype, m, n, k):
     assert_parity(got, want, terms(gtype, x, wq, n), what=f"t{gtype} m{m} n{n} k{k}")
 
 
+@pytest.mark.parametrize("gtype", [O.Q8_0, O.Q4_0, O.Q5_0])
+def test_mmq_subnormal_block_scales(gtype):
+    """The 32-value kernel's scale products (an f16 MFMA for Q4_0 / Q5_0) with f16 block scales in the subnormal range
+    (below 6.1e-5) on both sides: activation rows of magnitude 1e-3 .. 1e-6 and weight rows of 1e-3 .. 1e-4 of the
+    usual; rows whose every scale is subnormal must still match the CPU QMatMul to the relative bound."""
+    m, n, k = 64, 96, 1024
+    rng = np.random.default_rng(gtype + 77)
+    w = weights(rng, n, k)
+    w[::3] *= 1e-3
+    w[1::5] *= 1e-4
+    x = acts(rng, m, k)
+    x[::2] *= 1e-3
+    x[1::4] *= 1e-5
+    x[3::8] *= 1e-6
+    wq = O.quantize(gtype, w)
+    want = O.matmul(gtype, x, wq, n)
+    got = qmm.qmatmul_prefill(gtype, to_dev(wq), to_dev(x), n).cpu().numpy()
+    assert np.count_nonzero(want) > 0.75 * want.size  # (scales below f16's range round to zero, in both)
+    assert_parity(got, want, terms(gtype, x, wq, n), what=f"t{gtype} subnormal scales")
+
+
 # (gtype, m, n, k): f16 / bf16 outputs of every prefill kernel -- the K-quant kernel (Q4_K, Q6_K, Q5_K), the pipelined
 # 32-value kernel (Q8_0, Q4_0, Q5_0 with K a multiple of 256) and the simple Q8_0-layout kernel (K = 1056); the 17-row
 # cases take split K, whose plane sum rounds to the output type once; Q6_K at 130 rows takes the 128-row tile with its
