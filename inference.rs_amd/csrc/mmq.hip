@@ -222,7 +222,9 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   auto act_slot = [&](int u) { return lds + u * (kWS == 2 ? STG : AS::STAGE); };
   auto w_slot = [&](int u) { return kWS == 2 ? lds + u * STG + AS::STAGE : lds + 2 * AS::STAGE; };
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  // (the wave index as a scalar: the LDS addresses of the DMA loads, which go through M0, are then scalar arithmetic)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 5,
+            li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
   const int64_t nlast = (nrows_w - n0 < BNt ? nrows_w - n0 : BNt) - 1;
   const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;  // row within the tile, clamped
@@ -546,7 +548,9 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
   __shared__ __attribute__((aligned(16))) uint8_t s_qs[BM * QS_STRIDE];
   __shared__ float s_da[BM * 9];  // 8 block scales per row (stride 9 against bank conflicts)
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  // (the wave index as a scalar: the LDS addresses of the DMA loads, which go through M0, are then scalar arithmetic)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 5,
+            li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
   const int64_t n_ld = n < nrows_w ? n : nrows_w - 1;
   const uint8_t *wrow = W + n_ld * w_row_bytes;
@@ -789,7 +793,9 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
   typedef RunLoad<WR> RL;
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * AD::STAGE];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  // (the wave index as a scalar: the LDS addresses of the DMA loads, which go through M0, are then scalar arithmetic)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 5,
+            li = lane & 31;
   const int64_t n = n0 + 32 * wave + li;
   const int64_t nlast = (nrows_w - n0 < BN ? nrows_w - n0 : BN) - 1;
   const int64_t nl = 32 * wave + li < nlast ? 32 * wave + li : nlast;
