@@ -213,8 +213,10 @@ __device__ __forceinline__ void mmq_kq_tile(const uint8_t *__restrict__ W, int64
   // per CU, measured slower than two at two workgroups.)
   constexpr int kWS = 2 * STG <= (TM == 2 ? 80 : 160) * 1024 ? 2 : 1;
   constexpr int kPS = kRowMajor ? 16 : 16 * BNt;  // LDS bytes from one piece of a row to its next
-  // (only where two workgroups share each SIMD: at one wave per SIMD it measured no gain)
-  constexpr bool kPrio = kLw && TM == 2;
+  // (only where two workgroups share each SIMD: at one wave per SIMD it measured no gain.  On 32-row tiles for the
+  // two-plane Q4_K: M = 32, 14336x4096 18.3 -> 16.7 us, the 64-token MoE step 260 -> 252 us; Q5_K's three planes at
+  // 32-row tiles measured slower with it, M = 512 135.8 -> 141.5 us)
+  constexpr bool kPrio = kLw && (TM == 2 || (TM == 1 && WT::kPlanes == 2));
   static_assert(!kLw || AS::STAGE % 16 == 0, "16-byte aligned stages");
   static_assert(!kLw || kRowMajor || 64 * NW == 2 * BNt, "two pieces of every row per DMA round");
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLw ? 2 * AS::STAGE + kWS * WST : 3 * AS::STAGE];
