@@ -140,12 +140,12 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8k_tiles(const typename I
   if (r >= ne1) return;  // whole wave
   const int64_t nsb = ne0 / 256, sb = blockIdx.y;
   const int64_t src = (ids ? ids[r] : r) * s01;
-  float v[4];
+  // one vector load per lane for each input where the four values are in the row and aligned (load4)
+  float g[4], u[4], v[4];
+  load4<In>(gate + src, sb * 256 + lane * 4, ne00, g);
+  load4<In>(up + src, sb * 256 + lane * 4, ne00, u);
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int64_t k = sb * 256 + lane * 4 + i;
-    v[i] = k < ne00 ? glu_product<In>(In::load(gate, src + k), In::load(up, src + k), activation) : 0.0f;
-  }
+  for (int i = 0; i < 4; i++) v[i] = sb * 256 + lane * 4 + i < ne00 ? glu_product<In>(g[i], u[i], activation) : 0.0f;
   q8k_wave(v, lane, S16 ? q8k_tile16_dst(vy, ne1, nsb, sb, r) : q8k_tile_dst(vy, ne1, nsb, sb, r));
 }
 
@@ -162,12 +162,12 @@ __global__ __launch_bounds__(256) void k_quantize_glu_q8_0_tiles(const float *__
   const int64_t nsb = ne0 / 256;
   const int64_t sb = b / (ne1 * 8), r = (b / 8) % ne1, j = b % 8;
   const int64_t src = valid ? (ids ? ids[r] : r) * s01 : 0;
-  float v[4];
+  const int64_t k0 = sb * 256 + j * 32 + (lane & 7) * 4;
+  float g[4], u[4], v[4];
+  load4<in_f32>(gate + src, k0, valid ? ne00 : 0, g);
+  load4<in_f32>(up + src, k0, valid ? ne00 : 0, u);
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int64_t k = sb * 256 + j * 32 + (lane & 7) * 4 + i;
-    v[i] = (valid && k < ne00) ? glu_act(activation, gate[src + k]) * up[src + k] : 0.0f;
-  }
+  for (int i = 0; i < 4; i++) v[i] = (valid && k0 + i < ne00) ? glu_act(activation, g[i]) * u[i] : 0.0f;
   int8_t *qs = (int8_t *)(vy + (sb * ne1 + r) * 256 + j * 32);
   uint16_t *d = (uint16_t *)(vy + nsb * ne1 * 256) + (sb * ne1 + r) * 8 + j;
   q8_0_group(v, lane & 7, qs, d, valid);
