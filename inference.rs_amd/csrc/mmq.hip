@@ -626,8 +626,7 @@ __device__ __forceinline__ void mmq_q8_0_tile(const uint8_t *__restrict__ W, int
 // layout used by the Q8_0 kernel above).  Per block, the scale products da * dw (exact in f32: two f16 factors)
 // come from an outer-product MFMA in the accumulator layout, leaving one convert and one FMA per output: an f16 MFMA
 // on the scales' f16 bits (half the matrix-core cycles of the f32 one; the f16 MFMA keeps subnormal inputs, so the
-// products are the same bits) over Q8_0 activation tiles where the weight type's kHalfScales says so, else the f32
-// MFMA.
+// products are the same bits) over Q8_0 activation tiles, the f32 MFMA over Q8_K tiles (an f32 activation scale).
 __device__ __forceinline__ uint32_t run_dw(const uint32_t *R, int o) {  // dword at byte offset o of the run
   return o % 4 == 0 ? R[o / 4] : __builtin_amdgcn_alignbyte(R[o / 4 + 1], R[o / 4], (uint32_t)(o % 4));
 }
@@ -640,7 +639,6 @@ __device__ __forceinline__ uint32_t run_u16(const uint32_t *R, int o) { return (
 // f16 MFMA 137.1 us.  Q4_0 / Q5_0 keep two (one: 114.4 -> 122.5 us, 127.5 -> 138.1 us).
 struct wr_q8_0 {
   static constexpr int kBytes = 34, kDwords = 34;  // run: 136 bytes
-  static constexpr bool kHalfScales = true;
   static constexpr int kSets = 1;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
@@ -655,7 +653,6 @@ struct wr_q8_0 {
 };
 struct wr_q4_0 {
   static constexpr int kBytes = 18, kDwords = 18;  // run: 72 bytes
-  static constexpr bool kHalfScales = true;
   static constexpr int kSets = 2;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
@@ -672,7 +669,6 @@ struct wr_q4_0 {
 };
 struct wr_q5_0 {
   static constexpr int kBytes = 22, kDwords = 22;  // run: 88 bytes
-  static constexpr bool kHalfScales = true;
   static constexpr int kSets = 2;
   static __device__ __forceinline__ void decode(const uint32_t *R, int i, uint32_t &d, uint32_t (&h0)[4],
                                                 uint32_t (&h1)[4]) {
@@ -833,8 +829,8 @@ __device__ __forceinline__ void mmq_b32_tile(const uint8_t *__restrict__ W, int6
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // the scales take the f32 MFMA with Q8_K tiles (an f32 da) or where the weight type asks for it
-  constexpr bool F32S = F32D || !WR::kHalfScales;
+  // the scales take the f32 MFMA with Q8_K tiles (an f32 da), else the f16 one
+  constexpr bool F32S = F32D;
   v4i b[8];
   float dw[4];
   uint32_t dwh[2];
