@@ -139,8 +139,9 @@ def mixtral():
 
 def test_mixtral_moe_grouped_projections(mixtral):
     """Each projection through dispatch -> gathered prefill quantization -> expert-grouped matmul
-    (launch_mmq_gguf_q4_k_moe), as the grouped route of the MoE block runs it, against the oracle's matmul per route
-    at full shape; the down projection takes the oracle's own SiLU(gate) * up intermediate."""
+    (launch_mmq_gguf_q4_k_moe, and launch_mmq_gguf_q4_k_moe_q8k over `_q8k` tiles, the form the MoE block's grouped route
+    runs) against the oracle's matmul per route at full shape; the down projection takes the oracle's own
+    SiLU(gate) * up intermediate."""
     mats, ids, w, x = mixtral
     u32 = ids.astype(np.uint32)
     g = O.indexed_moe(O.Q4K, mats[0].reshape(E, -1), E, INTER, HIDDEN, x[:, None], u32).reshape(-1, INTER)
@@ -156,8 +157,18 @@ def test_mixtral_moe_grouped_projections(mixtral):
             ("down", mats[2], mid, tok, HIDDEN, INTER, d)):
         y, _ = qmm.quantize_prefill(O.Q4K, dev(xin), ids=rows_src)
         out = torch.full((routes, n), float("nan"), device="cuda")
-        qmm.mmq_moe(O.Q4K, dev(m), y, tok, bounds, E, k, n, routes, ncols_max, out)
+        md = dev(m)
+        qmm.mmq_moe(O.Q4K, md, y, tok, bounds, E, k, n, routes, ncols_max, out)
         assert_parity(out.cpu().numpy(), want, what=f"grouped {name}")
+        # the `_q8k` entry the host route takes, held to the oracle and to itself run again (the down projection splits
+        # K in two here, summed in split order)
+        y16, _ = qmm.quantize_prefill(O.Q4K, dev(xin), ids=rows_src, q8k=True)
+        o1, o2 = (torch.full((routes, n), float("nan"), device="cuda") for _ in range(2))
+        qmm.mmq_moe(O.Q4K, md, y16, tok, bounds, E, k, n, routes, ncols_max, o1, q8k=True)
+        qmm.mmq_moe(O.Q4K, md, y16, tok, bounds, E, k, n, routes, ncols_max, o2, q8k=True)
+        a = o1.cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), o2.cpu().numpy().view(np.uint32)), f"grouped {name} (q8k) repeat"
+        assert_parity(a, want, what=f"grouped {name} (q8k)")
 
 
 @pytest.mark.parametrize("tokens", [TOKENS, 8])
