@@ -69,6 +69,8 @@ CASES = [
     # 32-value types with K a multiple of 256: the run-loading kernel, 32-row tiles with K split across
     # workgroups (partial planes summed in split order), 64-row tiles, a ragged last weight tile
     (O.Q8_0, 17, 300, 4096), (O.Q4_0, 20, 130, 2048), (O.Q5_0, 64, 257, 1280), (O.Q8_0, 300, 129, 768),
+    # one superblock per row: every step of the ring past the first loads the same superblock again
+    (O.Q8_0, 33, 64, 256), (O.Q4_0, 70, 96, 256),
     # Q5_K: the K-quant kernel with the fifth-bit plane (32-row tiles with split K, ragged edges)
     (O.Q5K, 40, 64, 512), (O.Q5K, 130, 200, 1024), (O.Q5K, 17, 300, 4096), (O.Q5K, 255, 129, 256),
 ]
