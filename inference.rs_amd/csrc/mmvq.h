@@ -290,6 +290,66 @@ __global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx,
   }
 }
 
+// Wide rows at one column, four waves to a row: wave p of a workgroup takes units [64 p, 64 p + 64) of every row it
+// walks (one per lane; a lane past the row's units reads through an offset past the row's buffer, zeros with no
+// traffic), holds that activation unit in registers for the whole launch, and walks the workgroup's rows
+// b, b + G, ... (G workgroups, at most kP4Rows of them) with two in flight in place, as row_pairs does.  Each wave leaves
+// its partial sum of a row in LDS; after one barrier the workgroup adds the four in wave order and stores the rows.
+// Measured on MI355X at 4096 x 14336, b = 1, against k_mmvq_p / k_mmvq_p2: Q6_K 14.3 -> 13.5 us, Q5_K 12.0 -> 10.4,
+// Q4_K 9.8 -> 8.6, Q8_0 13.6 -> 12.4, Q4_0 9.6 -> 8.2, Q5_0 11.2 -> 10.1; 4 and 16 rows per workgroup measured slower
+// than 8 (Q6_K 15.1 and 14.9 us).
+constexpr int kP4Rows = 8;
+template <class U, class Out>
+__global__ __launch_bounds__(256) void k_mmvq_p4(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
+                                                 typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
+                                                 int nunits) {
+  __shared__ float part[4][kP4Rows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int u = 64 * wave + lane;
+  const bool has = u < nunits;
+  const int ul = has ? u : nunits + 64;  // (past the row: the buffer range check reads zeros)
+  typename U::A a;
+  U::load_a(act, has ? u : 0, a);
+  const int G = (int)gridDim.x, b = (int)blockIdx.x;
+  const int n = (nrows - b + G - 1) / G;  // this workgroup's rows, at most kP4Rows (the launcher's grid)
+  auto load = [&](int i, typename U::W &w) {
+    const bool live = i < n;
+    const row_buf src = make_row_buf(vx + (int64_t)(b + (live ? i : 0) * G) * row_bytes, live ? row_bytes : 0);
+    U::load_w(src, ul, w);
+  };
+  auto sum = [&](float acc) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc)), 63));
+  };
+  typename U::W wa, wb;
+  load(0, wa);
+  load(1, wb);
+  for (int i = 0; i < n; i += 2) {
+    float acc = has ? U::dot(wa, a, u) : 0.0f;
+    load(i + 2, wa);
+    part[wave][i] = sum(acc);  // (every lane writes the same value: no store behind a branch)
+    if (i + 1 >= n) break;
+    acc = has ? U::dot(wb, a, u) : 0.0f;
+    load(i + 3, wb);
+    part[wave][i + 1] = sum(acc);
+  }
+  __syncthreads();
+  const int t = (int)threadIdx.x;
+  if (t < n) Out::store(dst, (int64_t)b + (int64_t)t * G, ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t]);
+}
+
+// The four-wave form where the rows give every CU two workgroups of kP4Rows rows (fewer rows measured slower than
+// k_mmvq_p / k_mmvq_p2: Q6_K 1024 x 14336 5.1 -> 7.1 us)
+template <class U>
+bool use_p4(int units, int nc, int nrows) {
+  return nc == 1 && units > 128 && units <= 256 && qmm_ceil_div(nrows, kP4Rows) >= 2 * (int64_t)qmm_device_cus();
+}
+
+template <class U, class Out>
+void launch_p4(const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows, hipStream_t s) {
+  k_mmvq_p4<U, Out><<<dim3((unsigned)qmm_ceil_div(nrows, kP4Rows)), 256, 0, s>>>(vx, act, dst, nrows, U::row_bytes(k),
+                                                                                 U::units(k));
+}
+
 // Which types take k_mmvq_p2 for wide rows at one column.  On MI355X at 4096 x 14336, b = 1: Q4_K 10.7 -> 10.0 us,
 // IQ4_XS 10.65 -> 10.17, Q5_0 11.75 -> 11.22, Q4_0 9.8 -> 9.57, Q8_0 13.76 -> 13.54; slower for Q6_K (14.3 -> 14.9,
 // whose 84-byte units held twice over leave three waves per SIMD) and Q5_K (12.1 -> 12.5), which keep k_mmvq_p.
@@ -748,7 +808,9 @@ void launch_cols(const uint8_t *vx, const uint8_t *vy, typename Out::T *dst, int
     for (int j0 = 0; j0 < b; j0 += 8) {
       const int nc = b - j0 < 8 ? b - j0 : 8;
       const DecodeForm f = decode_form<U>(U::units(k), nc);
-      if (f.kernel == kFormP2)
+      if (use_p4<U>(U::units(k), nc, nrows))
+        launch_p4<U, Out>(vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows, s);
+      else if (f.kernel == kFormP2)
         launch_p2<U, Out>(nc, vx, vy + (int64_t)j0 * act_row_bytes, dst + (int64_t)j0 * stride_col_dst, k, nrows,
                           act_row_bytes, stride_col_dst, s);
       else

@@ -200,6 +200,23 @@ def test_wide_rows_at_one_column(gtype, shape):
     assert_parity(got, want, terms(gtype, aq, wq, b, n, k), what=f"type {gtype} n={n} k={k} b={b}")
 
 
+# Wide rows of at least 4,096 (two workgroups of 8 rows for every CU) at one column take the four-wave form
+# (k_mmvq_p4): 224 units (a half-idle fourth wave), 192 (an idle fourth wave), 132 (a mostly idle third wave), and a
+# ragged last workgroup (4,100 and 4,099 rows).
+P4_SHAPES = [(4100, 14336), (4096, 12288), (4099, 8448)]
+
+
+@pytest.mark.parametrize("gtype", [O.Q4K, O.Q8_0, O.Q4_0, O.Q5_0, O.IQ4XS, O.Q6K, O.Q5K])
+@pytest.mark.parametrize("shape", range(len(P4_SHAPES)))
+def test_wide_rows_four_waves(gtype, shape):
+    n, k = P4_SHAPES[shape]
+    rng = np.random.default_rng(1500 + 10 * gtype + shape)
+    wq = weight_bytes(gtype, n, k, rng, random_bytes=True)
+    x = acts(rng, 1, k)
+    got, want, _ = run_matvec(gtype, wq, x, n)
+    assert_parity(got, want, what=f"type {gtype} n={n} k={k}")
+
+
 @pytest.mark.parametrize("gtype", [O.Q4K, O.Q4_0])
 @pytest.mark.parametrize("out", ["f16", "bf16"])
 def test_wide_rows_half_outputs(gtype, out):
