@@ -137,7 +137,8 @@ def graph_time(torch, fn, steps, warmup):
 def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
     """The reference's decode step as two launches: launch_mmvq_gguf_quantize_* (f32 activation -> Q8 blocks) and
     launch_mmvq_gguf_<t>_f32_plain (the matvec), with the matvec alone timed in a second graph; for b <= 2 and
-    k <= 4096 also the same step as one launch, launch_mmvq_gguf_<t>_f32_quantize_plain (bit-identical output)."""
+    k <= 4096, or b = 1 and k <= 16384, also the same step as one launch, launch_mmvq_gguf_<t>_f32_quantize_plain
+    (bit-identical output)."""
     wq = quantized_weight(gtype, n, k, seed)
     ws = device_copies(torch, wq, copies)
     rng = np.random.default_rng(seed + 1)
@@ -169,7 +170,7 @@ def decode_workload(torch, qmm, gtype, n, k, b, copies, steps, warmup, seed):
         "kernel_gb_s": kernel_bytes / (t_kernel / steps) / 1e9, "kernel_bytes": kernel_bytes,
         "weights": wq, "x": x.cpu().numpy(), "y": y,
     }
-    if b <= 2 and k <= 4096 and gtype in (Q8_0, Q4K, Q6K):
+    if (b <= 2 and k <= 4096 or b == 1 and k <= 16384) and gtype in (Q8_0, Q4K, Q6K):
         t1 = graph_time(torch, one_launch, steps, warmup)
         if not np.array_equal(out.cpu().numpy().view(np.uint32), y.view(np.uint32)):
             raise RuntimeError("one-launch decode differs from the two-launch result")
@@ -212,7 +213,9 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     (launch_mmvq_gguf_q4_k_f32_fused_glu) over their shared input.  At b <= 2 the launches that can quantize their
     own f32 input do: q, k and v in one launch (launch_mmvq_gguf_q4_k_q6_k_f32_fused_qkv_quantize), o
     (launch_mmvq_gguf_q4_k_f32_quantize_plain) and gate / up (launch_mmvq_gguf_q4_k_f32_fused_glu_quantize), with the
-    same output bits as their two-launch forms; the down projection (K = 14336) keeps its quantizer.  Each input
+    same output bits as their two-launch forms; the down projection (K = 14336) quantizes its own input at b = 1
+    (launch_mmvq_gguf_q6_k_f32_quantize_plain, the same bits as its two launches) and keeps its quantizer at b = 2.
+    Each input
     takes QMatMul's route: the decode launcher up to 32 rows, except the Q6_K down projection (K = 14336) above 16
     rows, which takes the prefill matmul; one quantized activation per distinct input.  The inputs are synthetic, one
     per projection group."""
@@ -223,9 +226,10 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
     dev = {name: [torch.from_numpy(base[name]).cuda() for _ in range(layers)] for name, _, _, _ in shapes}
     total_bytes = sum(base[name].size for name, _, _, _ in shapes) * layers
     res = {"weight_bytes_per_step": total_bytes,
-           "launches_per_layer": "decode b <= 2: q/k/v in one launch, o and gate/up each in one, all three "
-                                 "quantizing their input, down quantize + matvec = 5; b 3..16: 4 quantize + 6 = 10; "
-                                 "b 17..32: the same with down on the prefill matmul = 10"}
+           "launches_per_layer": "decode b = 1: q/k/v in one launch, o, gate/up and down each in one, all four "
+                                 "quantizing their input = 4; b = 2: the same with down quantize + matvec = 5; "
+                                 "b 3..16: 4 quantize + 6 = 10; b 17..32: the same with down on the prefill matmul "
+                                 "= 10"}
     import qmm as Q
     for b in batches:
         rng = np.random.default_rng(seed + 100 + b)
@@ -248,7 +252,7 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
             for layer in range(layers):
                 for g, x in xs.items():
                     vy, kp = bufs[g]
-                    if one_launch and g != "down":
+                    if one_launch and (g != "down" or b == 1):
                         continue
                     if dec_of[g]:
                         Q.quantize_decode(Q4K, x, kp=kp, out=vy)
@@ -260,8 +264,11 @@ def stack_workload(torch, qmm, batches, steps, warmup, seed):
                     Q.mmvq_quantize(Q4K, dev["o"][layer], xs["o"], 4096, out=outs["o"])
                     Q.mmvq_fused_glu_quantize(Q4K, dev["gate"][layer], dev["up"][layer], xs["ffn"], 14336,
                                               out=outs["gate"])
-                    vy, kp = bufs["down"]
-                    Q.mmvq(Q6K, dev["down"][layer], vy, 14336, 4096, b, kp, out=outs["down"])
+                    if b == 1:
+                        Q.mmvq_quantize(Q6K, dev["down"][layer], xs["down"], 4096, out=outs["down"])
+                    else:
+                        vy, kp = bufs["down"]
+                        Q.mmvq(Q6K, dev["down"][layer], vy, 14336, 4096, b, kp, out=outs["down"])
                     continue
                 for name in ("q", "k", "v", "o", "gate", "down"):
                     vy, kp = bufs[group[name]]

@@ -138,8 +138,9 @@ QMM_DECLARE_MMVQ_PLAIN_SFX(q5_0, _q8_0)
  * gguf/ffi.rs:602-640, 846-876).  This one takes the f32 activation rows x[j * stride_col_x + k] (j < b_size,
  * k < ncols_x) and gives the same dst, bit for bit, as launch_mmvq_gguf_quantize_q8_1_f32 followed by
  * launch_mmvq_gguf_<t>_<dt>_plain (q4_k, q6_k) or launch_mmvq_gguf_quantize_q8_0_f32 followed by
- * launch_mmvq_gguf_q8_0_<dt>_plain_q8_0, in one launch and without the activation scratch buffer.  b_size 1 or 2;
- * ncols_x at most 4096 (a multiple of 64 for Q8_0). */
+ * launch_mmvq_gguf_q8_0_<dt>_plain_q8_0, in one launch and without the activation scratch buffer.  b_size 1 or 2
+ * with ncols_x at most 4096, or b_size 1 with ncols_x at most 16384 (x then 16-byte aligned); ncols_x a multiple
+ * of 64 for Q8_0. */
 #define QMM_DECLARE_MMVQ_QUANTIZE_PLAIN(t)                                                                        \
   void launch_mmvq_gguf_##t##_f32_quantize_plain(const void *vx, const float *x, void *dst, int ncols_x,          \
                                                  int nrows_x, int stride_col_x, int stride_col_dst, int b_size,  \

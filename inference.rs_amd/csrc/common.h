@@ -56,6 +56,11 @@ __device__ __forceinline__ int32_t sat_i8(float v) {
   v = v > 127.0f ? 127.0f : v;
   return (int32_t)v;
 }
+// The same value for an integral v (a rounded product), the clamp as one median of three (its NaN case never
+// reaches the conversion)
+__device__ __forceinline__ int32_t sat_i8_integral(float v) {
+  return v == v ? (int32_t)__builtin_amdgcn_fmed3f(v, -128.0f, 127.0f) : 0;
+}
 
 // Element loads of the three activation dtypes.
 // load4: the four values at p, p + 1, p + 2, p + 3 in one vector load (p aligned to four values)

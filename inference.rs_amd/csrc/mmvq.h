@@ -298,9 +298,13 @@ __global__ __launch_bounds__(256) void k_mmvq_p2(const uint8_t *__restrict__ vx,
 // Measured on MI355X at 4096 x 14336, b = 1, against k_mmvq_p / k_mmvq_p2: Q6_K 14.3 -> 13.5 us, Q5_K 12.0 -> 10.4,
 // Q4_K 9.8 -> 8.6, Q8_0 13.6 -> 12.4, Q4_0 9.6 -> 8.2, Q5_0 11.2 -> 10.1; 4 and 16 rows per workgroup measured slower
 // than 8 (Q6_K 15.1 and 14.9 us).
+//
+// QX: act is the f32 activation row, which every lane quantizes for its own unit (U::quantize_a) after requesting the
+// first two rows' weights, so the launch needs no quantizer before it.  Every workgroup quantizes the whole row again
+// (56 KB of f32 at K = 14336, from L2).
 constexpr int kP4Rows = 8;
-template <class U, class Out>
-__global__ __launch_bounds__(256) void k_mmvq_p4(const uint8_t *__restrict__ vx, const uint8_t *__restrict__ act,
+template <class U, class Out, bool QX = false>
+__global__ __launch_bounds__(256) void k_mmvq_p4(const uint8_t *__restrict__ vx, const void *__restrict__ act,
                                                  typename Out::T *__restrict__ dst, int nrows, int64_t row_bytes,
                                                  int nunits) {
   __shared__ float part[4][kP4Rows];
@@ -308,8 +312,6 @@ __global__ __launch_bounds__(256) void k_mmvq_p4(const uint8_t *__restrict__ vx,
   const int u = 64 * wave + lane;
   const bool has = u < nunits;
   const int ul = has ? u : nunits + 64;  // (past the row: the buffer range check reads zeros)
-  typename U::A a;
-  U::load_a(act, has ? u : 0, a);
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
   const int n = (nrows - b + G - 1) / G;  // this workgroup's rows, at most kP4Rows (the launcher's grid)
   auto load = [&](int i, typename U::W &w) {
@@ -320,9 +322,17 @@ __global__ __launch_bounds__(256) void k_mmvq_p4(const uint8_t *__restrict__ vx,
   auto sum = [&](float acc) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_to_lane63(acc)), 63));
   };
+  typename U::A a;
   typename U::W wa, wb;
-  load(0, wa);
-  load(1, wb);
+  if constexpr (QX) {
+    load(0, wa);
+    load(1, wb);
+    U::quantize_a((const float *)act, has ? u : 0, a);  // (a lane past the units quantizes the first, unused)
+  } else {
+    U::load_a((const uint8_t *)act, has ? u : 0, a);
+    load(0, wa);
+    load(1, wb);
+  }
   for (int i = 0; i < n; i += 2) {
     float acc = has ? U::dot(wa, a, u) : 0.0f;
     load(i + 2, wa);
@@ -344,10 +354,10 @@ bool use_p4(int units, int nc, int nrows) {
   return nc == 1 && units > 128 && units <= 256 && qmm_ceil_div(nrows, kP4Rows) >= 2 * (int64_t)qmm_device_cus();
 }
 
-template <class U, class Out>
-void launch_p4(const uint8_t *vx, const uint8_t *act, typename Out::T *dst, int k, int nrows, hipStream_t s) {
-  k_mmvq_p4<U, Out><<<dim3((unsigned)qmm_ceil_div(nrows, kP4Rows)), 256, 0, s>>>(vx, act, dst, nrows, U::row_bytes(k),
-                                                                                 U::units(k));
+template <class U, class Out, bool QX = false>
+void launch_p4(const uint8_t *vx, const void *act, typename Out::T *dst, int k, int nrows, hipStream_t s) {
+  k_mmvq_p4<U, Out, QX><<<dim3((unsigned)qmm_ceil_div(nrows, kP4Rows)), 256, 0, s>>>(vx, act, dst, nrows,
+                                                                                     U::row_bytes(k), U::units(k));
 }
 
 // Which types take k_mmvq_p2 for wide rows at one column.  On MI355X at 4096 x 14336, b = 1: Q4_K 10.7 -> 10.0 us,
@@ -1061,16 +1071,19 @@ void quantize_plain_t(const void *vx, const float *x, void *dst, int ncols_x, in
     qmm_set_error("%s: b_size=%d (1 or 2) stride_col_x=%d ncols_x=%d", who, b, stride_col_x, ncols_x);
     return;
   }
-  // one unit per lane; every activation block of the b rows within a few wave steps of one workgroup.  (Rows of
-  // four units per lane, K = 14336, quantized per workgroup the same way, measured slower on MI355X than the two
-  // launches: Q6_K 4096 x 14336 26.3 against 17.2 us, the 14336 values quantized again by every workgroup.)
-  if (ncols_x > 64 * 64) {
-    qmm_set_error("%s: ncols_x=%d (at most 4096)", who, ncols_x);
+  // Up to 4096 values: one unit per lane, every activation block of the b rows within a few wave steps of one
+  // workgroup, quantized into LDS.  (Rows of four units per lane, K = 14336, quantized into LDS the same way measured
+  // slower on MI355X than the two launches: Q6_K 4096 x 14336 26.3 against 17.2 us.)  Above, at one column: the
+  // four-wave form, each lane quantizing its own unit in registers.
+  const bool wide = ncols_x > 64 * 64;
+  if (wide && (b > 1 || ncols_x > 256 * 64)) {
+    qmm_set_error("%s: ncols_x=%d b_size=%d (at most 4096, or 16384 at b_size 1)", who, ncols_x, b);
     return;
   }
   const uintptr_t align = T == QMM_TYPE_Q6K ? 2 : (T == QMM_TYPE_Q8_0 ? 4 : 16);
-  if ((uintptr_t)vx % align != 0 || (uintptr_t)x % 4 != 0) {
-    qmm_set_error("%s: weights must be %zu-byte and x 4-byte aligned", who, (size_t)align);
+  const uintptr_t xalign = wide ? 16 : 4;
+  if ((uintptr_t)vx % align != 0 || (uintptr_t)x % xalign != 0) {
+    qmm_set_error("%s: weights must be %zu-byte and x %zu-byte aligned", who, (size_t)align, (size_t)xalign);
     return;
   }
   if (b == 0) return;
@@ -1079,7 +1092,9 @@ void quantize_plain_t(const void *vx, const float *x, void *dst, int ncols_x, in
   typename Out::T *d = (typename Out::T *)dst;
   typedef typename std::conditional<T == QMM_TYPE_Q4K, unit_q4k,
                                     typename std::conditional<T == QMM_TYPE_Q6K, unit_q6k, unit_q8_0>::type>::type U;
-  if (b == 1)
+  if (wide)
+    launch_p4<U, Out, true>(w, x, d, ncols_x, nrows_x, s);
+  else if (b == 1)
     launch_pq<U, Out, 1>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);
   else
     launch_pq<U, Out, 2>(w, x, stride_col_x, d, ncols_x, nrows_x, stride_col_dst, s);

@@ -80,6 +80,91 @@ __device__ __forceinline__ row_buf make_row_buf(const uint8_t *row, int64_t byte
   return {make_rsrc(row - m, bytes > 0 ? bytes + m : 0), m};
 }
 
+// Activations quantized by the lane that uses them (quantize_a, the one-launch decode over rows of more than 4096
+// values): one lane, one 64-value unit, read as 16 float4 from a 16-byte aligned f32 row.
+__device__ __forceinline__ void load_unit_f32(const float *x, const int (&off)[16], float (&v)[16][4]) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    const f32x4 f = *(const f32x4 *)(x + off[j]);
+    v[j][0] = f.x, v[j][1] = f.y, v[j][2] = f.z, v[j][3] = f.w;
+  }
+}
+
+// One lane's share of one 256-value Q8_K block: v[j] holds values off[j] .. off[j] + 3 of the block (off increasing in
+// j), and the block's four units sit on the four lanes of a quad, all of them live or none.  The block is quantized as
+// BlockQ8K::from_float does it (crates/inference-tensor/src/quantized/k_quants.rs:2721-2760), with the standalone
+// quantizer's single IEEE operations: m, the value of largest magnitude (the first in index order, which only matters
+// when both signs reach the maximum: then the quad finds the first), iscale = -127 / m, q = round(iscale * x)
+// saturated, d = 1 / iscale; a block whose maximum is 0 (or that holds no number) is zeros (iscale 0 makes every q 0:
+// 0 * x is a zero or a NaN).  NaNs are never the maximum (fmaxf / fminf drop them).  Leaves the lane's int8 values in
+// q (4 per dword, in v's order) and the sums of each four dwords in s16; returns d.
+__device__ __forceinline__ float q8k_unit(const float (&v)[16][4], const int (&off)[16], uint32_t (&q)[16],
+                                          int (&s16)[4]) {
+#pragma clang fp contract(off)
+  float hi = v[0][0], lo = v[0][0];
+#pragma unroll
+  for (int j = 0; j < 16; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) hi = fmaxf(hi, v[j][i]), lo = fminf(lo, v[j][i]);
+  float amax = fmaxf(hi, -lo);
+  amax = dpp_max<0xb1, 0xf>(amax);
+  amax = dpp_max<0x4e, 0xf>(amax);  // the block's, on its four lanes
+  int sg = (hi == amax ? 1 : 0) | (-lo == amax ? 2 : 0);
+  sg |= __builtin_amdgcn_update_dpp(0, sg, 0xb1, 0xf, 0xf, false);
+  sg |= __builtin_amdgcn_update_dpp(0, sg, 0x4e, 0xf, 0xf, false);
+  float m = sg == 2 ? -amax : amax;
+  if (sg == 3) {  // uniform over the quad
+    int key = 1024;  // 2 * index + sign of the lane's first value of magnitude amax
+#pragma unroll
+    for (int j = 15; j >= 0; j--)
+#pragma unroll
+      for (int i = 3; i >= 0; i--)
+        if (fabsf(v[j][i]) == amax) key = 2 * (off[j] + i) + (v[j][i] < 0.0f ? 1 : 0);
+    key = min(key, __builtin_amdgcn_update_dpp(0, key, 0xb1, 0xf, 0xf, false));
+    key = min(key, __builtin_amdgcn_update_dpp(0, key, 0x4e, 0xf, 0xf, false));
+    m = (key & 1) ? -amax : amax;
+  }
+  const bool nz = amax > 0.0f;
+  const float iscale = nz ? -127.0f / m : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w |= (uint32_t)(sat_i8_integral(roundf(iscale * v[j][i])) & 0xff) << (8 * i);
+    q[j] = w;
+  }
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    int s = 0;
+#pragma unroll
+    for (int j = 4 * g; j < 4 * g + 4; j++) s = sdot4((int)q[j], 0x01010101, s);
+    s16[g] = s;
+  }
+  return nz ? 1.0f / iscale : 0.0f;
+}
+
+// One 32-value Q8_0 block held by one lane (quantize_block32 + the f16 scale, crates/inference-tensor/src/quantized/
+// mod.rs:41-56, k_quants.rs:923-949, with the standalone quantizer's operations): v[0..8) are its values in order.
+// Leaves the int8 values in q and returns the scale as the matvec reads it back (f16-rounded).
+__device__ __forceinline__ float q8_0_unit_block(const float (*v)[4], uint32_t *q) {
+#pragma clang fp contract(off)
+  float amax = fmaxf(fmaxf(fabsf(v[0][0]), fabsf(v[0][1])), fmaxf(fabsf(v[0][2]), fabsf(v[0][3])));  // (NaN if all are)
+#pragma unroll
+  for (int j = 1; j < 8; j++)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][0]), fabsf(v[j][1])), fmaxf(fabsf(v[j][2]), fabsf(v[j][3]))));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w |= (uint32_t)(sat_i8_integral(roundf(v[j][i] * id)) & 0xff) << (8 * i);
+    q[j] = w;
+  }
+  return f16_bits_to_f32(f32_to_f16_bits(d));
+}
+
 // ------------------------------------------------------------------------------------------------ Q4_K
 struct unit_q4k {
   static constexpr int kType = QMM_TYPE_Q4K;
@@ -122,6 +207,18 @@ struct unit_q4k {
     a.b0 = (int)(int16_t)(s01 & 0xffff) + (int)(int16_t)(s01 >> 16);
     a.b1 = (int)(int16_t)(s23 & 0xffff) + (int)(int16_t)(s23 >> 16);
     a.d = __builtin_bit_cast(float, ld32(p));
+  }
+  // the same registers from the f32 row x (16-byte aligned): values 64c .. 64c + 63 of block u / 4
+  static __device__ __forceinline__ void quantize_a(const float *x, int u, A &a) {
+    int off[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) off[j] = 64 * (u & 3) + 4 * j;
+    float v[16][4];
+    load_unit_f32(x + 256 * (int64_t)(u >> 2), off, v);
+    int s[4];
+    a.d = q8k_unit(v, off, a.q, s);
+    a.b0 = s[0] + s[1];
+    a.b1 = s[2] + s[3];
   }
 
   // 6-bit scales and mins of sub-blocks 2c, 2c+1 (get_scale_min_k4, quantized/utils.rs:119-129)
@@ -224,6 +321,16 @@ struct unit_q6k {
     for (int q = 0; q < 4; q++) a.bs[q] = (int)(int16_t)(bw[q] >> (16 * p));  // bsums[8h + 2q + p]
     a.d = __builtin_bit_cast(float, ld32(p0));
   }
+  // the same registers from the f32 row x (16-byte aligned)
+  static __device__ __forceinline__ void quantize_a(const float *x, int u, A &a) {
+    const int h = (u >> 1) & 1, p = u & 1;
+    int off[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) off[j] = 128 * h + 32 * (j >> 2) + 16 * p + 4 * (j & 3);
+    float v[16][4];
+    load_unit_f32(x + 256 * (int64_t)(u >> 2), off, v);
+    a.d = q8k_unit(v, off, a.q, a.bs);
+  }
 
   static __device__ __forceinline__ float dot(const W &w, const A &a, int u) {
     uint32_t qa[4], qb[4], qh[4];
@@ -306,6 +413,16 @@ struct unit_q8_0 {
     uint32_t dw[17];
     load_raw(row + (int64_t)u * 68, dw);
     decode(dw, a);
+  }
+  // the same registers from the f32 row x (16-byte aligned): blocks 2u and 2u + 1
+  static __device__ __forceinline__ void quantize_a(const float *x, int u, A &a) {
+    int off[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) off[j] = 4 * j;
+    float v[16][4];
+    load_unit_f32(x + 64 * (int64_t)u, off, v);
+    a.da = q8_0_unit_block(v, a.qa);
+    a.db = q8_0_unit_block(v + 8, a.qb);
   }
 
   static __device__ __forceinline__ float dot(const W &wr, const A &a, int) {

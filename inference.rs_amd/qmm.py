@@ -240,8 +240,8 @@ def mmvq(wtype: int, w, vy, k: int, n: int, b: int, kp: int, out_dtype=None, out
 
 
 def mmvq_quantize(wtype: int, w, x, n: int, out_dtype=None, out=None):
-    """Decode matvec from f32 activations x [b, k] (b <= 2, k <= 4096), quantized inside the launch:
-    launch_mmvq_gguf_<t>_<dtype>_quantize_plain."""
+    """Decode matvec from f32 activations x [b, k] (b <= 2 and k <= 4096, or b = 1 and k <= 16384), quantized
+    inside the launch: launch_mmvq_gguf_<t>_<dtype>_quantize_plain."""
     torch = _torch()
     b, k = x.shape
     if out is None:

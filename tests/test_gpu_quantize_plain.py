@@ -76,7 +76,83 @@ def test_strided_unaligned_rows():
     assert_parity(one, O.matmul(O.Q6K, x, wq, n))
 
 
-@pytest.mark.parametrize("gtype,k,b", [(O.Q4K, 8192, 1), (O.Q4K, 1024, 3), (O.Q8_0, 1056, 1)])
+def wide_row(rng, k):
+    """One row over k > 4096 values with the blocks the per-lane quantizer must get right: a zero Q8_K block, tied
+    maxima of opposite signs in different lanes (the first in index order wins) both ways round and within one lane,
+    tied maxima of one sign, a block whose maximum sits in its last value."""
+    x = acts(rng, 1, k)
+    x[0, ::64] *= 60.0
+    x[0, 256:512] = 0.0
+    x[0, 512 + 3], x[0, 512 + 16] = 900.0, -900.0        # Q6_K: lane 0 before lane 1; Q4_K / Q8_0: one lane
+    x[0, 768 + 200], x[0, 768 + 40] = 900.0, -900.0      # the negative one first, in another quarter
+    x[0, 1024 + 130], x[0, 1024 + 131] = -900.0, 900.0   # adjacent, one lane
+    x[0, 1280 + 7], x[0, 1280 + 250] = 900.0, 900.0
+    x[0, 1536 + 255] = -900.0
+    x[0, k - 256 + 64], x[0, k - 256 + 192] = 900.0, -900.0
+    return x
+
+
+WIDE = [(O.Q6K, 4096, 14336), (O.Q6K, 37, 4352), (O.Q6K, 1000, 16384), (O.Q4K, 4096, 14336), (O.Q4K, 203, 8192),
+        (O.Q8_0, 4096, 14336), (O.Q8_0, 77, 4160), (O.Q8_0, 16, 16384)]
+
+
+def same_kernel_as_two_launches(n, k):
+    """The wide one-launch form is the four-wave matvec; the plain matvec takes that kernel itself for rows of 129 to
+    256 units when the rows give every CU two workgroups of 8 rows, and then the bits match."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return 128 < k // 64 <= 256 and (n + 7) // 8 >= 2 * cus
+
+
+@pytest.mark.parametrize("gtype,n,k", WIDE)
+def test_wide_rows_one_column(gtype, n, k):
+    """Above 4096 values at one column each lane quantizes its own unit in registers: parity with the oracle, the
+    same bits as the two launches where the matvec is the same kernel, and the same bits call after call."""
+    rng = np.random.default_rng(17 * gtype + n + k)
+    wq = O.quantize(gtype, weights(rng, n, k))
+    x = wide_row(rng, k)
+    wd, xd = to_dev(wq), to_dev(x)
+    one = qmm.mmvq_quantize(gtype, wd, xd, n).cpu().numpy()
+    assert_parity(one, O.matmul(gtype, x, wq, n), what=f"t{gtype} n{n} k{k}")
+    vy, kp = qmm.quantize_decode(gtype, xd)
+    two = qmm.mmvq(gtype, wd, vy, k, n, 1, kp).cpu().numpy()
+    if same_kernel_as_two_launches(n, k):
+        assert np.array_equal(one.view(np.uint32), two.view(np.uint32)), f"t{gtype} n{n} k{k}"
+    else:
+        assert_parity(two, O.matmul(gtype, x, wq, n), what=f"two launches t{gtype} n{n} k{k}")
+    again = qmm.mmvq_quantize(gtype, wd, xd, n).cpu().numpy()
+    assert np.array_equal(again.view(np.uint32), one.view(np.uint32))
+
+
+SPECIAL = {
+    "nan": lambda x, r: (x.__setitem__((0, 2048 + 5), np.nan), x.__setitem__((0, slice(2304, 2560)), np.nan)),
+    "inf_both_signs": lambda x, r: (x.__setitem__((0, 2560 + 100), np.inf), x.__setitem__((0, 2560 + 20), -np.inf)),
+    "inf": lambda x, r: x.__setitem__((0, 2816 + 33), -np.inf),
+    "tiny": lambda x, r: x.__setitem__((0, slice(3072, 3328)), r.standard_normal(256).astype(np.float32) * 1e-39),
+    "smallest": lambda x, r: x.__setitem__((0, slice(3328, 3584)), np.float32(1e-45)),
+    "negative_zero": lambda x, r: x.__setitem__((0, slice(3584, 3840)), -0.0),
+}
+
+
+@pytest.mark.parametrize("gtype", [O.Q6K, O.Q4K, O.Q8_0])
+def test_wide_rows_special_values(gtype):
+    """NaN (never the maximum, quantized to 0), infinities (tied of both signs, and alone), blocks of values so
+    small that -127 / max overflows (saturated quantization), negative zeros: the same bits as the two launches,
+    each case in a row of its own (an infinity makes every output NaN)."""
+    rng = np.random.default_rng(23 + gtype)
+    n, k = 4096, 14336
+    assert same_kernel_as_two_launches(n, k)
+    wd = to_dev(O.quantize(gtype, weights(rng, n, k)))
+    for name, plant in SPECIAL.items():
+        x = wide_row(rng, k)
+        plant(x, rng)
+        xd = to_dev(x)
+        vy, kp = qmm.quantize_decode(gtype, xd)
+        two = qmm.mmvq(gtype, wd, vy, k, n, 1, kp).cpu().numpy()
+        one = qmm.mmvq_quantize(gtype, wd, xd, n).cpu().numpy()
+        assert np.array_equal(one.view(np.uint32), two.view(np.uint32)), f"t{gtype} {name}"
+
+
+@pytest.mark.parametrize("gtype,k,b", [(O.Q4K, 8192, 2), (O.Q6K, 16640, 1), (O.Q4K, 1024, 3), (O.Q8_0, 1056, 1)])
 def test_rejected_shapes_launch_nothing(gtype, k, b):
     rng = np.random.default_rng(7)
     n = 16
