@@ -26,6 +26,7 @@
 #pragma clang fp contract(off)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 16 bytes from a 16-byte aligned address
 __device__ __forceinline__ u32x4 ld_a16(const uint8_t *p) { return *(const u32x4 *)p; }
@@ -56,6 +57,11 @@ struct row_ptr {
   __device__ __forceinline__ u32x4 a16(int o) const { return ld_a16(p + o); }
   __device__ __forceinline__ u32x4 a4x16(int o) const { return ld_a4(p + o); }
   __device__ __forceinline__ uint32_t x4(int o) const { return ld32(p + o); }
+  __device__ __forceinline__ u32x2 x8(int o) const {
+    u32x2 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p + o, 4), 8);
+    return v;
+  }
   __device__ __forceinline__ uint32_t x2(int o) const { return ld16(p + o); }
   __device__ __forceinline__ uint32_t mis(int o) const { return (uint32_t)((uintptr_t)(p + o) & 3); }
 };
@@ -68,6 +74,9 @@ struct row_buf {
   __device__ __forceinline__ u32x4 a4x16(int o) const { return a16(o); }
   __device__ __forceinline__ uint32_t x4(int o) const {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)(o + (int)m), 0, 0);
+  }
+  __device__ __forceinline__ u32x2 x8(int o) const {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)(o + (int)m), 0, 0);
   }
   __device__ __forceinline__ uint32_t x2(int o) const {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)(o + (int)m), 0, 0);
@@ -270,7 +279,8 @@ struct unit_q6k {
     u32x4 qa, qb, qh;      // the dwords covering 16 bytes at a 2-byte aligned address each
     uint32_t ea, eb, eh;   // and the dword after each
     uint32_t off;          // the unit's byte offset within those dwords: 0 or 2
-    uint32_t sc[4];        // 16-bit loads holding the four int8 scales
+    u32x2 sc;              // the dwords from the one holding the unit's first int8 scale (scales 8h .. 8h + 7)
+    uint32_t se;           // and the dword holding the last when off = 2 (the second again when off = 0)
     uint32_t d;            // f16 bits
   };
   struct A {
@@ -298,8 +308,8 @@ struct unit_q6k {
     w.eb = r.x4(a4 + 64 * h + 32 + 16 * p + 16);
     w.qh = r.a4x16(a4 + 128 + 32 * h + 16 * p);
     w.eh = r.x4(a4 + 128 + 32 * h + 16 * p + 16);
-#pragma unroll
-    for (int q = 0; q < 4; q++) w.sc[q] = r.x2(sb + 192 + 8 * h + 2 * q);
+    w.sc = r.x8(a4 + 192 + 8 * h);  // (8 scale bytes in 2 or 3 dwords: no dword past the block is read)
+    w.se = r.x4(a4 + 192 + 8 * h + (w.off ? 8 : 4));
     w.d = r.x2(sb + 208);
   }
   static __device__ __forceinline__ void load_w(const uint8_t *row, int u, W &w) { load_w(row_ptr{row}, u, w); }
@@ -338,6 +348,8 @@ struct unit_q6k {
     realign(w.qb, w.eb, w.off, qb);
     realign(w.qh, w.eh, w.off, qh);
     const int p = u & 1;
+    // scales 8h .. 8h + 7 as two dwords; scale q of this unit is byte 2q + p
+    const uint32_t scw[2] = {align_bytes(w.sc.y, w.sc.x, w.off), align_bytes(w.se, w.sc.y, w.off)};
     int isum = 0;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -349,7 +361,7 @@ struct unit_q6k {
         const uint32_t v = ((src[k] >> nsh) & 0x0f0f0f0fu) | (((qh[k] >> (2 * q)) & 0x03030303u) << 4);
         s = sdot4((int)v, (int)a.q[4 * q + k], s);
       }
-      const int sc = (int)(int8_t)(w.sc[q] >> (8 * p));
+      const int sc = (int)(int8_t)(scw[q >> 1] >> (16 * (q & 1) + 8 * p));
       isum += sc * (s - 32 * a.bs[q]);  // (q6 - 32) . q8 = q6 . q8 - 32 * bsum
     }
     return a.d * f16_bits_to_f32(w.d) * (float)isum;
