@@ -49,17 +49,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
-// Rust's `f32 as i8`: saturating, NaN -> 0
-__device__ __forceinline__ int32_t sat_i8(float v) {
-  if (v != v) return 0;
-  v = v < -128.0f ? -128.0f : v;
-  v = v > 127.0f ? 127.0f : v;
-  return (int32_t)v;
-}
-// The same value for an integral v (a rounded product), the clamp as one median of three (its NaN case never
-// reaches the conversion)
-__device__ __forceinline__ int32_t sat_i8_integral(float v) {
-  return v == v ? (int32_t)__builtin_amdgcn_fmed3f(v, -128.0f, 127.0f) : 0;
+// Rust's `p.round() as i8` (saturating, NaN -> 0) in four operations: round (half away from zero) is
+// trunc(p + copysign(0.5 - 2^-25, p)) with
+// the f32 add rounding to nearest even (equal for every f32 of magnitude below 256, checked exhaustively against
+// floor(|p| + 0.5) in double; above 128 the clamp decides either way), the clamp is one median of three before the
+// truncating conversion, and NaN gives 0 through a select.
+__device__ __forceinline__ int32_t round_sat_i8(float p) {
+#pragma clang fp contract(off)
+  const float t = p + __builtin_copysignf(0.49999997f, p);
+  return p == p ? (int32_t)__builtin_amdgcn_fmed3f(t, -128.0f, 127.0f) : 0;
 }
 
 // Element loads of the three activation dtypes.

@@ -96,7 +96,7 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
     const float iscale = nz ? -127.0f / m : 0.0f;
     int q[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) q[i] = nz ? sat_i8(roundf(iscale * x[i])) : 0;
+    for (int i = 0; i < 4; i++) q[i] = nz ? round_sat_i8(iscale * x[i]) : 0;
     const int s = quad_sum(q[0] + q[1] + q[2] + q[3]);  // values 16 (lane / 4) .. +16
     // row_shr:4: lane 8i + 4 adds the sum of the quad before it, values 32 i .. +32
     const int s32 = s + __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xf, false);
@@ -123,7 +123,8 @@ __device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst
 // `store`.  Every lane of the wave takes part (the 8-lane maximum goes through DPP within each group of 8).
 __device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs, uint16_t *d_out, bool store) {
 #pragma clang fp contract(off)
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  // from 0, as the reference's fold(0, max(|v|)) starts: a block of NaNs has d = 0
+  float amax = fmaxf(0.0f, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   amax = dpp_max<0xb1, 0xf>(amax);
   amax = dpp_max<0x4e, 0xf>(amax);
   amax = dpp_max<0x141, 0xf>(amax);  // row_half_mirror: the other quad of the group of 8
@@ -131,7 +132,7 @@ __device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   int q[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(v[i] * id));
+  for (int i = 0; i < 4; i++) q[i] = round_sat_i8(v[i] * id);
   if (!store) return;
   // qs may be only 2-byte aligned (34-byte blocks): two 16-bit stores
   uint16_t *q16 = (uint16_t *)(qs + 4 * sub);

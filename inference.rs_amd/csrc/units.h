@@ -140,7 +140,7 @@ __device__ __forceinline__ float q8k_unit(const float (&v)[16][4], const int (&o
   for (int j = 0; j < 16; j++) {
     uint32_t w = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) w |= (uint32_t)(sat_i8_integral(roundf(iscale * v[j][i])) & 0xff) << (8 * i);
+    for (int i = 0; i < 4; i++) w |= (uint32_t)(round_sat_i8(iscale * v[j][i]) & 0xff) << (8 * i);
     q[j] = w;
   }
 #pragma unroll
@@ -158,9 +158,9 @@ __device__ __forceinline__ float q8k_unit(const float (&v)[16][4], const int (&o
 // Leaves the int8 values in q and returns the scale as the matvec reads it back (f16-rounded).
 __device__ __forceinline__ float q8_0_unit_block(const float (*v)[4], uint32_t *q) {
 #pragma clang fp contract(off)
-  float amax = fmaxf(fmaxf(fabsf(v[0][0]), fabsf(v[0][1])), fmaxf(fabsf(v[0][2]), fabsf(v[0][3])));  // (NaN if all are)
+  float amax = 0.0f;  // (the reference's fold(0, max(|v|)): a block of NaNs has d = 0)
 #pragma unroll
-  for (int j = 1; j < 8; j++)
+  for (int j = 0; j < 8; j++)
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j][0]), fabsf(v[j][1])), fmaxf(fabsf(v[j][2]), fabsf(v[j][3]))));
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
@@ -168,7 +168,7 @@ __device__ __forceinline__ float q8_0_unit_block(const float (*v)[4], uint32_t *
   for (int j = 0; j < 8; j++) {
     uint32_t w = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) w |= (uint32_t)(sat_i8_integral(roundf(v[j][i] * id)) & 0xff) << (8 * i);
+    for (int i = 0; i < 4; i++) w |= (uint32_t)(round_sat_i8(v[j][i] * id) & 0xff) << (8 * i);
     q[j] = w;
   }
   return f16_bits_to_f32(f32_to_f16_bits(d));

@@ -66,6 +66,37 @@ def test_q8_0_decode_quantizer_is_bit_exact(k, src):
     assert np.array_equal(vy.cpu().numpy(), O.quantize(O.Q8_0, xp).reshape(-1))
 
 
+def special_value_row(k=2048):
+    """NaN (a whole 32-value block, a single value, a whole 256-value block), an infinity, tiny normal values for which
+    -127 / max overflows (saturated quantization) and negative zeros."""
+    x = np.random.default_rng(9).standard_normal((2, k)).astype(np.float32)
+    x[0, 0:32] = np.nan
+    x[0, 40] = np.nan
+    x[0, 256:512] = np.nan
+    x[0, 512 + 7] = np.inf
+    x[0, 768:1024] *= np.float32(1e-37)
+    x[0, 1024:1280] = -0.0
+    x[1, 300] = -np.inf
+    return x
+
+
+@pytest.mark.parametrize("qt", ["q8k", "q8_0"])
+def test_decode_quantizers_on_special_values(qt):
+    """The Q8_K slot quantizer and the Q8_0 block quantizer against the oracle, byte for byte, on NaN, infinite,
+    overflowing and zero blocks (a block of NaNs: d = 0, as the reference's fold from 0 gives it)."""
+    x = special_value_row()
+    k = x.shape[1]
+    if qt == "q8k":
+        vy, kp = qmm.quantize_decode(qmm.Q4K, to_dev(x))
+        xp = np.zeros((2, kp), np.float32)
+        xp[:, :k] = x
+        got = decode_act_blocks(O.Q4K, vy.cpu().numpy(), 2, kp)
+        assert np.array_equal(got.view(np.uint8), O.quantize(O.Q8K, xp).reshape(-1).view(np.uint8))
+    else:
+        vy, kp = qmm.quantize_decode(qmm.Q8_0, to_dev(x))
+        assert np.array_equal(vy.cpu().numpy(), O.quantize(O.Q8_0, x).reshape(-1))
+
+
 def test_q8_0_quantizer_on_the_reference_known_answer_blocks():
     import test_oracle as T
     x = np.stack(T.reference_test_blocks()).reshape(1, -1)
