@@ -96,7 +96,7 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
     const float iscale = nz ? -127.0f / m : 0.0f;
     int q[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) q[i] = nz ? round_sat_i8(iscale * x[i]) : 0;
+    for (int i = 0; i < 4; i++) q[i] = round_sat_i8(iscale * x[i]);  // (iscale 0: every q is 0)
     const int s = quad_sum(q[0] + q[1] + q[2] + q[3]);  // values 16 (lane / 4) .. +16
     // row_shr:4: lane 8i + 4 adds the sum of the quad before it, values 32 i .. +32
     const int s32 = s + __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xf, false);
