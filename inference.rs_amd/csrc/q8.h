@@ -90,8 +90,12 @@ __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, cons
     const float amax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[t]), 63));
     const bool nz = amax > 0.0f;
     const float *x = v[t];
-    const float first = fabsf(x[0]) == amax ? x[0] : fabsf(x[1]) == amax ? x[1] : fabsf(x[2]) == amax ? x[2] : x[3];
-    const int holder = __builtin_ctzll(__ballot(am[t] == amax)) & 63;
+    float first = x[3];  // this lane's first value of magnitude amax (selects, latest index first)
+    first = fabsf(x[2]) == amax ? x[2] : first;
+    first = fabsf(x[1]) == amax ? x[1] : first;
+    first = fabsf(x[0]) == amax ? x[0] : first;
+    // the first lane holding it (lane 63's bit keeps the count defined for a block with no number)
+    const int holder = __builtin_ctzll(__ballot(am[t] == amax) | (1ull << 63));
     const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, first), holder));
     const float iscale = nz ? -127.0f / m : 0.0f;
     int q[4];
