@@ -132,6 +132,12 @@ __device__ __forceinline__ float dpp_max(float v) {
   return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
                                                                         0xf, false)));
 }
+// The same over unsigned values (0 is the identity)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+  return v > o ? v : o;
+}
 __device__ __forceinline__ float wave_max_nonneg(float v) {
   v = dpp_max<0xb1, 0xf>(v);
   v = dpp_max<0x4e, 0xf>(v);

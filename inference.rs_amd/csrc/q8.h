@@ -69,25 +69,31 @@ template <int G>
 __device__ __forceinline__ void q8k_waves(const float (&v)[G][4], int lane, const q8k_dst (&dst)[G],
                                           const bool (&store)[G]) {
 #pragma clang fp contract(off)
-  float am[G], mx[G];
-#pragma unroll
-  for (int t = 0; t < G; t++)
-    am[t] = fmaxf(fmaxf(fabsf(v[t][0]), fabsf(v[t][1])), fmaxf(fabsf(v[t][2]), fabsf(v[t][3])));
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0xb1, 0xf>(am[t]);
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x4e, 0xf>(mx[t]);
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x141, 0xf>(mx[t]);
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x140, 0xf>(mx[t]);
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x142, 0xa>(mx[t]);
-#pragma unroll
-  for (int t = 0; t < G; t++) mx[t] = dpp_max<0x143, 0xc>(mx[t]);
+  // The wave maximum runs on the bit patterns: for non-negative floats their unsigned order is the numeric one, a
+  // lane whose four values are all NaN takes part as 0 (fmaxf drops NaNs), and one max per DPP step needs no
+  // canonicalizing of its operands.
+  float am[G];
+  uint32_t mx[G];
 #pragma unroll
   for (int t = 0; t < G; t++) {
-    const float amax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[t]), 63));
+    am[t] = fmaxf(fmaxf(fabsf(v[t][0]), fabsf(v[t][1])), fmaxf(fabsf(v[t][2]), fabsf(v[t][3])));
+    mx[t] = am[t] == am[t] ? __builtin_bit_cast(uint32_t, am[t]) : 0u;
+  }
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0xb1, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0x4e, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0x141, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0x140, 0xf>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0x142, 0xa>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) mx[t] = dpp_max_u32<0x143, 0xc>(mx[t]);
+#pragma unroll
+  for (int t = 0; t < G; t++) {
+    const float amax = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)mx[t], 63));
     const bool nz = amax > 0.0f;
     const float *x = v[t];
     float first = x[3];  // this lane's first value of magnitude amax (selects, latest index first)
@@ -128,10 +134,13 @@ __device__ __forceinline__ void q8k_wave(const float v[4], int lane, q8k_dst dst
 __device__ __forceinline__ void q8_0_group(const float v[4], int sub, int8_t *qs, uint16_t *d_out, bool store) {
 #pragma clang fp contract(off)
   // from 0, as the reference's fold(0, max(|v|)) starts: a block of NaNs has d = 0
-  float amax = fmaxf(0.0f, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-  amax = dpp_max<0xb1, 0xf>(amax);
-  amax = dpp_max<0x4e, 0xf>(amax);
-  amax = dpp_max<0x141, 0xf>(amax);  // row_half_mirror: the other quad of the group of 8
+  const float am = fmaxf(0.0f, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  // (on the bit patterns of these non-negative, NaN-free values, as in q8k_waves)
+  uint32_t mb = __builtin_bit_cast(uint32_t, am);
+  mb = dpp_max_u32<0xb1, 0xf>(mb);
+  mb = dpp_max_u32<0x4e, 0xf>(mb);
+  mb = dpp_max_u32<0x141, 0xf>(mb);  // row_half_mirror: the other quad of the group of 8
+  const float amax = __builtin_bit_cast(float, mb);
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   int q[4];

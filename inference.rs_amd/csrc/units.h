@@ -116,9 +116,13 @@ __device__ __forceinline__ float q8k_unit(const float (&v)[16][4], const int (&o
   for (int j = 0; j < 16; j++)
 #pragma unroll
     for (int i = 0; i < 4; i++) hi = fmaxf(hi, v[j][i]), lo = fminf(lo, v[j][i]);
-  float amax = fmaxf(hi, -lo);
-  amax = dpp_max<0xb1, 0xf>(amax);
-  amax = dpp_max<0x4e, 0xf>(amax);  // the block's, on its four lanes
+  // the block's on its four lanes, on the bit patterns (as in q8k_waves): fabsf keeps a zero maximum +0, and a lane of
+  // NaNs takes part as 0
+  const float la = fabsf(fmaxf(hi, -lo));
+  uint32_t mb = la == la ? __builtin_bit_cast(uint32_t, la) : 0u;
+  mb = dpp_max_u32<0xb1, 0xf>(mb);
+  mb = dpp_max_u32<0x4e, 0xf>(mb);
+  const float amax = __builtin_bit_cast(float, mb);
   int sg = (hi == amax ? 1 : 0) | (-lo == amax ? 2 : 0);
   sg |= __builtin_amdgcn_update_dpp(0, sg, 0xb1, 0xf, 0xf, false);
   sg |= __builtin_amdgcn_update_dpp(0, sg, 0x4e, 0xf, 0xf, false);
