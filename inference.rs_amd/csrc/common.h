@@ -50,14 +50,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 }
 
 // Rust's `p.round() as i8` (saturating, NaN -> 0) in four operations: round (half away from zero) is
-// trunc(p + copysign(0.5 - 2^-25, p)) with
-// the f32 add rounding to nearest even (equal for every f32 of magnitude below 256, checked exhaustively against
-// floor(|p| + 0.5) in double; above 128 the clamp decides either way), the clamp is one median of three before the
-// truncating conversion, and NaN gives 0 through a select.
+// trunc(p + copysign(0.5 - 2^-25, p)) with the f32 add rounding to nearest even (equal for every f32 of magnitude
+// below 256, checked exhaustively against floor(|p| + 0.5) in double; above 128 the saturation decides either way),
+// the truncation is the hardware conversion v_cvt_i32_f32 (NaN -> 0, out of range -> the nearest int32), and the
+// clamp to -128..127 one integer median of three.
 __device__ __forceinline__ int32_t round_sat_i8(float p) {
 #pragma clang fp contract(off)
   const float t = p + __builtin_copysignf(0.49999997f, p);
-  return p == p ? (int32_t)__builtin_amdgcn_fmed3f(t, -128.0f, 127.0f) : 0;
+  int32_t i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(t));  // the hardware conversion: NaN -> 0, out of range saturates
+  return i < -128 ? -128 : (i > 127 ? 127 : i);
 }
 
 // Element loads of the three activation dtypes.

@@ -28,7 +28,7 @@ def test_saturation_and_specials():
         if p != p:
             return 0
         t = np.float32(p + np.copysign(h, p))
-        return int(np.trunc(min(max(t, np.float32(-128.0)), np.float32(127.0))))
+        return int(min(max(np.trunc(t), -128.0), 127.0))  # truncating conversion, then the clamp
 
     def rust(p):
         if p != p:
